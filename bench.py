@@ -1,0 +1,200 @@
+"""WKV7 benchmark on one MI355X.
+
+Default workload: WKV7 forward (saving the state every 16
+steps) + backward, B=4, T=2048, H=80, N=64, bf16 I/O, fp32 state, s0 ~
+N(0,0.1), dsT = 0, synthetic inputs resident in HBM.  One step = one forward
+and one backward over the batch, through the C ABI (theseus.wkv7.extension()).
+
+Prints ONE JSON line: tokens/s, achieved algorithmic HBM GB/s of the whole
+fwd+bwd and, as ``roofline``, that of the dominant kernel timed with HIP
+events on the stream the kernels run on; ``cpu_baseline`` times the
+reference's PyTorch op sequence (float32, autograd) on the host cores over a
+bounded slice of the same workload.
+
+Algorithmic bytes (compulsory contract I/O; E = H*N, S_l = H*N*N*4 bytes):
+  forward  = B*T*E*2*7  + 2*B*S_l   (r,w,k,v,a,b in, y out; s0 in, sT out)
+  backward = B*T*E*2*13 + 3*B*S_l   (r..b, dy in; six grads out; s0, dsT in, ds0 out)
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "rwkv-theseus_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "WKV7 fwd+bwd tokens/s (H=80,N=64,bf16) + achieved HBM GB/s as % of peak"
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    # name: B, T, H, N, s0_std, seed
+    "c2": dict(B=4, T=2048, H=80, N=64, s0_std=0.1, seed=20262),
+    "c1": dict(B=1, T=4096, H=80, N=64, s0_std=0.0, seed=20261),
+    "c4": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
+}
+
+
+def alg_bytes(B, T, H, N, which):
+    E, Sl = H * N, H * N * N * 4
+    if which == "fwd":
+        return B * T * E * 2 * 7 + 2 * B * Sl
+    if which == "bwd":
+        return B * T * E * 2 * 13 + 3 * B * Sl
+    if which == "decode":  # one T=1 step over B lanes
+        return B * E * 2 * 7 + 2 * B * Sl
+    raise ValueError(which)
+
+
+def cpu_baseline(B, H, N, T_slice, seed):
+    """Reference op sequence (oracle.reference_torch = theseus/wkv7.py:16-28 restated),
+    float32 autograd fwd+bwd on the host cores over a T-slice of the workload."""
+    import torch
+    from oracle import wkv7_oracle as O
+    from theseus.synthetic import wkv7_inputs
+
+    cores = O.cpu_count()
+    torch.set_num_threads(cores)
+    inp = wkv7_inputs(B, T_slice, H, N, seed=seed, dtype=torch.float32, s0_std=0.1)
+    xs = [inp[n].clone().requires_grad_() for n in "rwkvab"]
+    s0 = inp["s0"].clone().requires_grad_()
+    t0 = time.perf_counter()
+    y, sT = O.reference_torch(*xs, s0)
+    torch.autograd.backward((y, sT), (inp["dy"], torch.zeros_like(sT)))
+    dt = time.perf_counter() - t0
+    return {"value": round(B * T_slice / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"B={B} H={H} N={N} T={T_slice} slice of the workload, fp32 torch autograd "
+                      f"fwd+bwd of the reference op sequence, {dt:.1f} s on {O.cpu_model()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-slice", type=int, default=128, help="T of the CPU baseline slice (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(the recurrence shards over batch x heads with no exchange; "
+                          "multi-GPU runs are out of scope here)"}))
+        sys.exit(2)
+
+    import torch
+    from theseus import wkv7 as W
+    from theseus.synthetic import wkv7_inputs
+
+    cfg = CONFIGS[args.config]
+    B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ext = W.extension()
+    inp = wkv7_inputs(B, T, H, N, seed=cfg["seed"], dtype=torch.bfloat16, s0_std=cfg["s0_std"])
+    xs = [inp[n].to(dev) for n in "rwkvab"]
+    s0 = inp["s0"].to(dev)
+    dy = inp["dy"].to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    if args.config == "c4":
+        # decode: T in-place single steps per "step"; compared with one fused T-step forward
+        steps_in = [[x[:, t:t + 1].contiguous() for x in xs] for t in range(T)]
+        state = s0.clone()
+
+        def one_step():
+            for t in range(T):
+                ext.decode_step(*steps_in[t], state)
+    else:
+        def one_step():
+            y, end, saved = ext.forward(*xs, s0, True)
+            if args.config == "c1":
+                return
+            ext.backward(*xs, saved, dy, None)
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+
+    # -- timed region: exactly K steps ---------------------------------------------------
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    tokens = B * T
+    value = tokens * args.steps / elapsed
+
+    # -- per-kernel durations with HIP events on the launch stream -----------------------
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    kern = {}
+    if args.config == "c4":
+        e0, e1 = ev(), ev()
+        e0.record(stream)
+        for t in range(T):
+            ext.decode_step(*steps_in[t], state)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kern["decode"] = (e0.elapsed_time(e1) / T, alg_bytes(B, 1, H, N, "decode"))
+    else:
+        fwd_ms, bwd_ms = [], []
+        for _ in range(max(3, min(args.steps, 10))):
+            a0, a1, a2 = ev(), ev(), ev()
+            a0.record(stream)
+            y, end, saved = ext.forward(*xs, s0, True)
+            a1.record(stream)
+            if args.config != "c1":
+                ext.backward(*xs, saved, dy, None)
+            a2.record(stream)
+            torch.cuda.synchronize()
+            fwd_ms.append(a0.elapsed_time(a1))
+            bwd_ms.append(a1.elapsed_time(a2))
+        kern["fwd"] = (sum(fwd_ms) / len(fwd_ms), alg_bytes(B, T, H, N, "fwd"))
+        if args.config != "c1":
+            kern["bwd"] = (sum(bwd_ms) / len(bwd_ms), alg_bytes(B, T, H, N, "bwd"))
+    dom = max(kern, key=lambda k: kern[k][0])
+    dom_ms, dom_bytes = kern[dom]
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+
+    if args.config == "c4":
+        step_bytes = alg_bytes(B, 1, H, N, "decode") * T
+    else:
+        step_bytes = alg_bytes(B, T, H, N, "fwd") + (0 if args.config == "c1" else alg_bytes(B, T, H, N, "bwd"))
+    step_gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    cpu = None
+    if args.cpu_slice and args.config == "c2":
+        cpu = cpu_baseline(B, H, N, args.cpu_slice, cfg["seed"])
+
+    workload = {"c2": "wkv7_fwd_bwd", "c1": "wkv7_fwd", "c4": "wkv7_decode"}[args.config]
+    line = {
+        "metric": METRIC if args.config == "c2" else f"WKV7 {workload} tokens/s ({args.config})",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": workload, "B": B, "T": T, "H": H, "N": N, "io_dtype": "bf16",
+                   "state_dtype": "fp32", "checkpoint_interval": ext.checkpoint_interval,
+                   "s0_std": cfg["s0_std"], "dsT": "zero", "parallelism": "single-gpu"},
+        "hbm_gbps_alg": round(step_gbps, 1),
+        "hbm_frac_alg": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "kernel_ms": {k: round(v[0], 4) for k, v in kern.items()},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "alg_bytes_per_launch": dom_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

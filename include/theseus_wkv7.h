@@ -1,0 +1,102 @@
+/*
+ * theseus_wkv7.h -- C ABI of the MI355X (gfx950) WKV7 state-recurrence library
+ * (libtheseus_wkv7.so).
+ *
+ * This ABI is the drop-in boundary for the reference's pybind11 module
+ * `theseus_wkv7_state_v1` (kernels/wkv7_state.cpp:38-41), which
+ * theseus/wkv7.py:31-36 JIT-builds and calls.  Python binds it with ctypes
+ * (rwkv-theseus_amd/theseus/wkv7.py); no torch or HIP C++ types appear here.
+ *
+ * Conventions (identical to the reference kernels):
+ *   token tensors r,w,k,v,a,b,y,dy and their gradients: [B,T,H,N], contiguous,
+ *     element (b,t,h,n) at ((b*T+t)*H+h)*N+n   (kernels/wkv7_state.cu:25);
+ *   w is the pre-sigmoid logit: decay = exp(-e^{-1/2} * sigmoid(w))  (cu:27);
+ *   states s0, sT, ds0, dsT: [B,H,N,N] float32, element (b,h,i,j) at
+ *     ((b*H+h)*N+i)*N+j with i = value row, j = key column  (cu:21);
+ *   dtype: THESEUS_WKV7_BF16 or THESEUS_WKV7_FP32 for all token tensors of a
+ *     call; the state is always float32.
+ *
+ * Ownership and threading: the caller allocates every buffer (outputs and
+ * workspace included) in device memory of the current HIP device; the library
+ * never allocates, frees or synchronises.  Each call enqueues its kernels on
+ * `stream` and returns; a return code other than THESEUS_WKV7_OK means that
+ * nothing was enqueued (argument errors) or that the launch failed
+ * (THESEUS_WKV7_ERR_LAUNCH, checked with hipGetLastError like
+ * C10_CUDA_KERNEL_LAUNCH_CHECK at kernels/wkv7_state.cpp:24,36).  The library
+ * keeps no mutable global state, so calls are reentrant.
+ */
+#ifndef THESEUS_WKV7_H
+#define THESEUS_WKV7_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+enum theseus_wkv7_dtype { THESEUS_WKV7_BF16 = 0, THESEUS_WKV7_FP32 = 1 };
+
+enum theseus_wkv7_status {
+    THESEUS_WKV7_OK = 0,
+    THESEUS_WKV7_ERR_SHAPE = 1,      /* B,H < 1, T < 1 or N outside 2..128 (cpp:12) */
+    THESEUS_WKV7_ERR_DTYPE = 2,      /* dtype is not BF16/FP32 (cpp:13)             */
+    THESEUS_WKV7_ERR_NULL = 3,       /* a required pointer is NULL                  */
+    THESEUS_WKV7_ERR_WORKSPACE = 4,  /* workspace smaller than required             */
+    THESEUS_WKV7_ERR_LAUNCH = 5      /* hipGetLastError reported a failure          */
+};
+
+/* ABI version of this header; bumped on any incompatible change. */
+int theseus_wkv7_abi_version(void);
+
+/* Static message for a status code (never NULL). */
+const char* theseus_wkv7_error_string(int status);
+
+/* Steps between saved states (16); the saved-state tensor of a T-step
+ * forward holds theseus_wkv7_checkpoint_count(T) states
+ * [B,H,count,N,N] float32: state after steps 0,16,32,... and, last, the final
+ * state after step T.  Replaces the full [B,H,T+1,N,N] history that
+ * kernels/wkv7_state.cpp:21-22 allocates. */
+int theseus_wkv7_checkpoint_interval(void);
+long long theseus_wkv7_checkpoint_count(int T);
+
+/* Bytes of device workspace theseus_wkv7_backward needs (may be 0). */
+size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N);
+
+/* Forward recurrence.  Replaces wkv_forward (kernels/wkv7_state.cpp:16-25)
+ * and launch_forward (kernels/wkv7_state.cu:81-86).
+ * ckpt may be NULL (no-grad path, like save_history=false at cpp:22); else it
+ * must hold theseus_wkv7_checkpoint_count(T) states per (b,h). */
+int theseus_wkv7_forward(int B, int T, int H, int N, int dtype,
+                         const void* r, const void* w, const void* k, const void* v,
+                         const void* a, const void* b, const float* s0,
+                         void* y, float* sT, float* ckpt, hipStream_t stream);
+
+/* Backward (adjoint) pass.  Replaces wkv_backward (kernels/wkv7_state.cpp:26-37)
+ * and launch_backward (kernels/wkv7_state.cu:87-92).  ckpt is the buffer the
+ * forward filled; dsT may be NULL (treated as zero, as _WKV.backward does at
+ * theseus/wkv7.py:53-54).  dr..db are written in `dtype` (the reference
+ * returns float32 and casts at theseus/wkv7.py:56); ds0 is float32. */
+int theseus_wkv7_backward(int B, int T, int H, int N, int dtype,
+                          const void* r, const void* w, const void* k, const void* v,
+                          const void* a, const void* b, const float* ckpt,
+                          const void* dy, const float* dsT,
+                          void* dr, void* dw, void* dk, void* dv, void* da, void* db,
+                          float* ds0, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream);
+
+/* One recurrent step (T = 1) that updates `state` [B,H,N,N] float32 IN PLACE
+ * and writes y [B,H,N].  r..b are [B,H,N] (a [B,1,H,N] tensor).  The
+ * reference has no in-place step: its decode is wkv_forward with T=1, which
+ * allocates a new end state per call (kernels/wkv7_state.cpp:21). */
+int theseus_wkv7_decode_step(int B, int H, int N, int dtype,
+                             const void* r, const void* w, const void* k, const void* v,
+                             const void* a, const void* b, float* state, void* y,
+                             hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THESEUS_WKV7_H */

@@ -1,0 +1,105 @@
+// C-ABI front end of libtheseus_wkv7.so (declared in include/theseus_wkv7.h).
+//
+// Validates sizes and pointers (the shape/dtype half of the reference's
+// check(), kernels/wkv7_state.cpp:10-15; the torch-side half -- device,
+// contiguity, same shapes -- is done by the Python wrapper, which owns the
+// tensors), picks the kernel family, launches on the caller's stream and
+// reports launch failures like C10_CUDA_KERNEL_LAUNCH_CHECK (cpp:24,36).
+#include "../../include/theseus_wkv7.h"
+
+#include <hip/hip_runtime.h>
+
+#include "wkv7_launch.h"
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+
+int check_dims(int B, int T, int H, int N, int dtype) {
+    if (B < 1 || H < 1 || T < 1 || N < 2 || N > 128) return THESEUS_WKV7_ERR_SHAPE;
+    if (dtype != THESEUS_WKV7_BF16 && dtype != THESEUS_WKV7_FP32) return THESEUS_WKV7_ERR_DTYPE;
+    return THESEUS_WKV7_OK;
+}
+
+int launch_status() {
+    return hipGetLastError() == hipSuccess ? THESEUS_WKV7_OK : THESEUS_WKV7_ERR_LAUNCH;
+}
+
+}  // namespace
+
+namespace wkv7 {
+
+void launch_forward(const Fwd& p) { launch_seq_forward(p); }
+void launch_backward(const Bwd& p) { launch_seq_backward(p); }
+size_t backward_workspace(int B, int T, int H, int N) {
+    (void)T;
+    return seq_backward_workspace(B, H, N);
+}
+
+}  // namespace wkv7
+
+extern "C" {
+
+int theseus_wkv7_abi_version(void) { return kAbiVersion; }
+
+const char* theseus_wkv7_error_string(int status) {
+    switch (status) {
+        case THESEUS_WKV7_OK: return "ok";
+        case THESEUS_WKV7_ERR_SHAPE: return "invalid T or head size (2..128)";
+        case THESEUS_WKV7_ERR_DTYPE: return "expected BF16 or FP32";
+        case THESEUS_WKV7_ERR_NULL: return "null pointer argument";
+        case THESEUS_WKV7_ERR_WORKSPACE: return "workspace too small";
+        case THESEUS_WKV7_ERR_LAUNCH: return "HIP kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+int theseus_wkv7_checkpoint_interval(void) { return wkv7::kCkptInterval; }
+
+long long theseus_wkv7_checkpoint_count(int T) {
+    return T < 1 ? 0 : (long long)(T + wkv7::kCkptInterval - 1) / wkv7::kCkptInterval + 1;
+}
+
+size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N) {
+    if (check_dims(B, T, H, N, THESEUS_WKV7_BF16) != THESEUS_WKV7_OK) return 0;
+    return wkv7::backward_workspace(B, T, H, N);
+}
+
+int theseus_wkv7_forward(int B, int T, int H, int N, int dtype, const void* r, const void* w,
+                         const void* k, const void* v, const void* a, const void* b,
+                         const float* s0, void* y, float* sT, float* ckpt, hipStream_t stream) {
+    if (int e = check_dims(B, T, H, N, dtype)) return e;
+    if (!r || !w || !k || !v || !a || !b || !s0 || !y || !sT) return THESEUS_WKV7_ERR_NULL;
+    wkv7::Fwd p{B, T, H, N, dtype, r, w, k, v, a, b, s0, y, sT, ckpt, stream};
+    wkv7::launch_forward(p);
+    return launch_status();
+}
+
+int theseus_wkv7_backward(int B, int T, int H, int N, int dtype, const void* r, const void* w,
+                          const void* k, const void* v, const void* a, const void* b,
+                          const float* ckpt, const void* dy, const float* dsT, void* dr,
+                          void* dw, void* dk, void* dv, void* da, void* db, float* ds0,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (int e = check_dims(B, T, H, N, dtype)) return e;
+    if (!r || !w || !k || !v || !a || !b || !ckpt || !dy || !dr || !dw || !dk || !dv || !da ||
+        !db || !ds0)
+        return THESEUS_WKV7_ERR_NULL;
+    const size_t need = wkv7::backward_workspace(B, T, H, N);
+    if (workspace_bytes < need || (need && !workspace)) return THESEUS_WKV7_ERR_WORKSPACE;
+    wkv7::Bwd p{B, T, H, N, dtype, r, w, k, v, a, b, ckpt, dy, dsT,
+                dr, dw, dk, dv, da, db, ds0, workspace, stream};
+    wkv7::launch_backward(p);
+    return launch_status();
+}
+
+int theseus_wkv7_decode_step(int B, int H, int N, int dtype, const void* r, const void* w,
+                             const void* k, const void* v, const void* a, const void* b,
+                             float* state, void* y, hipStream_t stream) {
+    if (int e = check_dims(B, 1, H, N, dtype)) return e;
+    if (!r || !w || !k || !v || !a || !b || !state || !y) return THESEUS_WKV7_ERR_NULL;
+    wkv7::Dec p{B, H, N, dtype, r, w, k, v, a, b, state, y, stream};
+    wkv7::launch_decode(p);
+    return launch_status();
+}
+
+}  // extern "C"

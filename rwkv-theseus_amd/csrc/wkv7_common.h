@@ -1,0 +1,46 @@
+// Shared device helpers for the WKV7 kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wkv7 {
+
+// e^{-1/2}; the decay is exp(-DECAY_SCALE * sigmoid(w)) (kernels/wkv7_state.cu:27).
+constexpr float DECAY_SCALE = 0.6065306597126334f;
+// Saved-state interval (steps) shared by every forward/backward kernel.
+constexpr int CKPT = 16;
+
+// bfloat16 stored as its raw 16 bits; conversions use round-to-nearest-even,
+// the rounding torch applies when it casts float32 to bfloat16.
+struct bf16_t { uint16_t bits; };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t u) {
+    return __uint_as_float(static_cast<uint32_t>(u) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))   // NaN stays quiet NaN
+        return static_cast<uint16_t>((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T> struct io;
+template <> struct io<float> {
+    __device__ __forceinline__ static float ld(const float* p, long i) { return p[i]; }
+    __device__ __forceinline__ static void st(float* p, long i, float x) { p[i] = x; }
+};
+template <> struct io<bf16_t> {
+    __device__ __forceinline__ static float ld(const bf16_t* p, long i) { return bf16_to_f32(p[i].bits); }
+    __device__ __forceinline__ static void st(bf16_t* p, long i, float x) { p[i].bits = f32_to_bf16(x); }
+};
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// log of the per-key decay: log d = -e^{-1/2} * sigmoid(w).
+__device__ __forceinline__ float log_decay(float w) { return -DECAY_SCALE * sigmoidf_(w); }
+
+__host__ __device__ constexpr inline long ckpt_count(int T) { return (T + CKPT - 1) / CKPT + 1; }
+
+}  // namespace wkv7

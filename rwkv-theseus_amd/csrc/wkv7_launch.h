@@ -1,0 +1,53 @@
+// Host-side launch descriptors shared by the kernel translation units and the
+// C-ABI front end.  dtype: 0 = bf16, 1 = fp32 (theseus_wkv7_dtype).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace wkv7 {
+
+constexpr int kCkptInterval = 16;  // must equal CKPT in wkv7_common.h
+
+struct Fwd {
+    int B, T, H, N, dtype;
+    const void *r, *w, *k, *v, *a, *b;
+    const float* s0;
+    void* y;
+    float* sT;
+    float* ckpt;  // may be null
+    hipStream_t stream;
+};
+
+struct Bwd {
+    int B, T, H, N, dtype;
+    const void *r, *w, *k, *v, *a, *b;
+    const float* ckpt;
+    const void* dy;
+    const float* dsT;  // may be null (zero)
+    void *dr, *dw, *dk, *dv, *da, *db;
+    float* ds0;
+    void* ws;
+    hipStream_t stream;
+};
+
+struct Dec {
+    int B, H, N, dtype;
+    const void *r, *w, *k, *v, *a, *b;
+    float* state;
+    void* y;
+    hipStream_t stream;
+};
+
+void launch_seq_forward(const Fwd& p);
+void launch_seq_backward(const Bwd& p);
+size_t seq_backward_workspace(int B, int H, int N);
+void launch_decode(const Dec& p);
+
+// Family dispatch (wkv7_capi.cpp): the chunked MFMA kernels when they cover
+// the call, else the step-serial ones.
+void launch_forward(const Fwd& p);
+void launch_backward(const Bwd& p);
+size_t backward_workspace(int B, int T, int H, int N);
+
+}  // namespace wkv7

@@ -1,0 +1,241 @@
+"""RWKV7 (WKV7) state recurrence for MI355X.  State layout: [batch, head, value, key].
+
+Drop-in for the reference operator module ``theseus/wkv7.py``: the same public
+names and meanings -- ``reference``, ``extension``, ``_WKV`` and
+``wkv7(r, w, k, v, a, b, state, backend="cuda")`` (theseus/wkv7.py:16-70).
+
+``backend="cuda"`` (the name is kept; on ROCm torch GPU tensors report
+``is_cuda``) runs hand-written gfx950 HIP kernels from ``libtheseus_wkv7.so``
+through its C ABI (``include/theseus_wkv7.h``), loaded with ctypes.  There is
+no CPU fallback: if the library is missing, ``extension()`` raises.
+``backend="reference"`` is the explicit pure-PyTorch loop for CPU use, as in
+the reference.
+
+Differences in what is saved for backward: the reference saves the full
+float32 state history ``[B,H,T+1,N,N]`` (kernels/wkv7_state.cpp:21-22); this
+implementation saves the state every 16 steps plus the final state
+``[B,H,ceil(T/16)+1,N,N]`` and replays inside the backward kernels.  Gradients
+come back in the input dtype (the reference computes float32 and casts,
+theseus/wkv7.py:56) and ``ds0`` in float32, as in the reference.  The chunk
+boundary is never detached by this operator; callers detach (wkv7.py:5).
+"""
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+from pathlib import Path
+
+import torch
+
+DECAY_SCALE = 0.6065306597126334  # e^{-1/2} (theseus/wkv7.py:19)
+LIB_PATH = Path(__file__).resolve().parent / "libtheseus_wkv7.so"
+
+_BF16, _FP32 = 0, 1
+
+
+def reference(r, w, k, v, a, b, state):
+    """Pure-PyTorch recurrence, float32 (theseus/wkv7.py:16-28).
+
+    Per step: sa = S a; S <- S*diag(d) + sa b^T + v k^T; y = S r, with
+    d = exp(-e^{-1/2} sigmoid(w)).  Returns y in the input dtype and the
+    float32 final state; differentiable through autograd.
+    """
+    dtype = r.dtype
+    r, w, k, v, a, b = [x.float() for x in (r, w, k, v, a, b)]
+    decay = torch.exp(-DECAY_SCALE * torch.sigmoid(w))
+    state = state.float()
+    ys = []
+    for t in range(r.shape[1]):
+        sa = (state * a[:, t, :, None, :]).sum(-1)
+        state = (state * decay[:, t, :, None, :]
+                 + sa[..., None] * b[:, t, :, None, :]
+                 + v[:, t, :, :, None] * k[:, t, :, None, :])
+        ys.append((state * r[:, t, :, None, :]).sum(-1))
+    return torch.stack(ys, 1).to(dtype), state
+
+
+def _ptr(x):
+    return ctypes.c_void_p(x.data_ptr()) if x is not None else ctypes.c_void_p(0)
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class Extension:
+    """ctypes binding of libtheseus_wkv7.so with the reference module's methods.
+
+    ``forward``/``backward`` take and return the same things as the pybind11
+    functions of kernels/wkv7_state.cpp:16-37, with the saved-state tensor in
+    place of the history; ``decode_step`` is the in-place T=1 step.
+    """
+
+    def __init__(self, lib):
+        self.lib = lib
+        vp, i32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        lib.theseus_wkv7_abi_version.restype = i32
+        lib.theseus_wkv7_error_string.argtypes = [i32]
+        lib.theseus_wkv7_error_string.restype = ctypes.c_char_p
+        lib.theseus_wkv7_checkpoint_interval.restype = i32
+        lib.theseus_wkv7_checkpoint_count.argtypes = [i32]
+        lib.theseus_wkv7_checkpoint_count.restype = ctypes.c_longlong
+        lib.theseus_wkv7_backward_workspace_size.argtypes = [i32] * 4
+        lib.theseus_wkv7_backward_workspace_size.restype = sz
+        lib.theseus_wkv7_forward.argtypes = [i32] * 5 + [vp] * 11 + [vp]
+        lib.theseus_wkv7_forward.restype = i32
+        lib.theseus_wkv7_backward.argtypes = [i32] * 5 + [vp] * 16 + [vp, sz, vp]
+        lib.theseus_wkv7_backward.restype = i32
+        lib.theseus_wkv7_decode_step.argtypes = [i32] * 4 + [vp] * 8 + [vp]
+        lib.theseus_wkv7_decode_step.restype = i32
+        self.abi_version = lib.theseus_wkv7_abi_version()
+        self.checkpoint_interval = lib.theseus_wkv7_checkpoint_interval()
+
+    # -- helpers ---------------------------------------------------------
+    def checkpoint_count(self, T):
+        return int(self.lib.theseus_wkv7_checkpoint_count(T))
+
+    def _raise(self, status):
+        if status:
+            msg = self.lib.theseus_wkv7_error_string(status).decode()
+            raise RuntimeError(f"theseus_wkv7: {msg}")
+
+    @staticmethod
+    def _check(r, xs):
+        """Mirror of check() in kernels/wkv7_state.cpp:10-15 (same messages)."""
+        if not (r.is_cuda and r.is_contiguous() and r.dim() == 4):
+            raise RuntimeError("expected contiguous CUDA [B,T,H,N]")
+        if not (r.size(1) > 0 and 2 <= r.size(3) <= 128):
+            raise RuntimeError("invalid T or head size (2..128)")
+        if r.dtype not in (torch.bfloat16, torch.float32):
+            raise RuntimeError("expected BF16 or FP32")
+        for x in xs:
+            if not (x.device == r.device and x.shape == r.shape and x.dtype == r.dtype
+                    and x.is_contiguous()):
+                raise RuntimeError("input mismatch")
+
+    # -- reference-compatible entry points --------------------------------
+    def forward(self, r, w, k, v, a, b, s0, save_history):
+        """-> [y, end, saved]; saved is empty when save_history is False (cpp:16-25)."""
+        self._check(r, (w, k, v, a, b))
+        B, T, H, N = r.shape
+        if not (s0.device == r.device and s0.dtype == torch.float32 and s0.is_contiguous()):
+            raise RuntimeError("s0 must be contiguous CUDA FP32")
+        if tuple(s0.shape) != (B, H, N, N):
+            raise RuntimeError("invalid s0 shape")
+        with torch.cuda.device(r.device):
+            y = torch.empty_like(r)
+            end = torch.empty_like(s0)
+            if save_history:
+                saved = torch.empty((B, H, self.checkpoint_count(T), N, N),
+                                    dtype=torch.float32, device=r.device)
+            else:
+                saved = torch.empty((0,), dtype=torch.float32, device=r.device)
+            status = self.lib.theseus_wkv7_forward(
+                B, T, H, N, _BF16 if r.dtype == torch.bfloat16 else _FP32,
+                *map(_ptr, (r, w, k, v, a, b, s0, y, end)),
+                _ptr(saved) if save_history else ctypes.c_void_p(0), _stream(r.device))
+        self._raise(status)
+        return [y, end, saved]
+
+    def backward(self, r, w, k, v, a, b, saved, dy, dend):
+        """-> [dr, dw, dk, dv, da, db, ds0] (cpp:26-37).  dend may be None (zero)."""
+        self._check(r, (w, k, v, a, b, dy))
+        B, T, H, N = r.shape
+        if not (saved.device == r.device and saved.dtype == torch.float32
+                and saved.is_contiguous()
+                and tuple(saved.shape) == (B, H, self.checkpoint_count(T), N, N)):
+            raise RuntimeError("invalid history")
+        if dend is not None and not (dend.device == r.device and dend.dtype == torch.float32
+                                     and dend.is_contiguous()
+                                     and tuple(dend.shape) == (B, H, N, N)):
+            raise RuntimeError("invalid dend")
+        with torch.cuda.device(r.device):
+            grads = [torch.empty_like(r) for _ in range(6)]
+            ds0 = torch.empty((B, H, N, N), dtype=torch.float32, device=r.device)
+            ws_bytes = int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N))
+            ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=r.device)
+            status = self.lib.theseus_wkv7_backward(
+                B, T, H, N, _BF16 if r.dtype == torch.bfloat16 else _FP32,
+                *map(_ptr, (r, w, k, v, a, b, saved, dy, dend, *grads, ds0, ws)),
+                ctypes.c_size_t(ws_bytes), _stream(r.device))
+        self._raise(status)
+        return grads + [ds0]
+
+    def decode_step(self, r, w, k, v, a, b, state):
+        """One step in place: r..b [B,1,H,N] (or [B,H,N]); state [B,H,N,N] fp32 is
+        updated in place; returns y shaped like r."""
+        xs = [x.reshape(x.shape[0], 1, x.shape[-2], x.shape[-1]) if x.dim() == 3 else x
+              for x in (r, w, k, v, a, b)]
+        self._check(xs[0], xs[1:])
+        B, T, H, N = xs[0].shape
+        if T != 1:
+            raise RuntimeError("decode_step expects T == 1")
+        if not (state.device == r.device and state.dtype == torch.float32
+                and state.is_contiguous() and tuple(state.shape) == (B, H, N, N)):
+            raise RuntimeError("invalid state")
+        with torch.cuda.device(r.device):
+            y = torch.empty_like(r)
+            status = self.lib.theseus_wkv7_decode_step(
+                B, H, N, _BF16 if r.dtype == torch.bfloat16 else _FP32,
+                *map(_ptr, (*xs, state, y)), _stream(r.device))
+        self._raise(status)
+        return y
+
+
+@lru_cache(maxsize=1)
+def extension():
+    """Load libtheseus_wkv7.so (built by ``make -C rwkv-theseus_amd/csrc``).
+
+    Counterpart of the reference's lru-cached JIT build (theseus/wkv7.py:31-36);
+    nothing is compiled at run time here.
+    """
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C rwkv-theseus_amd/csrc` "
+                           "(or __graft_entry__.build()); there is no CPU fallback")
+    return Extension(ctypes.CDLL(str(LIB_PATH)))
+
+
+class _WKV(torch.autograd.Function):
+    """Autograd Function over the HIP kernels (theseus/wkv7.py:39-56)."""
+
+    @staticmethod
+    def forward(ctx, r, w, k, v, a, b, state):
+        xs = [x.contiguous() for x in (r, w, k, v, a, b)]
+        state = state.float().contiguous()
+        y, end, saved = extension().forward(*xs, state, True)
+        ctx.save_for_backward(*xs, saved)
+        return y, end
+
+    @staticmethod
+    def backward(ctx, dy, dend):
+        *xs, saved = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(xs[0])
+        dend = None if dend is None else dend.float().contiguous()
+        grads = extension().backward(*xs, saved, dy.to(xs[0].dtype).contiguous(), dend)
+        return tuple(g.to(x.dtype) for g, x in zip(grads[:6], xs)) + (grads[6],)
+
+
+def wkv7(r, w, k, v, a, b, state, backend="cuda"):
+    """(y, final_state) of the recurrence (theseus/wkv7.py:59-70)."""
+    if backend == "reference":
+        return reference(r, w, k, v, a, b, state)
+    if backend != "cuda":
+        raise ValueError(f"Unknown WKV backend: {backend}")
+    if not r.is_cuda:
+        raise ValueError("CUDA backend requested on CPU; use backend='reference' for tests")
+    if not torch.is_grad_enabled() or not any(x.requires_grad for x in (r, w, k, v, a, b, state)):
+        xs = [x.contiguous() for x in (r, w, k, v, a, b)]
+        y, end, _ = extension().forward(*xs, state.float().contiguous(), False)
+        return y, end
+    return _WKV.apply(r, w, k, v, a, b, state)
+
+
+def decode_step_(r, w, k, v, a, b, state):
+    """In-place single step for serving: updates ``state`` and returns y.
+
+    The reference decodes by calling the forward with T=1, which allocates a
+    new end state per step (kernels/wkv7_state.cpp:21); this keeps the state
+    resident and rewrites it in place.
+    """
+    return extension().decode_step(r, w, k, v, a, b, state)

@@ -1,0 +1,94 @@
+"""CPU checks of the C-ABI library and of the Python boundary's host logic.
+
+No kernel is launched here: the library is loaded, every symbol declared in
+include/theseus_wkv7.h is looked up, and argument validation is exercised
+(it returns before any HIP call).
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import theseus.wkv7 as W
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "theseus_wkv7.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(theseus_wkv7_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_symbols()
+    for required in ("theseus_wkv7_forward", "theseus_wkv7_backward", "theseus_wkv7_decode_step",
+                     "theseus_wkv7_error_string", "theseus_wkv7_abi_version"):
+        assert required in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    assert W.LIB_PATH.exists(), "build first: make -C rwkv-theseus_amd/csrc"
+    lib = ctypes.CDLL(str(W.LIB_PATH))
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_host_queries():
+    ext = W.extension()
+    assert ext.abi_version == 1
+    assert ext.checkpoint_interval == 16
+    lib = ext.lib
+    assert ext.checkpoint_count(1) == 2
+    assert ext.checkpoint_count(16) == 2
+    assert ext.checkpoint_count(17) == 3
+    assert ext.checkpoint_count(2048) == 129
+    assert lib.theseus_wkv7_checkpoint_count(0) == 0
+    assert lib.theseus_wkv7_error_string(0) == b"ok"
+    assert lib.theseus_wkv7_error_string(1) == b"invalid T or head size (2..128)"
+    assert lib.theseus_wkv7_error_string(2) == b"expected BF16 or FP32"
+    assert lib.theseus_wkv7_error_string(99) == b"unknown status"
+    assert lib.theseus_wkv7_backward_workspace_size(1, 0, 1, 64) == 0  # invalid T
+
+
+@pytest.mark.parametrize("B,T,H,N,dtype,code", [
+    (1, 0, 1, 64, 0, 1), (1, 4, 1, 1, 0, 1), (1, 4, 1, 129, 0, 1), (0, 4, 1, 64, 0, 1),
+    (1, 4, 1, 64, 7, 2), (1, 4, 1, 64, 0, 3)])
+def test_c_abi_rejects_bad_arguments_without_launching(B, T, H, N, dtype, code):
+    lib = W.extension().lib
+    null = ctypes.c_void_p(0)
+    status = lib.theseus_wkv7_forward(B, T, H, N, dtype, *([null] * 11), null)
+    assert status == code
+    status = lib.theseus_wkv7_backward(B, T, H, N, dtype, *([null] * 16), null, 0, null)
+    assert status == code
+
+
+def test_backend_errors_match_reference():
+    x = torch.zeros(1, 2, 1, 4)
+    s = torch.zeros(1, 1, 4, 4)
+    with pytest.raises(ValueError, match="Unknown WKV backend"):
+        W.wkv7(x, x, x, x, x, x, s, backend="triton")
+    with pytest.raises(ValueError, match="CUDA backend requested on CPU"):
+        W.wkv7(x, x, x, x, x, x, s, backend="cuda")
+
+
+def test_extension_checks_match_reference_messages():
+    ext = W.extension()
+    x = torch.zeros(1, 2, 1, 4)
+    with pytest.raises(RuntimeError, match=r"expected contiguous CUDA \[B,T,H,N\]"):
+        ext.forward(x, x, x, x, x, x, torch.zeros(1, 1, 4, 4), True)
+    with pytest.raises(RuntimeError, match=r"expected contiguous CUDA \[B,T,H,N\]"):
+        ext.backward(x, x, x, x, x, x, torch.zeros(1, 1, 2, 4, 4), x, None)
+
+
+def test_reference_backend_on_cpu_matches_oracle():
+    import numpy as np
+    from oracle import wkv7_oracle as O
+    from theseus.synthetic import wkv7_inputs
+    inp = wkv7_inputs(1, 12, 2, 8, seed=11, dtype=torch.float32, s0_std=0.1)
+    y, sT = W.wkv7(*(inp[n] for n in "rwkvab"), inp["s0"], backend="reference")
+    yo, sTo = O.forward(*(inp[n].numpy() for n in "rwkvab"), inp["s0"].numpy())
+    np.testing.assert_allclose(y.numpy(), yo, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(sT.numpy(), sTo, atol=1e-4, rtol=1e-4)
