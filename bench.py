@@ -48,25 +48,32 @@ def alg_bytes(B, T, H, N, which):
     raise ValueError(which)
 
 
-def cpu_baseline(B, H, N, T_slice, seed):
+def cpu_baseline(B, H, N, T_slice, seed, budget_s=12.0, T_total=2048):
     """Reference op sequence (oracle.reference_torch = theseus/wkv7.py:16-28 restated),
-    float32 autograd fwd+bwd on the host cores over a T-slice of the workload."""
+    float32 autograd fwd+bwd on the host cores, over consecutive T_slice-step slices
+    of the workload (state carried, detached between slices, as TimeMix training
+    carries it between chunks) until ``budget_s`` seconds or T_total steps."""
     import torch
     from oracle import wkv7_oracle as O
     from theseus.synthetic import wkv7_inputs
 
     cores = O.cpu_count()
     torch.set_num_threads(cores)
-    inp = wkv7_inputs(B, T_slice, H, N, seed=seed, dtype=torch.float32, s0_std=0.1)
-    xs = [inp[n].clone().requires_grad_() for n in "rwkvab"]
-    s0 = inp["s0"].clone().requires_grad_()
-    t0 = time.perf_counter()
-    y, sT = O.reference_torch(*xs, s0)
-    torch.autograd.backward((y, sT), (inp["dy"], torch.zeros_like(sT)))
-    dt = time.perf_counter() - t0
-    return {"value": round(B * T_slice / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"B={B} H={H} N={N} T={T_slice} slice of the workload, fp32 torch autograd "
-                      f"fwd+bwd of the reference op sequence, {dt:.1f} s on {O.cpu_model()}"}
+    dt, steps, state = 0.0, 0, None
+    while steps < T_total and dt < budget_s:
+        inp = wkv7_inputs(B, T_slice, H, N, seed=seed + steps, dtype=torch.float32, s0_std=0.1)
+        xs = [inp[n].clone().requires_grad_() for n in "rwkvab"]
+        s0 = (inp["s0"] if state is None else state).clone().requires_grad_()
+        t0 = time.perf_counter()
+        y, sT = O.reference_torch(*xs, s0)
+        torch.autograd.backward((y, sT), (inp["dy"], torch.zeros_like(sT)))
+        dt += time.perf_counter() - t0
+        state = sT.detach()
+        steps += T_slice
+    return {"value": round(B * steps / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"B={B} H={H} N={N}: {steps // T_slice} consecutive T={T_slice} slices ({steps} steps) "
+                      f"of the workload, fp32 torch autograd fwd+bwd of the reference op sequence, "
+                      f"{dt:.1f} s on {O.cpu_model()}"}
 
 
 def main():
@@ -75,7 +82,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-slice", type=int, default=128, help="T of the CPU baseline slice (0: skip)")
+    ap.add_argument("--cpu-slice", type=int, default=256, help="T of each CPU baseline slice (0: skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "

@@ -262,6 +262,9 @@ size_t seq_backward_workspace(int B, int H, int N) {
 template <typename T, int NP>
 static void seq_backward_t(const Bwd& p) {
     const size_t lds = (size_t)(NP * NP + 10 * NP) * sizeof(float);
+    if (lds > 65536)  // above the default dynamic-LDS cap; gfx950 has 160 KB per CU
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&seq_backward<T, NP>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     hipLaunchKernelGGL((seq_backward<T, NP>), dim3(p.B * p.H), dim3(NP), lds, p.stream, p.T, p.H,
                        p.N, (const T*)p.r, (const T*)p.w, (const T*)p.k, (const T*)p.v,
                        (const T*)p.a, (const T*)p.b, p.ckpt, (const T*)p.dy, p.dsT, (T*)p.dr,

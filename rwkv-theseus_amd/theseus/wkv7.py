@@ -81,7 +81,7 @@ class Extension:
         lib.theseus_wkv7_checkpoint_count.restype = ctypes.c_longlong
         lib.theseus_wkv7_backward_workspace_size.argtypes = [i32] * 4
         lib.theseus_wkv7_backward_workspace_size.restype = sz
-        lib.theseus_wkv7_forward.argtypes = [i32] * 5 + [vp] * 11 + [vp]
+        lib.theseus_wkv7_forward.argtypes = [i32] * 5 + [vp] * 10 + [vp]
         lib.theseus_wkv7_forward.restype = i32
         lib.theseus_wkv7_backward.argtypes = [i32] * 5 + [vp] * 16 + [vp, sz, vp]
         lib.theseus_wkv7_backward.restype = i32

@@ -36,6 +36,26 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def declared_arity():
+    """{function: number of parameters} parsed from the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(theseus_wkv7_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_bindings_match_header_arity():
+    ext = W.extension()
+    arity = declared_arity()
+    assert arity["theseus_wkv7_forward"] == 16 and arity["theseus_wkv7_backward"] == 24
+    for name, n in arity.items():
+        fn = getattr(ext.lib, name)
+        bound = len(fn.argtypes) if fn.argtypes is not None else 0
+        assert bound == n, (name, bound, n)
+
+
 def test_host_queries():
     ext = W.extension()
     assert ext.abi_version == 1
@@ -59,9 +79,9 @@ def test_host_queries():
 def test_c_abi_rejects_bad_arguments_without_launching(B, T, H, N, dtype, code):
     lib = W.extension().lib
     null = ctypes.c_void_p(0)
-    status = lib.theseus_wkv7_forward(B, T, H, N, dtype, *([null] * 11), null)
+    status = lib.theseus_wkv7_forward(B, T, H, N, dtype, *([null] * 10), null)
     assert status == code
-    status = lib.theseus_wkv7_backward(B, T, H, N, dtype, *([null] * 16), null, 0, null)
+    status = lib.theseus_wkv7_backward(B, T, H, N, dtype, *([null] * 17), 0, null)
     assert status == code
 
 
