@@ -9,6 +9,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+#include <cstring>
+
 #include "wkv7_launch.h"
 
 namespace {
@@ -29,7 +32,18 @@ int launch_status() {
 
 namespace wkv7 {
 
-void launch_forward(const Fwd& p) { launch_seq_forward(p); }
+// THESEUS_WKV7_FAMILY=seq forces the step-serial kernels (used by the tests to
+// cross-check the two kernel families); anything else means automatic.
+static bool force_seq() {
+    const char* e = getenv("THESEUS_WKV7_FAMILY");
+    return e && strcmp(e, "seq") == 0;
+}
+static bool chunk_ok(int N, int dtype) { return N == 64 && dtype == THESEUS_WKV7_BF16 && !force_seq(); }
+
+void launch_forward(const Fwd& p) {
+    if (chunk_ok(p.N, p.dtype)) launch_chunk_forward(p);
+    else launch_seq_forward(p);
+}
 void launch_backward(const Bwd& p) { launch_seq_backward(p); }
 size_t backward_workspace(int B, int T, int H, int N) {
     (void)T;

@@ -18,12 +18,15 @@ struct bf16_t { uint16_t bits; };
 __device__ __forceinline__ float bf16_to_f32(uint16_t u) {
     return __uint_as_float(static_cast<uint32_t>(u) << 16);
 }
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32, round-to-nearest-even).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))   // NaN stays quiet NaN
-        return static_cast<uint16_t>((u >> 16) | 0x0040u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// two floats -> packed bf16 pair (element 0 in the low half), one instruction
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 template <typename T> struct io;

@@ -1,0 +1,111 @@
+// MFMA building blocks for the chunked WKV7 kernels (gfx950, wave64).
+//
+// Matrices that feed the matrix cores live in LDS as bfloat16 pairs (hi, lo)
+// with x = hi + lo to ~2^-16 relative precision; a product of two such
+// operands is formed from three bf16 MFMAs (hi*hi + hi*lo + lo*hi), which
+// keeps float32-level accuracy on the bf16 matrix pipe.
+//
+// Fragment layouts, verified on gfx950 (lane l, q = l / 16, e = element):
+//   v_mfma_f32_16x16x32_bf16: A[row = l%16][k = 8q+e], B[k = 8q+e][col = l%16]
+//   v_mfma_f32_16x16x16_bf16: A[row = l%16][k = 4q+e], B[k = 4q+e][col = l%16]
+//   accumulator (both):       D[row = 4q+e][col = l%16], e = 0..3
+// Every operand array is therefore stored "[outer][k]" with k contiguous:
+// A operands row-major, B operands as B^T.  Row strides are padded to
+// K + 8 elements so a 16-lane group reading 16-byte fragments hits every
+// LDS bank group exactly twice.
+#pragma once
+
+#include "wkv7_common.h"
+
+namespace wkv7 {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
+
+__device__ __forceinline__ f32x4_t mma32(f32x4_t acc, uint4 a, uint4 b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mma16(f32x4_t acc, uint2 a, uint2 b) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, a),
+                                                     __builtin_bit_cast(i16x4_t, b), acc, 0, 0, 0);
+}
+
+// hi = truncation of x to bf16 (exact remainder), lo = RNE(x - hi).
+__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+    const uint32_t u = __float_as_uint(x);
+    hi = static_cast<uint16_t>(u >> 16);
+    lo = f32_to_bf16(x - __uint_as_float(u & 0xffff0000u));
+}
+// Split two floats at once into packed (hi, lo) bf16 pairs.
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    const uint32_t u0 = __float_as_uint(x0), u1 = __float_as_uint(x1);
+    hi = (u0 >> 16) | (u1 & 0xffff0000u);
+    lo = f32x2_to_bf16x2(x0 - __uint_as_float(u0 & 0xffff0000u), x1 - __uint_as_float(u1 & 0xffff0000u));
+}
+__device__ __forceinline__ float join_bf16(uint16_t hi, uint16_t lo) {
+    return bf16_to_f32(hi) + bf16_to_f32(lo);
+}
+
+// An LDS operand: hi and lo planes, row stride ld (elements).
+struct Op {
+    uint16_t* hi;
+    uint16_t* lo;
+    int ld;
+    __device__ __forceinline__ void put(int x, int k, float v) const {
+        uint16_t h, l;
+        split_bf16(v, h, l);
+        hi[x * ld + k] = h;
+        lo[x * ld + k] = l;
+    }
+    __device__ __forceinline__ float get(int x, int k) const { return join_bf16(hi[x * ld + k], lo[x * ld + k]); }
+};
+
+// 16x32 (A) / 32x16 (B) fragment: outer index x0 + l%16, k = k0 + 8q .. +7.
+__device__ __forceinline__ uint4 frag32(const uint16_t* p, int ld, int x0, int k0, int lane) {
+    return *reinterpret_cast<const uint4*>(p + (x0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
+}
+// 16x16 (A) / 16x16 (B) fragment for the K=16 instruction: k = k0 + 4q .. +3.
+__device__ __forceinline__ uint2 frag16(const uint16_t* p, int ld, int x0, int k0, int lane) {
+    return *reinterpret_cast<const uint2*>(p + (x0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4));
+}
+
+// acc += A[a_x0.., k0..k0+K) * B[k0..k0+K, b_x0..] for K = 32*nk (split precision).
+// lo_a / lo_b: false when that operand is exact in bf16 (its lo plane is zero).
+// NOTE: an accumulator produced by one MFMA shape is never fed straight into
+// the SrcC of another shape (16x16x32 <-> 16x16x16): such back-to-back chains
+// returned stale accumulator elements on gfx950.  Mixed-shape sums go through
+// separate accumulators that are added with VALU instructions.
+template <int NK, bool LO_A = true, bool LO_B = true>
+__device__ __forceinline__ f32x4_t mma_k32(f32x4_t acc, const Op& A, int a_x0, const Op& B, int b_x0,
+                                           int k0, int lane) {
+    f32x4_t c1 = zero4(), c2 = zero4();
+#pragma unroll
+    for (int s = 0; s < NK; s++) {
+        const int k = k0 + 32 * s;
+        const uint4 ah = frag32(A.hi, A.ld, a_x0, k, lane);
+        const uint4 bh = frag32(B.hi, B.ld, b_x0, k, lane);
+        acc = mma32(acc, ah, bh);
+        if (LO_B) c1 = mma32(c1, ah, frag32(B.lo, B.ld, b_x0, k, lane));
+        if (LO_A) c2 = mma32(c2, frag32(A.lo, A.ld, a_x0, k, lane), bh);
+    }
+    return acc + c1 + c2;
+}
+
+// Same for one K=16 step.
+template <bool LO_A = true, bool LO_B = true>
+__device__ __forceinline__ f32x4_t mma_k16(f32x4_t acc, const Op& A, int a_x0, const Op& B, int b_x0,
+                                           int k0, int lane) {
+    const uint2 ah = frag16(A.hi, A.ld, a_x0, k0, lane);
+    const uint2 bh = frag16(B.hi, B.ld, b_x0, k0, lane);
+    acc = mma16(acc, ah, bh);
+    f32x4_t c = zero4();
+    if (LO_B) c = mma16(c, ah, frag16(B.lo, B.ld, b_x0, k0, lane));
+    if (LO_A) c = mma16(c, frag16(A.lo, A.ld, a_x0, k0, lane), bh);
+    return acc + c;
+}
+
+}  // namespace wkv7

@@ -184,6 +184,24 @@ def test_config4_decode_full_size():
     _check("sT", state[:2], s_ref, torch.bfloat16)
 
 
+# -- the two kernel families agree ----------------------------------------------------
+@pytest.mark.parametrize("T", [1, 15, 16, 17, 100, 512])
+def test_chunked_and_step_serial_families_agree(T, monkeypatch):
+    """bf16, N=64 runs the chunked MFMA kernels; THESEUS_WKV7_FAMILY=seq forces the
+    step-serial ones.  Both must give the same forward/backward to fp32 rounding."""
+    inp = wkv7_inputs(2, T, 3, 64, seed=300 + T, dtype=torch.bfloat16, s0_std=0.1, with_dsT=True)
+    outs = {}
+    for fam in ("auto", "seq"):
+        monkeypatch.setenv("THESEUS_WKV7_FAMILY", fam)
+        outs[fam] = _gpu_fwd_bwd(inp, torch.bfloat16, inp["dsT"])
+    for name, x, z in zip(NAMES, outs["auto"], outs["seq"]):
+        x = x.detach().float().cpu().numpy()
+        z = z.detach().float().cpu().numpy()
+        rl = rel_l2(x, z)
+        print(f"    {name:4s} chunk-vs-seq rel_l2={rl:.2e}", flush=True)
+        assert rl < 5e-3, (name, rl)
+
+
 # -- operator semantics ----------------------------------------------------------------
 def test_backward_is_deterministic_and_dend_none_is_zero():
     inp = wkv7_inputs(2, 70, 3, 64, seed=5, dtype=torch.bfloat16, s0_std=0.1)
