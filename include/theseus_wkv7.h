@@ -61,8 +61,9 @@ const char* theseus_wkv7_error_string(int status);
 int theseus_wkv7_checkpoint_interval(void);
 long long theseus_wkv7_checkpoint_count(int T);
 
-/* Bytes of device workspace theseus_wkv7_backward needs (may be 0). */
-size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N);
+/* Bytes of device workspace theseus_wkv7_backward needs for these sizes and
+ * dtype (0 when the chunked kernels run: they need none). */
+size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtype);
 
 /* Forward recurrence.  Replaces wkv_forward (kernels/wkv7_state.cpp:16-25)
  * and launch_forward (kernels/wkv7_state.cu:81-86).

@@ -44,10 +44,15 @@ void launch_forward(const Fwd& p) {
     if (chunk_ok(p.N, p.dtype)) launch_chunk_forward(p);
     else launch_seq_forward(p);
 }
-void launch_backward(const Bwd& p) { launch_seq_backward(p); }
-size_t backward_workspace(int B, int T, int H, int N) {
+void launch_backward(const Bwd& p) {
+    if (chunk_ok(p.N, p.dtype)) launch_chunk_backward(p);
+    else launch_seq_backward(p);
+}
+// The chunked backward needs no workspace; the step-serial one replays each
+// 16-step segment into it.
+size_t backward_workspace(int B, int T, int H, int N, int dtype) {
     (void)T;
-    return seq_backward_workspace(B, H, N);
+    return chunk_ok(N, dtype) ? 0 : seq_backward_workspace(B, H, N);
 }
 
 }  // namespace wkv7
@@ -74,9 +79,9 @@ long long theseus_wkv7_checkpoint_count(int T) {
     return T < 1 ? 0 : (long long)(T + wkv7::kCkptInterval - 1) / wkv7::kCkptInterval + 1;
 }
 
-size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N) {
-    if (check_dims(B, T, H, N, THESEUS_WKV7_BF16) != THESEUS_WKV7_OK) return 0;
-    return wkv7::backward_workspace(B, T, H, N);
+size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtype) {
+    if (check_dims(B, T, H, N, dtype) != THESEUS_WKV7_OK) return 0;
+    return wkv7::backward_workspace(B, T, H, N, dtype);
 }
 
 int theseus_wkv7_forward(int B, int T, int H, int N, int dtype, const void* r, const void* w,
@@ -98,7 +103,7 @@ int theseus_wkv7_backward(int B, int T, int H, int N, int dtype, const void* r, 
     if (!r || !w || !k || !v || !a || !b || !ckpt || !dy || !dr || !dw || !dk || !dv || !da ||
         !db || !ds0)
         return THESEUS_WKV7_ERR_NULL;
-    const size_t need = wkv7::backward_workspace(B, T, H, N);
+    const size_t need = wkv7::backward_workspace(B, T, H, N, dtype);
     if (workspace_bytes < need || (need && !workspace)) return THESEUS_WKV7_ERR_WORKSPACE;
     wkv7::Bwd p{B, T, H, N, dtype, r, w, k, v, a, b, ckpt, dy, dsT,
                 dr, dw, dk, dv, da, db, ds0, workspace, stream};

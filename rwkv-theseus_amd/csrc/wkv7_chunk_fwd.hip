@@ -50,20 +50,6 @@ __device__ __forceinline__ Op op(uint16_t (&a)[2][CH * LD64]) { return Op{a[0], 
 __device__ __forceinline__ Op op16(uint16_t (&a)[2][NK * LD16]) { return Op{a[0], a[1], LD16}; }
 __device__ __forceinline__ Op opc(uint16_t (&a)[2][CH * LD16]) { return Op{a[0], a[1], LD16}; }
 
-// 8 floats -> (hi, lo) bf16x8 fragments.
-__device__ __forceinline__ void pack8(const float* x, uint4& hi, uint4& lo) {
-    split2(x[0], x[1], hi.x, lo.x);
-    split2(x[2], x[3], hi.y, lo.y);
-    split2(x[4], x[5], hi.z, lo.z);
-    split2(x[6], x[7], hi.w, lo.w);
-}
-__device__ __forceinline__ void pack4(const f32x4_t& x, uint2& hi, uint2& lo) {
-    split2(x[0], x[1], hi.x, lo.x);
-    split2(x[2], x[3], hi.y, lo.y);
-}
-__device__ __forceinline__ uint4 cat(uint2 a, uint2 b) { return make_uint4(a.x, a.y, b.x, b.y); }
-__device__ __forceinline__ uint2 ld8B(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
-
 }  // namespace
 
 __global__ __launch_bounds__(256) void chunk_forward_bf16(

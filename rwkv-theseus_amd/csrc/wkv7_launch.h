@@ -43,12 +43,13 @@ void launch_seq_forward(const Fwd& p);
 void launch_seq_backward(const Bwd& p);
 size_t seq_backward_workspace(int B, int H, int N);
 void launch_decode(const Dec& p);
-void launch_chunk_forward(const Fwd& p);  // bf16, N == 64
+void launch_chunk_forward(const Fwd& p);   // bf16, N == 64
+void launch_chunk_backward(const Bwd& p);  // bf16, N == 64
 
 // Family dispatch (wkv7_capi.cpp): the chunked MFMA kernels when they cover
 // the call, else the step-serial ones.
 void launch_forward(const Fwd& p);
 void launch_backward(const Bwd& p);
-size_t backward_workspace(int B, int T, int H, int N);
+size_t backward_workspace(int B, int T, int H, int N, int dtype);
 
 }  // namespace wkv7

@@ -108,4 +108,28 @@ __device__ __forceinline__ f32x4_t mma_k16(f32x4_t acc, const Op& A, int a_x0, c
     return acc + c;
 }
 
+// 8 floats -> (hi, lo) bf16x8 fragments (element e in slot e).
+__device__ __forceinline__ void pack8(const float* x, uint4& hi, uint4& lo) {
+    split2(x[0], x[1], hi.x, lo.x);
+    split2(x[2], x[3], hi.y, lo.y);
+    split2(x[4], x[5], hi.z, lo.z);
+    split2(x[6], x[7], hi.w, lo.w);
+}
+// accumulator (4 floats) -> (hi, lo) bf16x4 fragments: a D-layout tile used as
+// the B operand of the K=16 instruction (its rows are the contraction index).
+__device__ __forceinline__ void pack4(const f32x4_t& x, uint2& hi, uint2& lo) {
+    split2(x[0], x[1], hi.x, lo.x);
+    split2(x[2], x[3], hi.y, lo.y);
+}
+// Two 4-element fragments as one 8-element fragment: slots 0-3 = a, 4-7 = b.
+// Used for K=32 steps whose k index is permuted (slot e <-> k0+4q+e,
+// slot 4+e <-> k0+16+4q+e) so that two accumulator tiles form one B operand.
+__device__ __forceinline__ uint4 cat(uint2 a, uint2 b) { return make_uint4(a.x, a.y, b.x, b.y); }
+__device__ __forceinline__ uint2 ld8B(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+// A-operand fragment of a [row][k] plane in the permuted K=32 order above.
+__device__ __forceinline__ uint4 fragp(const uint16_t* p, int ld, int row, int k0, int lane) {
+    const uint16_t* base = p + row * ld + k0 + 4 * (lane >> 4);
+    return cat(ld8B(base), ld8B(base + 16));
+}
+
 }  // namespace wkv7

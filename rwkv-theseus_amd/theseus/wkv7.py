@@ -79,7 +79,7 @@ class Extension:
         lib.theseus_wkv7_checkpoint_interval.restype = i32
         lib.theseus_wkv7_checkpoint_count.argtypes = [i32]
         lib.theseus_wkv7_checkpoint_count.restype = ctypes.c_longlong
-        lib.theseus_wkv7_backward_workspace_size.argtypes = [i32] * 4
+        lib.theseus_wkv7_backward_workspace_size.argtypes = [i32] * 5
         lib.theseus_wkv7_backward_workspace_size.restype = sz
         lib.theseus_wkv7_forward.argtypes = [i32] * 5 + [vp] * 10 + [vp]
         lib.theseus_wkv7_forward.restype = i32
@@ -152,10 +152,11 @@ class Extension:
         with torch.cuda.device(r.device):
             grads = [torch.empty_like(r) for _ in range(6)]
             ds0 = torch.empty((B, H, N, N), dtype=torch.float32, device=r.device)
-            ws_bytes = int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N))
+            dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
+            ws_bytes = int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N, dt))
             ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=r.device)
             status = self.lib.theseus_wkv7_backward(
-                B, T, H, N, _BF16 if r.dtype == torch.bfloat16 else _FP32,
+                B, T, H, N, dt,
                 *map(_ptr, (r, w, k, v, a, b, saved, dy, dend, *grads, ds0, ws)),
                 ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)

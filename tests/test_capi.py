@@ -70,7 +70,9 @@ def test_host_queries():
     assert lib.theseus_wkv7_error_string(1) == b"invalid T or head size (2..128)"
     assert lib.theseus_wkv7_error_string(2) == b"expected BF16 or FP32"
     assert lib.theseus_wkv7_error_string(99) == b"unknown status"
-    assert lib.theseus_wkv7_backward_workspace_size(1, 0, 1, 64) == 0  # invalid T
+    assert lib.theseus_wkv7_backward_workspace_size(1, 0, 1, 64, 0) == 0  # invalid T
+    assert lib.theseus_wkv7_backward_workspace_size(2, 32, 3, 64, 0) == 0  # chunked: none
+    assert lib.theseus_wkv7_backward_workspace_size(2, 32, 3, 64, 1) > 0   # step-serial replay
 
 
 @pytest.mark.parametrize("B,T,H,N,dtype,code", [
