@@ -41,8 +41,8 @@ struct FwdLds {
     uint16_t VT[NK * LD16];                       // V^T [i][t] (exact bf16)
     uint16_t Ti[2][CH * LD16], Brb[2][CH * LD16];  // [t][s]
     uint16_t Q1[2][CH * LD16], Q2[2][CH * LD16];   // Q', Q2 [t][s]
-    float Aab[CH * CH];
-    float part[4][NK];
+    float Brk[CH * CH];   // fp32 [t][s]
+    float part[8][NK];
     float egL[NK];
 };
 
@@ -79,88 +79,142 @@ __global__ __launch_bounds__(256) void chunk_forward_bf16(
     }
 
     const int nchunk = (Tn + CH - 1) / CH;
-    for (int c = 0; c < nchunk; c++) {
-        const int t0 = c * CH, L = min(CH, Tn - t0);
-        // ---- A1: raw loads (16 B per lane, 6 tensors x 16 rows x 8 segments) ----
+    // raw chunk inputs are prefetched into registers one chunk ahead:
+    // lane-slot m covers tensor id>>7, row (id>>3)&15, 8-element segment id&7
+    uint4 pre[3];
+    auto load_chunk = [&](int cc) {
+        const int tb = cc * CH, Lc = min(CH, Tn - tb);
 #pragma unroll
         for (int m = 0; m < 3; m++) {
             const int id = tid + 256 * m, ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
             const bf16_t* src = ts == 0 ? r : ts == 1 ? w : ts == 2 ? k : ts == 3 ? v : ts == 4 ? a : b;
-            uint4 x = make_uint4(0, 0, 0, 0);
-            if (row < L) x = *reinterpret_cast<const uint4*>(src + ((long)(bb * Tn + t0 + row) * H + h) * NK + 8 * seg);
-            *reinterpret_cast<uint4*>(&sm.raw[ts][row * LD64 + 8 * seg]) = x;
+            pre[m] = make_uint4(0, 0, 0, 0);
+            if (row < Lc) pre[m] = *reinterpret_cast<const uint4*>(src + ((long)(bb * Tn + tb + row) * H + h) * NK + 8 * seg);
         }
+    };
+    load_chunk(0);
+    for (int c = 0; c < nchunk; c++) {
+        const int t0 = c * CH, L = min(CH, Tn - t0);
+        // ---- A1: prefetched inputs to LDS; start loading the next chunk ----
+#pragma unroll
+        for (int m = 0; m < 3; m++) {
+            const int id = tid + 256 * m, ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
+            *reinterpret_cast<uint4*>(&sm.raw[ts][row * LD64 + 8 * seg]) = pre[m];
+        }
+        if (c + 1 < nchunk) load_chunk(c + 1);
         __syncthreads();  // raw ready; previous chunk's state phase done with all operands
-        // ---- A2: decay cumsum and scaled operands; lane = key j, tokens 4wv..4wv+3 ----
+        // ---- A2: decay cumsum and scaled operands; lane = key pair jp, token pair tp ----
         {
-            const int j = lane;
-            float lw[4], gc[4], run = 0.f;
+            const int jp = tid & 31, tp = tid >> 5, j0 = 2 * jp, tb = 2 * tp;
+            float lw[2][2];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = 4 * wv + u;
-                lw[u] = t < L ? log_decay(bf16_to_f32(sm.raw[1][t * LD64 + j])) : 0.f;
-                run += lw[u];
-                gc[u] = run;
+            for (int u = 0; u < 2; u++) {
+                const uint32_t wb = *reinterpret_cast<const uint32_t*>(&sm.raw[1][(tb + u) * LD64 + j0]);
+#pragma unroll
+                for (int x = 0; x < 2; x++)
+                    lw[u][x] = tb + u < L ? log_decay(bf16_to_f32((uint16_t)(wb >> (16 * x)))) : 0.f;
             }
-            sm.part[wv][j] = run;
+#pragma unroll
+            for (int x = 0; x < 2; x++) sm.part[tp][j0 + x] = lw[0][x] + lw[1][x];
             __syncthreads();
-            float pre = 0.f, tot = 0.f;
+            float pre_[2] = {0.f, 0.f}, tot[2] = {0.f, 0.f};
 #pragma unroll
-            for (int w2 = 0; w2 < 4; w2++) {
-                const float p = sm.part[w2][j];
-                tot += p;
-                if (w2 < wv) pre += p;
-            }
+            for (int u = 0; u < 8; u++)
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = 4 * wv + u;
-                const float g = pre + gc[u], gp = g - lw[u];
-                const float eg = __expf(g), eng = __expf(-g), egp = __expf(gp), eL = __expf(tot - g);
-                const float rr = bf16_to_f32(sm.raw[0][t * LD64 + j]);
-                const float kk = bf16_to_f32(sm.raw[2][t * LD64 + j]);
-                const float aa = bf16_to_f32(sm.raw[4][t * LD64 + j]);
-                const float bv = bf16_to_f32(sm.raw[5][t * LD64 + j]);
-                const float at = aa * egp;
-                At.put(t, j, at);
-                AtT.put(j, t, at);
-                Rt.put(t, j, rr * eg);
-                Bb.put(t, j, bv * eng);
-                Kb.put(t, j, kk * eng);
-                BhT.put(j, t, bv * eL);
-                KhT.put(j, t, kk * eL);
-                sm.VT[j * LD16 + t] = sm.raw[3][t * LD64 + j];  // V^T[i=j][t]
+                for (int x = 0; x < 2; x++) {
+                    const float p = sm.part[u][j0 + x];
+                    tot[x] += p;
+                    if (u < tp) pre_[x] += p;
+                }
+            float vat[2][2], vrt[2][2], vbb[2][2], vkb[2][2], vbh[2][2], vkh[2][2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int t = tb + u;
+                const uint32_t rb = *reinterpret_cast<const uint32_t*>(&sm.raw[0][t * LD64 + j0]);
+                const uint32_t kb = *reinterpret_cast<const uint32_t*>(&sm.raw[2][t * LD64 + j0]);
+                const uint32_t ab = *reinterpret_cast<const uint32_t*>(&sm.raw[4][t * LD64 + j0]);
+                const uint32_t bb2 = *reinterpret_cast<const uint32_t*>(&sm.raw[5][t * LD64 + j0]);
+#pragma unroll
+                for (int x = 0; x < 2; x++) {
+                    const float g = pre_[x] + lw[0][x] + (u ? lw[1][x] : 0.f), gp = g - lw[u][x];
+                    const float eg = __expf(g), eng = __expf(-g), egp = __expf(gp), eL = __expf(tot[x] - g);
+                    const float rr = bf16_to_f32((uint16_t)(rb >> (16 * x)));
+                    const float kk = bf16_to_f32((uint16_t)(kb >> (16 * x)));
+                    const float aa = bf16_to_f32((uint16_t)(ab >> (16 * x)));
+                    const float bv = bf16_to_f32((uint16_t)(bb2 >> (16 * x)));
+                    vat[u][x] = aa * egp;
+                    vrt[u][x] = rr * eg;
+                    vbb[u][x] = bv * eng;
+                    vkb[u][x] = kk * eng;
+                    vbh[u][x] = bv * eL;
+                    vkh[u][x] = kk * eL;
+                }
             }
-            if (wv == 0) sm.egL[j] = __expf(tot);
+            auto put_row = [&](const Op& o, const float (&vv)[2][2]) {  // [t][j] pairs along j
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    uint32_t hh, ll;
+                    split2(vv[u][0], vv[u][1], hh, ll);
+                    *reinterpret_cast<uint32_t*>(&o.hi[(tb + u) * o.ld + j0]) = hh;
+                    *reinterpret_cast<uint32_t*>(&o.lo[(tb + u) * o.ld + j0]) = ll;
+                }
+            };
+            auto put_col = [&](const Op& o, const float (&vv)[2][2]) {  // [j][t] pairs along t
+#pragma unroll
+                for (int x = 0; x < 2; x++) {
+                    uint32_t hh, ll;
+                    split2(vv[0][x], vv[1][x], hh, ll);
+                    *reinterpret_cast<uint32_t*>(&o.hi[(j0 + x) * o.ld + tb]) = hh;
+                    *reinterpret_cast<uint32_t*>(&o.lo[(j0 + x) * o.ld + tb]) = ll;
+                }
+            };
+            put_row(At, vat);
+            put_row(Rt, vrt);
+            put_row(Bb, vbb);
+            put_row(Kb, vkb);
+            put_col(AtT, vat);
+            put_col(BhT, vbh);
+            put_col(KhT, vkh);
+            {
+                const uint32_t v0 = *reinterpret_cast<const uint32_t*>(&sm.raw[3][tb * LD64 + j0]);
+                const uint32_t v1 = *reinterpret_cast<const uint32_t*>(&sm.raw[3][(tb + 1) * LD64 + j0]);
+                *reinterpret_cast<uint32_t*>(&sm.VT[j0 * LD16 + tb]) = (v0 & 0xffffu) | (v1 << 16);
+                *reinterpret_cast<uint32_t*>(&sm.VT[(j0 + 1) * LD16 + tb]) = (v0 >> 16) | (v1 & 0xffff0000u);
+            }
+            if (tp == 0) {
+                sm.egL[j0] = __expf(tot[0]);
+                sm.egL[j0 + 1] = __expf(tot[1]);
+            }
         }
         __syncthreads();
-        // ---- A3: chunk matrices; wave 0 Aab (-> Ti), wave 1 Aak (-> Q', Q2), wave 2 Brb ----
+        // ---- A3: chunk matrices; wave 0: Aab, Aab^T -> Ti; wave 1: Aak; wave 2: Brb; wave 3: Brk ----
         f32x4_t cm = zero4();
-        if (wv == 0) cm = mma_k32<2>(zero4(), At, 0, Bb, 0, 0, lane);
-        if (wv == 1) cm = mma_k32<2>(zero4(), At, 0, Kb, 0, 0, lane);
-        if (wv == 2) cm = mma_k32<2>(zero4(), Rt, 0, Bb, 0, 0, lane);
+        if (wv == 0) {
+            f32x4_t L = mma_k32<2>(zero4(), At, 0, Bb, 0, 0, lane);
+            f32x4_t LT = mma_k32<2>(zero4(), Bb, 0, At, 0, 0, lane);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {  // D layout: row t = 4q+e, column s = r16
-            const int t = 4 * q + e, s = r16;
-            if (wv < 2 ? s >= t : s > t) cm[e] = 0.f;
-            if (wv == 0) sm.Aab[t * CH + s] = cm[e];
-            if (wv == 2) Brb.put(t, s, cm[e]);
-        }
-        __syncthreads();
-        // ---- A4: Ti = (I - Aab)^{-1} by forward substitution, one lane per column ----
-        if (wv == 0 && lane < CH) {
-            float X[CH];
-#pragma unroll
-            for (int t = 0; t < CH; t++) {
-                float acc = t == lane ? 1.f : 0.f;
-#pragma unroll
-                for (int s = 0; s < t; s++) acc += sm.Aab[t * CH + s] * X[s];
-                X[t] = acc;
+            for (int e = 0; e < 4; e++) {  // keep s < t (L), row < column (L^T)
+                if (r16 >= 4 * q + e) L[e] = 0.f;
+                if (r16 <= 4 * q + e) LT[e] = 0.f;
             }
+            f32x4_t ti, tiT;
+            tri_inverse(L, LT, lane, ti, tiT);
 #pragma unroll
-            for (int t = 0; t < CH; t++) Ti.put(t, lane, X[t]);
+            for (int e = 0; e < 4; e++) Ti.put(4 * q + e, r16, ti[e]);
+        } else {
+            if (wv == 1) cm = mma_k32<2>(zero4(), At, 0, Kb, 0, 0, lane);
+            else if (wv == 2) cm = mma_k32<2>(zero4(), Rt, 0, Bb, 0, 0, lane);
+            else cm = mma_k32<2>(zero4(), Rt, 0, Kb, 0, 0, lane);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {  // D layout: row t = 4q+e, column s = r16
+                const int t = 4 * q + e, s = r16;
+                if (wv == 1 ? s >= t : s > t) cm[e] = 0.f;
+                if (wv == 2) Brb.put(t, s, cm[e]);
+                if (wv == 3) sm.Brk[t * CH + s] = cm[e];
+            }
         }
         __syncthreads();
-        // ---- A5: P = Ti A~ and P2 = R~ + Brb P on key strip 16wv..; wave 1: Q', Q2 ----
+        // ---- A5: P = Ti A~ and P2 = R~ + Brb P on key strip 16wv..; wave 1: Q' = Ti Aak, Q2 = Brk + Brb Q' ----
         {
             const int j = 16 * wv + r16;
             f32x4_t p = mma_k16(zero4(), Ti, 0, AtT, 16 * wv, 0, lane);
@@ -192,13 +246,11 @@ __global__ __launch_bounds__(256) void chunk_forward_bf16(
                 uint2 qh, ql;
                 pack4(q1, qh, ql);
                 const uint2 bh_ = frag16(Brb.hi, LD16, 0, 0, lane), bl_ = frag16(Brb.lo, LD16, 0, 0, lane);
-                // Brk: recompute R~ K-^T rows here (wave 3 owns it in registers); cheap K=64 product
-                f32x4_t brk = mma_k32<2>(zero4(), Rt, 0, Kb, 0, 0, lane);
                 f32x4_t q2 = mma16(zero4(), bh_, qh);
                 f32x4_t c3 = mma16(zero4(), bh_, ql);
                 c3 = mma16(c3, bl_, qh);
 #pragma unroll
-                for (int e = 0; e < 4; e++) q2[e] += c3[e] + (r16 > 4 * q + e ? 0.f : brk[e]);
+                for (int e = 0; e < 4; e++) q2[e] += c3[e] + sm.Brk[(4 * q + e) * CH + r16];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     Q1.put(4 * q + e, r16, q1[e]);

@@ -132,4 +132,55 @@ __device__ __forceinline__ uint4 fragp(const uint16_t* p, int ld, int row, int k
     return cat(ld8B(base), ld8B(base + 16));
 }
 
+// ---------------------------------------------------------------------------
+// 16x16 tile algebra entirely in accumulator registers.
+// A D-layout tile X (lane (q, r16) holds X[4q+e][r16]) is the B operand of
+// the K=16 instruction as it stands, and it is the A operand of X^T.  So a
+// product Z = X Y needs X^T and Y in D layout, and Z^T = Y^T X^T uses the same
+// two packed tiles with the roles swapped.
+// ---------------------------------------------------------------------------
+struct Pk {
+    uint2 h, l;
+};
+__device__ __forceinline__ Pk pk(const f32x4_t& x) {
+    Pk p;
+    pack4(x, p.h, p.l);
+    return p;
+}
+// split-precision product of packed tiles: A = packed D-layout of X^T, B = of Y
+__device__ __forceinline__ f32x4_t mm16s(const Pk& A, const Pk& B) {
+    const f32x4_t acc = mma16(zero4(), A.h, B.h);
+    f32x4_t c = mma16(zero4(), A.h, B.l);
+    c = mma16(c, A.l, B.h);
+    return acc + c;
+}
+// (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8) for a strictly lower
+// triangular 16x16 L (L^16 = 0), from L and L^T in D layout; returns the
+// inverse and its transpose in D layout.
+__device__ __forceinline__ void tri_inverse(const f32x4_t& L, const f32x4_t& LT, int lane, f32x4_t& Ti,
+                                            f32x4_t& TiT) {
+    const Pk pL = pk(L), pLT = pk(LT);
+    const f32x4_t L2 = mm16s(pLT, pL), L2T = mm16s(pL, pLT);
+    const Pk pL2 = pk(L2), pL2T = pk(L2T);
+    const f32x4_t L4 = mm16s(pL2T, pL2), L4T = mm16s(pL2, pL2T);
+    const Pk pL4 = pk(L4), pL4T = pk(L4T);
+    const Pk pL8T = pk(mm16s(pL4, pL4T));
+    f32x4_t M, MT;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float d = (4 * (lane >> 4) + e) == (lane & 15) ? 1.f : 0.f;
+        M[e] = L[e] + d;
+        MT[e] = LT[e] + d;
+    }
+    Pk pM = pk(M);
+    M += mm16s(pL2T, pM);
+    MT += mm16s(pM, pL2T);
+    pM = pk(M);
+    M += mm16s(pL4T, pM);
+    MT += mm16s(pM, pL4T);
+    pM = pk(M);
+    Ti = M + mm16s(pL8T, pM);
+    TiT = MT + mm16s(pM, pL8T);
+}
+
 }  // namespace wkv7
