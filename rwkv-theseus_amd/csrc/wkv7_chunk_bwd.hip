@@ -60,11 +60,10 @@ struct BwdLds {
     uint16_t VT[NK * LD16], dYT[NK * LD16];  // [i][t], exact bf16
     PlaneS HT, S0T;               // H^T, S0^T as [j][i]
     PlaneC Ti, TiT, BrbT, AakT, BrkT, Q1;  // [t][s]
-    float Aab[CH * CH];
     float g[CH * NK];             // cumulative log-decay [t][j]
     float zs[CH * NK];            // dlogd terms, then dlogd [t][j]
     float t2s[CH * NK];           // (a dA) terms [t][j]
-    float part[4][NK];
+    float part[8][NK];
     float egL[NK];
 };
 
@@ -147,100 +146,162 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
     }
 
     const int nchunk = (Tn + CH - 1) / CH;
+    // Inputs of the next chunk to process (c-1) are prefetched into registers:
+    // slot m of lane tid covers tensor id>>7, row (id>>3)&15, segment id&7.
+    uint4 pre[4];
+    float4 S0n[4];
+    auto load_chunk = [&](int cc) {
+        const int tb = cc * CH, Lc = min(CH, Tn - tb);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int id = tid + 256 * m, ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
+            pre[m] = make_uint4(0, 0, 0, 0);
+            if (id < 7 * 128 && row < Lc) {
+                const bf16_t* src = ts == 0 ? r : ts == 1 ? w : ts == 2 ? k : ts == 3 ? v : ts == 4 ? a : ts == 5 ? b : dy;
+                pre[m] = *reinterpret_cast<const uint4*>(src + ((long)(bb * Tn + tb + row) * H + h) * NK + 8 * seg);
+            }
+        }
+#pragma unroll
+        for (int tj = 0; tj < 4; tj++)
+            S0n[tj] = *reinterpret_cast<const float4*>(ckpt + (bh * ncp + cc) * NN + (long)i_own * NK + 16 * tj + 4 * q);
+    };
+    auto store_raw = [&]() {
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int id = tid + 256 * m, ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
+            if (id < 7 * 128) *reinterpret_cast<uint4*>(&sm.raw[ts][row * LD64 + 8 * seg]) = pre[m];
+        }
+    };
+    f32x4_t S0t[4];
+    load_chunk(nchunk - 1);
+    store_raw();
+#pragma unroll
+    for (int tj = 0; tj < 4; tj++) S0t[tj] = f32x4_t{S0n[tj].x, S0n[tj].y, S0n[tj].z, S0n[tj].w};
     for (int c = nchunk - 1; c >= 0; c--) {
         const int t0 = c * CH, L = min(CH, Tn - t0);
-        // ---- A1: raw loads (7 tensors x 16 rows x 8 segments of 16 B) + S0 ----
-        for (int id = tid; id < 7 * 128; id += 256) {
-            const int ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
-            const bf16_t* src = ts == 0 ? r : ts == 1 ? w : ts == 2 ? k : ts == 3 ? v : ts == 4 ? a : ts == 5 ? b : dy;
-            uint4 x = make_uint4(0, 0, 0, 0);
-            if (row < L) x = *reinterpret_cast<const uint4*>(src + ((long)(bb * Tn + t0 + row) * H + h) * NK + 8 * seg);
-            *reinterpret_cast<uint4*>(&sm.raw[ts][row * LD64 + 8 * seg]) = x;
-        }
-        f32x4_t S0t[4];
-#pragma unroll
-        for (int tj = 0; tj < 4; tj++) {
-            const float4 s = *reinterpret_cast<const float4*>(ckpt + (bh * ncp + c) * NN + (long)i_own * NK + 16 * tj + 4 * q);
-            S0t[tj] = f32x4_t{s.x, s.y, s.z, s.w};
-        }
+        // ---- A1: start loading chunk c-1; raw of chunk c is already in LDS ----
+        if (c > 0) load_chunk(c - 1);
         __syncthreads();  // raw ready; the later chunk's stage C is done with LDS
-        // ---- A2: decay cumsum and scaled operands; lane = key j, tokens 4wv.. ----
+        // ---- A2: decay cumsum and scaled operands; lane = key pair jp, token pair tp ----
         {
-            const int j = lane;
-            float lw[4], gc[4], run = 0.f;
+            const int jp = tid & 31, tp = tid >> 5, j0 = 2 * jp, tb = 2 * tp;
+            float lw[2][2];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = 4 * wv + u;
-                lw[u] = t < L ? log_decay(bf16_to_f32(sm.raw[1][t * LD64 + j])) : 0.f;
-                run += lw[u];
-                gc[u] = run;
+            for (int u = 0; u < 2; u++) {
+                const uint32_t wb = *reinterpret_cast<const uint32_t*>(&sm.raw[1][(tb + u) * LD64 + j0]);
+#pragma unroll
+                for (int x = 0; x < 2; x++)
+                    lw[u][x] = tb + u < L ? log_decay(bf16_to_f32((uint16_t)(wb >> (16 * x)))) : 0.f;
             }
-            sm.part[wv][j] = run;
+#pragma unroll
+            for (int x = 0; x < 2; x++) sm.part[tp][j0 + x] = lw[0][x] + lw[1][x];
             __syncthreads();
-            float pre = 0.f, tot = 0.f;
+            float pre_[2] = {0.f, 0.f}, tot[2] = {0.f, 0.f};
 #pragma unroll
-            for (int w2 = 0; w2 < 4; w2++) {
-                const float p = sm.part[w2][j];
-                tot += p;
-                if (w2 < wv) pre += p;
-            }
+            for (int u = 0; u < 8; u++)
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = 4 * wv + u;
-                const float g = pre + gc[u], gp = g - lw[u];
-                const float eg = __expf(g), eng = __expf(-g), egp = __expf(gp), eL = __expf(tot - g);
-                const float rr = bf16_to_f32(sm.raw[0][t * LD64 + j]);
-                const float kk = bf16_to_f32(sm.raw[2][t * LD64 + j]);
-                const float aa = bf16_to_f32(sm.raw[4][t * LD64 + j]);
-                const float bv = bf16_to_f32(sm.raw[5][t * LD64 + j]);
-                const float at = aa * egp, rt = rr * eg, bbar = bv * eng, kbar = kk * eng;
-                At.put(t, j, at);
-                AtT.put(j, t, at);
-                Rt.put(t, j, rt);
-                RtT.put(j, t, rt);
-                Bb.put(t, j, bbar);
-                BbT.put(j, t, bbar);
-                Kb.put(t, j, kbar);
-                KbT.put(j, t, kbar);
-                BhT.put(j, t, bv * eL);
-                Kh.put(t, j, kk * eL);
-                sm.VT[j * LD16 + t] = sm.raw[3][t * LD64 + j];
-                sm.dYT[j * LD16 + t] = sm.raw[6][t * LD64 + j];
-                sm.g[t * NK + j] = g;
+                for (int x = 0; x < 2; x++) {
+                    const float p = sm.part[u][j0 + x];
+                    tot[x] += p;
+                    if (u < tp) pre_[x] += p;
+                }
+            float vat[2][2], vrt[2][2], vbb[2][2], vkb[2][2], vbh[2][2], vkh[2][2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int t = tb + u;
+                const uint32_t rb = *reinterpret_cast<const uint32_t*>(&sm.raw[0][t * LD64 + j0]);
+                const uint32_t kb = *reinterpret_cast<const uint32_t*>(&sm.raw[2][t * LD64 + j0]);
+                const uint32_t ab = *reinterpret_cast<const uint32_t*>(&sm.raw[4][t * LD64 + j0]);
+                const uint32_t bb2 = *reinterpret_cast<const uint32_t*>(&sm.raw[5][t * LD64 + j0]);
+                float gv[2];
+#pragma unroll
+                for (int x = 0; x < 2; x++) {
+                    const float g = pre_[x] + lw[0][x] + (u ? lw[1][x] : 0.f), gp = g - lw[u][x];
+                    gv[x] = g;
+                    const float eg = __expf(g), eng = __expf(-g), egp = __expf(gp), eL = __expf(tot[x] - g);
+                    const float rr = bf16_to_f32((uint16_t)(rb >> (16 * x)));
+                    const float kk = bf16_to_f32((uint16_t)(kb >> (16 * x)));
+                    const float aa = bf16_to_f32((uint16_t)(ab >> (16 * x)));
+                    const float bv = bf16_to_f32((uint16_t)(bb2 >> (16 * x)));
+                    vat[u][x] = aa * egp;
+                    vrt[u][x] = rr * eg;
+                    vbb[u][x] = bv * eng;
+                    vkb[u][x] = kk * eng;
+                    vbh[u][x] = bv * eL;
+                    vkh[u][x] = kk * eL;
+                }
+                *reinterpret_cast<float2*>(&sm.g[t * NK + j0]) = make_float2(gv[0], gv[1]);
             }
-            if (wv == 0) sm.egL[j] = __expf(tot);
+            auto put_row = [&](const Op& o, const float (&vv)[2][2]) {  // [t][j] pairs along j
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    uint32_t hh, ll;
+                    split2(vv[u][0], vv[u][1], hh, ll);
+                    *reinterpret_cast<uint32_t*>(&o.hi[(tb + u) * o.ld + j0]) = hh;
+                    *reinterpret_cast<uint32_t*>(&o.lo[(tb + u) * o.ld + j0]) = ll;
+                }
+            };
+            auto put_col = [&](const Op& o, const float (&vv)[2][2]) {  // [j][t] pairs along t
+#pragma unroll
+                for (int x = 0; x < 2; x++) {
+                    uint32_t hh, ll;
+                    split2(vv[0][x], vv[1][x], hh, ll);
+                    *reinterpret_cast<uint32_t*>(&o.hi[(j0 + x) * o.ld + tb]) = hh;
+                    *reinterpret_cast<uint32_t*>(&o.lo[(j0 + x) * o.ld + tb]) = ll;
+                }
+            };
+            put_row(At, vat);
+            put_col(AtT, vat);
+            put_row(Rt, vrt);
+            put_col(RtT, vrt);
+            put_row(Bb, vbb);
+            put_col(BbT, vbb);
+            put_row(Kb, vkb);
+            put_col(KbT, vkb);
+            put_col(BhT, vbh);
+            put_row(Kh, vkh);
+            auto put_raw_col = [&](int ts, uint16_t* dst) {  // exact bf16 plane, transposed
+                const uint32_t v0 = *reinterpret_cast<const uint32_t*>(&sm.raw[ts][tb * LD64 + j0]);
+                const uint32_t v1 = *reinterpret_cast<const uint32_t*>(&sm.raw[ts][(tb + 1) * LD64 + j0]);
+                *reinterpret_cast<uint32_t*>(&dst[j0 * LD16 + tb]) = (v0 & 0xffffu) | (v1 << 16);
+                *reinterpret_cast<uint32_t*>(&dst[(j0 + 1) * LD16 + tb]) = (v0 >> 16) | (v1 & 0xffff0000u);
+            };
+            put_raw_col(3, sm.VT);
+            put_raw_col(6, sm.dYT);
+            if (tp == 0) {
+                sm.egL[j0] = __expf(tot[0]);
+                sm.egL[j0 + 1] = __expf(tot[1]);
+            }
         }
         __syncthreads();
-        // ---- A3: chunk matrices (one per wave), operand forms to LDS ----
-        f32x4_t cm;
-        if (wv == 0) cm = mm64(At, Bb, 0, lane);        // Aab
-        else if (wv == 1) cm = mm64(At, Kb, 0, lane);   // Aak
-        else if (wv == 2) cm = mm64(Rt, Bb, 0, lane);   // Brb
-        else cm = mm64(Rt, Kb, 0, lane);                // Brk
+        // ---- A3: chunk matrices; wave 0: Aab, Aab^T -> Ti, Ti^T; waves 1-3: Aak, Brb, Brk ----
+        f32x4_t cm = zero4();
+        if (wv == 0) {
+            f32x4_t Lm = mm64(At, Bb, 0, lane);
+            f32x4_t LT = mm64(Bb, At, 0, lane);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {  // D layout: row t = 4q+e, column s = r16
-            const int t = 4 * q + e, s = r16;
-            if (wv < 2 ? s >= t : s > t) cm[e] = 0.f;
-            if (wv == 0) sm.Aab[t * CH + s] = cm[e];
-            if (wv == 1) AakT.put(s, t, cm[e]);
-            if (wv == 2) BrbT.put(s, t, cm[e]);
-            if (wv == 3) BrkT.put(s, t, cm[e]);
-        }
-        __syncthreads();
-        // ---- A4: Ti = (I - Aab)^{-1}, one lane per column ----
-        if (wv == 0 && lane < CH) {
-            float X[CH];
-#pragma unroll
-            for (int t = 0; t < CH; t++) {
-                float acc = t == lane ? 1.f : 0.f;
-#pragma unroll
-                for (int s = 0; s < t; s++) acc += sm.Aab[t * CH + s] * X[s];
-                X[t] = acc;
+            for (int e = 0; e < 4; e++) {
+                if (r16 >= 4 * q + e) Lm[e] = 0.f;
+                if (r16 <= 4 * q + e) LT[e] = 0.f;
             }
+            f32x4_t ti, tiT;
+            tri_inverse(Lm, LT, lane, ti, tiT);
 #pragma unroll
-            for (int t = 0; t < CH; t++) {
-                Ti.put(t, lane, X[t]);
-                TiT.put(lane, t, X[t]);
+            for (int e = 0; e < 4; e++) {
+                Ti.put(4 * q + e, r16, ti[e]);
+                TiT.put(4 * q + e, r16, tiT[e]);
+            }
+        } else {
+            if (wv == 1) cm = mm64(At, Kb, 0, lane);        // Aak
+            else if (wv == 2) cm = mm64(Rt, Bb, 0, lane);   // Brb
+            else cm = mm64(Rt, Kb, 0, lane);                // Brk
+#pragma unroll
+            for (int e = 0; e < 4; e++) {  // D layout: row t = 4q+e, column s = r16
+                const int t = 4 * q + e, s = r16;
+                if (wv == 1 ? s >= t : s > t) cm[e] = 0.f;
+                if (wv == 1) AakT.put(s, t, cm[e]);
+                if (wv == 2) BrbT.put(s, t, cm[e]);
+                if (wv == 3) BrkT.put(s, t, cm[e]);
             }
         }
         __syncthreads();
@@ -269,6 +330,8 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
         __syncthreads();
         // ---- B: wave-local rows i_own: SA, Q, dV, and H update ----
         f32x4_t Hn[4];
+        f32x4_t dvk;              // dV[t = 4q+e][i_own], stored at the end of the chunk
+        float gk_[4], gb_[4], gr_[4], ga_[4], gw_[4];  // key-strip gradients, stored at the end
         {
             const uint2 vfr = ld8B(&sm.VT[i_own * LD16 + 4 * q]);   // V[t=4q..][i_own]
             const uint2 dyf = ld8B(&sm.dYT[i_own * LD16 + 4 * q]);  // dY[t=4q..][i_own]
@@ -329,10 +392,10 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
                 d2 = mma16(d2, frag16(BrkT.lo, LD16, 0, 0, lane), dyf);
                 dvv += d2 + d3;
             }
+            dvk = dvv;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int t = 4 * q + e;
-                if (t < L) dv[((long)(bb * Tn + t0 + t) * H + h) * NK + i_own].bits = f32_to_bf16(dvv[e]);
                 Qs.put(t, i_own, qq[e]);
                 SAs.put(t, i_own, sa[e]);
             }
@@ -444,13 +507,10 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
                 sg[e] = sigmoidf_(wv_);
                 z[e] = rr * vR - bv * vB - kk * vK;
                 t2v[e] = aa * vA;
-                if (t < L) {
-                    const long o = ((long)(bb * Tn + t0 + t) * H + h) * NK + j_own;
-                    dk[o].bits = f32_to_bf16(vK);
-                    db[o].bits = f32_to_bf16(vB);
-                    dr[o].bits = f32_to_bf16(vR);
-                    da[o].bits = f32_to_bf16(vA);
-                }
+                gk_[e] = vK;
+                gb_[e] = vB;
+                gr_[e] = vR;
+                ga_[e] = vA;
                 sm.zs[t * NK + j_own] = z[e];
                 sm.t2s[t * NK + j_own] = t2v[e];
             }
@@ -469,15 +529,32 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int t = 4 * q + e;
-                if (t < L) {
-                    const float dl = sm.zs[t * NK + j_own];
-                    dw[((long)(bb * Tn + t0 + t) * H + h) * NK + j_own].bits =
-                        f32_to_bf16(dl * (-DECAY_SCALE) * sg[e] * (1.f - sg[e]));
-                }
+                gw_[e] = sm.zs[t * NK + j_own] * (-DECAY_SCALE) * sg[e] * (1.f - sg[e]);
             }
         }
 #pragma unroll
         for (int tj = 0; tj < 4; tj++) Ht[tj] = Hn[tj];
+        // ---- D: next chunk's inputs into LDS, then this chunk's gradient stores ----
+        // (the prefetch wait comes before the stores are issued, so it never waits on them)
+        if (c > 0) {
+            __syncthreads();  // every wave is done reading raw
+            store_raw();
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++) S0t[tj] = f32x4_t{S0n[tj].x, S0n[tj].y, S0n[tj].z, S0n[tj].w};
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 4 * q + e;
+            if (t < L) {
+                dv[((long)(bb * Tn + t0 + t) * H + h) * NK + i_own].bits = f32_to_bf16(dvk[e]);
+                const long o = ((long)(bb * Tn + t0 + t) * H + h) * NK + j_own;
+                dk[o].bits = f32_to_bf16(gk_[e]);
+                db[o].bits = f32_to_bf16(gb_[e]);
+                dr[o].bits = f32_to_bf16(gr_[e]);
+                da[o].bits = f32_to_bf16(ga_[e]);
+                dw[o].bits = f32_to_bf16(gw_[e]);
+            }
+        }
     }
 #pragma unroll
     for (int tj = 0; tj < 4; tj++)

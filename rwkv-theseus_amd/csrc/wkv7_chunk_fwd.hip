@@ -92,16 +92,19 @@ __global__ __launch_bounds__(256) void chunk_forward_bf16(
             if (row < Lc) pre[m] = *reinterpret_cast<const uint4*>(src + ((long)(bb * Tn + tb + row) * H + h) * NK + 8 * seg);
         }
     };
-    load_chunk(0);
-    for (int c = 0; c < nchunk; c++) {
-        const int t0 = c * CH, L = min(CH, Tn - t0);
-        // ---- A1: prefetched inputs to LDS; start loading the next chunk ----
+    auto store_raw = [&]() {
 #pragma unroll
         for (int m = 0; m < 3; m++) {
             const int id = tid + 256 * m, ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
             *reinterpret_cast<uint4*>(&sm.raw[ts][row * LD64 + 8 * seg]) = pre[m];
         }
-        if (c + 1 < nchunk) load_chunk(c + 1);
+    };
+    load_chunk(0);
+    store_raw();
+    if (nchunk > 1) load_chunk(1);
+    for (int c = 0; c < nchunk; c++) {
+        const int t0 = c * CH, L = min(CH, Tn - t0);
+        // ---- A1: inputs of chunk c were put in LDS during the previous chunk ----
         __syncthreads();  // raw ready; previous chunk's state phase done with all operands
         // ---- A2: decay cumsum and scaled operands; lane = key pair jp, token pair tp ----
         {
@@ -260,6 +263,13 @@ __global__ __launch_bounds__(256) void chunk_forward_bf16(
         }
         __syncthreads();
         // ---- B: state phase, wave-local (value rows i_own) ----
+        // raw is dead after A2: park the prefetched chunk c+1 there and start
+        // loading chunk c+2 before this phase issues its y / state stores, so
+        // the next wait on the prefetch never waits on those stores
+        if (c + 1 < nchunk) {
+            store_raw();
+            if (c + 2 < nchunk) load_chunk(c + 2);
+        }
         {
             // V fragment, B operand for K=16 (rows t = 4q.., column i_own); exact in bf16
             const uint2 vfr = ld8B(&sm.VT[i_own * LD16 + 4 * q]);
