@@ -185,6 +185,13 @@ def main():
         step_bytes = alg_bytes(B, T, H, N, "fwd") + (0 if args.config == "c1" else alg_bytes(B, T, H, N, "bwd"))
     step_gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
 
+    traffic = None  # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC runs
+    tf = ROOT / "profiles" / f"wkv7_{args.config}_traffic.json"
+    if tf.exists():
+        rec = json.loads(tf.read_text())
+        if (rec.get("B"), rec.get("T"), rec.get("H"), rec.get("N")) == (B, T, H, N):
+            traffic = rec["bytes_per_launch"].get(dom)
+
     cpu = None
     if args.cpu_slice and args.config == "c2":
         cpu = cpu_baseline(B, H, N, args.cpu_slice, cfg["seed"])
@@ -210,7 +217,7 @@ def main():
         "hbm_frac_alg": round(step_gbps / HBM_PEAK_GBPS, 4),
         "kernel_ms": {k: round(v[0], 4) for k, v in kern.items()},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "alg_bytes_per_launch": dom_bytes},
         "cpu_baseline": cpu,
     }
