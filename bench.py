@@ -34,7 +34,67 @@ CONFIGS = {
     "c2": dict(B=4, T=2048, H=80, N=64, s0_std=0.1, seed=20262),
     "c1": dict(B=1, T=4096, H=80, N=64, s0_std=0.0, seed=20261),
     "c4": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
+    "c3": dict(B=2, T=4096, H=80, N=64, s0_std=0.0, seed=20263),
 }
+
+
+def timemix_step_flops(B, T, C, rank, grank):
+    """Matrix FLOPs of one TimeMix forward+backward: 4 dense CxC projections and the
+    w/a (rank) and g (grank) LoRAs, each 2*M*K*N forward and twice that backward."""
+    M = B * T
+    fwd = 4 * 2 * M * C * C + 2 * (2 * 2 * M * C * rank) + 2 * 2 * M * C * grank
+    return 3 * fwd
+
+
+def bench_timemix(args, cfg):
+    """Config 3: one TimeMix layer (C=5120, H=80, N=64, reference geometry: w/a LoRA rank 192,
+    g rank 352, no v-LoRA) forward+backward, bf16 autocast over fp32 parameters, weights
+    N(0,0.02), x ~ N(0,1)."""
+    import torch
+    from theseus.timemix import TimeMix
+
+    B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
+    C = H * N
+    torch.manual_seed(cfg["seed"])
+    m = TimeMix(C, 3, 8, head_size=N, backend="cuda").cuda()
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if p.dim() == 2 and name != "r_k":
+                p.normal_(0, .02)
+    if args.timemix_unfused:
+        import theseus.fused as fz
+        fz.available = lambda *a, **k: False
+    x = torch.randn(B, T, C, device="cuda", dtype=torch.bfloat16)
+    gy = torch.randn(B, T, C, device="cuda", dtype=torch.bfloat16)
+
+    def one_step():
+        m.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y, _ = m(x)
+        y.backward(gy)
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    rank = max(32, round(2.5 * (C ** .5) / 32) * 32)
+    grank = max(32, round(5 * (C ** .5) / 32) * 32)
+    fl = timemix_step_flops(B, T, C, rank, grank)
+    tflops = fl / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "TimeMix layer fwd+bwd tokens/s (C=5120, H=80, N=64, bf16 autocast)",
+        "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "timemix_fwd_bwd", "B": B, "T": T, "C": C, "lora_rank": rank,
+                   "gate_rank": grank, "fused_elementwise": not args.timemix_unfused},
+        "roofline": {"kernel": "layer (GEMM-dominated)", "bound": "mfma", "achieved": round(tflops, 1),
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None}}),
+        flush=True)
 
 
 def alg_bytes(B, T, H, N, which):
@@ -83,6 +143,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-slice", type=int, default=256, help="T of each CPU baseline slice (0: skip)")
+    ap.add_argument("--timemix-unfused", action="store_true",
+                    help="config c3 only: run TimeMix's elementwise parts as torch ops (comparison)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (3 launches), to scale rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against known traffic")
@@ -109,6 +171,9 @@ def main():
     from theseus.synthetic import wkv7_inputs
 
     cfg = CONFIGS[args.config]
+    if args.config == "c3":
+        torch.cuda.set_device(0)
+        return bench_timemix(args, cfg)
     B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -1,0 +1,68 @@
+/*
+ * theseus_timemix.h -- C ABI of the fused TimeMix elementwise kernels in
+ * libtheseus_wkv7.so (gfx950).  They replace the torch op sequences around the
+ * recurrence in TimeMix.forward (theseus/timemix.py:66-89); the reference has no
+ * native counterpart (it runs ~20 separate torch kernels there).
+ *
+ * Activations are [B,T,C] contiguous bf16 except `a` (float32, the dtype
+ * sigmoid(a0 + ...) has under bf16 autocast with float32 parameters); per-channel
+ * parameters are float32 [C] (r_k is [H,N] = [C]).  Parameter gradients are
+ * reduced over B*T in a fixed order through a caller-provided float32 workspace
+ * (theseus_tm_*_workspace gives its size), then written to [C] outputs.
+ * Head size N must be 64 (8 lanes x 8 channels per head row).  All calls are
+ * asynchronous on `stream`; status codes are those of theseus_wkv7.h.
+ */
+#ifndef THESEUS_TIMEMIX_H
+#define THESEUS_TIMEMIX_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+/* mixed_n = x + (shift(x) - x) * coef_n for n in r,w,k,v,a,g
+ * (theseus/timemix.py:70-71); shift(x)[t] = x[t-1], shift(x)[0] = shift_state.
+ * coef: [6][C] float32 in the order r,w,k,v,a,g; out: 6 pointers, same order. */
+int theseus_tm_shift_lerp_fwd(int B, int T, int C, const void* x, const void* shift_state,
+                              const float* coef, void* const* out, hipStream_t stream);
+size_t theseus_tm_shift_lerp_workspace(int B, int T, int C);
+/* dmixed: 6 pointers (bf16); writes dx [B,T,C] bf16, dshift [B,C] bf16, dcoef [6][C] f32 */
+int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dmixed, const void* x,
+                              const void* shift_state, const float* coef, void* dx, void* dshift,
+                              float* dcoef, float* workspace, size_t workspace_bytes,
+                              hipStream_t stream);
+
+/* WKV operands (theseus/timemix.py:78-80): kk = normalize(k * k_k) per head (eps 1e-12),
+ * kw = k * (1 + (a - 1) * k_a), aw = -kk, bw = kk * a, all written as bf16. */
+int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const float* a, const float* k_k,
+                      const float* k_a, void* kw, void* aw, void* bw, hipStream_t stream);
+size_t theseus_tm_kk_workspace(int B, int T, int C);
+/* writes dk (bf16), da (f32), dk_k, dk_a ([C] f32) */
+int theseus_tm_kk_bwd(int B, int T, int C, const void* dkw, const void* daw, const void* dbw,
+                      const void* k, const float* a, const float* k_k, const float* k_a, void* dk,
+                      float* da, float* dk_k, float* dk_a, float* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/* out = (GroupNorm_H(y; ln_w, ln_b, eps) + (sum_n r*kmod*r_k) v) * g, all float32
+ * arithmetic, written as bf16 (theseus/timemix.py:83-88); kmod = k * (1 + (a-1) * k_a). */
+int theseus_tm_gn_fwd(int B, int T, int C, const void* y, const void* r, const void* k,
+                      const float* a, const float* k_a, const void* v, const void* g,
+                      const float* r_k, const float* ln_w, const float* ln_b, float eps, void* out,
+                      hipStream_t stream);
+size_t theseus_tm_gn_workspace(int B, int T, int C);
+/* writes dy, dr, dk, dv, dg (bf16), da (f32), and [C] f32 dr_k, dln_w, dln_b, dk_a */
+int theseus_tm_gn_bwd(int B, int T, int C, const void* dout, const void* y, const void* r,
+                      const void* k, const float* a, const float* k_a, const void* v, const void* g,
+                      const float* r_k, const float* ln_w, const float* ln_b, float eps, void* dy,
+                      void* dr, void* dk, void* dv, void* dg, float* da, float* dr_k, float* dln_w,
+                      float* dln_b, float* dk_a, float* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THESEUS_TIMEMIX_H */

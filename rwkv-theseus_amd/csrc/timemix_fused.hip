@@ -1,0 +1,529 @@
+// Fused elementwise kernels around the WKV7 recurrence in TimeMix (gfx950).
+//
+// Each replaces a chain of torch ops of theseus/timemix.py:66-89 with one pass
+// over HBM (forward) or one pass plus a small fixed-order reduction of the
+// parameter gradients (backward):
+//   shift-lerp     mixed_n = x + (x[t-1] - x) * coef_n, six outputs   (:70-71)
+//   kk / k-mod     kk = normalize(k*k_k), kw = k*(1+(a-1)k_a), -kk, kk*a  (:78-80)
+//   GN+bonus+gate  ((GroupNorm(y) + (sum r*kmod*r_k) v) * g)        (:83-88)
+// Head rows of 64 channels are handled by 8 lanes x 8 channels (16-byte bf16
+// vectors); row sums are 8-lane butterflies.  Parameter gradients are
+// accumulated per (head, token block) and reduced over token blocks by
+// reduce_blocks in a fixed order, so results are deterministic.
+#include "../../include/theseus_timemix.h"
+#include "../../include/theseus_wkv7.h"
+#include "wkv7_common.h"
+
+namespace tmix {
+using namespace wkv7;
+
+constexpr int HN = 64;   // head size handled here
+constexpr int TB = 64;   // tokens per block for the parameter-gradient partials
+
+struct V8 {
+    float x[8];
+};
+__device__ __forceinline__ V8 ld_bf8(const uint16_t* p) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    V8 r;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.x[2 * i] = bf16_to_f32((uint16_t)(w[i] & 0xffffu));
+        r.x[2 * i + 1] = bf16_to_f32((uint16_t)(w[i] >> 16));
+    }
+    return r;
+}
+__device__ __forceinline__ V8 ld_f8(const float* p) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    return V8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+}
+__device__ __forceinline__ void st_bf8(uint16_t* p, const V8& v) {
+    uint4 u;
+    u.x = f32x2_to_bf16x2(v.x[0], v.x[1]);
+    u.y = f32x2_to_bf16x2(v.x[2], v.x[3]);
+    u.z = f32x2_to_bf16x2(v.x[4], v.x[5]);
+    u.w = f32x2_to_bf16x2(v.x[6], v.x[7]);
+    *reinterpret_cast<uint4*>(p) = u;
+}
+__device__ __forceinline__ void st_f8(float* p, const V8& v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v.x[0], v.x[1], v.x[2], v.x[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v.x[4], v.x[5], v.x[6], v.x[7]);
+}
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+__device__ __forceinline__ float sum8(float x) {  // over the 8 lanes of a head row
+    x += __shfl_xor(x, 1, 8);
+    x += __shfl_xor(x, 2, 8);
+    x += __shfl_xor(x, 4, 8);
+    return x;
+}
+
+// ---------------------------------------------------------------- shift-lerp
+__global__ __launch_bounds__(256) void shift_lerp_fwd(long M, int T, int C, const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ st,
+                                                      const float* __restrict__ coef, uint16_t* o0,
+                                                      uint16_t* o1, uint16_t* o2, uint16_t* o3,
+                                                      uint16_t* o4, uint16_t* o5) {
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+    const int cv = C / 8;
+    if (gid >= M * cv) return;
+    const long m = gid / cv;
+    const int c = (int)(gid % cv) * 8;
+    const int t = (int)(m % T), b = (int)(m / T);
+    const V8 xv = ld_bf8(x + m * C + c);
+    const V8 pv = t > 0 ? ld_bf8(x + (m - 1) * C + c) : ld_bf8(st + (long)b * C + c);
+    uint16_t* outs[6] = {o0, o1, o2, o3, o4, o5};
+    float d[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) d[e] = round_bf16(pv.x[e] - xv.x[e]);  // delta is a bf16 tensor
+#pragma unroll
+    for (int n = 0; n < 6; n++) {
+        const V8 cf = ld_f8(coef + n * C + c);
+        V8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o.x[e] = xv.x[e] + d[e] * cf.x[e];
+        st_bf8(outs[n] + m * C + c, o);
+    }
+}
+
+// grid (ceil(C/512), ceil(M/TB)), 64 lanes, 8 channels per lane
+__global__ __launch_bounds__(64) void shift_lerp_bwd(long M, int T, int C, const uint16_t* d0,
+                                                     const uint16_t* d1, const uint16_t* d2,
+                                                     const uint16_t* d3, const uint16_t* d4,
+                                                     const uint16_t* d5, const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ st,
+                                                     const float* __restrict__ coef, uint16_t* dx,
+                                                     uint16_t* dshift, float* __restrict__ part) {
+    const int c = (blockIdx.x * 64 + threadIdx.x) * 8;
+    if (c >= C) return;
+    const long m0 = (long)blockIdx.y * TB, m1 = min(M, m0 + TB);
+    const uint16_t* dn[6] = {d0, d1, d2, d3, d4, d5};
+    V8 cf[6];
+#pragma unroll
+    for (int n = 0; n < 6; n++) cf[n] = ld_f8(coef + n * C + c);
+    float acc[6][8];
+#pragma unroll
+    for (int n = 0; n < 6; n++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[n][e] = 0.f;
+    V8 cur[6];
+#pragma unroll
+    for (int n = 0; n < 6; n++) cur[n] = ld_bf8(dn[n] + m0 * C + c);
+    for (long m = m0; m < m1; m++) {
+        const int t = (int)(m % T), b = (int)(m / T);
+        V8 nxt[6];
+        const bool has_next = m + 1 < M;
+#pragma unroll
+        for (int n = 0; n < 6; n++) {
+            if (has_next) nxt[n] = ld_bf8(dn[n] + (m + 1) * C + c);
+            else
+#pragma unroll
+                for (int e = 0; e < 8; e++) nxt[n].x[e] = 0.f;
+        }
+        const V8 xv = ld_bf8(x + m * C + c);
+        const V8 pv = t > 0 ? ld_bf8(x + (m - 1) * C + c) : ld_bf8(st + (long)b * C + c);
+        V8 gx, gs;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float delta = round_bf16(pv.x[e] - xv.x[e]);
+            float dsum = 0.f, dc = 0.f, nx = 0.f;
+#pragma unroll
+            for (int n = 0; n < 6; n++) {
+                dsum += cur[n].x[e];
+                dc += cur[n].x[e] * cf[n].x[e];
+                nx += nxt[n].x[e] * cf[n].x[e];
+                acc[n][e] += cur[n].x[e] * delta;
+            }
+            gx.x[e] = dsum - dc + (t + 1 < T ? nx : 0.f);
+            gs.x[e] = dc;
+        }
+        st_bf8(dx + m * C + c, gx);
+        if (t == 0) st_bf8(dshift + (long)b * C + c, gs);
+#pragma unroll
+        for (int n = 0; n < 6; n++) cur[n] = nxt[n];
+    }
+    float* pb = part + (long)blockIdx.y * 6 * C;
+#pragma unroll
+    for (int n = 0; n < 6; n++) st_f8(pb + n * C + c, V8{{acc[n][0], acc[n][1], acc[n][2], acc[n][3], acc[n][4],
+                                                         acc[n][5], acc[n][6], acc[n][7]}});
+}
+
+// part is [nblk][P][C]; outs[p][c] = sum_b part[b][p][c], summed in block order
+struct Outs {
+    float* p[6];
+};
+__global__ __launch_bounds__(256) void reduce_blocks(const float* __restrict__ part, int nblk, int P, int C,
+                                                     Outs outs) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= P * C) return;
+    float s = 0.f;
+    for (int b = 0; b < nblk; b++) s += part[(long)b * P * C + j];
+    outs.p[j / C][j % C] = s;
+}
+
+// ---------------------------------------------------------------- kk / k-mod
+__global__ __launch_bounds__(256) void kk_fwd(long rows, int H, int C, const uint16_t* __restrict__ k,
+                                              const float* __restrict__ a, const float* __restrict__ kkp,
+                                              const float* __restrict__ kap, uint16_t* kw, uint16_t* aw,
+                                              uint16_t* bw) {
+    const long row = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const int sub = threadIdx.x & 7;
+    const bool ok = row < rows;
+    const long m = ok ? row / H : 0;
+    const int h = ok ? (int)(row % H) : 0;
+    const int c = h * HN + 8 * sub;
+    const long o = m * C + c;
+    V8 kv{}, av{};
+    if (ok) {
+        kv = ld_bf8(k + o);
+        av = ld_f8(a + o);
+    }
+    const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c);
+    float u[8], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        u[e] = kv.x[e] * kk_.x[e];
+        ss += u[e] * u[e];
+    }
+    ss = sum8(ss);
+    const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+    V8 ow, oa, ob;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float kkv = u[e] * inv;
+        ow.x[e] = kv.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e]);
+        oa.x[e] = -kkv;
+        ob.x[e] = kkv * av.x[e];
+    }
+    if (ok) {
+        st_bf8(kw + o, ow);
+        st_bf8(aw + o, oa);
+        st_bf8(bw + o, ob);
+    }
+}
+
+// grid (H, ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
+__global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16_t* __restrict__ dkw,
+                                              const uint16_t* __restrict__ daw,
+                                              const uint16_t* __restrict__ dbw, const uint16_t* __restrict__ k,
+                                              const float* __restrict__ a, const float* __restrict__ kkp,
+                                              const float* __restrict__ kap, uint16_t* dk, float* da,
+                                              float* __restrict__ part) {
+    __shared__ float red[2][32][HN + 1];
+    const int h = blockIdx.x, rs = threadIdx.x >> 3, sub = threadIdx.x & 7;
+    const int c = h * HN + 8 * sub;
+    const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c);
+    float acc_kk[8] = {}, acc_ka[8] = {};
+    for (int it = 0; it < TB / 32; it++) {
+        const long m = (long)blockIdx.y * TB + it * 32 + rs;
+        const bool ok = m < M;
+        const long o = m * C + c;
+        V8 kv{}, av{}, gw{}, ga{}, gb{};
+        if (ok) {
+            kv = ld_bf8(k + o);
+            av = ld_f8(a + o);
+            gw = ld_bf8(dkw + o);
+            ga = ld_bf8(daw + o);
+            gb = ld_bf8(dbw + o);
+        }
+        float u[8], ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            u[e] = kv.x[e] * kk_.x[e];
+            ss += u[e] * u[e];
+        }
+        ss = sum8(ss);
+        const float nrm = sqrtf(ss);
+        const bool clamped = nrm <= 1e-12f;
+        const float inv = 1.f / fmaxf(nrm, 1e-12f);
+        float kkv[8], dkk[8], dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kkv[e] = u[e] * inv;
+            dkk[e] = -ga.x[e] + gb.x[e] * av.x[e];
+            dot += kkv[e] * dkk[e];
+        }
+        dot = sum8(dot);
+        V8 gk, gav;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float du = clamped ? dkk[e] * inv : (dkk[e] - kkv[e] * dot) * inv;
+            gk.x[e] = du * kk_.x[e] + gw.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e]);
+            gav.x[e] = gb.x[e] * kkv[e] + gw.x[e] * kv.x[e] * ka.x[e];
+            acc_kk[e] += du * kv.x[e];
+            acc_ka[e] += gw.x[e] * kv.x[e] * (av.x[e] - 1.f);
+        }
+        if (ok) {
+            st_bf8(dk + o, gk);
+            st_f8(da + o, gav);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        red[0][rs][8 * sub + e] = acc_kk[e];
+        red[1][rs][8 * sub + e] = acc_ka[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * HN) {
+        const int p = threadIdx.x / HN, n = threadIdx.x % HN;
+        float s = 0.f;
+        for (int i = 0; i < 32; i++) s += red[p][i][n];
+        part[((long)blockIdx.y * 2 + p) * C + h * HN + n] = s;
+    }
+}
+
+// ---------------------------------------------------------------- GroupNorm + bonus + gate
+__global__ __launch_bounds__(256) void gn_fwd(long rows, int H, int C, const uint16_t* __restrict__ y,
+                                              const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
+                                              const float* __restrict__ a, const float* __restrict__ kap,
+                                              const uint16_t* __restrict__ v, const uint16_t* __restrict__ g,
+                                              const float* __restrict__ rkp, const float* __restrict__ lwp,
+                                              const float* __restrict__ lbp, float eps, uint16_t* out) {
+    const long row = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const int sub = threadIdx.x & 7;
+    const bool ok = row < rows;
+    const long m = ok ? row / H : 0;
+    const int h = ok ? (int)(row % H) : 0;
+    const int c = h * HN + 8 * sub;
+    const long o = m * C + c;
+    V8 yv{}, rv{}, kv{}, av{}, vv{}, gv{};
+    if (ok) {
+        yv = ld_bf8(y + o);
+        rv = ld_bf8(r + o);
+        kv = ld_bf8(k + o);
+        av = ld_f8(a + o);
+        vv = ld_bf8(v + o);
+        gv = ld_bf8(g + o);
+    }
+    const V8 ka = ld_f8(kap + c), rk = ld_f8(rkp + c), lw = ld_f8(lwp + c), lb = ld_f8(lbp + c);
+    float s = 0.f, cd = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        s += yv.x[e];
+        cd += rv.x[e] * (kv.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e])) * rk.x[e];
+    }
+    const float mean = sum8(s) * (1.f / HN);
+    cd = sum8(cd);
+    float var = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) var += (yv.x[e] - mean) * (yv.x[e] - mean);
+    const float rstd = rsqrtf(sum8(var) * (1.f / HN) + eps);
+    V8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        ov.x[e] = ((yv.x[e] - mean) * rstd * lw.x[e] + lb.x[e] + cd * vv.x[e]) * gv.x[e];
+    if (ok) st_bf8(out + o, ov);
+}
+
+// grid (H, ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
+__global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16_t* __restrict__ dout,
+                                              const uint16_t* __restrict__ y, const uint16_t* __restrict__ r,
+                                              const uint16_t* __restrict__ k, const float* __restrict__ a,
+                                              const float* __restrict__ kap, const uint16_t* __restrict__ v,
+                                              const uint16_t* __restrict__ g, const float* __restrict__ rkp,
+                                              const float* __restrict__ lwp, const float* __restrict__ lbp,
+                                              float eps, uint16_t* dy, uint16_t* dr, uint16_t* dk,
+                                              uint16_t* dv, uint16_t* dg, float* da, float* __restrict__ part) {
+    __shared__ float red[4][32][HN + 1];
+    const int h = blockIdx.x, rs = threadIdx.x >> 3, sub = threadIdx.x & 7;
+    const int c = h * HN + 8 * sub;
+    const V8 ka = ld_f8(kap + c), rk = ld_f8(rkp + c), lw = ld_f8(lwp + c), lb = ld_f8(lbp + c);
+    float acc[4][8] = {};  // dr_k, dln_w, dln_b, dk_a
+    for (int it = 0; it < TB / 32; it++) {
+        const long m = (long)blockIdx.y * TB + it * 32 + rs;
+        const bool ok = m < M;
+        const long o = m * C + c;
+        V8 yv{}, rv{}, kv{}, av{}, vv{}, gv{}, go{};
+        if (ok) {
+            yv = ld_bf8(y + o);
+            rv = ld_bf8(r + o);
+            kv = ld_bf8(k + o);
+            av = ld_f8(a + o);
+            vv = ld_bf8(v + o);
+            gv = ld_bf8(g + o);
+            go = ld_bf8(dout + o);
+        }
+        float km[8], s = 0.f, cd = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            km[e] = kv.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e]);
+            s += yv.x[e];
+            cd += rv.x[e] * km[e] * rk.x[e];
+        }
+        const float mean = sum8(s) * (1.f / HN);
+        cd = sum8(cd);
+        float var = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) var += (yv.x[e] - mean) * (yv.x[e] - mean);
+        const float rstd = rsqrtf(sum8(var) * (1.f / HN) + eps);
+        float yh[8], ds[8], dyh[8], m1 = 0.f, m2 = 0.f, dc = 0.f;
+        V8 ogg, ogv;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            yh[e] = (yv.x[e] - mean) * rstd;
+            const float sv = yh[e] * lw.x[e] + lb.x[e] + cd * vv.x[e];
+            ds[e] = go.x[e] * gv.x[e];
+            ogg.x[e] = go.x[e] * sv;
+            ogv.x[e] = ds[e] * cd;
+            dyh[e] = ds[e] * lw.x[e];
+            m1 += dyh[e];
+            m2 += dyh[e] * yh[e];
+            dc += ds[e] * vv.x[e];
+            acc[1][e] += ds[e] * yh[e];
+            acc[2][e] += ds[e];
+        }
+        m1 = sum8(m1) * (1.f / HN);
+        m2 = sum8(m2) * (1.f / HN);
+        dc = sum8(dc);
+        V8 ogy, ogr, ogk, oga;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            ogy.x[e] = rstd * (dyh[e] - m1 - yh[e] * m2);
+            ogr.x[e] = dc * km[e] * rk.x[e];
+            const float dkm = dc * rv.x[e] * rk.x[e];
+            ogk.x[e] = dkm * (1.f + (av.x[e] - 1.f) * ka.x[e]);
+            oga.x[e] = dkm * kv.x[e] * ka.x[e];
+            acc[0][e] += dc * rv.x[e] * km[e];
+            acc[3][e] += dkm * kv.x[e] * (av.x[e] - 1.f);
+        }
+        if (ok) {
+            st_bf8(dy + o, ogy);
+            st_bf8(dr + o, ogr);
+            st_bf8(dk + o, ogk);
+            st_bf8(dv + o, ogv);
+            st_bf8(dg + o, ogg);
+            st_f8(da + o, oga);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) red[p][rs][8 * sub + e] = acc[p][e];
+    __syncthreads();
+    {
+        const int p = threadIdx.x / HN, n = threadIdx.x % HN;  // 256 = 4 x 64
+        float s = 0.f;
+        for (int i = 0; i < 32; i++) s += red[p][i][n];
+        part[((long)blockIdx.y * 4 + p) * C + h * HN + n] = s;
+    }
+}
+
+}  // namespace tmix
+
+// ------------------------------------------------------------------ C ABI
+namespace {
+int tm_check(int B, int T, int C) {
+    if (B < 1 || T < 1 || C < tmix::HN || C % tmix::HN) return THESEUS_WKV7_ERR_SHAPE;
+    return THESEUS_WKV7_OK;
+}
+int tm_status() { return hipGetLastError() == hipSuccess ? THESEUS_WKV7_OK : THESEUS_WKV7_ERR_LAUNCH; }
+long nblk_t(int B, int T) { return ((long)B * T + tmix::TB - 1) / tmix::TB; }
+}  // namespace
+
+extern "C" {
+
+int theseus_tm_shift_lerp_fwd(int B, int T, int C, const void* x, const void* st, const float* coef,
+                              void* const* out, hipStream_t stream) {
+    if (int e = tm_check(B, T, C)) return e;
+    if (!x || !st || !coef || !out) return THESEUS_WKV7_ERR_NULL;
+    for (int n = 0; n < 6; n++)
+        if (!out[n]) return THESEUS_WKV7_ERR_NULL;
+    const long M = (long)B * T, total = M * (C / 8);
+    hipLaunchKernelGGL(tmix::shift_lerp_fwd, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, M, T, C,
+                       (const uint16_t*)x, (const uint16_t*)st, coef, (uint16_t*)out[0], (uint16_t*)out[1],
+                       (uint16_t*)out[2], (uint16_t*)out[3], (uint16_t*)out[4], (uint16_t*)out[5]);
+    return tm_status();
+}
+
+size_t theseus_tm_shift_lerp_workspace(int B, int T, int C) {
+    return tm_check(B, T, C) ? 0 : (size_t)nblk_t(B, T) * 6 * C * sizeof(float);
+}
+
+int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const void* x, const void* st,
+                              const float* coef, void* dx, void* dshift, float* dcoef, float* ws,
+                              size_t ws_bytes, hipStream_t stream) {
+    if (int e = tm_check(B, T, C)) return e;
+    if (!dm || !x || !st || !coef || !dx || !dshift || !dcoef) return THESEUS_WKV7_ERR_NULL;
+    for (int n = 0; n < 6; n++)
+        if (!dm[n]) return THESEUS_WKV7_ERR_NULL;
+    if (!ws || ws_bytes < theseus_tm_shift_lerp_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
+    const long M = (long)B * T;
+    const int nb = (int)nblk_t(B, T);
+    hipLaunchKernelGGL(tmix::shift_lerp_bwd, dim3((C + 511) / 512, nb), dim3(64), 0, stream, M, T, C,
+                       (const uint16_t*)dm[0], (const uint16_t*)dm[1], (const uint16_t*)dm[2],
+                       (const uint16_t*)dm[3], (const uint16_t*)dm[4], (const uint16_t*)dm[5],
+                       (const uint16_t*)x, (const uint16_t*)st, coef, (uint16_t*)dx, (uint16_t*)dshift, ws);
+    tmix::Outs o6{{dcoef, dcoef + C, dcoef + 2 * C, dcoef + 3 * C, dcoef + 4 * C, dcoef + 5 * C}};
+    hipLaunchKernelGGL(tmix::reduce_blocks, dim3((6 * C + 255) / 256), dim3(256), 0, stream, ws, nb, 6, C, o6);
+    return tm_status();
+}
+
+int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const float* a, const float* k_k, const float* k_a,
+                      void* kw, void* aw, void* bw, hipStream_t stream) {
+    if (int e = tm_check(B, T, C)) return e;
+    if (!k || !a || !k_k || !k_a || !kw || !aw || !bw) return THESEUS_WKV7_ERR_NULL;
+    const int H = C / tmix::HN;
+    const long rows = (long)B * T * H;
+    hipLaunchKernelGGL(tmix::kk_fwd, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, stream, rows, H, C,
+                       (const uint16_t*)k, a, k_k, k_a, (uint16_t*)kw, (uint16_t*)aw, (uint16_t*)bw);
+    return tm_status();
+}
+
+size_t theseus_tm_kk_workspace(int B, int T, int C) {
+    return tm_check(B, T, C) ? 0 : (size_t)nblk_t(B, T) * 2 * C * sizeof(float);
+}
+
+int theseus_tm_kk_bwd(int B, int T, int C, const void* dkw, const void* daw, const void* dbw, const void* k,
+                      const float* a, const float* k_k, const float* k_a, void* dk, float* da, float* dk_k,
+                      float* dk_a, float* ws, size_t ws_bytes, hipStream_t stream) {
+    if (int e = tm_check(B, T, C)) return e;
+    if (!dkw || !daw || !dbw || !k || !a || !k_k || !k_a || !dk || !da || !dk_k || !dk_a)
+        return THESEUS_WKV7_ERR_NULL;
+    if (!ws || ws_bytes < theseus_tm_kk_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
+    const int H = C / tmix::HN, nb = (int)nblk_t(B, T);
+    hipLaunchKernelGGL(tmix::kk_bwd, dim3(H, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dkw,
+                       (const uint16_t*)daw, (const uint16_t*)dbw, (const uint16_t*)k, a, k_k, k_a,
+                       (uint16_t*)dk, da, ws);
+    tmix::Outs o2{{dk_k, dk_a, nullptr, nullptr, nullptr, nullptr}};
+    hipLaunchKernelGGL(tmix::reduce_blocks, dim3((2 * C + 255) / 256), dim3(256), 0, stream, ws, nb, 2, C, o2);
+    return tm_status();
+}
+
+int theseus_tm_gn_fwd(int B, int T, int C, const void* y, const void* r, const void* k, const float* a,
+                      const float* k_a, const void* v, const void* g, const float* r_k, const float* ln_w,
+                      const float* ln_b, float eps, void* out, hipStream_t stream) {
+    if (int e = tm_check(B, T, C)) return e;
+    if (!y || !r || !k || !a || !k_a || !v || !g || !r_k || !ln_w || !ln_b || !out) return THESEUS_WKV7_ERR_NULL;
+    const int H = C / tmix::HN;
+    const long rows = (long)B * T * H;
+    hipLaunchKernelGGL(tmix::gn_fwd, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, stream, rows, H, C,
+                       (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, a, k_a, (const uint16_t*)v,
+                       (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)out);
+    return tm_status();
+}
+
+size_t theseus_tm_gn_workspace(int B, int T, int C) {
+    return tm_check(B, T, C) ? 0 : (size_t)nblk_t(B, T) * 4 * C * sizeof(float);
+}
+
+int theseus_tm_gn_bwd(int B, int T, int C, const void* dout, const void* y, const void* r, const void* k,
+                      const float* a, const float* k_a, const void* v, const void* g, const float* r_k,
+                      const float* ln_w, const float* ln_b, float eps, void* dy, void* dr, void* dk, void* dv,
+                      void* dg, float* da, float* dr_k, float* dln_w, float* dln_b, float* dk_a, float* ws,
+                      size_t ws_bytes, hipStream_t stream) {
+    if (int e = tm_check(B, T, C)) return e;
+    if (!dout || !y || !r || !k || !a || !k_a || !v || !g || !r_k || !ln_w || !ln_b || !dy || !dr || !dk ||
+        !dv || !dg || !da || !dr_k || !dln_w || !dln_b || !dk_a)
+        return THESEUS_WKV7_ERR_NULL;
+    if (!ws || ws_bytes < theseus_tm_gn_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
+    const int H = C / tmix::HN, nb = (int)nblk_t(B, T);
+    hipLaunchKernelGGL(tmix::gn_bwd, dim3(H, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dout,
+                       (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, a, k_a, (const uint16_t*)v,
+                       (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)dy, (uint16_t*)dr, (uint16_t*)dk,
+                       (uint16_t*)dv, (uint16_t*)dg, da, ws);
+    tmix::Outs o4{{dr_k, dln_w, dln_b, dk_a, nullptr, nullptr}};
+    hipLaunchKernelGGL(tmix::reduce_blocks, dim3((4 * C + 255) / 256), dim3(256), 0, stream, ws, nb, 4, C, o4);
+    return tm_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,206 @@
+"""Autograd wrappers over the fused TimeMix kernels of libtheseus_wkv7.so
+(C ABI: include/theseus_timemix.h).
+
+Each Function replaces one torch op chain of TimeMix.forward
+(theseus/timemix.py:70-71, 78-80, 83-88) and returns the same values and
+gradients (to bf16 rounding) with bf16 activations:
+
+* ``shift_lerp(x, shift, coefs)`` -> 6 mixes (r, w, k, v, a, g order);
+* ``kk_kmod(k, a, k_k, k_a, N, dtype)`` -> (kw, aw, bw, k) where kw, aw, bw are
+  the WKV operands k*(1+(a-1)k_a), -kk, kk*a as [B,T,H,N] tensors of ``dtype``
+  and k is passed through unchanged (the bonus term recomputes the modulation
+  from it);
+* ``gn_bonus_gate(y, r, k, v, g, r_k, ln_w, ln_b, eps, out_dtype)`` -> fp32
+  GroupNorm over heads + (sum r*kmod*r_k) v, times g, as ``out_dtype``.
+
+Parameters are handed to the kernels as float32 and their gradients come back
+in the parameter's dtype.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .wkv7 import extension
+
+_ready = None
+
+
+def _lib():
+    global _ready
+    lib = extension().lib
+    if _ready is None:
+        vp, i32, sz, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+        try:
+            lib.theseus_tm_shift_lerp_fwd.argtypes = [i32] * 3 + [vp] * 4 + [vp]
+            lib.theseus_tm_shift_lerp_workspace.argtypes = [i32] * 3
+            lib.theseus_tm_shift_lerp_workspace.restype = sz
+            lib.theseus_tm_shift_lerp_bwd.argtypes = [i32] * 3 + [vp] * 8 + [sz, vp]
+            lib.theseus_tm_kk_fwd.argtypes = [i32] * 3 + [vp] * 7 + [vp]
+            lib.theseus_tm_kk_workspace.argtypes = [i32] * 3
+            lib.theseus_tm_kk_workspace.restype = sz
+            lib.theseus_tm_kk_bwd.argtypes = [i32] * 3 + [vp] * 12 + [sz, vp]
+            lib.theseus_tm_gn_fwd.argtypes = [i32] * 3 + [vp] * 10 + [f32, vp, vp]
+            lib.theseus_tm_gn_workspace.argtypes = [i32] * 3
+            lib.theseus_tm_gn_workspace.restype = sz
+            lib.theseus_tm_gn_bwd.argtypes = [i32] * 3 + [vp] * 11 + [f32] + [vp] * 11 + [sz, vp]
+            for n in ("shift_lerp_fwd", "shift_lerp_bwd", "kk_fwd", "kk_bwd", "gn_fwd", "gn_bwd"):
+                getattr(lib, "theseus_tm_" + n).restype = i32
+            _ready = True
+        except AttributeError:
+            _ready = False
+    return lib if _ready else None
+
+
+def available(x, head_size):
+    """True when the fused kernels cover this call: bf16 CUDA activations, N = 64."""
+    return x.dtype == torch.bfloat16 and head_size == 64 and x.shape[-1] % 64 == 0 and _lib() is not None
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _s(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _check(status):
+    if status:
+        raise RuntimeError("theseus_timemix: " + extension().lib.theseus_wkv7_error_string(status).decode())
+
+
+def _vec(p, C):
+    return p.detach().reshape(C).float().contiguous()
+
+
+class _ShiftLerp(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, shift, *coefs):
+        B, T, C = x.shape
+        x = x.contiguous()
+        shift = shift.to(x.dtype).contiguous()
+        cf = torch.stack([_vec(c, C) for c in coefs]).contiguous()
+        outs = [torch.empty_like(x) for _ in range(6)]
+        arr = (ctypes.c_void_p * 6)(*[o.data_ptr() for o in outs])
+        with torch.cuda.device(x.device):
+            _check(_lib().theseus_tm_shift_lerp_fwd(B, T, C, _p(x), _p(shift), _p(cf), arr, _s(x.device)))
+        ctx.save_for_backward(x, shift, cf)
+        ctx.coef_meta = [(c.shape, c.dtype) for c in coefs]
+        ctx.shift_dtype = shift.dtype
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *douts):
+        x, shift, cf = ctx.saved_tensors
+        B, T, C = x.shape
+        ds = [(d if d is not None else torch.zeros_like(x)).to(x.dtype).contiguous() for d in douts]
+        dx = torch.empty_like(x)
+        dshift = torch.empty_like(shift)
+        dcoef = torch.empty(6, C, dtype=torch.float32, device=x.device)
+        lib = _lib()
+        ws_bytes = int(lib.theseus_tm_shift_lerp_workspace(B, T, C))
+        ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device=x.device)
+        arr = (ctypes.c_void_p * 6)(*[d.data_ptr() for d in ds])
+        with torch.cuda.device(x.device):
+            _check(lib.theseus_tm_shift_lerp_bwd(B, T, C, arr, _p(x), _p(shift), _p(cf), _p(dx), _p(dshift),
+                                                 _p(dcoef), _p(ws), ctypes.c_size_t(ws_bytes), _s(x.device)))
+        dcs = [dcoef[n].reshape(shape).to(dt) for n, (shape, dt) in enumerate(ctx.coef_meta)]
+        return (dx, dshift, *dcs)
+
+
+def shift_lerp(x, shift, coefs):
+    return _ShiftLerp.apply(x, shift, *coefs)
+
+
+class _KkKmod(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, k, a, k_k, k_a, N, dtype):
+        B, T, C = k.shape
+        k = k.to(torch.bfloat16).contiguous()
+        af = a.float().contiguous()
+        kk_, ka = _vec(k_k, C), _vec(k_a, C)
+        kw, aw, bw = (torch.empty((B, T, C // N, N), dtype=torch.bfloat16, device=k.device) for _ in range(3))
+        with torch.cuda.device(k.device):
+            _check(_lib().theseus_tm_kk_fwd(B, T, C, _p(k), _p(af), _p(kk_), _p(ka), _p(kw), _p(aw), _p(bw),
+                                            _s(k.device)))
+        ctx.save_for_backward(k, af, kk_, ka)
+        ctx.meta = (a.dtype, k_k.shape, k_k.dtype, k_a.shape, k_a.dtype)
+        if dtype != torch.bfloat16:
+            kw, aw, bw = kw.to(dtype), aw.to(dtype), bw.to(dtype)
+        return kw, aw, bw
+
+    @staticmethod
+    def backward(ctx, dkw, daw, dbw):
+        k, af, kk_, ka = ctx.saved_tensors
+        B, T, C = k.shape
+        z = torch.zeros(B, T, C, dtype=torch.bfloat16, device=k.device)
+        g = [(d.to(torch.bfloat16).reshape(B, T, C).contiguous() if d is not None else z) for d in (dkw, daw, dbw)]
+        dk = torch.empty_like(k)
+        da = torch.empty_like(af)
+        dkk, dka = (torch.empty(C, dtype=torch.float32, device=k.device) for _ in range(2))
+        lib = _lib()
+        ws_bytes = int(lib.theseus_tm_kk_workspace(B, T, C))
+        ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device=k.device)
+        with torch.cuda.device(k.device):
+            _check(lib.theseus_tm_kk_bwd(B, T, C, *map(_p, g), _p(k), _p(af), _p(kk_), _p(ka), _p(dk), _p(da),
+                                         _p(dkk), _p(dka), _p(ws), ctypes.c_size_t(ws_bytes), _s(k.device)))
+        a_dt, kk_shape, kk_dt, ka_shape, ka_dt = ctx.meta
+        return dk, da.to(a_dt), dkk.reshape(kk_shape).to(kk_dt), dka.reshape(ka_shape).to(ka_dt), None, None
+
+
+def kk_kmod(k, a, k_k, k_a, N, dtype):
+    """WKV operands (kw, aw, bw) as [B,T,H,N] plus k itself for the bonus term."""
+    kw, aw, bw = _KkKmod.apply(k, a, k_k, k_a, N, dtype)
+    return kw, aw, bw, _KMod(k, a, k_a)
+
+
+class _KMod:
+    """Carries (k, a, k_a) to gn_bonus_gate, which recomputes k*(1+(a-1)k_a) itself."""
+
+    def __init__(self, k, a, k_a):
+        self.k, self.a, self.k_a = k, a, k_a
+
+
+class _GnBonusGate(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, y, r, k, a, k_a, v, g, r_k, ln_w, ln_b, eps, out_dtype):
+        B, T, C = r.shape
+        bf = torch.bfloat16
+        ys = y.reshape(B, T, C).to(bf).contiguous()
+        rs, ks, vs, gs = (t.to(bf).contiguous() for t in (r, k, v, g))
+        af = a.float().contiguous()
+        ka, rk, lw, lb = _vec(k_a, C), _vec(r_k, C), _vec(ln_w, C), _vec(ln_b, C)
+        out = torch.empty(B, T, C, dtype=bf, device=r.device)
+        with torch.cuda.device(r.device):
+            _check(_lib().theseus_tm_gn_fwd(B, T, C, _p(ys), _p(rs), _p(ks), _p(af), _p(ka), _p(vs), _p(gs),
+                                            _p(rk), _p(lw), _p(lb), ctypes.c_float(eps), _p(out), _s(r.device)))
+        ctx.save_for_backward(ys, rs, ks, af, ka, vs, gs, rk, lw, lb)
+        ctx.eps = eps
+        ctx.meta = [(t.shape, t.dtype) for t in (y, r, k, a, k_a, v, g, r_k, ln_w, ln_b)]
+        return out if out_dtype == bf else out.to(out_dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        ys, rs, ks, af, ka, vs, gs, rk, lw, lb = ctx.saved_tensors
+        B, T, C = rs.shape
+        do = dout.to(torch.bfloat16).contiguous()
+        dy, dr, dk, dv, dg = (torch.empty_like(rs) for _ in range(5))
+        da = torch.empty_like(af)
+        drk, dlw, dlb, dka = (torch.empty(C, dtype=torch.float32, device=rs.device) for _ in range(4))
+        lib = _lib()
+        ws_bytes = int(lib.theseus_tm_gn_workspace(B, T, C))
+        ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device=rs.device)
+        with torch.cuda.device(rs.device):
+            _check(lib.theseus_tm_gn_bwd(B, T, C, _p(do), _p(ys), _p(rs), _p(ks), _p(af), _p(ka), _p(vs), _p(gs),
+                                         _p(rk), _p(lw), _p(lb), ctypes.c_float(ctx.eps), _p(dy), _p(dr), _p(dk),
+                                         _p(dv), _p(dg), _p(da), _p(drk), _p(dlw), _p(dlb), _p(dka), _p(ws),
+                                         ctypes.c_size_t(ws_bytes), _s(rs.device)))
+        grads = [dy, dr, dk, da, dka, dv, dg, drk, dlw, dlb]
+        outs = [gr.reshape(shape).to(dt) for gr, (shape, dt) in zip(grads, ctx.meta)]
+        return (*outs, None, None)
+
+
+def gn_bonus_gate(y, r, kmod, v, g, r_k, ln_w, ln_b, eps, out_dtype):
+    return _GnBonusGate.apply(y, r, kmod.k, kmod.a, kmod.k_a, v, g, r_k, ln_w, ln_b, eps, out_dtype)

@@ -1,0 +1,134 @@
+"""RWKV7 TimeMix layer on MI355X (drop-in for theseus/timemix.py).
+
+Same constructor, parameter schema (23 tensors, names and shapes), initialisation
+and forward contract as the reference module (theseus/timemix.py:18-93), so state
+dicts, exports and seeds carry over unchanged: the schema is what
+replace_timemix_lightning.py:66-72 and the checkpoints pin, and the
+initialisation calls are issued in the reference's order so a seeded
+construction consumes the RNG identically.
+
+With ``backend="cuda"`` and CUDA tensors, the elementwise work around the
+recurrence runs as three fused HIP kernel pairs (theseus.fused): the token-shift
+lerp that produces the six mixes (timemix.py:70-71), the kk normalisation / k
+modulation that produces the WKV operands (:78-80), and the fp32 GroupNorm +
+r*k*r_k bonus + gate (:83-88).  Projections and LoRAs stay torch GEMMs
+(hipBLASLt).  ``backend="reference"`` runs the reference's torch op sequence
+for all of it.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from .wkv7 import wkv7
+
+
+class TimeMix(nn.Module):
+    def __init__(self, width, layer_idx, depth, head_size=64, backend="cuda"):
+        super().__init__()
+        if width % head_size or head_size < 2:
+            raise ValueError("width must be divisible by head_size >= 2")
+        self.width, self.head_size = width, head_size
+        self.heads, self.backend = width // head_size, backend
+        C, N = width, head_size
+        ratio = layer_idx / max(depth - 1, 1)       # 0 at the first layer, 1 at the last
+        reverse = 1 - layer_idx / depth
+        pos = torch.arange(C).reshape(1, 1, C) / C  # channel position in [0, 1)
+        # token-shift mix coefficients x_r, x_w, x_k, x_v, x_a, x_g
+        for name, power in (("r", .2), ("w", .9), ("k", .7), ("v", .7), ("a", .9), ("g", .2)):
+            setattr(self, "x_" + name, nn.Parameter(1 - pos.pow(power * reverse)))
+        ramp = torch.arange(C) / (C - 1) - .5
+        zz = (torch.arange(C) % N - (N - 1) / 2) / ((N - 1) / 2)
+        zz = zz * zz.abs()
+        decay_base = -6 + 6 * (torch.arange(C) / (C - 1)).pow(1 + ratio ** .3)
+        rank = max(32, round(2.5 * math.sqrt(C) / 32) * 32)
+        gate_rank = max(32, round(5 * math.sqrt(C) / 32) * 32)
+        for name in ("w", "a"):
+            setattr(self, name + "1", nn.Parameter(torch.zeros(C, rank)))
+            lora_out = nn.Parameter(torch.empty(rank, C))
+            nn.init.orthogonal_(lora_out, gain=.1 * max(1, math.sqrt(rank / C)))
+            setattr(self, name + "2", lora_out)
+        self.w0 = nn.Parameter((decay_base + .5 + zz * 2.5).reshape(1, 1, C))
+        self.a0 = nn.Parameter((-.19 + zz * .3 + ramp * .4).reshape(1, 1, C))
+        self.g1 = nn.Parameter(torch.empty(C, gate_rank))
+        self.g2 = nn.Parameter(torch.empty(gate_rank, C))
+        nn.init.zeros_(self.g1)  # sigmoid(0) = 0.5, so the gate starts non-zero
+        nn.init.orthogonal_(self.g2, gain=.1 * max(1, math.sqrt(gate_rank / C)))
+        self.k_k = nn.Parameter((.71 - ramp * .1).reshape(1, 1, C))
+        self.k_a = nn.Parameter(torch.full((1, 1, C), 1.02))
+        self.r_k = nn.Parameter(torch.full((self.heads, N), -.04))
+        for name, gain in (("receptance", 1.), ("key", .1), ("value", 1.), ("output", 0.)):
+            lin = nn.Linear(C, C, bias=False)
+            if gain:
+                nn.init.orthogonal_(lin.weight, gain=gain)
+            else:
+                nn.init.zeros_(lin.weight)
+            setattr(self, name, lin)
+        self.ln_x = nn.GroupNorm(self.heads, C, eps=64e-5)
+        nn.init.constant_(self.ln_x.weight, ((1 + layer_idx) / depth) ** .7)
+
+    def initial_state(self, x):
+        """Zero carried state: {"shift": [B,C] in x's dtype, "wkv": [B,H,N,N] fp32}."""
+        return {"shift": torch.zeros(x.shape[0], self.width, device=x.device, dtype=x.dtype),
+                "wkv": torch.zeros(x.shape[0], self.heads, self.head_size, self.head_size,
+                                   device=x.device, dtype=torch.float32)}
+
+    def _fused(self, x):
+        if self.backend != "cuda" or not x.is_cuda:
+            return False
+        from . import fused
+        return fused.available(x, self.head_size)
+
+    def forward(self, x, state=None):
+        """x [B,T,C] -> (out [B,T,C] in x.dtype, {"shift": x[:, -1], "wkv": end state})."""
+        if state is None:
+            state = self.initial_state(x)
+        B, T, _ = x.shape
+        shape = (B, T, self.heads, self.head_size)
+        fused_ok = self._fused(x)
+        if fused_ok:
+            from . import fused
+            mixed = dict(zip("rwkvag", fused.shift_lerp(
+                x, state["shift"], [getattr(self, "x_" + n) for n in "rwkvag"])))
+        else:
+            delta = torch.cat([state["shift"].unsqueeze(1), x[:, :-1]], 1) - x
+            mixed = {n: (x + delta * getattr(self, "x_" + n)).to(x.dtype) for n in "rwkvag"}
+        r = self.receptance(mixed["r"])
+        w = self.w0 + torch.tanh(mixed["w"] @ self.w1) @ self.w2
+        k, v = self.key(mixed["k"]), self.value(mixed["v"])
+        a = torch.sigmoid(self.a0 + (mixed["a"] @ self.a1) @ self.a2)
+        g = torch.sigmoid(mixed["g"] @ self.g1) @ self.g2
+        if fused_ok:
+            from . import fused
+            kw, aw, bw, kmod = fused.kk_kmod(k, a, self.k_k, self.k_a, self.head_size, r.dtype)
+            args = [r.reshape(shape).to(r.dtype).contiguous(), w.reshape(shape).to(r.dtype).contiguous(),
+                    kw, v.reshape(shape).to(r.dtype).contiguous(), aw, bw]
+        else:
+            kk = F.normalize((k.float() * self.k_k).reshape(shape), dim=-1, eps=1e-12)
+            k = k * (1 + (a - 1) * self.k_a)
+            args = [z.reshape(shape).to(r.dtype).contiguous()
+                    for z in (r, w, k, v, -kk, kk * a.reshape(shape))]
+            kmod = k
+        y, end = wkv7(*args, state["wkv"], backend=self.backend)
+        if fused_ok:
+            from . import fused
+            out = fused.gn_bonus_gate(y, r, kmod, v, g, self.r_k, self.ln_x.weight, self.ln_x.bias,
+                                      self.ln_x.eps, x.dtype)
+        else:
+            # norms in fp32 with autocast off, cast back for the output projection
+            with torch.autocast(x.device.type, enabled=False):
+                yn = F.group_norm(y.float().reshape(B * T, self.width), self.heads,
+                                  self.ln_x.weight.float(), self.ln_x.bias.float(),
+                                  self.ln_x.eps).reshape(B, T, self.width)
+                bonus = ((r.float().reshape(shape) * kmod.float().reshape(shape) * self.r_k)
+                         .sum(-1, keepdim=True) * v.float().reshape(shape)).reshape(B, T, self.width)
+                out = ((yn + bonus) * g.float()).to(x.dtype)
+        return self.output(out).to(x.dtype), {"shift": x[:, -1], "wkv": end}
+
+
+def detach_state(state):
+    """Cut the graph at a chunk boundary (theseus/timemix.py:92-93)."""
+    return None if state is None else {k: v.detach() for k, v in state.items()}

@@ -21,12 +21,18 @@ def small_threads():
     torch.manual_seed(123)
 
 
+def _np(x):
+    if isinstance(x, torch.Tensor):
+        return x.detach().double().cpu().numpy()
+    return np.asarray(x, dtype=np.float64)
+
+
 def rel_l2(x, ref):
-    x = np.asarray(x, dtype=np.float64)
-    ref = np.asarray(ref, dtype=np.float64)
+    x, ref = _np(x), _np(ref)
     den = np.linalg.norm(ref)
     return float(np.linalg.norm(x - ref) / (den if den > 0 else 1.0))
 
 
 def max_abs(x, ref):
-    return float(np.max(np.abs(np.asarray(x, np.float64) - np.asarray(ref, np.float64)))) if np.size(ref) else 0.0
+    x, ref = _np(x), _np(ref)
+    return float(np.max(np.abs(x - ref))) if np.size(ref) else 0.0

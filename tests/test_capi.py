@@ -36,11 +36,11 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert not missing, missing
 
 
-def declared_arity():
-    """{function: number of parameters} parsed from the header."""
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+def declared_arity(header=HEADER):
+    """{function: number of parameters} parsed from a header."""
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     out = {}
-    for name, params in re.findall(r"\b(theseus_wkv7_\w+)\s*\(([^)]*)\)\s*;", text):
+    for name, params in re.findall(r"\b(theseus_\w+)\s*\(([^)]*)\)\s*;", text):
         params = params.strip()
         out[name] = 0 if params in ("", "void") else params.count(",") + 1
     return out
@@ -54,6 +54,17 @@ def test_ctypes_bindings_match_header_arity():
         fn = getattr(ext.lib, name)
         bound = len(fn.argtypes) if fn.argtypes is not None else 0
         assert bound == n, (name, bound, n)
+
+
+def test_timemix_abi_exported_and_bound_with_header_arity():
+    from theseus import fused
+    lib = fused._lib()
+    assert lib is not None
+    arity = declared_arity(ROOT / "include" / "theseus_timemix.h")
+    assert len(arity) == 9
+    for name, n in arity.items():
+        fn = getattr(lib, name)
+        assert fn.argtypes is not None and len(fn.argtypes) == n, (name, n)
 
 
 def test_host_queries():

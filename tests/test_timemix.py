@@ -1,0 +1,229 @@
+"""TimeMix drop-in: the reference's own TimeMix tests (tests/test_timemix.py of the
+reference: CPU streaming/learning/TBPTT on backend="reference", the GPU stream and
+fp32-optimizer tests) plus parity of the fused HIP elementwise kernels against the
+reference's torch op sequence, op by op and for the whole layer."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import rel_l2
+from theseus.timemix import TimeMix, detach_state
+
+
+# ---------------------------------------------------------------- CPU (reference backend)
+def test_streaming_output_and_state():
+    model = TimeMix(32, 3, 8, head_size=8, backend="reference")
+    torch.nn.init.normal_(model.output.weight, std=.03)
+    x = torch.randn(2, 9, 32)
+    full, end = model(x)
+    a, state = model(x[:, :4])
+    b, state = model(x[:, 4:], state)
+    torch.testing.assert_close(torch.cat([a, b], 1), full)
+    for key in state:
+        torch.testing.assert_close(state[key], end[key])
+
+
+def test_initialization_can_learn():
+    model = TimeMix(32, 3, 8, head_size=8, backend="reference")
+    opt = torch.optim.AdamW(model.parameters(), lr=.01)
+    x, target = torch.randn(1, 5, 32), torch.randn(1, 5, 32)
+    for step in range(3):
+        opt.zero_grad()
+        y, _ = model(x)
+        (y - target).square().mean().backward()
+        assert model.output.weight.grad.abs().sum() > 0
+        if step:
+            assert model.receptance.weight.grad.abs().sum() > 0
+            assert model.g1.grad.abs().sum() > 0
+        opt.step()
+
+
+def test_tbptt_detaches_only_at_chunk_boundary():
+    model = TimeMix(16, 1, 4, head_size=4, backend="reference")
+    torch.nn.init.normal_(model.output.weight, std=.05)
+    x1 = torch.randn(1, 3, 16, requires_grad=True)
+    x2 = torch.randn(1, 4, 16, requires_grad=True)
+    _, state = model(x1)
+    y, _ = model(x2, detach_state(state))
+    y.sum().backward()
+    assert x1.grad is None
+    assert x2.grad is not None and x2.grad.abs().sum() > 0
+
+
+def test_parameter_schema_and_init():
+    """23 tensors with the reference's names and shapes (replace_timemix_lightning.py:66-72
+    pins them), LoRA ranks max(32, round(k*sqrt(C)/32)*32), and the closed-form inits."""
+    C, N, layer, depth = 5120, 64, 3, 8
+    with torch.device("meta"):
+        m = TimeMix(C, layer, depth, head_size=N, backend="reference")
+    shapes = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    rank, grank = 192, 352
+    expect = {**{f"x_{n}": (1, 1, C) for n in "rwkvag"}, "w1": (C, rank), "w2": (rank, C), "a1": (C, rank),
+              "a2": (rank, C), "w0": (1, 1, C), "a0": (1, 1, C), "g1": (C, grank), "g2": (grank, C),
+              "k_k": (1, 1, C), "k_a": (1, 1, C), "r_k": (C // N, N), "receptance.weight": (C, C),
+              "key.weight": (C, C), "value.weight": (C, C), "output.weight": (C, C), "ln_x.weight": (C,),
+              "ln_x.bias": (C,)}
+    assert shapes == expect
+    small = TimeMix(128, 2, 4, head_size=64, backend="reference")
+    c = torch.arange(128)
+    reverse = 1 - 2 / 4
+    torch.testing.assert_close(small.x_w.detach().reshape(-1), 1 - (c / 128).pow(.9 * reverse))
+    assert torch.all(small.k_a == 1.02) and torch.all(small.r_k == -.04)
+    assert torch.all(small.w1 == 0) and torch.all(small.g1 == 0) and torch.all(small.output.weight == 0)
+    torch.testing.assert_close(small.ln_x.weight.detach(), torch.full((128,), (3 / 4) ** .7))
+    w2 = small.w2.detach()
+    gain = .1 * max(1, math.sqrt(32 / 128))
+    torch.testing.assert_close(w2 @ w2.T, gain ** 2 * torch.eye(32), atol=1e-5, rtol=0)
+
+
+# ---------------------------------------------------------------- GPU: fused ops vs torch
+gpu = pytest.mark.gpu
+
+
+def _torch_mix(x, shift, coefs):
+    delta = torch.cat([shift.unsqueeze(1), x[:, :-1]], 1) - x
+    return [(x + delta * c).to(x.dtype) for c in coefs]
+
+
+@gpu
+def test_fused_shift_lerp_matches_torch():
+    from theseus import fused
+    torch.manual_seed(1)
+    B, T, C = 3, 37, 256
+    x = torch.randn(B, T, C, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    sh = torch.randn(B, C, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    coefs = [torch.rand(1, 1, C, device="cuda", requires_grad=True) for _ in range(6)]
+    outs = fused.shift_lerp(x, sh, coefs)
+    x2, sh2 = x.detach().clone().requires_grad_(), sh.detach().clone().requires_grad_()
+    c2 = [c.detach().clone().requires_grad_() for c in coefs]
+    refs = _torch_mix(x2, sh2, c2)
+    for o, r in zip(outs, refs):
+        torch.testing.assert_close(o.float(), r.float(), atol=1e-2, rtol=1e-2)
+    gs = [torch.randn_like(o) for o in outs]
+    torch.autograd.backward(outs, gs)
+    torch.autograd.backward(refs, gs)
+    # fp32 ground truth of the same math: the reference's bf16 chain rounds the
+    # delta gradient several times, the fused kernel once, so compare both to it
+    x3, sh3 = x.detach().float().requires_grad_(), sh.detach().float().requires_grad_()
+    c3 = [c.detach().clone().requires_grad_() for c in coefs]
+    d3 = torch.cat([sh3.unsqueeze(1), x3[:, :-1]], 1) - x3
+    torch.autograd.backward([x3 + d3 * c for c in c3], [g.float() for g in gs])
+    for got, ref_bf, truth in ((x.grad, x2.grad, x3.grad), (sh.grad, sh2.grad, sh3.grad),
+                               *zip([c.grad for c in coefs], [c.grad for c in c2], [c.grad for c in c3])):
+        e_fused = rel_l2(got.float().cpu(), truth.cpu())
+        e_ref = rel_l2(ref_bf.float().cpu(), truth.cpu())
+        print(f"    rel_l2 vs fp32: fused {e_fused:.2e}  reference-bf16 {e_ref:.2e}", flush=True)
+        assert e_fused < 5e-3 and e_fused <= 1.5 * e_ref + 1e-4
+
+
+@gpu
+def test_fused_kk_and_gn_match_torch():
+    from theseus import fused
+    torch.manual_seed(2)
+    B, T, H, N = 2, 29, 4, 64
+    C = H * N
+    bf = torch.bfloat16
+    mk = lambda *s, dt=bf: torch.randn(*s, device="cuda", dtype=dt)  # noqa: E731
+    k = mk(B, T, C).requires_grad_()
+    a = torch.sigmoid(mk(B, T, C, dt=torch.float32)).requires_grad_()
+    k_k = (.71 + .1 * torch.rand(1, 1, C, device="cuda")).requires_grad_()
+    k_a = torch.full((1, 1, C), 1.02, device="cuda").requires_grad_()
+    r, v, g = (mk(B, T, C).requires_grad_() for _ in range(3))
+    y = mk(B, T, H, N).requires_grad_()
+    r_k = torch.full((H, N), -.04, device="cuda").requires_grad_()
+    ln_w = (1 + .1 * torch.randn(C, device="cuda")).requires_grad_()
+    ln_b = (.1 * torch.randn(C, device="cuda")).requires_grad_()
+    leaves = [k, a, k_k, k_a, r, v, g, y, r_k, ln_w, ln_b]
+    refl = [t.detach().clone().requires_grad_() for t in leaves]
+
+    kw, aw, bw, km = fused.kk_kmod(k, a, k_k, k_a, N, bf)
+    out = fused.gn_bonus_gate(y, r, km, v, g, r_k, ln_w, ln_b, 64e-5, bf)
+
+    kR, aR, kkR, kaR, rR, vR, gR, yR, rkR, lwR, lbR = refl
+    shape = (B, T, H, N)
+    kk = F.normalize((kR.float() * kkR).reshape(shape), dim=-1, eps=1e-12)
+    kmod = kR * (1 + (aR - 1) * kaR)
+    refs = [z.reshape(shape).to(bf) for z in (kmod, -kk, kk * aR.reshape(shape))]
+    yn = F.group_norm(yR.float().reshape(B * T, C), H, lwR, lbR, 64e-5).reshape(B, T, C)
+    bonus = ((rR.float().reshape(shape) * kmod.float().reshape(shape) * rkR).sum(-1, keepdim=True)
+             * vR.float().reshape(shape)).reshape(B, T, C)
+    outR = ((yn + bonus) * gR.float()).to(bf)
+    for o, rr in zip((kw, aw, bw, out), (*refs, outR)):
+        assert rel_l2(o.float().cpu(), rr.float().cpu()) < 5e-3
+    gs = [torch.randn_like(t) for t in (kw, aw, bw, out)]
+    torch.autograd.backward((kw, aw, bw, out), gs)
+    torch.autograd.backward((*refs, outR), gs)
+    names = ["k", "a", "k_k", "k_a", "r", "v", "g", "y", "r_k", "ln_w", "ln_b"]
+    for n, t, tr in zip(names, leaves, refl):
+        e = rel_l2(t.grad.float().cpu(), tr.grad.float().cpu())
+        print(f"    grad {n}: rel_l2 {e:.2e}", flush=True)
+        assert e < 5e-3, (n, e)
+
+
+@gpu
+def test_fused_timemix_layer_matches_reference_backend():
+    """The whole layer: backend="cuda" (HIP WKV + fused elementwise) vs the reference torch
+    sequence on the same weights, bf16 autocast over fp32 parameters."""
+    torch.manual_seed(3)
+    C, N = 256, 64
+    m = TimeMix(C, 2, 6, head_size=N, backend="cuda").cuda()
+    for p in (m.w1, m.a1, m.g1, m.output.weight):
+        torch.nn.init.normal_(p, std=.05)
+    ref = TimeMix(C, 2, 6, head_size=N, backend="reference").cuda()
+    ref.load_state_dict(m.state_dict())
+    x = torch.randn(2, 45, C, device="cuda", dtype=torch.bfloat16)
+    st = {"shift": torch.randn(2, C, device="cuda", dtype=torch.bfloat16),
+          "wkv": .1 * torch.randn(2, C // N, N, N, device="cuda")}
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y, s = m(x, st)
+        yr, sr = ref(x, st)
+    assert rel_l2(y.float().cpu(), yr.float().cpu()) < 1e-2
+    assert rel_l2(s["wkv"].cpu(), sr["wkv"].cpu()) < 5e-3
+    gy = torch.randn_like(y)
+    (y.float() * gy.float()).sum().backward()
+    (yr.float() * gy.float()).sum().backward()
+    for (n, p), (_, pr) in zip(m.named_parameters(), ref.named_parameters()):
+        e = rel_l2(p.grad.float().cpu(), pr.grad.float().cpu())
+        print(f"    {n}: rel_l2 {e:.2e}", flush=True)
+        assert e < 2e-2, (n, e)
+
+
+# ---------------------------------------------------------------- GPU: the reference's own tests
+@gpu
+def test_cuda_inference_chunking_and_current_stream():
+    model = TimeMix(128, 3, 8, head_size=64, backend="cuda").cuda().to(torch.bfloat16)
+    torch.nn.init.normal_(model.output.weight, std=.01)
+    x = torch.randn(2, 17, 128, device="cuda", dtype=torch.bfloat16)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream), torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        full, final = model(x)
+        a, state = model(x[:, :5])
+        b, state = model(x[:, 5:], state)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.testing.assert_close(torch.cat([a, b], 1), full, atol=.006, rtol=.025)
+    torch.testing.assert_close(state["wkv"], final["wkv"], atol=.0005, rtol=.02)
+
+
+@gpu
+def test_cuda_fp32_optimizer_states_and_learning():
+    model = TimeMix(128, 3, 8, head_size=64, backend="cuda").cuda()
+    optimizer = torch.optim.AdamW(model.parameters(), lr=.003)
+    x = torch.randn(1, 7, 128, device="cuda", dtype=torch.bfloat16)
+    target = torch.randn_like(x)
+    losses = []
+    for _ in range(4):
+        optimizer.zero_grad()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y, _ = model(x)
+        loss = (y.float() - target.float()).square().mean()
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1., error_if_nonfinite=True)
+        optimizer.step()
+        losses.append(loss.item())
+    assert losses[-1] < losses[0]
+    for param, state in optimizer.state.items():
+        assert param.dtype == param.grad.dtype == torch.float32
+        assert state["exp_avg"].dtype == state["exp_avg_sq"].dtype == torch.float32
