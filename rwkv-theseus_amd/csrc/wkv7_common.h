@@ -39,7 +39,8 @@ template <> struct io<bf16_t> {
     __device__ __forceinline__ static void st(bf16_t* p, long i, float x) { p[i].bits = f32_to_bf16(x); }
 };
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+// v_rcp_f32 (1 ulp) instead of an IEEE division sequence
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // log of the per-key decay: log d = -e^{-1/2} * sigmoid(w).
 __device__ __forceinline__ float log_decay(float w) { return -DECAY_SCALE * sigmoidf_(w); }

@@ -133,6 +133,72 @@ __device__ __forceinline__ uint4 fragp(const uint16_t* p, int ld, int row, int k
 }
 
 // ---------------------------------------------------------------------------
+// LDS transpose read (gfx950 ds_read_b64_tr_b16).  For a row-major bf16
+// matrix X in LDS (row stride ld elements, 8-byte aligned rows), lane (q, r16)
+// supplies &X[4q + r16/4][4*(r16%4)] and receives X[4q + e][r16], e = 0..3
+// (layout verified with an in-bounds probe).  That is the B operand of the
+// K=16 instruction for X, the A operand for X^T, and the D layout of X, read
+// from memory whose rows run along the other index.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+__device__ __forceinline__ uint2 ldtr(const uint16_t* x, int ld, int lane) {
+    const uint16_t* p = x + (4 * (lane >> 4) + ((lane & 15) >> 2)) * ld + 4 * (lane & 3);
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(uint16_t*)p));
+}
+// Orders this wave's earlier LDS accesses before its later ones (LDS executes
+// one wave's instructions in order; this also stops the compiler from moving
+// loads above stores it cannot prove disjoint).
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Row operations over the 16 lanes that share q (a "row" of the wave):
+// inclusive prefix sum along r16, value of lane r16-1 (lane 0: `first`), and
+// the value of lane 15 broadcast to the row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float old, float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row_prefix_sum(float x) {
+    x += dpp_f<0x111>(0.f, x);  // row_shr:1
+    x += dpp_f<0x112>(0.f, x);  // row_shr:2
+    x += dpp_f<0x114>(0.f, x);  // row_shr:4
+    x += dpp_f<0x118>(0.f, x);  // row_shr:8
+    return x;
+}
+__device__ __forceinline__ float row_prev(float x, float first) { return dpp_f<0x111>(first, x); }
+__device__ __forceinline__ float row_last(float x) {  // ds_swizzle, and_mask 0x10, or_mask 0x0f
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f0));
+}
+
+// Four 16-key tiles of a [token][key] operand held by a lane as
+// x[tj][e] = X[t = r16][16 tj + 4q + e], split into (hi, lo) bf16 pairs.
+// As the A or B operand of the K=32 instruction (slots e <-> 32s + 4q + e,
+// 4 + e <-> 32s + 16 + 4q + e) it contracts over keys.
+struct Pk4 {
+    uint2 h[4], l[4];
+};
+__device__ __forceinline__ Pk4 pk4(const f32x4_t (&x)[4]) {
+    Pk4 p;
+#pragma unroll
+    for (int tj = 0; tj < 4; tj++) pack4(x[tj], p.h[tj], p.l[tj]);
+    return p;
+}
+// X Y^T over the 64 keys (split precision): D[t][s] = sum_j X[t][j] Y[s][j].
+__device__ __forceinline__ f32x4_t mm_keys(const Pk4& X, const Pk4& Y) {
+    f32x4_t acc = zero4(), c1 = zero4(), c2 = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const uint4 ah = make_uint4(X.h[2 * s].x, X.h[2 * s].y, X.h[2 * s + 1].x, X.h[2 * s + 1].y);
+        const uint4 al = make_uint4(X.l[2 * s].x, X.l[2 * s].y, X.l[2 * s + 1].x, X.l[2 * s + 1].y);
+        const uint4 bh = make_uint4(Y.h[2 * s].x, Y.h[2 * s].y, Y.h[2 * s + 1].x, Y.h[2 * s + 1].y);
+        const uint4 bl = make_uint4(Y.l[2 * s].x, Y.l[2 * s].y, Y.l[2 * s + 1].x, Y.l[2 * s + 1].y);
+        acc = mma32(acc, ah, bh);
+        c1 = mma32(c1, ah, bl);
+        c2 = mma32(c2, al, bh);
+    }
+    return acc + c1 + c2;
+}
+
+// ---------------------------------------------------------------------------
 // 16x16 tile algebra entirely in accumulator registers.
 // A D-layout tile X (lane (q, r16) holds X[4q+e][r16]) is the B operand of
 // the K=16 instruction as it stands, and it is the A operand of X^T.  So a
