@@ -1,31 +1,41 @@
 // Chunked WKV7 backward on the matrix cores (bf16 I/O, fp32 state, N = 64).
 //
-// The forward's chunk form (see wkv7_chunk_fwd.hip for A~, R~, B-, K-, B^,
-// K^, Aab, Aak, Brb, Brk, Ti, P, Q', SA) is differentiated per chunk.  With
-// H = dL/dS at the chunk end (H = dsT for the last chunk) and dY the chunk's
-// output gradient:
-//   Q   = Ti^T (B^ H^T + Brb^T dY)         (Q[t] = dL/d sa_t)
-//   dV  = K^ H^T + Aak^T Q + Brk^T dY
-//   dK  = e^{-g} o [ (V H) diag(e^{gL}) + triu_s(V Q^T) A~ + triu(V dY^T) R~ ]
-//   dB  = e^{-g} o [ (SA H) diag(e^{gL}) + triu_s(SA Q^T) A~ + triu(SA dY^T) R~ ]
+// The forward's chunk form (see wkv7_chunk_fwd.hip for A~, R~, B-, K-, Aab,
+// Aak, Brb, Brk, Ti) is differentiated per chunk.  With H = dL/dS at the chunk
+// end (H = dsT for the last chunk), H' = H diag(e^{gL}), S0 the state at the
+// chunk start (a saved state) and dY the chunk's output gradient:
+//   SA  = Ti (A~ S0^T + Aak V)                 (SA[t] = S_{t-1} a_t)
+//   Q   = Ti^T (B- H'^T + Brb^T dY)            (Q[t] = dL/d sa_t)
+//   dV  = K- H'^T + Aak^T Q + Brk^T dY
+//   dK  = e^{-g} o [ V H' + triu_s(V Q^T) A~ + triu(V dY^T) R~ ]
+//   dB  = e^{-g} o [ SA H' + triu_s(SA Q^T) A~ + triu(SA dY^T) R~ ]
 //   dR  = e^{g}  o [ dY S0 + tril(dY SA^T) B- + tril(dY V^T) K- ]
 //   dA  = e^{gp} o [ Q S0 + tril_s(Q SA^T) B- + tril_s(Q V^T) K- ]
-//   H_0 = H diag(e^{gL}) + Q^T A~ + dY^T R~      (dL/dS at the chunk start)
+//   H_0 = H' + Q^T A~ + dY^T R~                (dL/dS at the chunk start)
 // and the decay gradient uses the identity (derived from S_t = S_{t-1} D_t +
 // sa_t b_t^T + v_t k_t^T)
 //   dlogd_t = sum_{s>=t} (r dR - b dB - k dK)_s + sum_{s>t} (a dA)_s
 //             + colsum(dsT o S_T),      dw = dlogd * (-e^{-1/2}) sig(w)(1-sig(w)),
-// a reverse cumulative sum carried across chunks.  Together these equal the
-// step adjoint of kernels/wkv7_state.cu:52-78 (checked against it on the CPU
-// oracle in float64).
+// a reverse cumulative sum carried across chunks (r dR = R~ o [..], b dB =
+// B- o [..], ...), with sig(w_t) = (g_{t-1} - g_t) / e^{-1/2}.  Together these
+// equal the step adjoint of kernels/wkv7_state.cu:52-78 (checked against it on
+// the CPU oracle in float64).
 //
-// Mapping: one 256-lane workgroup per (b,h), chunks in reverse.  Each wave w
-// owns value rows 16w..16w+15: it keeps H^T and the chunk's S0^T (from the
-// saved states) for those rows in registers, and computes Q, SA and dV for
-// them without any barrier.  The key-indexed gradients contract over all
-// value rows, so Q, SA, H and S0 are then shared through LDS and each wave
-// produces one 16-key strip of dK, dB, dR, dA, dw in a fixed summation order
-// (deterministic; the reference accumulates with fp32 atomics, cu:68-72).
+// Mapping: one 448-lane workgroup per (b,h), chunks in reverse, lock-step
+// ticks of two LDS barriers (no global-memory fence).
+//  * Producers (waves 4-6) build everything that depends only on a chunk's
+//    inputs -- A~, R~, B-, K-, g, e^{gL}, Ti, Aak, Brb, Brk, V dY^T -- one
+//    chunk each, in three phases over the three ticks before it is consumed,
+//    into a 3-slot LDS ring (as the forward's producers do).  Their inputs
+//    arrive by LDS DMA (global_load_lds_dwordx4) two ticks ahead, so no
+//    prefetch registers are held across ticks.
+//  * Consumers (waves 0-3).  Stage B: wave c owns value rows 16c..16c+15 of H
+//    in registers and computes SA, Q, dV and the new H for them; it publishes
+//    H', S0, Q^T and SA^T rows.  Barrier.  Stage C: wave c produces the key
+//    strip 16c..16c+15 of dK, dB, dR, dA and dw, contracting over all value
+//    rows in a fixed order (deterministic; the reference accumulates with fp32
+//    atomics, cu:68-72), reading the other orientation of every exchanged
+//    matrix with ds_read_b64_tr_b16.
 #include "wkv7_launch.h"
 #include "wkv7_mfma.h"
 
@@ -34,65 +44,120 @@ namespace {
 
 constexpr int CH = CKPT;
 constexpr int NK = 64;
-constexpr int LD64 = 72;
-constexpr int LD16 = 24;
-constexpr int LD32 = 40;
+constexpr int NPROD = 3;  // producer waves = ring slots
+constexpr int LDQ = 16;   // [64][16] exchange planes
+constexpr int LDC = 16;   // [16][16] matrices
+constexpr int LDG = 68;   // fp32 [16][64] plane
 
-typedef uint16_t Plane16[2][CH * LD64];   // [16][64] hi/lo
-typedef uint16_t Plane64[2][NK * LD16];   // [64][16] hi/lo
-typedef uint16_t PlaneC[2][CH * LD16];    // [16][16] hi/lo
-typedef uint16_t PlaneC2[2][CH * LD32];   // [16][32] hi/lo
-typedef uint16_t PlaneS[2][NK * LD64];    // [64][64] hi/lo
+// [16][64] and [64][64] bf16 planes are unpadded and row-swizzled (pl()).
+typedef uint16_t Plane[CH * NK];
+// A 16x16 matrix M from its D-layout tile is stored as M^T rows (lane (q, r16)
+// writes M[4q..4q+3][r16] at row r16): a plain fragment read of it is the A
+// operand of M^T, a transpose read the A operand of M.
+typedef uint16_t Mat[2][CH * LDC];
 
-struct BwdLds {
-    uint16_t raw[7][CH * LD64];  // r,w,k,v,a,b,dy bf16 bits, [t][x]
-    union {
-        struct {                  // chunk-matrix stage only
-            Plane16 At, Rt, Bb, Kb;
-        } a;
-        struct {                  // state / gradient stages
-            Plane16 Qs, SAs;      // Q, SA [t][i]
-            PlaneC2 KC, BC, RC, AC;  // masked combine matrices [t][s']
-        } b;
-    } u;
-    Plane16 Kh, P, Pb;            // K^, P, Pb [t][j]
-    Plane64 AtT, RtT, BbT, KbT, BhT;  // [j][t]
-    uint16_t VT[NK * LD16], dYT[NK * LD16];  // [i][t], exact bf16
-    PlaneS HT, S0T;               // H^T, S0^T as [j][i]
-    PlaneC Ti, TiT, BrbT, AakT, BrkT, Q1;  // [t][s]
-    float g[CH * NK];             // cumulative log-decay [t][j]
-    float zs[CH * NK];            // dlogd terms, then dlogd [t][j]
-    float t2s[CH * NK];           // (a dA) terms [t][j]
-    float part[8][NK];
+struct Slot {
+    Plane At[2], Rt[2], Bb[2], Kb[2];  // A~, R~, B-, K- [t][j] (hi, lo)
+    Plane V, dY;                       // [t][i], exact bf16
+    Mat Ti, Aak, Brb, Brk, M2;         // M2 = triu(V dY^T); Ti..Brk are dead after stage B
+    float g[CH * LDG];                 // cumulative log-decay [t][j]
     float egL[NK];
 };
+struct BwdLds {
+    Slot slot[NPROD];
+    uint16_t Hx[2][NK * NK], S0x[2][NK * NK];    // H', S0 [i][j] (swizzled)
+    uint16_t QT[2][NK * LDQ], SAT[2][NK * LDQ];  // Q^T, SA^T [i][t]
+    Plane raw[NPROD][5];                         // producer input staging: r, w, k, a, b
+};
+static_assert(sizeof(BwdLds) <= 160 * 1024, "backward LDS budget");
 
-__device__ __forceinline__ Op op(Plane16& a) { return Op{a[0], a[1], LD64}; }
-__device__ __forceinline__ Op op(Plane64& a) { return Op{a[0], a[1], LD16}; }
-__device__ __forceinline__ Op op(PlaneC& a) { return Op{a[0], a[1], LD16}; }
-__device__ __forceinline__ Op op(PlaneC2& a) { return Op{a[0], a[1], LD32}; }
-__device__ __forceinline__ Op op(PlaneS& a) { return Op{a[0], a[1], LD64}; }
-
-// acc += A(16 x 64, [t][x] plane) * B^T where B is a [64-row][x] plane (outer =
-// output column), K = 64 over x, split precision on both sides.
-__device__ __forceinline__ f32x4_t mm64(const Op& A, const Op& B, int b_x0, int lane) {
-    return mma_k32<2>(zero4(), A, 0, B, b_x0, 0, lane);
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void vm_wait0() {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    asm volatile("" ::: "memory");
 }
-// Same with A exact in bf16 (one plane, e.g. raw V or dY).
-__device__ __forceinline__ f32x4_t mm64x(const uint16_t* A, const Op& B, int b_x0, int lane) {
-    f32x4_t acc = zero4(), c1 = zero4();
+__device__ __forceinline__ void vm_wait10() {
+    __builtin_amdgcn_s_waitcnt(0x0f7a);  // vmcnt(10)
+    asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void st8(uint16_t* p, uint2 v) { *reinterpret_cast<uint2*>(p) = v; }
+__device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ float lo_bf(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+__device__ __forceinline__ float bf_el8(uint4 u, int e) {
+    const uint32_t w = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
+    return (e & 1) ? hi_bf(w) : lo_bf(w);
+}
+__device__ __forceinline__ void put_mat(Mat& m, const f32x4_t& d, int lane) {
+    uint2 h, l;
+    pack4(d, h, l);
+    const int o = (lane & 15) * LDC + 4 * (lane >> 4);
+    st8(&m[0][o], h);
+    st8(&m[1][o], l);
+}
+__device__ __forceinline__ Pk mat_t(const Mat& m, int lane) {  // A operand of M^T
+    return Pk{frag16(m[0], LDC, 0, 0, lane), frag16(m[1], LDC, 0, 0, lane)};
+}
+__device__ __forceinline__ Pk mat_n(const Mat& m, int lane) {  // A operand of M
+    return Pk{ldtr(m[0], LDC, lane), ldtr(m[1], LDC, lane)};
+}
+// split-precision K=32 product (both operands split)
+__device__ __forceinline__ f32x4_t mm32s(uint4 ah, uint4 al, uint4 bh, uint4 bl) {
+    const f32x4_t acc = mma32(zero4(), ah, bh);
+    f32x4_t c = mma32(zero4(), ah, bl);
+    c = mma32(c, al, bh);
+    return acc + c;
+}
+// X Y^T over 64 keys, both in the K=32 operand layout (x[hf] = X[t][32hf + 8q ..])
+__device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&xl)[2], const uint4 (&yh)[2],
+                                            const uint4 (&yl)[2]) {
+    f32x4_t acc = zero4(), c1 = zero4(), c2 = zero4();
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-        const uint4 ah = frag32(A, LD64, 0, 32 * s, lane);
-        acc = mma32(acc, ah, frag32(B.hi, B.ld, b_x0, 32 * s, lane));
-        c1 = mma32(c1, ah, frag32(B.lo, B.ld, b_x0, 32 * s, lane));
+        acc = mma32(acc, xh[s], yh[s]);
+        c1 = mma32(c1, xh[s], yl[s]);
+        c2 = mma32(c2, xl[s], yh[s]);
     }
-    return acc + c1;
+    return acc + c1 + c2;
+}
+// permuted K=32 fragments over the rows of a [64][*] plane (k = 32s + 4q + e, 32s + 16 + 4q + e)
+__device__ __forceinline__ uint4 rows_tr(const uint16_t* x, int s, int lane) {  // [64][LDQ], unswizzled
+    return cat(ldtr(x + (32 * s) * LDQ, LDQ, lane), ldtr(x + (32 * s + 16) * LDQ, LDQ, lane));
+}
+__device__ __forceinline__ uint4 rows_tr_sw(const uint16_t* x, int s, int col0, int lane) {  // [64][64], swizzled
+    return cat(ldtr_sw(x, 32 * s, col0, lane), ldtr_sw(x, 32 * s + 16, col0, lane));
+}
+
+// Copy rows [t0, t0+16) of one head of a [B,T,H,64] bf16 tensor into a swizzled
+// LDS plane.  Full chunks go by LDS DMA (lane l fills physical 16-byte chunk
+// l%8 of row 8m + l/8, fetching the logical chunk that belongs there); a
+// partial chunk goes through registers with zeros past the end.
+__device__ __forceinline__ void stage_plane(uint16_t* dst, const bf16_t* src, long row0, long rstride, int L,
+                                            int lane) {
+    if (L == CH) {
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const int rho = 8 * m + (lane >> 3), pc = lane & 7;
+            const int lc = pc ^ (swz8(rho) >> 1);
+            const bf16_t* g = src + row0 + rho * rstride + 8 * lc;
+            __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
+                                             (void __attribute__((address_space(3)))*)(dst + 512 * m), 16, 0, 0);
+        }
+    } else {
+        const int r16 = lane & 15, q = lane >> 4;
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            uint4 x = make_uint4(0, 0, 0, 0);
+            if (r16 < L) x = *reinterpret_cast<const uint4*>(src + row0 + r16 * rstride + 32 * hf + 8 * q);
+            st16(dst + pl(r16, 32 * hf + 8 * q), x);
+        }
+    }
 }
 
 }  // namespace
 
-__global__ __launch_bounds__(256) void chunk_backward_bf16(
+__global__ __launch_bounds__(448) void chunk_backward_bf16(
     int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ k, const bf16_t* __restrict__ v, const bf16_t* __restrict__ a,
     const bf16_t* __restrict__ b, const float* __restrict__ ckpt, const bf16_t* __restrict__ dy,
@@ -104,22 +169,39 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
     const long ncp = ckpt_count(Tn);
-    const int i_own = 16 * wv + r16;   // value row (state registers, stage B)
-    const int j_own = 16 * wv + r16;   // key column (gradient strip, stage C)
+    const int nchunk = (Tn + CH - 1) / CH;
+    const bool consumer = wv < 4;
+    const int cw = wv;      // consumer: value-row block / key strip
+    const int pw = wv - 4;  // producer index
+    const int i_own = 16 * cw + r16;
+    const int j_own = 16 * cw + r16;
+    const long rstride = (long)H * NK;  // between consecutive tokens of one head
 
-    const Op At = op(sm.u.a.At), Rt = op(sm.u.a.Rt), Bb = op(sm.u.a.Bb), Kb = op(sm.u.a.Kb);
-    const Op Qs = op(sm.u.b.Qs), SAs = op(sm.u.b.SAs);
-    const Op KC = op(sm.u.b.KC), BC = op(sm.u.b.BC), RC = op(sm.u.b.RC), AC = op(sm.u.b.AC);
-    const Op Kh = op(sm.Kh), P = op(sm.P), Pb = op(sm.Pb);
-    const Op AtT = op(sm.AtT), RtT = op(sm.RtT), BbT = op(sm.BbT), KbT = op(sm.KbT), BhT = op(sm.BhT);
-    const Op HT = op(sm.HT), S0T = op(sm.S0T);
-    const Op Ti = op(sm.Ti), TiT = op(sm.TiT), BrbT = op(sm.BrbT), AakT = op(sm.AakT), BrkT = op(sm.BrkT),
-             Q1 = op(sm.Q1);
+    // ---------------- producer (lane: token r16, keys 32 hf + 8q + e) ----------------
+    float gq[2][8];  // cumulative log-decay, phase 0 -> 1
+    // processing index xx -> chunk nchunk-1-xx: first row offset and valid length
+    auto chunk_row0 = [&](int xx) { return ((long)(bb * Tn + (nchunk - 1 - xx) * CH) * H + h) * NK; };
+    auto chunk_len = [&](int xx) { return min(CH, Tn - (nchunk - 1 - xx) * CH); };
+    auto stage_raw = [&](int xx) {
+        const long r0 = chunk_row0(xx);
+        const int L = chunk_len(xx);
+        const bf16_t* src[5] = {r, w, k, a, b};
+#pragma unroll
+        for (int ts = 0; ts < 5; ts++) stage_plane(sm.raw[pw][ts], src[ts], r0, rstride, L, lane);
+    };
 
-    // H^T tiles: Ht[tj][e] = H[i_own][16*tj + 4q + e]
-    f32x4_t Ht[4];
-    float carry = 0.f;  // dlogd carry for key j_own (meaningful in lanes q == 0)
-    {
+    // ---------------- consumer ----------------
+    // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e]; the next chunk's saved state in the same layout
+    f32x4_t Ht[4], S0n[4];
+    float carry = 0.f;  // dlogd carry for key j_own
+    auto load_state = [&](int cc) {
+#pragma unroll
+        for (int tj = 0; tj < 4; tj++) {
+            const float4 s = *reinterpret_cast<const float4*>(ckpt + (bh * ncp + cc) * NN + (long)i_own * NK + 16 * tj + 4 * q);
+            S0n[tj] = f32x4_t{s.x, s.y, s.z, s.w};
+        }
+    };
+    if (consumer) {
         f32x4_t STt[4];
 #pragma unroll
         for (int tj = 0; tj < 4; tj++) {
@@ -130,8 +212,9 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
             const float4 s = *reinterpret_cast<const float4*>(ckpt + (bh * ncp + ncp - 1) * NN + off);
             STt[tj] = f32x4_t{s.x, s.y, s.z, s.w};
         }
-        // carry_j = sum_i dsT[i][j] * S_T[i][j]: reduce over the 16 rows of the
-        // lane group, then over the 4 waves in a fixed order
+        load_state(nchunk - 1);
+        // carry_j = sum_i dsT[i][j] S_T[i][j]: 16 rows per lane group, then the 4 waves in order
+        float* part = reinterpret_cast<float*>(&sm.Hx[0][0]);
 #pragma unroll
         for (int tj = 0; tj < 4; tj++)
 #pragma unroll
@@ -139,431 +222,377 @@ __global__ __launch_bounds__(256) void chunk_backward_bf16(
                 float p = Ht[tj][e] * STt[tj][e];
 #pragma unroll
                 for (int off = 1; off < 16; off <<= 1) p += __shfl_xor(p, off, 16);
-                if (r16 == 0) sm.part[wv][16 * tj + 4 * q + e] = p;
+                if (r16 == 0) part[cw * NK + 16 * tj + 4 * q + e] = p;
             }
-        __syncthreads();
-        carry = sm.part[0][j_own] + sm.part[1][j_own] + sm.part[2][j_own] + sm.part[3][j_own];
+        // consumers load nothing else before use: drain, so the tick loop never
+        // waits on the (in-order) memory counter for earlier stores
+        vm_wait0();
+    } else {
+        if (pw < nchunk) stage_raw(pw);
     }
+    lds_barrier();
+    if (consumer) {
+        const float* part = reinterpret_cast<const float*>(&sm.Hx[0][0]);
+        carry = part[j_own] + part[NK + j_own] + part[2 * NK + j_own] + part[3 * NK + j_own];
+    }
+    lds_barrier();
 
-    const int nchunk = (Tn + CH - 1) / CH;
-    // Inputs of the next chunk to process (c-1) are prefetched into registers:
-    // slot m of lane tid covers tensor id>>7, row (id>>3)&15, segment id&7.
-    uint4 pre[4];
-    float4 S0n[4];
-    auto load_chunk = [&](int cc) {
-        const int tb = cc * CH, Lc = min(CH, Tn - tb);
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const int id = tid + 256 * m, ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
-            pre[m] = make_uint4(0, 0, 0, 0);
-            if (id < 7 * 128 && row < Lc) {
-                const bf16_t* src = ts == 0 ? r : ts == 1 ? w : ts == 2 ? k : ts == 3 ? v : ts == 4 ? a : ts == 5 ? b : dy;
-                pre[m] = *reinterpret_cast<const uint4*>(src + ((long)(bb * Tn + tb + row) * H + h) * NK + 8 * seg);
-            }
-        }
-#pragma unroll
-        for (int tj = 0; tj < 4; tj++)
-            S0n[tj] = *reinterpret_cast<const float4*>(ckpt + (bh * ncp + cc) * NN + (long)i_own * NK + 16 * tj + 4 * q);
-    };
-    auto store_raw = [&]() {
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const int id = tid + 256 * m, ts = id >> 7, row = (id >> 3) & 15, seg = id & 7;
-            if (id < 7 * 128) *reinterpret_cast<uint4*>(&sm.raw[ts][row * LD64 + 8 * seg]) = pre[m];
-        }
-    };
-    f32x4_t S0t[4];
-    load_chunk(nchunk - 1);
-    store_raw();
-#pragma unroll
-    for (int tj = 0; tj < 4; tj++) S0t[tj] = f32x4_t{S0n[tj].x, S0n[tj].y, S0n[tj].z, S0n[tj].w};
-    for (int c = nchunk - 1; c >= 0; c--) {
-        const int t0 = c * CH, L = min(CH, Tn - t0);
-        // ---- A1: start loading chunk c-1; raw of chunk c is already in LDS ----
-        if (c > 0) load_chunk(c - 1);
-        __syncthreads();  // raw ready; the later chunk's stage C is done with LDS
-        // ---- A2: decay cumsum and scaled operands; lane = key pair jp, token pair tp ----
-        {
-            const int jp = tid & 31, tp = tid >> 5, j0 = 2 * jp, tb = 2 * tp;
-            float lw[2][2];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t wb = *reinterpret_cast<const uint32_t*>(&sm.raw[1][(tb + u) * LD64 + j0]);
-#pragma unroll
-                for (int x = 0; x < 2; x++)
-                    lw[u][x] = tb + u < L ? log_decay(bf16_to_f32((uint16_t)(wb >> (16 * x)))) : 0.f;
-            }
-#pragma unroll
-            for (int x = 0; x < 2; x++) sm.part[tp][j0 + x] = lw[0][x] + lw[1][x];
-            __syncthreads();
-            float pre_[2] = {0.f, 0.f}, tot[2] = {0.f, 0.f};
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-#pragma unroll
-                for (int x = 0; x < 2; x++) {
-                    const float p = sm.part[u][j0 + x];
-                    tot[x] += p;
-                    if (u < tp) pre_[x] += p;
-                }
-            float vat[2][2], vrt[2][2], vbb[2][2], vkb[2][2], vbh[2][2], vkh[2][2];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int t = tb + u;
-                const uint32_t rb = *reinterpret_cast<const uint32_t*>(&sm.raw[0][t * LD64 + j0]);
-                const uint32_t kb = *reinterpret_cast<const uint32_t*>(&sm.raw[2][t * LD64 + j0]);
-                const uint32_t ab = *reinterpret_cast<const uint32_t*>(&sm.raw[4][t * LD64 + j0]);
-                const uint32_t bb2 = *reinterpret_cast<const uint32_t*>(&sm.raw[5][t * LD64 + j0]);
-                float gv[2];
-#pragma unroll
-                for (int x = 0; x < 2; x++) {
-                    const float g = pre_[x] + lw[0][x] + (u ? lw[1][x] : 0.f), gp = g - lw[u][x];
-                    gv[x] = g;
-                    const float eg = __expf(g), eng = __expf(-g), egp = __expf(gp), eL = __expf(tot[x] - g);
-                    const float rr = bf16_to_f32((uint16_t)(rb >> (16 * x)));
-                    const float kk = bf16_to_f32((uint16_t)(kb >> (16 * x)));
-                    const float aa = bf16_to_f32((uint16_t)(ab >> (16 * x)));
-                    const float bv = bf16_to_f32((uint16_t)(bb2 >> (16 * x)));
-                    vat[u][x] = aa * egp;
-                    vrt[u][x] = rr * eg;
-                    vbb[u][x] = bv * eng;
-                    vkb[u][x] = kk * eng;
-                    vbh[u][x] = bv * eL;
-                    vkh[u][x] = kk * eL;
-                }
-                *reinterpret_cast<float2*>(&sm.g[t * NK + j0]) = make_float2(gv[0], gv[1]);
-            }
-            auto put_row = [&](const Op& o, const float (&vv)[2][2]) {  // [t][j] pairs along j
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    uint32_t hh, ll;
-                    split2(vv[u][0], vv[u][1], hh, ll);
-                    *reinterpret_cast<uint32_t*>(&o.hi[(tb + u) * o.ld + j0]) = hh;
-                    *reinterpret_cast<uint32_t*>(&o.lo[(tb + u) * o.ld + j0]) = ll;
-                }
-            };
-            auto put_col = [&](const Op& o, const float (&vv)[2][2]) {  // [j][t] pairs along t
-#pragma unroll
-                for (int x = 0; x < 2; x++) {
-                    uint32_t hh, ll;
-                    split2(vv[0][x], vv[1][x], hh, ll);
-                    *reinterpret_cast<uint32_t*>(&o.hi[(j0 + x) * o.ld + tb]) = hh;
-                    *reinterpret_cast<uint32_t*>(&o.lo[(j0 + x) * o.ld + tb]) = ll;
-                }
-            };
-            put_row(At, vat);
-            put_col(AtT, vat);
-            put_row(Rt, vrt);
-            put_col(RtT, vrt);
-            put_row(Bb, vbb);
-            put_col(BbT, vbb);
-            put_row(Kb, vkb);
-            put_col(KbT, vkb);
-            put_col(BhT, vbh);
-            put_row(Kh, vkh);
-            auto put_raw_col = [&](int ts, uint16_t* dst) {  // exact bf16 plane, transposed
-                const uint32_t v0 = *reinterpret_cast<const uint32_t*>(&sm.raw[ts][tb * LD64 + j0]);
-                const uint32_t v1 = *reinterpret_cast<const uint32_t*>(&sm.raw[ts][(tb + 1) * LD64 + j0]);
-                *reinterpret_cast<uint32_t*>(&dst[j0 * LD16 + tb]) = (v0 & 0xffffu) | (v1 << 16);
-                *reinterpret_cast<uint32_t*>(&dst[(j0 + 1) * LD16 + tb]) = (v0 >> 16) | (v1 & 0xffff0000u);
-            };
-            put_raw_col(3, sm.VT);
-            put_raw_col(6, sm.dYT);
-            if (tp == 0) {
-                sm.egL[j0] = __expf(tot[0]);
-                sm.egL[j0 + 1] = __expf(tot[1]);
-            }
-        }
-        __syncthreads();
-        // ---- A3: chunk matrices; wave 0: Aab, Aab^T -> Ti, Ti^T; waves 1-3: Aak, Brb, Brk ----
-        f32x4_t cm = zero4();
-        if (wv == 0) {
-            f32x4_t Lm = mm64(At, Bb, 0, lane);
-            f32x4_t LT = mm64(Bb, At, 0, lane);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                if (r16 >= 4 * q + e) Lm[e] = 0.f;
-                if (r16 <= 4 * q + e) LT[e] = 0.f;
-            }
-            f32x4_t ti, tiT;
-            tri_inverse(Lm, LT, lane, ti, tiT);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                Ti.put(4 * q + e, r16, ti[e]);
-                TiT.put(4 * q + e, r16, tiT[e]);
-            }
-        } else {
-            if (wv == 1) cm = mm64(At, Kb, 0, lane);        // Aak
-            else if (wv == 2) cm = mm64(Rt, Bb, 0, lane);   // Brb
-            else cm = mm64(Rt, Kb, 0, lane);                // Brk
-#pragma unroll
-            for (int e = 0; e < 4; e++) {  // D layout: row t = 4q+e, column s = r16
-                const int t = 4 * q + e, s = r16;
-                if (wv == 1 ? s >= t : s > t) cm[e] = 0.f;
-                if (wv == 1) AakT.put(s, t, cm[e]);
-                if (wv == 2) BrbT.put(s, t, cm[e]);
-                if (wv == 3) BrkT.put(s, t, cm[e]);
-            }
-        }
-        __syncthreads();
-        // ---- A5: P = Ti A~, Pb = Ti^T B^ on key strip 16wv..; wave 1: Q' = Ti Aak ----
-        {
-            const int j = 16 * wv + r16;
-            const f32x4_t p = mma_k16(zero4(), Ti, 0, AtT, 16 * wv, 0, lane);
-            const f32x4_t pb = mma_k16(zero4(), TiT, 0, BhT, 16 * wv, 0, lane);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                P.put(4 * q + e, j, p[e]);
-                Pb.put(4 * q + e, j, pb[e]);
-            }
-            if (wv == 1) {  // cm = Aak in D layout: rows s = 4q+e (the K index), column s' = r16
-                uint2 ah, al;
-                pack4(cm, ah, al);
-                const uint2 th = frag16(Ti.hi, LD16, 0, 0, lane), tl = frag16(Ti.lo, LD16, 0, 0, lane);
-                f32x4_t q1 = mma16(zero4(), th, ah);
-                f32x4_t c1 = mma16(zero4(), th, al);
-                c1 = mma16(c1, tl, ah);
-                q1 += c1;
-#pragma unroll
-                for (int e = 0; e < 4; e++) Q1.put(4 * q + e, r16, q1[e]);
-            }
-        }
-        __syncthreads();
-        // ---- B: wave-local rows i_own: SA, Q, dV, and H update ----
-        f32x4_t Hn[4];
-        f32x4_t dvk;              // dV[t = 4q+e][i_own], stored at the end of the chunk
-        float gk_[4], gb_[4], gr_[4], ga_[4], gw_[4];  // key-strip gradients, stored at the end
-        {
-            const uint2 vfr = ld8B(&sm.VT[i_own * LD16 + 4 * q]);   // V[t=4q..][i_own]
-            const uint2 dyf = ld8B(&sm.dYT[i_own * LD16 + 4 * q]);  // dY[t=4q..][i_own]
-            // X = Brb^T dY ; Qc = Ti^T X
-            f32x4_t X = mma16(zero4(), frag16(BrbT.hi, LD16, 0, 0, lane), dyf);
-            X = mma16(X, frag16(BrbT.lo, LD16, 0, 0, lane), dyf);
-            uint2 xh, xl;
-            pack4(X, xh, xl);
-            const uint2 tth = frag16(TiT.hi, LD16, 0, 0, lane), ttl = frag16(TiT.lo, LD16, 0, 0, lane);
-            f32x4_t Qc = mma16(zero4(), tth, xh);
-            f32x4_t c0 = mma16(zero4(), tth, xl);
-            c0 = mma16(c0, ttl, xh);
-            Qc += c0;
-            // SA = P S0^T + Q' V ; Q = Pb H^T + Qc ; dV (K^ H^T part)
-            f32x4_t sa = zero4(), qq = zero4(), dvv = zero4();
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                float sv[8], hv[8];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    sv[e] = S0t[2 * s][e];
-                    sv[4 + e] = S0t[2 * s + 1][e];
-                    hv[e] = Ht[2 * s][e];
-                    hv[4 + e] = Ht[2 * s + 1][e];
-                }
-                uint4 sh, sl, hh, hl;
-                pack8(sv, sh, sl);
-                pack8(hv, hh, hl);
-                const int k0 = 32 * s;
-                const uint4 pah = fragp(P.hi, LD64, r16, k0, lane), pal = fragp(P.lo, LD64, r16, k0, lane);
-                const uint4 bah = fragp(Pb.hi, LD64, r16, k0, lane), bal = fragp(Pb.lo, LD64, r16, k0, lane);
-                const uint4 kah = fragp(Kh.hi, LD64, r16, k0, lane), kal = fragp(Kh.lo, LD64, r16, k0, lane);
-                sa = mma32(sa, pah, sh);
-                sa = mma32(sa, pah, sl);
-                sa = mma32(sa, pal, sh);
-                qq = mma32(qq, bah, hh);
-                qq = mma32(qq, bah, hl);
-                qq = mma32(qq, bal, hh);
-                dvv = mma32(dvv, kah, hh);
-                dvv = mma32(dvv, kah, hl);
-                dvv = mma32(dvv, kal, hh);
-            }
-            {
-                f32x4_t sv2 = mma16(zero4(), frag16(Q1.hi, LD16, 0, 0, lane), vfr);
-                sv2 = mma16(sv2, frag16(Q1.lo, LD16, 0, 0, lane), vfr);
-                sa += sv2;
-            }
-            qq += Qc;
-            // dV += Aak^T Q + Brk^T dY
-            uint2 qh, ql;
-            pack4(qq, qh, ql);
-            {
-                const uint2 aah = frag16(AakT.hi, LD16, 0, 0, lane), aal = frag16(AakT.lo, LD16, 0, 0, lane);
-                f32x4_t d2 = mma16(zero4(), aah, qh);
-                f32x4_t d3 = mma16(zero4(), aah, ql);
-                d3 = mma16(d3, aal, qh);
-                d2 = mma16(d2, frag16(BrkT.hi, LD16, 0, 0, lane), dyf);
-                d2 = mma16(d2, frag16(BrkT.lo, LD16, 0, 0, lane), dyf);
-                dvv += d2 + d3;
-            }
-            dvk = dvv;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int t = 4 * q + e;
-                Qs.put(t, i_own, qq[e]);
-                SAs.put(t, i_own, sa[e]);
-            }
-#pragma unroll
-            for (int tj = 0; tj < 4; tj++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    HT.put(16 * tj + 4 * q + e, i_own, Ht[tj][e]);
-                    S0T.put(16 * tj + 4 * q + e, i_own, S0t[tj][e]);
-                }
-            // H_new^T = H^T diag(e^{gL}) + [A~^T R~^T] [Q; dY]
-            const uint4 bhi = cat(qh, dyf), blo = cat(ql, make_uint2(0, 0));
+    for (int n = -NPROD; n < nchunk; n++) {
+        // ================= consumers, stage B (chunk n, rows i_own) =================
+        if (consumer && n >= 0) {
+            const Slot& S = sm.slot[n % NPROD];
+            const int c = nchunk - 1 - n, t0 = c * CH, L = min(CH, Tn - t0);
+            f32x4_t S0r[4], Hp[4];
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
-                const int jr = 16 * tj + r16;
-                const uint4 ah = cat(ld8B(&AtT.hi[jr * LD16 + 4 * q]), ld8B(&RtT.hi[jr * LD16 + 4 * q]));
-                const uint4 al = cat(ld8B(&AtT.lo[jr * LD16 + 4 * q]), ld8B(&RtT.lo[jr * LD16 + 4 * q]));
-                f32x4_t acc;
+                S0r[tj] = S0n[tj];
+                const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
+                Hp[tj] = Ht[tj] * f32x4_t{el.x, el.y, el.z, el.w};
+            }
+            const uint2 vfr = ldtr_sw(S.V, 0, 16 * cw, lane);   // V[s = 4q+e][i_own]
+            const uint2 dyf = ldtr_sw(S.dY, 0, 16 * cw, lane);  // dY[s = 4q+e][i_own]
+            // X1 = A~ S0^T + Aak V ; X2 = B- H'^T + Brb^T dY ; dV0 = K- H'^T + Brk^T dY
+            f32x4_t x1 = zero4(), x2 = zero4(), dv0 = zero4();
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc[e] = Ht[tj][e] * sm.egL[16 * tj + 4 * q + e];
-                acc = mma32(acc, ah, bhi);
+            for (int s = 0; s < 2; s++) {
+                float hv[8], sv[8];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    hv[e] = Hp[2 * s][e];
+                    hv[4 + e] = Hp[2 * s + 1][e];
+                    sv[e] = S0r[2 * s][e];
+                    sv[4 + e] = S0r[2 * s + 1][e];
+                }
+                uint4 hbh, hbl, sbh, sbl;
+                pack8(hv, hbh, hbl);
+                pack8(sv, sbh, sbl);
+                const uint4 ah = fragp_sw(S.At[0], r16, 32 * s, lane), al = fragp_sw(S.At[1], r16, 32 * s, lane);
+                x1 = mma32(x1, ah, sbh);
+                x1 = mma32(x1, ah, sbl);
+                x1 = mma32(x1, al, sbh);
+                const uint4 bh_ = fragp_sw(S.Bb[0], r16, 32 * s, lane), bl_ = fragp_sw(S.Bb[1], r16, 32 * s, lane);
+                x2 = mma32(x2, bh_, hbh);
+                x2 = mma32(x2, bh_, hbl);
+                x2 = mma32(x2, bl_, hbh);
+                const uint4 kh = fragp_sw(S.Kb[0], r16, 32 * s, lane), kl = fragp_sw(S.Kb[1], r16, 32 * s, lane);
+                dv0 = mma32(dv0, kh, hbh);
+                dv0 = mma32(dv0, kh, hbl);
+                dv0 = mma32(dv0, kl, hbh);
+            }
+            {
+                f32x4_t c1 = zero4(), c2 = zero4(), c3 = zero4();
+                const Pk aak = mat_n(S.Aak, lane), brbT = mat_t(S.Brb, lane), brkT = mat_t(S.Brk, lane);
+                c1 = mma16(c1, aak.h, vfr);
+                c1 = mma16(c1, aak.l, vfr);
+                c2 = mma16(c2, brbT.h, dyf);
+                c2 = mma16(c2, brbT.l, dyf);
+                c3 = mma16(c3, brkT.h, dyf);
+                c3 = mma16(c3, brkT.l, dyf);
+                x1 += c1;
+                x2 += c2;
+                dv0 += c3;
+            }
+            const f32x4_t sa = mm16s(mat_n(S.Ti, lane), pk(x1));   // SA = Ti X1
+            const f32x4_t qq = mm16s(mat_t(S.Ti, lane), pk(x2));   // Q  = Ti^T X2
+            const Pk pq = pk(qq), psa = pk(sa);
+            const f32x4_t dvv = dv0 + mm16s(mat_t(S.Aak, lane), pq);
+            // publish this block's rows for stage C
+            st8(&sm.QT[0][i_own * LDQ + 4 * q], pq.h);
+            st8(&sm.QT[1][i_own * LDQ + 4 * q], pq.l);
+            st8(&sm.SAT[0][i_own * LDQ + 4 * q], psa.h);
+            st8(&sm.SAT[1][i_own * LDQ + 4 * q], psa.l);
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++) {
+                uint2 hh, ll;
+                pack4(Hp[tj], hh, ll);
+                st8(&sm.Hx[0][pl(i_own, 16 * tj + 4 * q)], hh);
+                st8(&sm.Hx[1][pl(i_own, 16 * tj + 4 * q)], ll);
+                pack4(S0r[tj], hh, ll);
+                st8(&sm.S0x[0][pl(i_own, 16 * tj + 4 * q)], hh);
+                st8(&sm.S0x[1][pl(i_own, 16 * tj + 4 * q)], ll);
+            }
+            // H_0^T = H'^T + [A~^T R~^T] [Q; dY]
+            const uint4 bhi = cat(pq.h, dyf), blo = cat(pq.l, make_uint2(0, 0));
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++) {
+                const uint4 ah = cat(ldtr_sw(S.At[0], 0, 16 * tj, lane), ldtr_sw(S.Rt[0], 0, 16 * tj, lane));
+                const uint4 al = cat(ldtr_sw(S.At[1], 0, 16 * tj, lane), ldtr_sw(S.Rt[1], 0, 16 * tj, lane));
+                f32x4_t acc = mma32(Hp[tj], ah, bhi);
                 f32x4_t c1 = mma32(zero4(), ah, blo);
                 c1 = mma32(c1, al, bhi);
-                Hn[tj] = acc + c1;
+                Ht[tj] = acc + c1;
+            }
+            bf16_t* dvp = dv + ((long)(bb * Tn + t0 + 4 * q) * H + h) * NK + i_own;
+            if (L == CH) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) dvp[(long)e * rstride].bits = f32_to_bf16(dvv[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (4 * q + e < L) dvp[(long)e * rstride].bits = f32_to_bf16(dvv[e]);
             }
         }
-        __syncthreads();
-        // ---- C1: the 16x16 contractions over i (one per wave) and masked combine forms ----
-        {
-            const uint16_t* Vr = sm.raw[3];
-            const uint16_t* dYr = sm.raw[6];
-            f32x4_t m;
-            if (wv == 0) m = mm64x(Vr, Qs, 0, lane);            // M1 = V Q^T
-            else if (wv == 1) {                                 // M2 = V dY^T (exact x exact)
-                m = zero4();
+        lds_barrier();
+        if (consumer) {
+            // ================= consumers, stage C (chunk n, key strip j_own) =================
+            if (n >= 0) {
+                Slot& S = sm.slot[n % NPROD];
+                const int c = nchunk - 1 - n, t0 = c * CH, L = min(CH, Tn - t0);
+                if (c > 0) load_state(c - 1);  // saved state of the next chunk processed
+                f32x4_t m1 = zero4(), n1 = zero4(), xm = zero4(), gK = zero4(), gB = zero4(), gR = zero4(), gA = zero4();
+                {
+                    f32x4_t c1 = zero4(), c2 = zero4(), c3 = zero4();
 #pragma unroll
-                for (int s = 0; s < 2; s++)
-                    m = mma32(m, frag32(Vr, LD64, 0, 32 * s, lane), frag32(dYr, LD64, 0, 32 * s, lane));
-            } else if (wv == 2) m = mm64(SAs, Qs, 0, lane);     // N1 = SA Q^T
-            else m = mm64x(dYr, SAs, 0, lane);                  // N2^T = dY SA^T
-            // element (t = 4q+e, s = r16)
+                    for (int s = 0; s < 2; s++) {
+                        const uint4 va = fragp_sw(S.V, r16, 32 * s, lane);    // V[t][i], exact
+                        const uint4 ya = fragp_sw(S.dY, r16, 32 * s, lane);   // dY[t][i], exact
+                        const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
+                        const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
+                        m1 = mma32(m1, va, qh);   // V Q^T
+                        m1 = mma32(m1, va, ql);
+                        n1 = mma32(n1, sh, qh);   // SA Q^T
+                        n1 = mma32(n1, sh, ql);
+                        c1 = mma32(c1, sl, qh);
+                        xm = mma32(xm, ya, sh);   // dY SA^T
+                        xm = mma32(xm, ya, sl);
+                        const uint4 hh = rows_tr_sw(sm.Hx[0], s, 16 * cw, lane), hl = rows_tr_sw(sm.Hx[1], s, 16 * cw, lane);
+                        gK = mma32(gK, va, hh);   // V H'
+                        gK = mma32(gK, va, hl);
+                        gB = mma32(gB, sh, hh);   // SA H'
+                        gB = mma32(gB, sh, hl);
+                        c2 = mma32(c2, sl, hh);
+                        const uint4 oh = rows_tr_sw(sm.S0x[0], s, 16 * cw, lane), ol = rows_tr_sw(sm.S0x[1], s, 16 * cw, lane);
+                        gR = mma32(gR, ya, oh);   // dY S0
+                        gR = mma32(gR, ya, ol);
+                        gA = mma32(gA, qh, oh);   // Q S0
+                        gA = mma32(gA, qh, ol);
+                        c3 = mma32(c3, ql, oh);
+                    }
+                    n1 += c1;
+                    gB += c2;
+                    gA += c3;
+                }
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int t = 4 * q + e, s = r16;
-                const float x = m[e];
-                if (wv == 0) {  // M1: dK uses triu_s(M1); dA uses tril_s(M1^T)
-                    KC.put(t, s, s > t ? x : 0.f);
-                    AC.put(s, 16 + t, t < s ? x : 0.f);
-                } else if (wv == 1) {  // M2: dK uses triu(M2); dR uses tril(M2^T)
-                    KC.put(t, 16 + s, s >= t ? x : 0.f);
-                    RC.put(s, 16 + t, t <= s ? x : 0.f);
-                } else if (wv == 2) {  // N1: dB uses triu_s(N1); dA uses tril_s(N1^T)
-                    BC.put(t, s, s > t ? x : 0.f);
-                    AC.put(s, t, t < s ? x : 0.f);
-                } else {  // x = (dY SA^T)[t][s] = N2[s][t]: dR uses tril(dY SA^T); dB uses triu(N2)
-                    RC.put(t, s, s <= t ? x : 0.f);
-                    BC.put(s, 16 + t, t >= s ? x : 0.f);
+                for (int e = 0; e < 4; e++) {  // D layout: row t = 4q+e, column s = r16
+                    const int t = 4 * q + e;
+                    if (r16 <= t) m1[e] = 0.f, n1[e] = 0.f;  // keep s > t
+                    if (r16 > t) xm[e] = 0.f;                // keep s <= t
+                }
+                // [A~; R~] and [B-; K-] strips as K=32 B operands (also their values in D layout)
+                const uint4 arh = cat(ldtr_sw(S.At[0], 0, 16 * cw, lane), ldtr_sw(S.Rt[0], 0, 16 * cw, lane));
+                const uint4 arl = cat(ldtr_sw(S.At[1], 0, 16 * cw, lane), ldtr_sw(S.Rt[1], 0, 16 * cw, lane));
+                const uint4 bkh = cat(ldtr_sw(S.Bb[0], 0, 16 * cw, lane), ldtr_sw(S.Kb[0], 0, 16 * cw, lane));
+                const uint4 bkl = cat(ldtr_sw(S.Bb[1], 0, 16 * cw, lane), ldtr_sw(S.Kb[1], 0, 16 * cw, lane));
+                // the 16x16 masked products go through this wave's scratch matrix (in the
+                // slot's Ti/Aak/Brb/Brk area, dead after stage B) to get both orientations
+                Mat& P = cw == 0 ? S.Ti : cw == 1 ? S.Aak : cw == 2 ? S.Brb : S.Brk;
+                const Pk m2n = mat_n(S.M2, lane), m2t = mat_t(S.M2, lane);
+                put_mat(P, m1, lane);
+                wave_lds_fence();
+                const Pk m1n = mat_n(P, lane), m1t = mat_t(P, lane);
+                wave_lds_fence();
+                const f32x4_t cK = mm32s(cat(m1n.h, m2n.h), cat(m1n.l, m2n.l), arh, arl);  // [triu_s(M1) | triu(M2)]
+                put_mat(P, xm, lane);
+                wave_lds_fence();
+                const Pk xmn = mat_n(P, lane), xmt = mat_t(P, lane);
+                wave_lds_fence();
+                const f32x4_t cR = mm32s(cat(xmn.h, m2t.h), cat(xmn.l, m2t.l), bkh, bkl);  // [tril(dY SA^T) | tril(dY V^T)]
+                put_mat(P, n1, lane);
+                wave_lds_fence();
+                const Pk n1n = mat_n(P, lane), n1t = mat_t(P, lane);
+                const f32x4_t cB = mm32s(cat(n1n.h, xmt.h), cat(n1n.l, xmt.l), arh, arl);  // [triu_s(N1) | triu(SA dY^T)]
+                const f32x4_t cA = mm32s(cat(n1t.h, m1t.h), cat(n1t.l, m1t.l), bkh, bkl);  // [tril_s(Q SA^T) | tril_s(Q V^T)]
+                float gk_[4], gb_[4], gr_[4], ga_[4], gw_[4], z[4], t2[4], fw[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = 4 * q + e;
+                    const float gv = S.g[t * LDG + j_own];
+                    const float gp = t > 0 ? S.g[(t - 1) * LDG + j_own] : 0.f;
+                    const float uK = gK[e] + cK[e], uB = gB[e] + cB[e], uR = gR[e] + cR[e], uA = gA[e] + cA[e];
+                    const float eng = __expf(-gv);
+                    gk_[e] = eng * uK;
+                    gb_[e] = eng * uB;
+                    gr_[e] = __expf(gv) * uR;
+                    ga_[e] = __expf(gp) * uA;
+                    const float At_ = bf_el8(arh, e) + bf_el8(arl, e);
+                    const float Rt_ = bf_el8(arh, 4 + e) + bf_el8(arl, 4 + e);
+                    const float Bb_ = bf_el8(bkh, e) + bf_el8(bkl, e);
+                    const float Kb_ = bf_el8(bkh, 4 + e) + bf_el8(bkl, 4 + e);
+                    z[e] = Rt_ * uR - Bb_ * uB - Kb_ * uK;
+                    t2[e] = At_ * uA;
+                    const float sg = (gp - gv) * (1.f / DECAY_SCALE);  // sigmoid(w_t)
+                    fw[e] = -DECAY_SCALE * sg * (1.f - sg);
+                }
+                // dlogd_t = carry + sum_{s>=t} z_s + sum_{s>t} t2_s over the chunk (t = 4q + e)
+                float tot = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) tot += z[e] + t2[e];
+                const float s1 = __shfl(tot, (lane & 15) + 16), s2 = __shfl(tot, (lane & 15) + 32),
+                            s3 = __shfl(tot, (lane & 15) + 48), s0 = __shfl(tot, lane & 15);
+                float run = carry + (q < 1 ? s1 : 0.f) + (q < 2 ? s2 : 0.f) + (q < 3 ? s3 : 0.f);
+#pragma unroll
+                for (int e = 3; e >= 0; e--) {
+                    run += z[e];
+                    gw_[e] = run * fw[e];
+                    run += t2[e];
+                }
+                carry += ((s0 + s1) + s2) + s3;
+                const long o = ((long)(bb * Tn + t0 + 4 * q) * H + h) * NK + j_own;
+                if (L == CH) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const long oe = o + (long)e * rstride;
+                        dk[oe].bits = f32_to_bf16(gk_[e]);
+                        db[oe].bits = f32_to_bf16(gb_[e]);
+                        dr[oe].bits = f32_to_bf16(gr_[e]);
+                        da[oe].bits = f32_to_bf16(ga_[e]);
+                        dw[oe].bits = f32_to_bf16(gw_[e]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (4 * q + e < L) {
+                            const long oe = o + (long)e * rstride;
+                            dk[oe].bits = f32_to_bf16(gk_[e]);
+                            db[oe].bits = f32_to_bf16(gb_[e]);
+                            dr[oe].bits = f32_to_bf16(gr_[e]);
+                            da[oe].bits = f32_to_bf16(ga_[e]);
+                            dw[oe].bits = f32_to_bf16(gw_[e]);
+                        }
+                }
+            }
+        } else {
+            // ================= producers: chunk x (processing order), phase ph =================
+            const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
+            const int ph = n + NPROD - x;
+            if (x >= 0 && x < nchunk) {  // (prologue ticks have no chunk for some producers)
+                Slot& S = sm.slot[x % NPROD];
+                const Plane* raw = sm.raw[pw];
+                if (ph == 0) {
+                    // ---- phase 0: log-decays and their cumulative sum ----
+                    vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
+                    const int L = chunk_len(x);
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) {
+                        const uint4 wr = ld16(&raw[1][pl(r16, 32 * hf + 8 * q)]);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            float ld = log_decay(bf_el8(wr, e));
+                            if (L < CH) ld = r16 < L ? ld : 0.f;
+                            gq[hf][e] = row_prefix_sum(ld);
+                        }
+                    }
+                } else if (ph == 1) {
+                    // ---- phase 1: scaled operands, g and e^{gL} into the slot; V, dY of this
+                    //      chunk and the inputs of this producer's next chunk by LDS DMA ----
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) {
+                        const int o = pl(r16, 32 * hf + 8 * q);
+                        const uint4 rr = ld16(&raw[0][o]), kk = ld16(&raw[2][o]), aa = ld16(&raw[3][o]), bv = ld16(&raw[4][o]);
+                        float at[8], rt[8], bbv[8], kbv[8], el[8];
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            const float eg = __expf(gq[hf][e]), eng = __expf(-gq[hf][e]);
+                            at[e] = bf_el8(aa, e) * row_prev(eg, 1.f);
+                            rt[e] = bf_el8(rr, e) * eg;
+                            bbv[e] = bf_el8(bv, e) * eng;
+                            kbv[e] = bf_el8(kk, e) * eng;
+                            el[e] = row_last(eg);
+                        }
+                        uint4 hh, ll;
+                        pack8(at, hh, ll);
+                        st16(&S.At[0][o], hh);
+                        st16(&S.At[1][o], ll);
+                        pack8(rt, hh, ll);
+                        st16(&S.Rt[0][o], hh);
+                        st16(&S.Rt[1][o], ll);
+                        pack8(bbv, hh, ll);
+                        st16(&S.Bb[0][o], hh);
+                        st16(&S.Bb[1][o], ll);
+                        pack8(kbv, hh, ll);
+                        st16(&S.Kb[0][o], hh);
+                        st16(&S.Kb[1][o], ll);
+                        float* gp_ = &S.g[r16 * LDG + 32 * hf + 8 * q];
+                        *reinterpret_cast<float4*>(gp_) = make_float4(gq[hf][0], gq[hf][1], gq[hf][2], gq[hf][3]);
+                        *reinterpret_cast<float4*>(gp_ + 4) = make_float4(gq[hf][4], gq[hf][5], gq[hf][6], gq[hf][7]);
+                        if (r16 == 0) {
+                            *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q]) = make_float4(el[0], el[1], el[2], el[3]);
+                            *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q + 4]) = make_float4(el[4], el[5], el[6], el[7]);
+                        }
+                    }
+                    stage_plane(S.V, v, chunk_row0(x), rstride, chunk_len(x), lane);
+                    stage_plane(S.dY, dy, chunk_row0(x), rstride, chunk_len(x), lane);
+                    wave_lds_fence();  // staging reads done before the DMA overwrites it
+                    if (x + NPROD < nchunk) stage_raw(x + NPROD);
+                } else {
+                    // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
+                    // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
+                    if (x + NPROD < nchunk) vm_wait10();
+                    else vm_wait0();
+                    auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            xh[hf] = ld16(&pl2[0][pl(r16, 32 * hf + 8 * q)]);
+                            xl[hf] = ld16(&pl2[1][pl(r16, 32 * hf + 8 * q)]);
+                        }
+                    };
+                    f32x4_t Aab, AabT, Aak, Brb, Brk, M2;
+                    {
+                        uint4 ath[2], atl[2], xh[2], xl[2];
+                        rd(S.At, ath, atl);
+                        rd(S.Bb, xh, xl);
+                        Aab = mm_keys8(ath, atl, xh, xl);
+                        AabT = mm_keys8(xh, xl, ath, atl);
+                        rd(S.Kb, xh, xl);
+                        Aak = mm_keys8(ath, atl, xh, xl);
+                    }
+                    {
+                        uint4 rth[2], rtl[2], xh[2], xl[2];
+                        rd(S.Rt, rth, rtl);
+                        rd(S.Bb, xh, xl);
+                        Brb = mm_keys8(rth, rtl, xh, xl);
+                        rd(S.Kb, xh, xl);
+                        Brk = mm_keys8(rth, rtl, xh, xl);
+                    }
+                    {
+                        uint4 vv[2], yy[2];
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            vv[hf] = ld16(&S.V[pl(r16, 32 * hf + 8 * q)]);
+                            yy[hf] = ld16(&S.dY[pl(r16, 32 * hf + 8 * q)]);
+                        }
+                        M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
+                        const int rw = 4 * q + e;
+                        if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;  // [t][s]: s < t
+                        if (rw >= r16) AabT[e] = 0.f;               // [s][t]: s < t
+                        if (r16 > rw) Brb[e] = 0.f, Brk[e] = 0.f;   // [t][s]: s <= t
+                        if (r16 < rw) M2[e] = 0.f;                  // [t][s]: s >= t
+                    }
+                    f32x4_t Ti, TiT;
+                    tri_inverse(Aab, AabT, lane, Ti, TiT);
+                    put_mat(S.Ti, Ti, lane);
+                    put_mat(S.Aak, Aak, lane);
+                    put_mat(S.Brb, Brb, lane);
+                    put_mat(S.Brk, Brk, lane);
+                    put_mat(S.M2, M2, lane);
                 }
             }
         }
-        __syncthreads();
-        // ---- C2: key strip j_own: dK, dB, dR, dA and the decay gradient ----
-        {
-            const uint16_t* Vr = sm.raw[3];
-            const uint16_t* dYr = sm.raw[6];
-            const int x0 = 16 * wv;
-            // [A~; R~] and [B-; K-] as B operands with K = 32 (rows s' of the combine matrices)
-            uint4 arh, arl, bkh, bkl;
-            {
-                const int jr = x0 + r16;
-                const bool fst = q < 2;
-                const int kk0 = 8 * (q & 1);
-                arh = *reinterpret_cast<const uint4*>((fst ? AtT.hi : RtT.hi) + jr * LD16 + kk0);
-                arl = *reinterpret_cast<const uint4*>((fst ? AtT.lo : RtT.lo) + jr * LD16 + kk0);
-                bkh = *reinterpret_cast<const uint4*>((fst ? BbT.hi : KbT.hi) + jr * LD16 + kk0);
-                bkl = *reinterpret_cast<const uint4*>((fst ? BbT.lo : KbT.lo) + jr * LD16 + kk0);
-            }
-            auto combine = [&](const Op& M, const uint4& bh_, const uint4& bl_) {
-                const uint4 mh = frag32(M.hi, LD32, 0, 0, lane), ml = frag32(M.lo, LD32, 0, 0, lane);
-                f32x4_t acc = mma32(zero4(), mh, bh_);
-                f32x4_t c1 = mma32(zero4(), mh, bl_);
-                c1 = mma32(c1, ml, bh_);
-                return acc + c1;
-            };
-            f32x4_t gK = mm64x(Vr, HT, x0, lane);      // (V H)[t][j]
-            f32x4_t gB = mm64(SAs, HT, x0, lane);      // (SA H)[t][j]
-            f32x4_t gR = mm64x(dYr, S0T, x0, lane);    // (dY S0)[t][j]
-            f32x4_t gA = mm64(Qs, S0T, x0, lane);      // (Q S0)[t][j]
-            const f32x4_t cK = combine(KC, arh, arl);
-            const f32x4_t cB = combine(BC, arh, arl);
-            const f32x4_t cR = combine(RC, bkh, bkl);
-            const f32x4_t cA = combine(AC, bkh, bkl);
-            const float eL = sm.egL[j_own];
-            float z[4], t2v[4], sg[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int t = 4 * q + e;
-                const float g = sm.g[t * NK + j_own];
-                const float gp = t > 0 ? sm.g[(t - 1) * NK + j_own] : 0.f;
-                const float vK = __expf(-g) * (gK[e] * eL + cK[e]);
-                const float vB = __expf(-g) * (gB[e] * eL + cB[e]);
-                const float vR = __expf(g) * (gR[e] + cR[e]);
-                const float vA = __expf(gp) * (gA[e] + cA[e]);
-                const float rr = bf16_to_f32(sm.raw[0][t * LD64 + j_own]);
-                const float kk = bf16_to_f32(sm.raw[2][t * LD64 + j_own]);
-                const float aa = bf16_to_f32(sm.raw[4][t * LD64 + j_own]);
-                const float bv = bf16_to_f32(sm.raw[5][t * LD64 + j_own]);
-                const float wv_ = bf16_to_f32(sm.raw[1][t * LD64 + j_own]);
-                sg[e] = sigmoidf_(wv_);
-                z[e] = rr * vR - bv * vB - kk * vK;
-                t2v[e] = aa * vA;
-                gk_[e] = vK;
-                gb_[e] = vB;
-                gr_[e] = vR;
-                ga_[e] = vA;
-                sm.zs[t * NK + j_own] = z[e];
-                sm.t2s[t * NK + j_own] = t2v[e];
-            }
-            __syncthreads();
-            // dlogd_t = carry + sum_{s>=t} z_s + sum_{s>t} (a dA)_s  (16 lanes, one key each)
-            if (q == 0) {
-                float run = carry;
-#pragma unroll
-                for (int t = CH - 1; t >= 0; t--) {
-                    run += sm.zs[t * NK + j_own] + (t + 1 < CH ? sm.t2s[(t + 1) * NK + j_own] : 0.f);
-                    sm.zs[t * NK + j_own] = run;
-                }
-                carry = run + sm.t2s[j_own];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int t = 4 * q + e;
-                gw_[e] = sm.zs[t * NK + j_own] * (-DECAY_SCALE) * sg[e] * (1.f - sg[e]);
-            }
-        }
-#pragma unroll
-        for (int tj = 0; tj < 4; tj++) Ht[tj] = Hn[tj];
-        // ---- D: next chunk's inputs into LDS, then this chunk's gradient stores ----
-        // (the prefetch wait comes before the stores are issued, so it never waits on them)
-        if (c > 0) {
-            __syncthreads();  // every wave is done reading raw
-            store_raw();
-#pragma unroll
-            for (int tj = 0; tj < 4; tj++) S0t[tj] = f32x4_t{S0n[tj].x, S0n[tj].y, S0n[tj].z, S0n[tj].w};
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int t = 4 * q + e;
-            if (t < L) {
-                dv[((long)(bb * Tn + t0 + t) * H + h) * NK + i_own].bits = f32_to_bf16(dvk[e]);
-                const long o = ((long)(bb * Tn + t0 + t) * H + h) * NK + j_own;
-                dk[o].bits = f32_to_bf16(gk_[e]);
-                db[o].bits = f32_to_bf16(gb_[e]);
-                dr[o].bits = f32_to_bf16(gr_[e]);
-                da[o].bits = f32_to_bf16(ga_[e]);
-                dw[o].bits = f32_to_bf16(gw_[e]);
-            }
-        }
+        lds_barrier();
     }
+    if (consumer) {
 #pragma unroll
-    for (int tj = 0; tj < 4; tj++)
-        *reinterpret_cast<float4*>(ds0 + bh * NN + (long)i_own * NK + 16 * tj + 4 * q) =
-            make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+        for (int tj = 0; tj < 4; tj++)
+            *reinterpret_cast<float4*>(ds0 + bh * NN + (long)i_own * NK + 16 * tj + 4 * q) =
+                make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+    }
 }
 
 void launch_chunk_backward(const Bwd& p) {
-    hipLaunchKernelGGL(chunk_backward_bf16, dim3(p.B * p.H), dim3(256), 0, p.stream, p.T, p.H,
+    hipLaunchKernelGGL(chunk_backward_bf16, dim3(p.B * p.H), dim3(448), 0, p.stream, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
                        (const bf16_t*)p.a, (const bf16_t*)p.b, p.ckpt, (const bf16_t*)p.dy, p.dsT,
                        (bf16_t*)p.dr, (bf16_t*)p.dw, (bf16_t*)p.dk, (bf16_t*)p.dv, (bf16_t*)p.da,

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             Slot& S = sm.slot[x & 3];
             const int o = r16 * LDA + 4 * q;  // [t][j] position of a 4-key D-layout piece (plus 16 tj)
             const int o8 = r16 * LDA + 8 * q; // [t][j] position of this lane's 8-key run (plus 32 hf)
-            if (x < nchunk) {
+            if (x >= 0 && x < nchunk) {  // (prologue ticks have no chunk for some producers)
                 if (ph == 0) {
                     // ---- phase 0: log-decays, their cumulative sum, e^{+-g} ----
                     const int L = min(CH, Tn - x * CH);

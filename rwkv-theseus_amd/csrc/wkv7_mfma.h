@@ -145,6 +145,29 @@ __device__ __forceinline__ uint2 ldtr(const uint16_t* x, int ld, int lane) {
     const uint16_t* p = x + (4 * (lane >> 4) + ((lane & 15) >> 2)) * ld + 4 * (lane & 3);
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(uint16_t*)p));
 }
+// Row-swizzled [rows][64] bf16 planes (128-byte rows, no padding): the 8-byte
+// chunk c of row p is stored at chunk c ^ swz8(p).  swz8 keeps 16-byte pairs
+// together (bit 0 clear); a transpose read (4 rows x 4 chunks) touches 16
+// distinct chunks and a fragment read down 16 rows touches 8.
+__device__ __forceinline__ int swz8(int row) { return ((row & 3) << 2) | ((row >> 1) & 2); }
+// element offset of (row, col), col a multiple of 4
+__device__ __forceinline__ int pl(int row, int col) { return row * 64 + ((((col >> 2) ^ swz8(row))) << 2); }
+// transpose read of a swizzled plane: lane gets X[row0 + 4q + e][col0 + l%16]
+__device__ __forceinline__ uint2 ldtr_sw(const uint16_t* x, int row0, int col0, int lane) {
+    const int rho = row0 + 4 * (lane >> 4) + ((lane & 15) >> 2);
+    const uint16_t* p = x + pl(rho, col0 + 4 * (lane & 3));
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(uint16_t*)p));
+}
+// 8 bytes of a swizzled plane at (row, col), col a multiple of 4
+__device__ __forceinline__ uint2 ld8_sw(const uint16_t* x, int row, int col) {
+    return *reinterpret_cast<const uint2*>(x + pl(row, col));
+}
+// permuted K=32 A-operand fragment of row `row` (k = k0 + 4q + e, k0 + 16 + 4q + e)
+__device__ __forceinline__ uint4 fragp_sw(const uint16_t* x, int row, int k0, int lane) {
+    const int c = k0 + 4 * (lane >> 4);
+    return cat(ld8_sw(x, row, c), ld8_sw(x, row, c + 16));
+}
+
 // Orders this wave's earlier LDS accesses before its later ones (LDS executes
 // one wave's instructions in order; this also stops the compiler from moving
 // loads above stores it cannot prove disjoint).
