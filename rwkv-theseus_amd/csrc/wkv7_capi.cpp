@@ -38,21 +38,24 @@ static bool force_seq() {
     const char* e = getenv("THESEUS_WKV7_FAMILY");
     return e && strcmp(e, "seq") == 0;
 }
-static bool chunk_ok(int N, int dtype) { return N == 64 && dtype == THESEUS_WKV7_BF16 && !force_seq(); }
+// The chunked kernels cover bf16, N = 64, and token tensors under 2 GiB (the
+// backward addresses them with 32-bit buffer offsets).
+static bool chunk_ok(int B, int T, int H, int N, int dtype) {
+    return N == 64 && dtype == THESEUS_WKV7_BF16 && (long long)B * T * H * N * 2 < (1ll << 31) && !force_seq();
+}
 
 void launch_forward(const Fwd& p) {
-    if (chunk_ok(p.N, p.dtype)) launch_chunk_forward(p);
+    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_forward(p);
     else launch_seq_forward(p);
 }
 void launch_backward(const Bwd& p) {
-    if (chunk_ok(p.N, p.dtype)) launch_chunk_backward(p);
+    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_backward(p);
     else launch_seq_backward(p);
 }
 // The chunked backward needs no workspace; the step-serial one replays each
 // 16-step segment into it.
 size_t backward_workspace(int B, int T, int H, int N, int dtype) {
-    (void)T;
-    return chunk_ok(N, dtype) ? 0 : seq_backward_workspace(B, H, N);
+    return chunk_ok(B, T, H, N, dtype) ? 0 : seq_backward_workspace(B, H, N);
 }
 
 }  // namespace wkv7

@@ -49,7 +49,9 @@ constexpr int LDQ = 16;   // [64][16] exchange planes
 constexpr int LDC = 16;   // [16][16] matrices
 constexpr int LDG = 68;   // fp32 [16][64] plane
 
-// [16][64] and [64][64] bf16 planes are unpadded and row-swizzled (pl()).
+// [16][64] and [64][64] bf16 planes are unpadded and row-swizzled (pl<>):
+// planes written by lanes use SwLane, planes filled by LDS DMA SwDma; the
+// [*][16] planes (Q^T, SA^T, 16x16 matrices) use pl16.
 typedef uint16_t Plane[CH * NK];
 // A 16x16 matrix M from its D-layout tile is stored as M^T rows (lane (q, r16)
 // writes M[4q..4q+3][r16] at row r16): a plain fragment read of it is the A
@@ -81,8 +83,6 @@ __device__ __forceinline__ void vm_wait10() {
     asm volatile("" ::: "memory");
 }
 __device__ __forceinline__ void st8(uint16_t* p, uint2 v) { *reinterpret_cast<uint2*>(p) = v; }
-__device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
-__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ float lo_bf(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 __device__ __forceinline__ float bf_el8(uint4 u, int e) {
@@ -92,15 +92,16 @@ __device__ __forceinline__ float bf_el8(uint4 u, int e) {
 __device__ __forceinline__ void put_mat(Mat& m, const f32x4_t& d, int lane) {
     uint2 h, l;
     pack4(d, h, l);
-    const int o = (lane & 15) * LDC + 4 * (lane >> 4);
+    const int o = pl16(lane & 15, 4 * (lane >> 4));
     st8(&m[0][o], h);
     st8(&m[1][o], l);
 }
 __device__ __forceinline__ Pk mat_t(const Mat& m, int lane) {  // A operand of M^T
-    return Pk{frag16(m[0], LDC, 0, 0, lane), frag16(m[1], LDC, 0, 0, lane)};
+    const int o = pl16(lane & 15, 4 * (lane >> 4));
+    return Pk{*reinterpret_cast<const uint2*>(&m[0][o]), *reinterpret_cast<const uint2*>(&m[1][o])};
 }
 __device__ __forceinline__ Pk mat_n(const Mat& m, int lane) {  // A operand of M
-    return Pk{ldtr(m[0], LDC, lane), ldtr(m[1], LDC, lane)};
+    return Pk{ldtr16(m[0], 0, lane), ldtr16(m[1], 0, lane)};
 }
 // split-precision K=32 product (both operands split)
 __device__ __forceinline__ f32x4_t mm32s(uint4 ah, uint4 al, uint4 bh, uint4 bl) {
@@ -122,37 +123,52 @@ __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&
     return acc + c1 + c2;
 }
 // permuted K=32 fragments over the rows of a [64][*] plane (k = 32s + 4q + e, 32s + 16 + 4q + e)
-__device__ __forceinline__ uint4 rows_tr(const uint16_t* x, int s, int lane) {  // [64][LDQ], unswizzled
-    return cat(ldtr(x + (32 * s) * LDQ, LDQ, lane), ldtr(x + (32 * s + 16) * LDQ, LDQ, lane));
+__device__ __forceinline__ uint4 rows_tr(const uint16_t* x, int s, int lane) {  // [64][16] plane
+    return cat(ldtr16(x, 32 * s, lane), ldtr16(x, 32 * s + 16, lane));
 }
-__device__ __forceinline__ uint4 rows_tr_sw(const uint16_t* x, int s, int col0, int lane) {  // [64][64], swizzled
-    return cat(ldtr_sw(x, 32 * s, col0, lane), ldtr_sw(x, 32 * s + 16, col0, lane));
+__device__ __forceinline__ uint4 rows_tr_sw(const uint16_t* x, int s, int col0, int lane) {  // [64][64] SwLane plane
+    return cat(ldtr_sw<SwLane>(x, 32 * s, col0, lane), ldtr_sw<SwLane>(x, 32 * s + 16, col0, lane));
 }
 
+// Raw-buffer descriptor for a bf16 tensor (gfx9 word 3: 0x00020000).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
 // Copy rows [t0, t0+16) of one head of a [B,T,H,64] bf16 tensor into a swizzled
-// LDS plane.  Full chunks go by LDS DMA (lane l fills physical 16-byte chunk
-// l%8 of row 8m + l/8, fetching the logical chunk that belongs there); a
+// LDS plane.  Full chunks go by LDS DMA: lane l fills physical 16-byte chunk
+// l%8 of row 8m + l/8 with the logical chunk that belongs there (voff[m],
+// loop-invariant per lane; soff = byte offset of the chunk's first row).  A
 // partial chunk goes through registers with zeros past the end.
-__device__ __forceinline__ void stage_plane(uint16_t* dst, const bf16_t* src, long row0, long rstride, int L,
-                                            int lane) {
+__device__ __forceinline__ void stage_plane(uint16_t* dst, __amdgpu_buffer_rsrc_t rs, const bf16_t* src, uint32_t soff,
+                                            const uint32_t (&voff)[2], long rstride, int L, int lane) {
     if (L == CH) {
 #pragma unroll
-        for (int m = 0; m < 2; m++) {
-            const int rho = 8 * m + (lane >> 3), pc = lane & 7;
-            const int lc = pc ^ (swz8(rho) >> 1);
-            const bf16_t* g = src + row0 + rho * rstride + 8 * lc;
-            __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
-                                             (void __attribute__((address_space(3)))*)(dst + 512 * m), 16, 0, 0);
-        }
+        for (int m = 0; m < 2; m++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void __attribute__((address_space(3)))*)(dst + 512 * m), 16,
+                                                     voff[m], soff, 0, 0);
     } else {
         const int r16 = lane & 15, q = lane >> 4;
+        const bf16_t* s0 = src + soff / 2;
 #pragma unroll
         for (int hf = 0; hf < 2; hf++) {
             uint4 x = make_uint4(0, 0, 0, 0);
-            if (r16 < L) x = *reinterpret_cast<const uint4*>(src + row0 + r16 * rstride + 32 * hf + 8 * q);
-            st16(dst + pl(r16, 32 * hf + 8 * q), x);
+            if (r16 < L) x = *reinterpret_cast<const uint4*>(s0 + r16 * rstride + 32 * hf + 8 * q);
+            st16_sw<SwDma>(dst, r16, 32 * hf + 8 * q, x);
         }
     }
+}
+// LDS DMA of a full chunk (the steady-state path of stage_plane)
+__device__ __forceinline__ void dma_plane(uint16_t* dst, __amdgpu_buffer_rsrc_t rs, uint32_t soff, const uint32_t (&voff)[2]) {
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void __attribute__((address_space(3)))*)(dst + 512 * m), 16, voff[m],
+                                                 soff, 0, 0);
+}
+// the value of x, hidden from the optimiser: lane-derived addresses recomputed
+// per tick instead of being hoisted out of the loop into spilled registers
+__device__ __forceinline__ int opaque(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
 }
 
 }  // namespace
@@ -166,29 +182,32 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
     bf16_t* __restrict__ db, float* __restrict__ ds0) {
     __shared__ BwdLds sm;
     const int bh = blockIdx.x, bb = bh / H, h = bh % H;
-    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, q = lane >> 4, r16 = lane & 15;
+    const int tid = threadIdx.x, wv = tid >> 6;
+    int lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
     const long ncp = ckpt_count(Tn);
     const int nchunk = (Tn + CH - 1) / CH;
     const bool consumer = wv < 4;
     const int cw = wv;      // consumer: value-row block / key strip
     const int pw = wv - 4;  // producer index
-    const int i_own = 16 * cw + r16;
-    const int j_own = 16 * cw + r16;
+    int i_own = 16 * cw + r16;
+    int j_own = 16 * cw + r16;
+    const int lane0 = lane;
     const long rstride = (long)H * NK;  // between consecutive tokens of one head
 
     // ---------------- producer (lane: token r16, keys 32 hf + 8q + e) ----------------
     float gq[2][8];  // cumulative log-decay, phase 0 -> 1
-    // processing index xx -> chunk nchunk-1-xx: first row offset and valid length
-    auto chunk_row0 = [&](int xx) { return ((long)(bb * Tn + (nchunk - 1 - xx) * CH) * H + h) * NK; };
+    // processing index xx -> chunk nchunk-1-xx: byte offset of its first row, valid length
+    auto chunk_off = [&](int xx) { return (uint32_t)(((long)(bb * Tn + (nchunk - 1 - xx) * CH) * H + h) * NK * 2); };
     auto chunk_len = [&](int xx) { return min(CH, Tn - (nchunk - 1 - xx) * CH); };
-    auto stage_raw = [&](int xx) {
-        const long r0 = chunk_row0(xx);
-        const int L = chunk_len(xx);
-        const bf16_t* src[5] = {r, w, k, a, b};
+    const uint32_t tbytes = (uint32_t)((long)gridDim.x * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
+    uint32_t voff[2];
 #pragma unroll
-        for (int ts = 0; ts < 5; ts++) stage_plane(sm.raw[pw][ts], src[ts], r0, rstride, L, lane);
-    };
+    for (int m = 0; m < 2; m++) {
+        const int rho = 8 * m + (lane >> 3);
+        voff[m] = (uint32_t)(rho * rstride * 2 + 16 * ((lane & 7) ^ (swz<SwDma>(rho) >> 1)));
+    }
+    const bf16_t* const rsrc_src[5] = {r, w, k, a, b};
 
     // ---------------- consumer ----------------
     // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e]; the next chunk's saved state in the same layout
@@ -227,8 +246,17 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
         // consumers load nothing else before use: drain, so the tick loop never
         // waits on the (in-order) memory counter for earlier stores
         vm_wait0();
-    } else {
-        if (pw < nchunk) stage_raw(pw);
+    } else if (pw < nchunk) {
+        // the first chunk of each producer; only processing index 0 can be partial,
+        // and its V, dY go into its slot here too so the loop only ever runs DMA
+#pragma unroll
+        for (int ts = 0; ts < 5; ts++)
+            stage_plane(sm.raw[pw][ts], make_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(pw), voff, rstride,
+                        chunk_len(pw), lane);
+        if (pw == 0) {
+            stage_plane(sm.slot[0].V, make_rsrc(v, tbytes), v, chunk_off(0), voff, rstride, chunk_len(0), lane);
+            stage_plane(sm.slot[0].dY, make_rsrc(dy, tbytes), dy, chunk_off(0), voff, rstride, chunk_len(0), lane);
+        }
     }
     lds_barrier();
     if (consumer) {
@@ -238,6 +266,11 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
     lds_barrier();
 
     for (int n = -NPROD; n < nchunk; n++) {
+        lane = opaque(lane0);
+        q = lane >> 4;
+        r16 = lane & 15;
+        i_own = 16 * cw + r16;
+        j_own = i_own;
         // ================= consumers, stage B (chunk n, rows i_own) =================
         if (consumer && n >= 0) {
             const Slot& S = sm.slot[n % NPROD];
@@ -249,8 +282,8 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                 const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
                 Hp[tj] = Ht[tj] * f32x4_t{el.x, el.y, el.z, el.w};
             }
-            const uint2 vfr = ldtr_sw(S.V, 0, 16 * cw, lane);   // V[s = 4q+e][i_own]
-            const uint2 dyf = ldtr_sw(S.dY, 0, 16 * cw, lane);  // dY[s = 4q+e][i_own]
+            const uint2 vfr = ldtr_sw<SwDma>(S.V, 0, 16 * cw, lane);   // V[s = 4q+e][i_own]
+            const uint2 dyf = ldtr_sw<SwDma>(S.dY, 0, 16 * cw, lane);  // dY[s = 4q+e][i_own]
             // X1 = A~ S0^T + Aak V ; X2 = B- H'^T + Brb^T dY ; dV0 = K- H'^T + Brk^T dY
             f32x4_t x1 = zero4(), x2 = zero4(), dv0 = zero4();
 #pragma unroll
@@ -266,15 +299,15 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                 uint4 hbh, hbl, sbh, sbl;
                 pack8(hv, hbh, hbl);
                 pack8(sv, sbh, sbl);
-                const uint4 ah = fragp_sw(S.At[0], r16, 32 * s, lane), al = fragp_sw(S.At[1], r16, 32 * s, lane);
+                const uint4 ah = fragp_sw<SwLane>(S.At[0], r16, 32 * s, lane), al = fragp_sw<SwLane>(S.At[1], r16, 32 * s, lane);
                 x1 = mma32(x1, ah, sbh);
                 x1 = mma32(x1, ah, sbl);
                 x1 = mma32(x1, al, sbh);
-                const uint4 bh_ = fragp_sw(S.Bb[0], r16, 32 * s, lane), bl_ = fragp_sw(S.Bb[1], r16, 32 * s, lane);
+                const uint4 bh_ = fragp_sw<SwLane>(S.Bb[0], r16, 32 * s, lane), bl_ = fragp_sw<SwLane>(S.Bb[1], r16, 32 * s, lane);
                 x2 = mma32(x2, bh_, hbh);
                 x2 = mma32(x2, bh_, hbl);
                 x2 = mma32(x2, bl_, hbh);
-                const uint4 kh = fragp_sw(S.Kb[0], r16, 32 * s, lane), kl = fragp_sw(S.Kb[1], r16, 32 * s, lane);
+                const uint4 kh = fragp_sw<SwLane>(S.Kb[0], r16, 32 * s, lane), kl = fragp_sw<SwLane>(S.Kb[1], r16, 32 * s, lane);
                 dv0 = mma32(dv0, kh, hbh);
                 dv0 = mma32(dv0, kh, hbl);
                 dv0 = mma32(dv0, kl, hbh);
@@ -297,26 +330,26 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
             const Pk pq = pk(qq), psa = pk(sa);
             const f32x4_t dvv = dv0 + mm16s(mat_t(S.Aak, lane), pq);
             // publish this block's rows for stage C
-            st8(&sm.QT[0][i_own * LDQ + 4 * q], pq.h);
-            st8(&sm.QT[1][i_own * LDQ + 4 * q], pq.l);
-            st8(&sm.SAT[0][i_own * LDQ + 4 * q], psa.h);
-            st8(&sm.SAT[1][i_own * LDQ + 4 * q], psa.l);
+            st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
+            st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
+            st8(&sm.SAT[0][pl16(i_own, 4 * q)], psa.h);
+            st8(&sm.SAT[1][pl16(i_own, 4 * q)], psa.l);
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
                 uint2 hh, ll;
                 pack4(Hp[tj], hh, ll);
-                st8(&sm.Hx[0][pl(i_own, 16 * tj + 4 * q)], hh);
-                st8(&sm.Hx[1][pl(i_own, 16 * tj + 4 * q)], ll);
+                st8_sw<SwLane>(sm.Hx[0], i_own, 16 * tj + 4 * q, hh);
+                st8_sw<SwLane>(sm.Hx[1], i_own, 16 * tj + 4 * q, ll);
                 pack4(S0r[tj], hh, ll);
-                st8(&sm.S0x[0][pl(i_own, 16 * tj + 4 * q)], hh);
-                st8(&sm.S0x[1][pl(i_own, 16 * tj + 4 * q)], ll);
+                st8_sw<SwLane>(sm.S0x[0], i_own, 16 * tj + 4 * q, hh);
+                st8_sw<SwLane>(sm.S0x[1], i_own, 16 * tj + 4 * q, ll);
             }
             // H_0^T = H'^T + [A~^T R~^T] [Q; dY]
             const uint4 bhi = cat(pq.h, dyf), blo = cat(pq.l, make_uint2(0, 0));
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
-                const uint4 ah = cat(ldtr_sw(S.At[0], 0, 16 * tj, lane), ldtr_sw(S.Rt[0], 0, 16 * tj, lane));
-                const uint4 al = cat(ldtr_sw(S.At[1], 0, 16 * tj, lane), ldtr_sw(S.Rt[1], 0, 16 * tj, lane));
+                const uint4 ah = cat(ldtr_sw<SwLane>(S.At[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[0], 0, 16 * tj, lane));
+                const uint4 al = cat(ldtr_sw<SwLane>(S.At[1], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[1], 0, 16 * tj, lane));
                 f32x4_t acc = mma32(Hp[tj], ah, bhi);
                 f32x4_t c1 = mma32(zero4(), ah, blo);
                 c1 = mma32(c1, al, bhi);
@@ -339,31 +372,32 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                 Slot& S = sm.slot[n % NPROD];
                 const int c = nchunk - 1 - n, t0 = c * CH, L = min(CH, Tn - t0);
                 if (c > 0) load_state(c - 1);  // saved state of the next chunk processed
+                // contractions over all value rows i (each fragment read once)
                 f32x4_t m1 = zero4(), n1 = zero4(), xm = zero4(), gK = zero4(), gB = zero4(), gR = zero4(), gA = zero4();
                 {
                     f32x4_t c1 = zero4(), c2 = zero4(), c3 = zero4();
 #pragma unroll
                     for (int s = 0; s < 2; s++) {
-                        const uint4 va = fragp_sw(S.V, r16, 32 * s, lane);    // V[t][i], exact
-                        const uint4 ya = fragp_sw(S.dY, r16, 32 * s, lane);   // dY[t][i], exact
+                        const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);    // V[t][i], exact
+                        const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);   // dY[t][i], exact
                         const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
                         const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
+                        const uint4 hh = rows_tr_sw(sm.Hx[0], s, 16 * cw, lane), hl = rows_tr_sw(sm.Hx[1], s, 16 * cw, lane);
+                        const uint4 oh = rows_tr_sw(sm.S0x[0], s, 16 * cw, lane), ol = rows_tr_sw(sm.S0x[1], s, 16 * cw, lane);
                         m1 = mma32(m1, va, qh);   // V Q^T
                         m1 = mma32(m1, va, ql);
+                        gK = mma32(gK, va, hh);   // V H'
+                        gK = mma32(gK, va, hl);
+                        xm = mma32(xm, ya, sh);   // dY SA^T
+                        xm = mma32(xm, ya, sl);
+                        gR = mma32(gR, ya, oh);   // dY S0
+                        gR = mma32(gR, ya, ol);
                         n1 = mma32(n1, sh, qh);   // SA Q^T
                         n1 = mma32(n1, sh, ql);
                         c1 = mma32(c1, sl, qh);
-                        xm = mma32(xm, ya, sh);   // dY SA^T
-                        xm = mma32(xm, ya, sl);
-                        const uint4 hh = rows_tr_sw(sm.Hx[0], s, 16 * cw, lane), hl = rows_tr_sw(sm.Hx[1], s, 16 * cw, lane);
-                        gK = mma32(gK, va, hh);   // V H'
-                        gK = mma32(gK, va, hl);
                         gB = mma32(gB, sh, hh);   // SA H'
                         gB = mma32(gB, sh, hl);
                         c2 = mma32(c2, sl, hh);
-                        const uint4 oh = rows_tr_sw(sm.S0x[0], s, 16 * cw, lane), ol = rows_tr_sw(sm.S0x[1], s, 16 * cw, lane);
-                        gR = mma32(gR, ya, oh);   // dY S0
-                        gR = mma32(gR, ya, ol);
                         gA = mma32(gA, qh, oh);   // Q S0
                         gA = mma32(gA, qh, ol);
                         c3 = mma32(c3, ql, oh);
@@ -379,10 +413,10 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                     if (r16 > t) xm[e] = 0.f;                // keep s <= t
                 }
                 // [A~; R~] and [B-; K-] strips as K=32 B operands (also their values in D layout)
-                const uint4 arh = cat(ldtr_sw(S.At[0], 0, 16 * cw, lane), ldtr_sw(S.Rt[0], 0, 16 * cw, lane));
-                const uint4 arl = cat(ldtr_sw(S.At[1], 0, 16 * cw, lane), ldtr_sw(S.Rt[1], 0, 16 * cw, lane));
-                const uint4 bkh = cat(ldtr_sw(S.Bb[0], 0, 16 * cw, lane), ldtr_sw(S.Kb[0], 0, 16 * cw, lane));
-                const uint4 bkl = cat(ldtr_sw(S.Bb[1], 0, 16 * cw, lane), ldtr_sw(S.Kb[1], 0, 16 * cw, lane));
+                const uint4 arh = cat(ldtr_sw<SwLane>(S.At[0], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Rt[0], 0, 16 * cw, lane));
+                const uint4 arl = cat(ldtr_sw<SwLane>(S.At[1], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Rt[1], 0, 16 * cw, lane));
+                const uint4 bkh = cat(ldtr_sw<SwLane>(S.Bb[0], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[0], 0, 16 * cw, lane));
+                const uint4 bkl = cat(ldtr_sw<SwLane>(S.Bb[1], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[1], 0, 16 * cw, lane));
                 // the 16x16 masked products go through this wave's scratch matrix (in the
                 // slot's Ti/Aak/Brb/Brk area, dead after stage B) to get both orientations
                 Mat& P = cw == 0 ? S.Ti : cw == 1 ? S.Aak : cw == 2 ? S.Brb : S.Brk;
@@ -474,7 +508,7 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                     const int L = chunk_len(x);
 #pragma unroll
                     for (int hf = 0; hf < 2; hf++) {
-                        const uint4 wr = ld16(&raw[1][pl(r16, 32 * hf + 8 * q)]);
+                        const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
                             float ld = log_decay(bf_el8(wr, e));
@@ -487,8 +521,9 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                     //      chunk and the inputs of this producer's next chunk by LDS DMA ----
 #pragma unroll
                     for (int hf = 0; hf < 2; hf++) {
-                        const int o = pl(r16, 32 * hf + 8 * q);
-                        const uint4 rr = ld16(&raw[0][o]), kk = ld16(&raw[2][o]), aa = ld16(&raw[3][o]), bv = ld16(&raw[4][o]);
+                        const int c8 = 32 * hf + 8 * q;
+                        const uint4 rr = ld16_sw<SwDma>(raw[0], r16, c8), kk = ld16_sw<SwDma>(raw[2], r16, c8);
+                        const uint4 aa = ld16_sw<SwDma>(raw[3], r16, c8), bv = ld16_sw<SwDma>(raw[4], r16, c8);
                         float at[8], rt[8], bbv[8], kbv[8], el[8];
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
@@ -501,17 +536,17 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                         }
                         uint4 hh, ll;
                         pack8(at, hh, ll);
-                        st16(&S.At[0][o], hh);
-                        st16(&S.At[1][o], ll);
+                        st16_sw<SwLane>(S.At[0], r16, c8, hh);
+                        st16_sw<SwLane>(S.At[1], r16, c8, ll);
                         pack8(rt, hh, ll);
-                        st16(&S.Rt[0][o], hh);
-                        st16(&S.Rt[1][o], ll);
+                        st16_sw<SwLane>(S.Rt[0], r16, c8, hh);
+                        st16_sw<SwLane>(S.Rt[1], r16, c8, ll);
                         pack8(bbv, hh, ll);
-                        st16(&S.Bb[0][o], hh);
-                        st16(&S.Bb[1][o], ll);
+                        st16_sw<SwLane>(S.Bb[0], r16, c8, hh);
+                        st16_sw<SwLane>(S.Bb[1], r16, c8, ll);
                         pack8(kbv, hh, ll);
-                        st16(&S.Kb[0][o], hh);
-                        st16(&S.Kb[1][o], ll);
+                        st16_sw<SwLane>(S.Kb[0], r16, c8, hh);
+                        st16_sw<SwLane>(S.Kb[1], r16, c8, ll);
                         float* gp_ = &S.g[r16 * LDG + 32 * hf + 8 * q];
                         *reinterpret_cast<float4*>(gp_) = make_float4(gq[hf][0], gq[hf][1], gq[hf][2], gq[hf][3]);
                         *reinterpret_cast<float4*>(gp_ + 4) = make_float4(gq[hf][4], gq[hf][5], gq[hf][6], gq[hf][7]);
@@ -519,11 +554,18 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                             *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q]) = make_float4(el[0], el[1], el[2], el[3]);
                             *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q + 4]) = make_float4(el[4], el[5], el[6], el[7]);
                         }
+                        __builtin_amdgcn_sched_barrier(0);
                     }
-                    stage_plane(S.V, v, chunk_row0(x), rstride, chunk_len(x), lane);
-                    stage_plane(S.dY, dy, chunk_row0(x), rstride, chunk_len(x), lane);
+                    if (x > 0) {  // (chunk 0's V, dY were staged before the loop)
+                        dma_plane(S.V, make_rsrc(v, tbytes), chunk_off(x), voff);
+                        dma_plane(S.dY, make_rsrc(dy, tbytes), chunk_off(x), voff);
+                    }
                     wave_lds_fence();  // staging reads done before the DMA overwrites it
-                    if (x + NPROD < nchunk) stage_raw(x + NPROD);
+                    if (x + NPROD < nchunk) {
+#pragma unroll
+                        for (int ts = 0; ts < 5; ts++)
+                            dma_plane(sm.raw[pw][ts], make_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
+                    }
                 } else {
                     // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
                     // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
@@ -532,8 +574,8 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                     auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
 #pragma unroll
                         for (int hf = 0; hf < 2; hf++) {
-                            xh[hf] = ld16(&pl2[0][pl(r16, 32 * hf + 8 * q)]);
-                            xl[hf] = ld16(&pl2[1][pl(r16, 32 * hf + 8 * q)]);
+                            xh[hf] = ld16_sw<SwLane>(pl2[0], r16, 32 * hf + 8 * q);
+                            xl[hf] = ld16_sw<SwLane>(pl2[1], r16, 32 * hf + 8 * q);
                         }
                     };
                     f32x4_t Aab, AabT, Aak, Brb, Brk, M2;
@@ -545,6 +587,7 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                         AabT = mm_keys8(xh, xl, ath, atl);
                         rd(S.Kb, xh, xl);
                         Aak = mm_keys8(ath, atl, xh, xl);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                     {
                         uint4 rth[2], rtl[2], xh[2], xl[2];
@@ -553,13 +596,14 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                         Brb = mm_keys8(rth, rtl, xh, xl);
                         rd(S.Kb, xh, xl);
                         Brk = mm_keys8(rth, rtl, xh, xl);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                     {
                         uint4 vv[2], yy[2];
 #pragma unroll
                         for (int hf = 0; hf < 2; hf++) {
-                            vv[hf] = ld16(&S.V[pl(r16, 32 * hf + 8 * q)]);
-                            yy[hf] = ld16(&S.dY[pl(r16, 32 * hf + 8 * q)]);
+                            vv[hf] = ld16_sw<SwDma>(S.V, r16, 32 * hf + 8 * q);
+                            yy[hf] = ld16_sw<SwDma>(S.dY, r16, 32 * hf + 8 * q);
                         }
                         M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
                     }

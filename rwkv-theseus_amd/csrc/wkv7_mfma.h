@@ -145,27 +145,53 @@ __device__ __forceinline__ uint2 ldtr(const uint16_t* x, int ld, int lane) {
     const uint16_t* p = x + (4 * (lane >> 4) + ((lane & 15) >> 2)) * ld + 4 * (lane & 3);
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(uint16_t*)p));
 }
-// Row-swizzled [rows][64] bf16 planes (128-byte rows, no padding): the 8-byte
-// chunk c of row p is stored at chunk c ^ swz8(p).  swz8 keeps 16-byte pairs
-// together (bit 0 clear); a transpose read (4 rows x 4 chunks) touches 16
-// distinct chunks and a fragment read down 16 rows touches 8.
-__device__ __forceinline__ int swz8(int row) { return ((row & 3) << 2) | ((row >> 1) & 2); }
-// element offset of (row, col), col a multiple of 4
-__device__ __forceinline__ int pl(int row, int col) { return row * 64 + ((((col >> 2) ^ swz8(row))) << 2); }
-// transpose read of a swizzled plane: lane gets X[row0 + 4q + e][col0 + l%16]
-__device__ __forceinline__ uint2 ldtr_sw(const uint16_t* x, int row0, int col0, int lane) {
-    const int rho = row0 + 4 * (lane >> 4) + ((lane & 15) >> 2);
-    const uint16_t* p = x + pl(rho, col0 + 4 * (lane & 3));
+// Row-swizzled bf16 planes without padding (gfx950 LDS, measured: 8-byte
+// reads serve 32 lanes per cycle over 64 banks, 8-byte writes 16 lanes per
+// cycle over 32 banks; 16-byte reads run at half the bandwidth of two 8-byte
+// reads, so operands are read 8 bytes at a time).
+//  * [rows][64] planes, 8-byte chunk c of row p stored at chunk c ^ swz(p):
+//    SwLane = 4((p>>1)&3) + 2((p>>3)&1) + (p&1), conflict-free for 8-byte writes
+//    down 16 rows, 8-byte reads down 16 rows and transpose reads;
+//    SwDma  = the same without the last term, which keeps 16-byte pairs together
+//    for planes filled by LDS DMA (8-byte writes down 16 rows then meet 2-way).
+//  * [rows][16] planes (32-byte rows), chunk c of row p at c ^ ((p>>2)&3):
+//    conflict-free for 8-byte writes and reads down 16 rows and transpose reads.
+enum Sw { SwLane, SwDma };
+template <Sw S> __device__ __forceinline__ int swz(int row) {
+    return 4 * ((row >> 1) & 3) + 2 * ((row >> 3) & 1) + (S == SwLane ? (row & 1) : 0);
+}
+// element offset of (row, col) in a [rows][64] plane, col a multiple of 4
+template <Sw S> __device__ __forceinline__ int pl(int row, int col) { return row * 64 + (((col >> 2) ^ swz<S>(row)) << 2); }
+// element offset of (row, col) in a [rows][16] plane, col a multiple of 4
+__device__ __forceinline__ int pl16(int row, int col) { return row * 16 + (((col >> 2) ^ ((row >> 2) & 3)) << 2); }
+__device__ __forceinline__ uint2 tr_at(const uint16_t* p) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(uint16_t*)p));
 }
-// 8 bytes of a swizzled plane at (row, col), col a multiple of 4
-__device__ __forceinline__ uint2 ld8_sw(const uint16_t* x, int row, int col) {
-    return *reinterpret_cast<const uint2*>(x + pl(row, col));
+// transpose read: lane gets X[row0 + 4q + e][col0 + l%16]
+template <Sw S> __device__ __forceinline__ uint2 ldtr_sw(const uint16_t* x, int row0, int col0, int lane) {
+    return tr_at(x + pl<S>(row0 + 4 * (lane >> 4) + ((lane & 15) >> 2), col0 + 4 * (lane & 3)));
+}
+__device__ __forceinline__ uint2 ldtr16(const uint16_t* x, int row0, int lane) {  // [rows][16] plane
+    return tr_at(x + pl16(row0 + 4 * (lane >> 4) + ((lane & 15) >> 2), 4 * (lane & 3)));
+}
+template <Sw S> __device__ __forceinline__ uint2 ld8_sw(const uint16_t* x, int row, int col) {
+    return *reinterpret_cast<const uint2*>(x + pl<S>(row, col));
+}
+template <Sw S> __device__ __forceinline__ void st8_sw(uint16_t* x, int row, int col, uint2 v) {
+    *reinterpret_cast<uint2*>(x + pl<S>(row, col)) = v;
+}
+// 8 consecutive elements (two 8-byte reads / writes)
+template <Sw S> __device__ __forceinline__ uint4 ld16_sw(const uint16_t* x, int row, int col) {
+    return cat(ld8_sw<S>(x, row, col), ld8_sw<S>(x, row, col + 4));
+}
+template <Sw S> __device__ __forceinline__ void st16_sw(uint16_t* x, int row, int col, uint4 v) {
+    st8_sw<S>(x, row, col, make_uint2(v.x, v.y));
+    st8_sw<S>(x, row, col + 4, make_uint2(v.z, v.w));
 }
 // permuted K=32 A-operand fragment of row `row` (k = k0 + 4q + e, k0 + 16 + 4q + e)
-__device__ __forceinline__ uint4 fragp_sw(const uint16_t* x, int row, int k0, int lane) {
+template <Sw S> __device__ __forceinline__ uint4 fragp_sw(const uint16_t* x, int row, int k0, int lane) {
     const int c = k0 + 4 * (lane >> 4);
-    return cat(ld8_sw(x, row, c), ld8_sw(x, row, c + 16));
+    return cat(ld8_sw<S>(x, row, c), ld8_sw<S>(x, row, c + 16));
 }
 
 // Orders this wave's earlier LDS accesses before its later ones (LDS executes
