@@ -28,7 +28,9 @@
 //    chunk each, in three phases over the three ticks before it is consumed,
 //    into a 3-slot LDS ring (as the forward's producers do).  Their inputs
 //    arrive by LDS DMA (global_load_lds_dwordx4) two ticks ahead, so no
-//    prefetch registers are held across ticks.
+//    prefetch registers are held across ticks.  Each phase is split in two
+//    parts, one run beside each consumer stage, so the producers' work spans
+//    the whole tick.
 //  * Consumers (waves 0-3).  Stage B: wave c owns value rows 16c..16c+15 of H
 //    in registers and computes SA, Q, dV and the new H for them; it publishes
 //    H', S0, Q^T and SA^T rows.  Barrier.  Stage C: wave c produces the key
@@ -265,12 +267,154 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
     }
     lds_barrier();
 
+    // Producer work for chunk x (processing order) in phase ph, split into the part
+    // done while consumers run stage B (part 0) and the part done during stage C.
+    f32x4_t Aab, AabT, Aak, Brb, Brk, M2;  // phase 2, part 0 -> part 1
+    auto produce = [&](int x, int ph, int part) {
+        Slot& S = sm.slot[x % NPROD];
+        const Plane* raw = sm.raw[pw];
+        if (ph == 0) {
+            if (part == 0) {
+                // ---- phase 0: log-decays and their cumulative sum ----
+                vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
+                const int L = chunk_len(x);
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        float ld = log_decay(bf_el8(wr, e));
+                        if (L < CH) ld = r16 < L ? ld : 0.f;
+                        gq[hf][e] = row_prefix_sum(ld);
+                    }
+                }
+            }
+        } else if (ph == 1) {
+            // ---- phase 1: scaled operands, g and e^{gL} into the slot (keys 0-31 in
+            //      part 0, 32-63 in part 1); then V, dY of this chunk and the inputs of
+            //      this producer's next chunk by LDS DMA ----
+            auto half = [&](auto hfc) {
+                constexpr int hf = decltype(hfc)::value;
+                const int c8 = 32 * hf + 8 * q;
+                const uint4 rr = ld16_sw<SwDma>(raw[0], r16, c8), kk = ld16_sw<SwDma>(raw[2], r16, c8);
+                const uint4 aa = ld16_sw<SwDma>(raw[3], r16, c8), bv = ld16_sw<SwDma>(raw[4], r16, c8);
+                float at[8], rt[8], bbv[8], kbv[8], el[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float eg = __expf(gq[hf][e]), eng = __expf(-gq[hf][e]);
+                    at[e] = bf_el8(aa, e) * row_prev(eg, 1.f);
+                    rt[e] = bf_el8(rr, e) * eg;
+                    bbv[e] = bf_el8(bv, e) * eng;
+                    kbv[e] = bf_el8(kk, e) * eng;
+                    el[e] = row_last(eg);
+                }
+                uint4 hh, ll;
+                pack8(at, hh, ll);
+                st16_sw<SwLane>(S.At[0], r16, c8, hh);
+                st16_sw<SwLane>(S.At[1], r16, c8, ll);
+                pack8(rt, hh, ll);
+                st16_sw<SwLane>(S.Rt[0], r16, c8, hh);
+                st16_sw<SwLane>(S.Rt[1], r16, c8, ll);
+                pack8(bbv, hh, ll);
+                st16_sw<SwLane>(S.Bb[0], r16, c8, hh);
+                st16_sw<SwLane>(S.Bb[1], r16, c8, ll);
+                pack8(kbv, hh, ll);
+                st16_sw<SwLane>(S.Kb[0], r16, c8, hh);
+                st16_sw<SwLane>(S.Kb[1], r16, c8, ll);
+                float* gp_ = &S.g[r16 * LDG + 32 * hf + 8 * q];
+                *reinterpret_cast<float4*>(gp_) = make_float4(gq[hf][0], gq[hf][1], gq[hf][2], gq[hf][3]);
+                *reinterpret_cast<float4*>(gp_ + 4) = make_float4(gq[hf][4], gq[hf][5], gq[hf][6], gq[hf][7]);
+                if (r16 == 0) {
+                    *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q]) = make_float4(el[0], el[1], el[2], el[3]);
+                    *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q + 4]) = make_float4(el[4], el[5], el[6], el[7]);
+                }
+            };
+            if (part == 0) {
+                half(std::integral_constant<int, 0>{});
+            } else {
+                half(std::integral_constant<int, 1>{});
+                if (x > 0) {  // (chunk 0's V, dY were staged before the loop)
+                    dma_plane(S.V, make_rsrc(v, tbytes), chunk_off(x), voff);
+                    dma_plane(S.dY, make_rsrc(dy, tbytes), chunk_off(x), voff);
+                }
+                wave_lds_fence();  // staging reads done before the DMA overwrites it
+                if (x + NPROD < nchunk) {
+#pragma unroll
+                    for (int ts = 0; ts < 5; ts++)
+                        dma_plane(sm.raw[pw][ts], make_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
+                }
+            }
+        } else if (part == 0) {
+            // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
+            // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
+            if (x + NPROD < nchunk) vm_wait10();
+            else vm_wait0();
+            auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    xh[hf] = ld16_sw<SwLane>(pl2[0], r16, 32 * hf + 8 * q);
+                    xl[hf] = ld16_sw<SwLane>(pl2[1], r16, 32 * hf + 8 * q);
+                }
+            };
+            {
+                uint4 ath[2], atl[2], xh[2], xl[2];
+                rd(S.At, ath, atl);
+                rd(S.Bb, xh, xl);
+                Aab = mm_keys8(ath, atl, xh, xl);
+                AabT = mm_keys8(xh, xl, ath, atl);
+                rd(S.Kb, xh, xl);
+                Aak = mm_keys8(ath, atl, xh, xl);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            {
+                uint4 rth[2], rtl[2], xh[2], xl[2];
+                rd(S.Rt, rth, rtl);
+                rd(S.Bb, xh, xl);
+                Brb = mm_keys8(rth, rtl, xh, xl);
+                rd(S.Kb, xh, xl);
+                Brk = mm_keys8(rth, rtl, xh, xl);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            {
+                uint4 vv[2], yy[2];
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    vv[hf] = ld16_sw<SwDma>(S.V, r16, 32 * hf + 8 * q);
+                    yy[hf] = ld16_sw<SwDma>(S.dY, r16, 32 * hf + 8 * q);
+                }
+                M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
+                const int rw = 4 * q + e;
+                if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;  // [t][s]: s < t
+                if (rw >= r16) AabT[e] = 0.f;               // [s][t]: s < t
+                if (r16 > rw) Brb[e] = 0.f, Brk[e] = 0.f;   // [t][s]: s <= t
+                if (r16 < rw) M2[e] = 0.f;                  // [t][s]: s >= t
+            }
+            f32x4_t Ti, TiT;
+            tri_inverse(Aab, AabT, lane, Ti, TiT);
+            put_mat(S.Ti, Ti, lane);
+            put_mat(S.Aak, Aak, lane);
+            put_mat(S.Brb, Brb, lane);
+            put_mat(S.Brk, Brk, lane);
+            put_mat(S.M2, M2, lane);
+        }
+    };
+
     for (int n = -NPROD; n < nchunk; n++) {
         lane = opaque(lane0);
         q = lane >> 4;
         r16 = lane & 15;
         i_own = 16 * cw + r16;
         j_own = i_own;
+        // the chunk a producer works on at tick n (x = pw mod 3, so slot x % 3 is its
+        // own) and its phase; prologue ticks have no chunk for some producers
+        const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
+        const int ph = n + NPROD - x;
+        const bool pact = !consumer && x >= 0 && x < nchunk;
+        if (pact) produce(x, ph, 0);
         // ================= consumers, stage B (chunk n, rows i_own) =================
         if (consumer && n >= 0) {
             const Slot& S = sm.slot[n % NPROD];
@@ -299,6 +443,16 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                 uint4 hbh, hbl, sbh, sbl;
                 pack8(hv, hbh, hbl);
                 pack8(sv, sbh, sbl);
+                // the halves are this lane's 4-key pieces of H' and S0 (tiles 2s, 2s+1):
+                // publish them for stage C now (no second split)
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int col = 16 * (2 * s + u) + 4 * q;
+                    st8_sw<SwLane>(sm.Hx[0], i_own, col, u ? make_uint2(hbh.z, hbh.w) : make_uint2(hbh.x, hbh.y));
+                    st8_sw<SwLane>(sm.Hx[1], i_own, col, u ? make_uint2(hbl.z, hbl.w) : make_uint2(hbl.x, hbl.y));
+                    st8_sw<SwLane>(sm.S0x[0], i_own, col, u ? make_uint2(sbh.z, sbh.w) : make_uint2(sbh.x, sbh.y));
+                    st8_sw<SwLane>(sm.S0x[1], i_own, col, u ? make_uint2(sbl.z, sbl.w) : make_uint2(sbl.x, sbl.y));
+                }
                 const uint4 ah = fragp_sw<SwLane>(S.At[0], r16, 32 * s, lane), al = fragp_sw<SwLane>(S.At[1], r16, 32 * s, lane);
                 x1 = mma32(x1, ah, sbh);
                 x1 = mma32(x1, ah, sbl);
@@ -334,16 +488,6 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
             st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
             st8(&sm.SAT[0][pl16(i_own, 4 * q)], psa.h);
             st8(&sm.SAT[1][pl16(i_own, 4 * q)], psa.l);
-#pragma unroll
-            for (int tj = 0; tj < 4; tj++) {
-                uint2 hh, ll;
-                pack4(Hp[tj], hh, ll);
-                st8_sw<SwLane>(sm.Hx[0], i_own, 16 * tj + 4 * q, hh);
-                st8_sw<SwLane>(sm.Hx[1], i_own, 16 * tj + 4 * q, ll);
-                pack4(S0r[tj], hh, ll);
-                st8_sw<SwLane>(sm.S0x[0], i_own, 16 * tj + 4 * q, hh);
-                st8_sw<SwLane>(sm.S0x[1], i_own, 16 * tj + 4 * q, ll);
-            }
             // H_0^T = H'^T + [A~^T R~^T] [Q; dY]
             const uint4 bhi = cat(pq.h, dyf), blo = cat(pq.l, make_uint2(0, 0));
 #pragma unroll
@@ -496,134 +640,8 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                 }
             }
         } else {
-            // ================= producers: chunk x (processing order), phase ph =================
-            const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
-            const int ph = n + NPROD - x;
-            if (x >= 0 && x < nchunk) {  // (prologue ticks have no chunk for some producers)
-                Slot& S = sm.slot[x % NPROD];
-                const Plane* raw = sm.raw[pw];
-                if (ph == 0) {
-                    // ---- phase 0: log-decays and their cumulative sum ----
-                    vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
-                    const int L = chunk_len(x);
-#pragma unroll
-                    for (int hf = 0; hf < 2; hf++) {
-                        const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
-#pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            float ld = log_decay(bf_el8(wr, e));
-                            if (L < CH) ld = r16 < L ? ld : 0.f;
-                            gq[hf][e] = row_prefix_sum(ld);
-                        }
-                    }
-                } else if (ph == 1) {
-                    // ---- phase 1: scaled operands, g and e^{gL} into the slot; V, dY of this
-                    //      chunk and the inputs of this producer's next chunk by LDS DMA ----
-#pragma unroll
-                    for (int hf = 0; hf < 2; hf++) {
-                        const int c8 = 32 * hf + 8 * q;
-                        const uint4 rr = ld16_sw<SwDma>(raw[0], r16, c8), kk = ld16_sw<SwDma>(raw[2], r16, c8);
-                        const uint4 aa = ld16_sw<SwDma>(raw[3], r16, c8), bv = ld16_sw<SwDma>(raw[4], r16, c8);
-                        float at[8], rt[8], bbv[8], kbv[8], el[8];
-#pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            const float eg = __expf(gq[hf][e]), eng = __expf(-gq[hf][e]);
-                            at[e] = bf_el8(aa, e) * row_prev(eg, 1.f);
-                            rt[e] = bf_el8(rr, e) * eg;
-                            bbv[e] = bf_el8(bv, e) * eng;
-                            kbv[e] = bf_el8(kk, e) * eng;
-                            el[e] = row_last(eg);
-                        }
-                        uint4 hh, ll;
-                        pack8(at, hh, ll);
-                        st16_sw<SwLane>(S.At[0], r16, c8, hh);
-                        st16_sw<SwLane>(S.At[1], r16, c8, ll);
-                        pack8(rt, hh, ll);
-                        st16_sw<SwLane>(S.Rt[0], r16, c8, hh);
-                        st16_sw<SwLane>(S.Rt[1], r16, c8, ll);
-                        pack8(bbv, hh, ll);
-                        st16_sw<SwLane>(S.Bb[0], r16, c8, hh);
-                        st16_sw<SwLane>(S.Bb[1], r16, c8, ll);
-                        pack8(kbv, hh, ll);
-                        st16_sw<SwLane>(S.Kb[0], r16, c8, hh);
-                        st16_sw<SwLane>(S.Kb[1], r16, c8, ll);
-                        float* gp_ = &S.g[r16 * LDG + 32 * hf + 8 * q];
-                        *reinterpret_cast<float4*>(gp_) = make_float4(gq[hf][0], gq[hf][1], gq[hf][2], gq[hf][3]);
-                        *reinterpret_cast<float4*>(gp_ + 4) = make_float4(gq[hf][4], gq[hf][5], gq[hf][6], gq[hf][7]);
-                        if (r16 == 0) {
-                            *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q]) = make_float4(el[0], el[1], el[2], el[3]);
-                            *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q + 4]) = make_float4(el[4], el[5], el[6], el[7]);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    if (x > 0) {  // (chunk 0's V, dY were staged before the loop)
-                        dma_plane(S.V, make_rsrc(v, tbytes), chunk_off(x), voff);
-                        dma_plane(S.dY, make_rsrc(dy, tbytes), chunk_off(x), voff);
-                    }
-                    wave_lds_fence();  // staging reads done before the DMA overwrites it
-                    if (x + NPROD < nchunk) {
-#pragma unroll
-                        for (int ts = 0; ts < 5; ts++)
-                            dma_plane(sm.raw[pw][ts], make_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
-                    }
-                } else {
-                    // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
-                    // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
-                    if (x + NPROD < nchunk) vm_wait10();
-                    else vm_wait0();
-                    auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
-#pragma unroll
-                        for (int hf = 0; hf < 2; hf++) {
-                            xh[hf] = ld16_sw<SwLane>(pl2[0], r16, 32 * hf + 8 * q);
-                            xl[hf] = ld16_sw<SwLane>(pl2[1], r16, 32 * hf + 8 * q);
-                        }
-                    };
-                    f32x4_t Aab, AabT, Aak, Brb, Brk, M2;
-                    {
-                        uint4 ath[2], atl[2], xh[2], xl[2];
-                        rd(S.At, ath, atl);
-                        rd(S.Bb, xh, xl);
-                        Aab = mm_keys8(ath, atl, xh, xl);
-                        AabT = mm_keys8(xh, xl, ath, atl);
-                        rd(S.Kb, xh, xl);
-                        Aak = mm_keys8(ath, atl, xh, xl);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    {
-                        uint4 rth[2], rtl[2], xh[2], xl[2];
-                        rd(S.Rt, rth, rtl);
-                        rd(S.Bb, xh, xl);
-                        Brb = mm_keys8(rth, rtl, xh, xl);
-                        rd(S.Kb, xh, xl);
-                        Brk = mm_keys8(rth, rtl, xh, xl);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    {
-                        uint4 vv[2], yy[2];
-#pragma unroll
-                        for (int hf = 0; hf < 2; hf++) {
-                            vv[hf] = ld16_sw<SwDma>(S.V, r16, 32 * hf + 8 * q);
-                            yy[hf] = ld16_sw<SwDma>(S.dY, r16, 32 * hf + 8 * q);
-                        }
-                        M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
-                    }
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
-                        const int rw = 4 * q + e;
-                        if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;  // [t][s]: s < t
-                        if (rw >= r16) AabT[e] = 0.f;               // [s][t]: s < t
-                        if (r16 > rw) Brb[e] = 0.f, Brk[e] = 0.f;   // [t][s]: s <= t
-                        if (r16 < rw) M2[e] = 0.f;                  // [t][s]: s >= t
-                    }
-                    f32x4_t Ti, TiT;
-                    tri_inverse(Aab, AabT, lane, Ti, TiT);
-                    put_mat(S.Ti, Ti, lane);
-                    put_mat(S.Aak, Aak, lane);
-                    put_mat(S.Brb, Brb, lane);
-                    put_mat(S.Brk, Brk, lane);
-                    put_mat(S.M2, M2, lane);
-                }
-            }
+            // ================= producers, second part of the tick's phase =================
+            if (pact) produce(x, ph, 1);
         }
         lds_barrier();
     }
