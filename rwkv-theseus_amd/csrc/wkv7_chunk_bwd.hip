@@ -50,6 +50,7 @@ constexpr int NPROD = 3;  // producer waves = ring slots
 constexpr int LDQ = 16;   // [64][16] exchange planes
 constexpr int LDC = 16;   // [16][16] matrices
 constexpr int LDG = 68;   // fp32 [16][64] plane
+constexpr uint32_t OUT_OF_RANGE = 0x80000000u;  // buffer offset past every tensor (< 2 GiB)
 
 // [16][64] and [64][64] bf16 planes are unpadded and row-swizzled (pl<>):
 // planes written by lanes use SwLane, planes filled by LDS DMA SwDma; the
@@ -132,22 +133,52 @@ __device__ __forceinline__ uint4 rows_tr_sw(const uint16_t* x, int s, int col0, 
     return cat(ldtr_sw<SwLane>(x, 32 * s, col0, lane), ldtr_sw<SwLane>(x, 32 * s + 16, col0, lane));
 }
 
-// Raw-buffer descriptor for a bf16 tensor (gfx9 word 3: 0x00020000).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw-buffer descriptor for a bf16 tensor (gfx9 word 3: 0x00020000).  Accesses
+// at byte offsets >= bytes are dropped by the hardware (stores) or read as zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
-// Copy rows [t0, t0+16) of one head of a [B,T,H,64] bf16 tensor into a swizzled
-// LDS plane.  Full chunks go by LDS DMA: lane l fills physical 16-byte chunk
-// l%8 of row 8m + l/8 with the logical chunk that belongs there (voff[m],
-// loop-invariant per lane; soff = byte offset of the chunk's first row).  A
-// partial chunk goes through registers with zeros past the end.
-__device__ __forceinline__ void stage_plane(uint16_t* dst, __amdgpu_buffer_rsrc_t rs, const bf16_t* src, uint32_t soff,
+// The same descriptor as four scalar words, for the LDS DMA below.
+__device__ __forceinline__ i32x4_t dma_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    return i32x4_t{(int)(uint32_t)p, (int)((p >> 32) & 0xffff), (int)bytes, 0x00020000};
+}
+// 8-byte store into a bf16 tensor of `bytes` bytes; offsets past it (OUT_OF_RANGE
+// for rows beyond a chunk's end) are dropped by the hardware, so partial chunks
+// need no branches and every tick issues the same stores.
+__device__ __forceinline__ void store8(bf16_t* base, uint32_t bytes, uint32_t off, uint2 v) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{v.x, v.y}, make_rsrc(base, bytes), off, 0, 0);
+}
+// One LDS DMA of 16 bytes per lane (lane l fills lds + 16 l from rsrc + soff +
+// voff).  It is issued from inline asm so that the compiler does not model it:
+// the compiler would otherwise wait for it (vmcnt(0), which also waits for every
+// pending global store) before each later LDS read anywhere in the loop.  Its
+// completion is awaited explicitly (vm_wait*) before its data is read.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const uint16_t* lds, i32x4_t rs, uint32_t voff, uint32_t soff) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)lds;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(m0), "v"(voff), "s"(rs), "s"(soff) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// LDS DMA of a full chunk: rows [t0, t0+16) of one head of a [B,T,H,64] bf16
+// tensor into a swizzled (SwDma) plane.  Lane l fills physical 16-byte chunk l%8
+// of row 8m + l/8 with the logical chunk that belongs there (voff[m],
+// loop-invariant per lane; soff = byte offset of the chunk's first row).
+__device__ __forceinline__ void dma_plane(uint16_t* dst, i32x4_t rs, uint32_t soff, const uint32_t (&voff)[2]) {
+#pragma unroll
+    for (int m = 0; m < 2; m++) dma16(dst + 512 * m, rs, voff[m], soff);
+}
+// The same for a chunk of any length L: a partial chunk goes through registers
+// with zeros past the end.
+__device__ __forceinline__ void stage_plane(uint16_t* dst, i32x4_t rs, const bf16_t* src, uint32_t soff,
                                             const uint32_t (&voff)[2], long rstride, int L, int lane) {
     if (L == CH) {
-#pragma unroll
-        for (int m = 0; m < 2; m++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void __attribute__((address_space(3)))*)(dst + 512 * m), 16,
-                                                     voff[m], soff, 0, 0);
+        dma_plane(dst, rs, soff, voff);
     } else {
         const int r16 = lane & 15, q = lane >> 4;
         const bf16_t* s0 = src + soff / 2;
@@ -158,13 +189,6 @@ __device__ __forceinline__ void stage_plane(uint16_t* dst, __amdgpu_buffer_rsrc_
             st16_sw<SwDma>(dst, r16, 32 * hf + 8 * q, x);
         }
     }
-}
-// LDS DMA of a full chunk (the steady-state path of stage_plane)
-__device__ __forceinline__ void dma_plane(uint16_t* dst, __amdgpu_buffer_rsrc_t rs, uint32_t soff, const uint32_t (&voff)[2]) {
-#pragma unroll
-    for (int m = 0; m < 2; m++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void __attribute__((address_space(3)))*)(dst + 512 * m), 16, voff[m],
-                                                 soff, 0, 0);
 }
 // the value of x, hidden from the optimiser: lane-derived addresses recomputed
 // per tick instead of being hoisted out of the loop into spilled registers
@@ -184,7 +208,7 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
     bf16_t* __restrict__ db, float* __restrict__ ds0) {
     __shared__ BwdLds sm;
     const int bh = blockIdx.x, bb = bh / H, h = bh % H;
-    const int tid = threadIdx.x, wv = tid >> 6;
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     int lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
     const long ncp = ckpt_count(Tn);
@@ -253,11 +277,11 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
         // and its V, dY go into its slot here too so the loop only ever runs DMA
 #pragma unroll
         for (int ts = 0; ts < 5; ts++)
-            stage_plane(sm.raw[pw][ts], make_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(pw), voff, rstride,
+            stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(pw), voff, rstride,
                         chunk_len(pw), lane);
         if (pw == 0) {
-            stage_plane(sm.slot[0].V, make_rsrc(v, tbytes), v, chunk_off(0), voff, rstride, chunk_len(0), lane);
-            stage_plane(sm.slot[0].dY, make_rsrc(dy, tbytes), dy, chunk_off(0), voff, rstride, chunk_len(0), lane);
+            stage_plane(sm.slot[0].V, dma_rsrc(v, tbytes), v, chunk_off(0), voff, rstride, chunk_len(0), lane);
+            stage_plane(sm.slot[0].dY, dma_rsrc(dy, tbytes), dy, chunk_off(0), voff, rstride, chunk_len(0), lane);
         }
     }
     lds_barrier();
@@ -334,14 +358,14 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
             } else {
                 half(std::integral_constant<int, 1>{});
                 if (x > 0) {  // (chunk 0's V, dY were staged before the loop)
-                    dma_plane(S.V, make_rsrc(v, tbytes), chunk_off(x), voff);
-                    dma_plane(S.dY, make_rsrc(dy, tbytes), chunk_off(x), voff);
+                    dma_plane(S.V, dma_rsrc(v, tbytes), chunk_off(x), voff);
+                    dma_plane(S.dY, dma_rsrc(dy, tbytes), chunk_off(x), voff);
                 }
                 wave_lds_fence();  // staging reads done before the DMA overwrites it
                 if (x + NPROD < nchunk) {
 #pragma unroll
                     for (int ts = 0; ts < 5; ts++)
-                        dma_plane(sm.raw[pw][ts], make_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
+                        dma_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
                 }
             }
         } else if (part == 0) {
@@ -499,14 +523,11 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                 c1 = mma32(c1, al, bhi);
                 Ht[tj] = acc + c1;
             }
-            bf16_t* dvp = dv + ((long)(bb * Tn + t0 + 4 * q) * H + h) * NK + i_own;
-            if (L == CH) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) dvp[(long)e * rstride].bits = f32_to_bf16(dvv[e]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (4 * q + e < L) dvp[(long)e * rstride].bits = f32_to_bf16(dvv[e]);
+            {  // lane (q, 4m + jj) stores row 4q + jj, values 16c + 4m .. +3
+                const int tr = 4 * q + (lane & 3);
+                const uint32_t o = tr < L ? (uint32_t)((((long)(bb * Tn + t0 + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
+                                          : OUT_OF_RANGE;
+                store8(dv, tbytes, o, quad_rows_bf16(dvv, lane));
             }
         }
         lds_barrier();
@@ -615,29 +636,15 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                     run += t2[e];
                 }
                 carry += ((s0 + s1) + s2) + s3;
-                const long o = ((long)(bb * Tn + t0 + 4 * q) * H + h) * NK + j_own;
-                if (L == CH) {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const long oe = o + (long)e * rstride;
-                        dk[oe].bits = f32_to_bf16(gk_[e]);
-                        db[oe].bits = f32_to_bf16(gb_[e]);
-                        dr[oe].bits = f32_to_bf16(gr_[e]);
-                        da[oe].bits = f32_to_bf16(ga_[e]);
-                        dw[oe].bits = f32_to_bf16(gw_[e]);
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        if (4 * q + e < L) {
-                            const long oe = o + (long)e * rstride;
-                            dk[oe].bits = f32_to_bf16(gk_[e]);
-                            db[oe].bits = f32_to_bf16(gb_[e]);
-                            dr[oe].bits = f32_to_bf16(gr_[e]);
-                            da[oe].bits = f32_to_bf16(ga_[e]);
-                            dw[oe].bits = f32_to_bf16(gw_[e]);
-                        }
-                }
+                // lane (q, 4m + jj) stores row 4q + jj, keys 16c + 4m .. +3 of each gradient
+                const int tr = 4 * q + (lane & 3);
+                const uint32_t o = tr < L ? (uint32_t)((((long)(bb * Tn + t0 + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
+                                          : OUT_OF_RANGE;
+                store8(dk, tbytes, o, quad_rows_bf16(f32x4_t{gk_[0], gk_[1], gk_[2], gk_[3]}, lane));
+                store8(db, tbytes, o, quad_rows_bf16(f32x4_t{gb_[0], gb_[1], gb_[2], gb_[3]}, lane));
+                store8(dr, tbytes, o, quad_rows_bf16(f32x4_t{gr_[0], gr_[1], gr_[2], gr_[3]}, lane));
+                store8(da, tbytes, o, quad_rows_bf16(f32x4_t{ga_[0], ga_[1], ga_[2], ga_[3]}, lane));
+                store8(dw, tbytes, o, quad_rows_bf16(f32x4_t{gw_[0], gw_[1], gw_[2], gw_[3]}, lane));
             }
         } else {
             // ================= producers, second part of the tick's phase =================

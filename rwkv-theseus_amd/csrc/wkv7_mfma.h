@@ -214,6 +214,25 @@ __device__ __forceinline__ float row_prefix_sum(float x) {
     return x;
 }
 __device__ __forceinline__ float row_prev(float x, float first) { return dpp_f<0x111>(first, x); }
+
+// A D-layout tile (lane (q, r16) holds rows 4q..4q+3 of column r16) rounded to
+// bf16 and regrouped within each quad of lanes (r16 = 4m + jj) so that lane
+// (q, 4m + jj) holds row 4q + jj, columns 4m..4m+3: an 8-byte piece of a row,
+// stored with one instruction instead of four 2-byte ones.  Two DPP exchanges
+// (quad_perm) and byte permutes, no LDS.
+__device__ __forceinline__ uint2 quad_rows_bf16(const f32x4_t& d, int lane) {
+    const uint32_t d0 = f32x2_to_bf16x2(d[0], d[1]), d1 = f32x2_to_bf16x2(d[2], d[3]);  // rows (0,1), (2,3)
+    const bool lo2 = (lane & 2) == 0, odd = lane & 1;
+    // lanes jj, jj^2 swap halves of the column: jj < 2 keeps rows 0,1 of columns jj, jj+2,
+    // jj >= 2 keeps rows 2,3 of columns jj-2, jj (a0: the even column, a1: the odd+2 one)
+    const uint32_t ra = __builtin_amdgcn_update_dpp(0, lo2 ? d1 : d0, 0x4e, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+    const uint32_t a0 = lo2 ? d0 : ra, a1 = lo2 ? ra : d1;
+    // lanes jj, jj^1 swap rows: even lanes send their second row, odd lanes their first
+    const uint32_t sb = __builtin_amdgcn_perm(a1, a0, odd ? 0x05040100u : 0x07060302u);
+    const uint32_t rb = __builtin_amdgcn_update_dpp(0, sb, 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+    return make_uint2(__builtin_amdgcn_perm(rb, a0, odd ? 0x03020504u : 0x05040100u),
+                      __builtin_amdgcn_perm(rb, a1, odd ? 0x03020706u : 0x07060100u));
+}
 __device__ __forceinline__ float row_last(float x) {  // ds_swizzle, and_mask 0x10, or_mask 0x0f
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f0));
 }
