@@ -39,7 +39,7 @@
 //    atomics, cu:68-72), reading the other orientation of every exchanged
 //    matrix with ds_read_b64_tr_b16.
 #include "wkv7_launch.h"
-#include "wkv7_mfma.h"
+#include "wkv7_io.h"
 
 namespace wkv7 {
 namespace {
@@ -50,7 +50,6 @@ constexpr int NPROD = 3;  // producer waves = ring slots
 constexpr int LDQ = 16;   // [64][16] exchange planes
 constexpr int LDC = 16;   // [16][16] matrices
 constexpr int LDG = 68;   // fp32 [16][64] plane
-constexpr uint32_t OUT_OF_RANGE = 0x80000000u;  // buffer offset past every tensor (< 2 GiB)
 
 // [16][64] and [64][64] bf16 planes are unpadded and row-swizzled (pl<>):
 // planes written by lanes use SwLane, planes filled by LDS DMA SwDma; the
@@ -76,15 +75,6 @@ struct BwdLds {
 };
 static_assert(sizeof(BwdLds) <= 160 * 1024, "backward LDS budget");
 
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-__device__ __forceinline__ void vm_wait0() {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    asm volatile("" ::: "memory");
-}
-__device__ __forceinline__ void vm_wait10() {
-    __builtin_amdgcn_s_waitcnt(0x0f7a);  // vmcnt(10)
-    asm volatile("" ::: "memory");
-}
 __device__ __forceinline__ void st8(uint16_t* p, uint2 v) { *reinterpret_cast<uint2*>(p) = v; }
 __device__ __forceinline__ float lo_bf(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
@@ -133,63 +123,6 @@ __device__ __forceinline__ uint4 rows_tr_sw(const uint16_t* x, int s, int col0, 
     return cat(ldtr_sw<SwLane>(x, 32 * s, col0, lane), ldtr_sw<SwLane>(x, 32 * s + 16, col0, lane));
 }
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Raw-buffer descriptor for a bf16 tensor (gfx9 word 3: 0x00020000).  Accesses
-// at byte offsets >= bytes are dropped by the hardware (stores) or read as zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
-}
-// The same descriptor as four scalar words, for the LDS DMA below.
-__device__ __forceinline__ i32x4_t dma_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t p = reinterpret_cast<uint64_t>(base);
-    return i32x4_t{(int)(uint32_t)p, (int)((p >> 32) & 0xffff), (int)bytes, 0x00020000};
-}
-// 8-byte store into a bf16 tensor of `bytes` bytes; offsets past it (OUT_OF_RANGE
-// for rows beyond a chunk's end) are dropped by the hardware, so partial chunks
-// need no branches and every tick issues the same stores.
-__device__ __forceinline__ void store8(bf16_t* base, uint32_t bytes, uint32_t off, uint2 v) {
-    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-    __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{v.x, v.y}, make_rsrc(base, bytes), off, 0, 0);
-}
-// One LDS DMA of 16 bytes per lane (lane l fills lds + 16 l from rsrc + soff +
-// voff).  It is issued from inline asm so that the compiler does not model it:
-// the compiler would otherwise wait for it (vmcnt(0), which also waits for every
-// pending global store) before each later LDS read anywhere in the loop.  Its
-// completion is awaited explicitly (vm_wait*) before its data is read.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const uint16_t* lds, i32x4_t rs, uint32_t voff, uint32_t soff) {
-    const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)lds;
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :: "s"(m0), "v"(voff), "s"(rs), "s"(soff) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-// LDS DMA of a full chunk: rows [t0, t0+16) of one head of a [B,T,H,64] bf16
-// tensor into a swizzled (SwDma) plane.  Lane l fills physical 16-byte chunk l%8
-// of row 8m + l/8 with the logical chunk that belongs there (voff[m],
-// loop-invariant per lane; soff = byte offset of the chunk's first row).
-__device__ __forceinline__ void dma_plane(uint16_t* dst, i32x4_t rs, uint32_t soff, const uint32_t (&voff)[2]) {
-#pragma unroll
-    for (int m = 0; m < 2; m++) dma16(dst + 512 * m, rs, voff[m], soff);
-}
-// The same for a chunk of any length L: a partial chunk goes through registers
-// with zeros past the end.
-__device__ __forceinline__ void stage_plane(uint16_t* dst, i32x4_t rs, const bf16_t* src, uint32_t soff,
-                                            const uint32_t (&voff)[2], long rstride, int L, int lane) {
-    if (L == CH) {
-        dma_plane(dst, rs, soff, voff);
-    } else {
-        const int r16 = lane & 15, q = lane >> 4;
-        const bf16_t* s0 = src + soff / 2;
-#pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            uint4 x = make_uint4(0, 0, 0, 0);
-            if (r16 < L) x = *reinterpret_cast<const uint4*>(s0 + r16 * rstride + 32 * hf + 8 * q);
-            st16_sw<SwDma>(dst, r16, 32 * hf + 8 * q, x);
-        }
-    }
-}
 // the value of x, hidden from the optimiser: lane-derived addresses recomputed
 // per tick instead of being hoisted out of the loop into spilled registers
 __device__ __forceinline__ int opaque(int x) {
@@ -227,12 +160,8 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
     auto chunk_off = [&](int xx) { return (uint32_t)(((long)(bb * Tn + (nchunk - 1 - xx) * CH) * H + h) * NK * 2); };
     auto chunk_len = [&](int xx) { return min(CH, Tn - (nchunk - 1 - xx) * CH); };
     const uint32_t tbytes = (uint32_t)((long)gridDim.x * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
-    uint32_t voff[2];
-#pragma unroll
-    for (int m = 0; m < 2; m++) {
-        const int rho = 8 * m + (lane >> 3);
-        voff[m] = (uint32_t)(rho * rstride * 2 + 16 * ((lane & 7) ^ (swz<SwDma>(rho) >> 1)));
-    }
+    uint32_t voff[2];  // this lane's LDS DMA offsets
+    dma_lane_offsets(voff, rstride, lane);
     const bf16_t* const rsrc_src[5] = {r, w, k, a, b};
 
     // ---------------- consumer ----------------

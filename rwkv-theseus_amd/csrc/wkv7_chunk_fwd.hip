@@ -21,42 +21,55 @@
 //    state depends only on the chunk's inputs, so producer p builds the
 //    operands of chunks p, p+4, p+8, ... alone -- no barrier inside -- in four
 //    phases spread over the four ticks before the chunk is consumed; at any
-//    tick the four producers are in four different phases.  A lane holds one
-//    token and 16 keys (X[t = l%16][32 hf + 8q + e], the K=32 operand layout),
-//    so the decay cumsum over tokens is a 16-lane DPP scan, the key
-//    contractions (Aab, ...) take the operands straight from registers, and the products over tokens
-//    read their transposed operand back with ds_read_b64_tr_b16.
+//    tick the four producers are in four different phases, each phase about a
+//    quarter of the work.  A chunk's inputs arrive by LDS DMA three ticks
+//    ahead into the producer's staging planes (no prefetch registers).  A lane
+//    holds one token and 8 keys of a 32-key half (X[t = l%16][32 hf + 8q + e],
+//    the K=32 operand layout), so the decay cumsum over tokens is a 16-lane
+//    DPP scan, the key contractions (Aab, ...) take the operands straight from
+//    registers, and the products over tokens read their transposed operand
+//    back with ds_read_b64_tr_b16.
 //  * Consumers (waves 4-7).  Wave 4+c keeps value rows 16c..16c+15 of the
 //    state in registers (value rows never interact) and advances them by one
-//    chunk per tick from the operands the producers left in a 4-slot LDS ring.
+//    chunk per tick from the operands the producers left in a 5-slot LDS ring
+//    (chunk x in slot x % 5, free from tick x-4 since its last reader was
+//    chunk x-5).
 #include "wkv7_launch.h"
-#include "wkv7_mfma.h"
+#include "wkv7_io.h"
 
 namespace wkv7 {
 namespace {
 
-constexpr int CH = CKPT;  // chunk length
-constexpr int NK = 64;    // head size of this kernel
-constexpr int LDA = 72;   // row stride of [16][64] planes (elements)
-constexpr int LDC = 24;   // row stride of [16][16] planes
+constexpr int CH = CKPT;   // chunk length
+constexpr int NK = 64;     // head size of this kernel
+constexpr int NPROD = 4;   // producer waves (= phases per chunk)
+constexpr int NSLOT = 5;   // operand ring
+
+// [16][64] bf16 planes are unpadded and row-swizzled (pl<>): SwLane for planes
+// the producers write from registers, SwDma for planes filled by LDS DMA;
+// [16][16] matrices use pl16.
+typedef uint16_t Plane[CH * NK];
+typedef uint16_t Mat[2][CH * 16];
 
 // One chunk's operands, as the consumers read them.
 struct Slot {
-    uint16_t P[2][CH * LDA];    // P [t][j] (hi, lo); A~ [t][j] until the producer replaces it
-    uint16_t P2[2][CH * LDA];   // P2 [t][j]; R~ [t][j] until the producer replaces it
-    uint16_t Bh[2][CH * LDA];   // B^ [t][j]
-    uint16_t Kh[2][CH * LDA];   // K^ [t][j]
-    uint16_t Q1T[2][CH * LDC];  // Q'^T [s][t]
-    uint16_t Q2[2][CH * LDC];   // Q2 [t][s]
-    uint16_t V[CH * LDA];       // V [t][i], exact bf16
-    float egL[NK];              // e^{gL} per key
+    Plane P[2];    // P [t][j] (hi, lo); A~ until phases 2-3 replace it
+    Plane P2[2];   // P2 [t][j]; R~ until phase 3 replaces it
+    Plane Bh[2];   // B^ [t][j]
+    Plane Kh[2];   // K^ [t][j]
+    Mat Q1T;       // Q'^T [s][t]
+    Mat Q2;        // Q2 [t][s]
+    Plane V;       // V [t][i], exact bf16 (SwDma)
+    float egL[NK]; // e^{gL} per key
 };
 struct FwdLds {
-    Slot slot[4];
+    Slot slot[NSLOT];
+    Plane raw[NPROD][5];  // producer input staging: r, w, k, a, b (SwDma)
 };
+static_assert(sizeof(FwdLds) <= 160 * 1024, "forward LDS budget");
 
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ void st8(uint16_t* p, uint2 v) { *reinterpret_cast<uint2*>(p) = v; }
+__device__ __forceinline__ uint2 ld8(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
 __device__ __forceinline__ float lo_bf(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 // element e of 4 / 8 packed bf16
@@ -68,7 +81,6 @@ __device__ __forceinline__ float bf_el8(uint4 u, int e) {
     const uint32_t w = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
     return (e & 1) ? hi_bf(w) : lo_bf(w);
 }
-__device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 // X Y^T over the 64 keys for operands in the standard K=32 layout
 // (x[hf] = X[t = l%16][32 hf + 8q .. +7], split into hi / lo)
 __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&xl)[2], const uint4 (&yh)[2],
@@ -82,7 +94,6 @@ __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&
     }
     return acc + c1 + c2;
 }
-
 }  // namespace
 
 __global__ __launch_bounds__(512) void chunk_forward_bf16(
@@ -92,40 +103,91 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     float* __restrict__ sT, float* __restrict__ ckpt) {
     __shared__ FwdLds sm;
     const int bh = blockIdx.x, bb = bh / H, h = bh % H;
-    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, q = lane >> 4, r16 = lane & 15;
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
     const long ncp = ckpt_count(Tn);
     const int nchunk = (Tn + CH - 1) / CH;
-    const bool producer = wv < 4;
+    const bool producer = wv < NPROD;
+    const int pw = wv, cw = wv - NPROD;
+    const long rstride = (long)H * NK;                                  // between consecutive tokens of one head
+    const uint32_t tbytes = (uint32_t)((long)gridDim.x * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
+    auto chunk_off = [&](int cc) { return (uint32_t)(((long)(bb * Tn + cc * CH) * H + h) * NK * 2); };
+    auto chunk_len = [&](int cc) { return min(CH, Tn - cc * CH); };
 
-    // ---------------- producer state (lane: token r16, keys 32 hf + 8q + e) ----------------
-    uint4 pre[6][2];             // prefetched inputs r, w, k, v, a, b
-    float eg[2][8], eng[2][8];   // e^{g}, e^{-g} (phase 0 -> 1)
-    f32x4_t Aab, AabT, Aak, BrbT, BrkT;  // phase 1 -> 2, 3
-    f32x4_t Ti, TiT;             // phase 2 -> 3
-    auto load_chunk = [&](int cc) {
-        const int Lc = min(CH, Tn - cc * CH);
-        const long row = ((long)(bb * Tn + cc * CH + r16) * H + h) * NK + 8 * q;
-        const bf16_t* src[6] = {r, w, k, v, a, b};
-        if (Lc == CH) {  // wave-uniform: full chunks load without predication
+    // ---------------- producer state ----------------
+    uint32_t voff[2];  // this lane's LDS DMA offsets
+    dma_lane_offsets(voff, rstride, lane);
+    const bf16_t* const src5[5] = {r, w, k, a, b};
+    float g1[8];  // cumulative log-decay, keys 32 + 8q + e (phase 0 -> 1)
+    Pk pTiT, pB;  // Ti^T, Brb^T packed (phase 2 -> 3)
+
+    // scaled operands of one key half from the staged inputs and g: written to
+    // the slot (P <- A~, P2 <- R~, B^, K^, e^{gL}); B- and K- (hi, lo) go to the
+    // same half of the staging planes just read (r, k, a, b), for phase 2
+    auto operands = [&](Slot& S, Plane* raw, const float (&g)[8], int hf) {
+        const int c8 = 32 * hf + 8 * q;
+        const uint4 rr = ld16_sw<SwDma>(raw[0], r16, c8), kk = ld16_sw<SwDma>(raw[2], r16, c8);
+        const uint4 aa = ld16_sw<SwDma>(raw[3], r16, c8), bv = ld16_sw<SwDma>(raw[4], r16, c8);
+        float at[8], rt[8], bbv[8], kbv[8], bhv[8], khv[8], el[8];
 #pragma unroll
-            for (int ts = 0; ts < 6; ts++)
+        for (int e = 0; e < 8; e++) {
+            const float eg = __expf(g[e]), eng = __expf(-g[e]);
+            el[e] = row_last(eg);
+            at[e] = bf_el8(aa, e) * row_prev(eg, 1.f);
+            rt[e] = bf_el8(rr, e) * eg;
+            bbv[e] = bf_el8(bv, e) * eng;
+            kbv[e] = bf_el8(kk, e) * eng;
+            bhv[e] = bbv[e] * el[e];
+            khv[e] = kbv[e] * el[e];
+        }
+        uint4 hh, ll;
+        pack8(at, hh, ll);
+        st16_sw<SwLane>(S.P[0], r16, c8, hh);
+        st16_sw<SwLane>(S.P[1], r16, c8, ll);
+        pack8(rt, hh, ll);
+        st16_sw<SwLane>(S.P2[0], r16, c8, hh);
+        st16_sw<SwLane>(S.P2[1], r16, c8, ll);
+        pack8(bbv, hh, ll);
+        st16_sw<SwDma>(raw[0], r16, c8, hh);
+        st16_sw<SwDma>(raw[2], r16, c8, ll);
+        pack8(kbv, hh, ll);
+        st16_sw<SwDma>(raw[3], r16, c8, hh);
+        st16_sw<SwDma>(raw[4], r16, c8, ll);
+        pack8(bhv, hh, ll);
+        st16_sw<SwLane>(S.Bh[0], r16, c8, hh);
+        st16_sw<SwLane>(S.Bh[1], r16, c8, ll);
+        pack8(khv, hh, ll);
+        st16_sw<SwLane>(S.Kh[0], r16, c8, hh);
+        st16_sw<SwLane>(S.Kh[1], r16, c8, ll);
+        if (r16 == 0) {
+            *reinterpret_cast<float4*>(&S.egL[c8]) = make_float4(el[0], el[1], el[2], el[3]);
+            *reinterpret_cast<float4*>(&S.egL[c8 + 4]) = make_float4(el[4], el[5], el[6], el[7]);
+        }
+    };
+    // P = Ti A~ for 16-key tiles [tj0, tj1): tile tj of A~ (read transposed) is
+    // replaced by tile tj of P
+    auto p_tiles = [&](Slot& S, int tj0, int tj1) {
 #pragma unroll
-                for (int hf = 0; hf < 2; hf++) pre[ts][hf] = *reinterpret_cast<const uint4*>(src[ts] + row + 32 * hf);
-        } else {
-#pragma unroll
-            for (int ts = 0; ts < 6; ts++)
-#pragma unroll
-                for (int hf = 0; hf < 2; hf++)
-                    pre[ts][hf] = r16 < Lc ? *reinterpret_cast<const uint4*>(src[ts] + row + 32 * hf) : make_uint4(0, 0, 0, 0);
+        for (int tj = tj0; tj < tj1; tj++) {
+            const Pk pa = {ldtr_sw<SwLane>(S.P[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.P[1], 0, 16 * tj, lane)};
+            const Pk pp = pk(mm16s(pa, pTiT));  // lane: P[t = r16][16tj + 4q + e]
+            st8_sw<SwLane>(S.P[0], r16, 16 * tj + 4 * q, pp.h);
+            st8_sw<SwLane>(S.P[1], r16, 16 * tj + 4 * q, pp.l);
         }
     };
 
     // ---------------- consumer state: S^T tiles St[tj][e] = S[i_own][16tj + 4q + e] ----------------
-    const int cw = wv - 4, i_own = 16 * cw + r16;
+    const int i_own = 16 * cw + r16;
     f32x4_t St[4];
     if (producer) {
-        if (wv < nchunk) load_chunk(wv);
+        // this producer's first chunk (only the last chunk of the sequence can be partial)
+        if (pw < nchunk) {
+#pragma unroll
+            for (int ts = 0; ts < 5; ts++)
+                stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(pw), voff, rstride,
+                            chunk_len(pw), lane);
+        }
     } else {
 #pragma unroll
         for (int tj = 0; tj < 4; tj++) {
@@ -136,81 +198,70 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
         }
         // nothing else is loaded by consumers: drain here so the tick loop never
         // waits on the (in-order) memory counter, which also counts its stores
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        vm_wait0();
     }
 
-    for (int n = -4; n < nchunk; n++) {
+    for (int n = -NPROD; n < nchunk; n++) {
         if (producer) {
-            // the chunk this producer works on at tick n, and its phase; chunk x
-            // owns slot x & 3 from tick x-3 (its last reader was chunk x-4)
-            const int x = n + 1 + ((wv - n - 1) & 3);
-            const int ph = n + 4 - x;
-            Slot& S = sm.slot[x & 3];
-            const int o = r16 * LDA + 4 * q;  // [t][j] position of a 4-key D-layout piece (plus 16 tj)
-            const int o8 = r16 * LDA + 8 * q; // [t][j] position of this lane's 8-key run (plus 32 hf)
+            // the chunk this producer works on at tick n (x = pw mod 4), and its phase
+            const int x = n + 1 + ((pw - n - 1) & 3);
+            const int ph = n + NPROD - x;
             if (x >= 0 && x < nchunk) {  // (prologue ticks have no chunk for some producers)
+                Slot& S = sm.slot[x % NSLOT];
+                Plane* raw = sm.raw[pw];
                 if (ph == 0) {
-                    // ---- phase 0: log-decays, their cumulative sum, e^{+-g} ----
-                    const int L = min(CH, Tn - x * CH);
-#pragma unroll
-                    for (int hf = 0; hf < 2; hf++)
-#pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            float ld = log_decay(bf_el8(pre[1][hf], e));
-                            if (L < CH) ld = r16 < L ? ld : 0.f;  // padded steps keep the state
-                            const float gv = row_prefix_sum(ld);
-                            eg[hf][e] = __expf(gv);
-                            eng[hf][e] = __expf(-gv);
-                        }
-                } else if (ph == 1) {
-                    // ---- phase 1: scaled operands, the chunk matrices over the keys (from
-                    //      registers), and the slot planes P <- A~, P2 <- R~, Bh, Kh, V,
-                    //      e^{gL}; then prefetch this producer's next chunk ----
-                    uint4 ath[2], atl[2], rth[2], rtl[2], bbh[2], bbl[2], kbh[2], kbl[2];
+                    // ---- phase 0: log-decays and their cumulative sum; V by LDS DMA;
+                    //      the operands of keys 0-31 ----
+                    vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
+                    stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(x), voff, rstride, chunk_len(x), lane);
+                    const int L = chunk_len(x);
+                    float g0[8];
 #pragma unroll
                     for (int hf = 0; hf < 2; hf++) {
-                        float el[8];
-#pragma unroll
-                        for (int e = 0; e < 8; e++) el[e] = row_last(eg[hf][e]);
-                        float at[8], rt[8], bbv[8], kbv[8], bhv[8], khv[8];
+                        const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
-                            at[e] = bf_el8(pre[4][hf], e) * row_prev(eg[hf][e], 1.f);
-                            rt[e] = bf_el8(pre[0][hf], e) * eg[hf][e];
-                            bbv[e] = bf_el8(pre[5][hf], e) * eng[hf][e];
-                            kbv[e] = bf_el8(pre[2][hf], e) * eng[hf][e];
-                            bhv[e] = bbv[e] * el[e];
-                            khv[e] = kbv[e] * el[e];
-                        }
-                        pack8(at, ath[hf], atl[hf]);
-                        pack8(rt, rth[hf], rtl[hf]);
-                        pack8(bbv, bbh[hf], bbl[hf]);
-                        pack8(kbv, kbh[hf], kbl[hf]);
-                        uint4 hh, ll;
-                        pack8(bhv, hh, ll);
-                        st16(&S.Bh[0][o8 + 32 * hf], hh);
-                        st16(&S.Bh[1][o8 + 32 * hf], ll);
-                        pack8(khv, hh, ll);
-                        st16(&S.Kh[0][o8 + 32 * hf], hh);
-                        st16(&S.Kh[1][o8 + 32 * hf], ll);
-                        st16(&S.P[0][o8 + 32 * hf], ath[hf]);
-                        st16(&S.P[1][o8 + 32 * hf], atl[hf]);
-                        st16(&S.P2[0][o8 + 32 * hf], rth[hf]);
-                        st16(&S.P2[1][o8 + 32 * hf], rtl[hf]);
-                        st16(&S.V[o8 + 32 * hf], pre[3][hf]);
-                        if (r16 == 0) {
-                            *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q]) = make_float4(el[0], el[1], el[2], el[3]);
-                            *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q + 4]) = make_float4(el[4], el[5], el[6], el[7]);
+                            float ld = log_decay(bf_el8(wr, e));
+                            if (L < CH) ld = r16 < L ? ld : 0.f;  // padded steps keep the state
+                            const float gv = row_prefix_sum(ld);
+                            if (hf) g1[e] = gv; else g0[e] = gv;
                         }
                     }
-                    if (x + 4 < nchunk) load_chunk(x + 4);
-                    Aab = mm_keys8(ath, atl, bbh, bbl);
-                    AabT = mm_keys8(bbh, bbl, ath, atl);
-                    Aak = mm_keys8(ath, atl, kbh, kbl);
-                    BrbT = mm_keys8(bbh, bbl, rth, rtl);
-                    BrkT = mm_keys8(kbh, kbl, rth, rtl);
+                    operands(S, raw, g0, 0);
+                } else if (ph == 1) {
+                    // ---- phase 1: the operands of keys 32-63 ----
+                    operands(S, raw, g1, 1);
                 } else if (ph == 2) {
-                    // ---- phase 2: triangular inverse, Q' = Ti Aak, P^T = A~^T Ti^T ----
+                    // ---- phase 2: the chunk matrices over the keys, triangular inverse,
+                    //      Q' = Ti Aak, Q2; then this producer's next chunk ----
+                    f32x4_t Aab, AabT, Aak, BrbT, BrkT;
+                    {
+                        uint4 ath[2], atl[2], rth[2], rtl[2], bbh[2], bbl[2], kbh[2], kbl[2];
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            const int c8 = 32 * hf + 8 * q;
+                            ath[hf] = ld16_sw<SwLane>(S.P[0], r16, c8);
+                            atl[hf] = ld16_sw<SwLane>(S.P[1], r16, c8);
+                            rth[hf] = ld16_sw<SwLane>(S.P2[0], r16, c8);
+                            rtl[hf] = ld16_sw<SwLane>(S.P2[1], r16, c8);
+                            bbh[hf] = ld16_sw<SwDma>(raw[0], r16, c8);
+                            bbl[hf] = ld16_sw<SwDma>(raw[2], r16, c8);
+                            kbh[hf] = ld16_sw<SwDma>(raw[3], r16, c8);
+                            kbl[hf] = ld16_sw<SwDma>(raw[4], r16, c8);
+                        }
+                        Aab = mm_keys8(ath, atl, bbh, bbl);
+                        AabT = mm_keys8(bbh, bbl, ath, atl);
+                        Aak = mm_keys8(ath, atl, kbh, kbl);
+                        BrbT = mm_keys8(bbh, bbl, rth, rtl);
+                        BrkT = mm_keys8(kbh, kbl, rth, rtl);
+                    }
+                    wave_lds_fence();  // staging reads done before the DMA overwrites them
+                    if (x + NPROD < nchunk) {
+#pragma unroll
+                        for (int ts = 0; ts < 5; ts++)
+                            stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(x + NPROD),
+                                        voff, rstride, chunk_len(x + NPROD), lane);
+                    }
 #pragma unroll
                     for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
                         const int rw = 4 * q + e;
@@ -218,43 +269,42 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                         if (rw >= r16) AabT[e] = 0.f;                // [s][t]: s < t
                         if (rw > r16) BrbT[e] = 0.f, BrkT[e] = 0.f;  // [s][t]: s <= t
                     }
+                    f32x4_t Ti, TiT;
                     tri_inverse(Aab, AabT, lane, Ti, TiT);
-                    const Pk pTiT = pk(TiT);
+                    pTiT = pk(TiT);
+                    pB = pk(BrbT);
                     // Q' (D layout [t][s]) stored as Q'^T [s][t]
                     const Pk pq1 = pk(mm16s(pTiT, pk(Aak)));
-                    st8(&S.Q1T[0][r16 * LDC + 4 * q], pq1.h);
-                    st8(&S.Q1T[1][r16 * LDC + 4 * q], pq1.l);
-                    // P^T per 16-key tile; tile tj of A~ (read transposed) is replaced by tile tj of P
-#pragma unroll
-                    for (int tj = 0; tj < 4; tj++) {
-                        const Pk pa = {ldtr(&S.P[0][16 * tj], LDA, lane), ldtr(&S.P[1][16 * tj], LDA, lane)};
-                        const Pk pp = pk(mm16s(pa, pTiT));  // lane: P[t = r16][16tj + 4q + e]
-                        st8(&S.P[0][o + 16 * tj], pp.h);
-                        st8(&S.P[1][o + 16 * tj], pp.l);
-                    }
+                    st8(&S.Q1T[0][pl16(r16, 4 * q)], pq1.h);
+                    st8(&S.Q1T[1][pl16(r16, 4 * q)], pq1.l);
                     // Q2^T = Brk^T + Q'^T Brb^T  (lane: Q2[t = r16][s = 4q + e])
-                    const Pk q2 = pk(BrkT + mm16s(pq1, pk(BrbT)));
-                    st8(&S.Q2[0][r16 * LDC + 4 * q], q2.h);
-                    st8(&S.Q2[1][r16 * LDC + 4 * q], q2.l);
+                    const Pk q2 = pk(BrkT + mm16s(pq1, pB));
+                    st8(&S.Q2[0][pl16(r16, 4 * q)], q2.h);
+                    st8(&S.Q2[1][pl16(r16, 4 * q)], q2.l);
                 } else {
-                    // ---- phase 3: P2^T = R~^T + P^T Brb^T (R~ read from the P2 plane first) ----
-                    const Pk pB = pk(BrbT);
+                    // ---- phase 3: P = Ti A~, P2^T = R~^T + P^T Brb^T (R~ read from the P2
+                    //      plane first); then V has landed ----
+                    p_tiles(S, 0, 4);
 #pragma unroll
                     for (int tj = 0; tj < 4; tj++) {
-                        const uint2 hh = ld8B(&S.P2[0][o + 16 * tj]), ll = ld8B(&S.P2[1][o + 16 * tj]);
+                        const uint2 hh = ld8_sw<SwLane>(S.P2[0], r16, 16 * tj + 4 * q);
+                        const uint2 ll = ld8_sw<SwLane>(S.P2[1], r16, 16 * tj + 4 * q);
                         f32x4_t rt;
 #pragma unroll
                         for (int e = 0; e < 4; e++) rt[e] = bf_el(hh, e) + bf_el(ll, e);
-                        const Pk pp = {ldtr(&S.P[0][16 * tj], LDA, lane), ldtr(&S.P[1][16 * tj], LDA, lane)};
+                        const Pk pp = {ldtr_sw<SwLane>(S.P[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.P[1], 0, 16 * tj, lane)};
                         const Pk p2 = pk(rt + mm16s(pp, pB));
-                        st8(&S.P2[0][o + 16 * tj], p2.h);
-                        st8(&S.P2[1][o + 16 * tj], p2.l);
+                        st8_sw<SwLane>(S.P2[0], r16, 16 * tj + 4 * q, p2.h);
+                        st8_sw<SwLane>(S.P2[1], r16, 16 * tj + 4 * q, p2.l);
                     }
+                    // V (phase 0) was followed only by the 10 staging DMA ops of phase 2
+                    if (x + NPROD < nchunk) vm_wait10();
+                    else vm_wait0();
                 }
             }
         } else if (n >= 0) {
             // ---------------- consumer: rows i_own through chunk n ----------------
-            const Slot& S = sm.slot[n & 3];
+            const Slot& S = sm.slot[n % NSLOT];
             const int t0 = n * CH, L = min(CH, Tn - t0);
             f32x4_t sa = zero4(), yy = zero4();
 #pragma unroll
@@ -267,8 +317,8 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 }
                 uint4 sh, sl;
                 pack8(sv, sh, sl);
-                const uint4 pah = fragp(S.P[0], LDA, r16, 32 * s, lane), pal = fragp(S.P[1], LDA, r16, 32 * s, lane);
-                const uint4 p2h = fragp(S.P2[0], LDA, r16, 32 * s, lane), p2l = fragp(S.P2[1], LDA, r16, 32 * s, lane);
+                const uint4 pah = fragp_sw<SwLane>(S.P[0], r16, 32 * s, lane), pal = fragp_sw<SwLane>(S.P[1], r16, 32 * s, lane);
+                const uint4 p2h = fragp_sw<SwLane>(S.P2[0], r16, 32 * s, lane), p2l = fragp_sw<SwLane>(S.P2[1], r16, 32 * s, lane);
                 sa = mma32(sa, pah, sh);
                 sa = mma32(sa, pah, sl);
                 sa = mma32(sa, pal, sh);
@@ -277,12 +327,12 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 yy = mma32(yy, p2l, sh);
             }
             // V parts on the K=16 instruction, in their own accumulators
-            const uint2 vfr = ldtr(&S.V[16 * cw], LDA, lane);  // V[s = 4q+e][i_own]
+            const uint2 vfr = ldtr_sw<SwDma>(S.V, 0, 16 * cw, lane);  // V[s = 4q+e][i_own]
             {
-                f32x4_t sv = mma16(zero4(), ldtr(S.Q1T[0], LDC, lane), vfr);
-                sv = mma16(sv, ldtr(S.Q1T[1], LDC, lane), vfr);
-                f32x4_t yv = mma16(zero4(), frag16(S.Q2[0], LDC, 0, 0, lane), vfr);
-                yv = mma16(yv, frag16(S.Q2[1], LDC, 0, 0, lane), vfr);
+                f32x4_t sv = mma16(zero4(), ldtr16(S.Q1T[0], 0, lane), vfr);
+                sv = mma16(sv, ldtr16(S.Q1T[1], 0, lane), vfr);
+                f32x4_t yv = mma16(zero4(), ld8(&S.Q2[0][pl16(r16, 4 * q)]), vfr);
+                yv = mma16(yv, ld8(&S.Q2[1][pl16(r16, 4 * q)]), vfr);
                 sa += sv;
                 yy += yv;
             }
@@ -292,8 +342,8 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             const uint4 bhi = cat(sah, vfr), blo = cat(sal, make_uint2(0, 0));
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
-                const uint4 ah = cat(ldtr(&S.Bh[0][16 * tj], LDA, lane), ldtr(&S.Kh[0][16 * tj], LDA, lane));
-                const uint4 al = cat(ldtr(&S.Bh[1][16 * tj], LDA, lane), ldtr(&S.Kh[1][16 * tj], LDA, lane));
+                const uint4 ah = cat(ldtr_sw<SwLane>(S.Bh[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Kh[0], 0, 16 * tj, lane));
+                const uint4 al = cat(ldtr_sw<SwLane>(S.Bh[1], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Kh[1], 0, 16 * tj, lane));
                 const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
                 f32x4_t acc = St[tj] * f32x4_t{el.x, el.y, el.z, el.w};
                 acc = mma32(acc, ah, bhi);
@@ -301,14 +351,11 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 c1 = mma32(c1, al, bhi);
                 St[tj] = acc + c1;
             }
-            bf16_t* yp = y + ((long)(bb * Tn + t0 + 4 * q) * H + h) * NK + i_own;
-            if (L == CH) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) yp[(long)e * H * NK].bits = f32_to_bf16(yy[e]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (4 * q + e < L) yp[(long)e * H * NK].bits = f32_to_bf16(yy[e]);
+            {  // lane (q, 4m + jj) stores row 4q + jj, values 16c + 4m .. +3 (rows past the end dropped)
+                const int tr = 4 * q + (lane & 3);
+                const uint32_t o = tr < L ? (uint32_t)((((long)(bb * Tn + t0 + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
+                                          : OUT_OF_RANGE;
+                store8(y, tbytes, o, quad_rows_bf16(yy, lane));
             }
             if (ckpt) {
 #pragma unroll
