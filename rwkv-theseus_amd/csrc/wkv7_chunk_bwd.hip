@@ -69,8 +69,10 @@ struct Slot {
 };
 struct BwdLds {
     Slot slot[NPROD];
-    uint16_t Hx[2][NK * NK], S0x[2][NK * NK];    // H', S0 [i][j] (swizzled)
+    uint16_t Hx[2][NK * NK];                     // H' [i][j] (swizzled)
     uint16_t QT[2][NK * LDQ], SAT[2][NK * LDQ];  // Q^T, SA^T [i][t]
+    float dlp[2][4][64 * 4];                     // H side's dw part of a chunk, per key strip (D layout)
+    float dls[4][64 * 4];                        // S side's dw part of the previous chunk
     Plane raw[NPROD][5];                         // producer input staging: r, w, k, a, b
 };
 static_assert(sizeof(BwdLds) <= 160 * 1024, "backward LDS budget");
@@ -132,7 +134,7 @@ __device__ __forceinline__ int opaque(int x) {
 
 }  // namespace
 
-__global__ __launch_bounds__(448) void chunk_backward_bf16(
+__global__ __launch_bounds__(704) void chunk_backward_bf16(
     int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ k, const bf16_t* __restrict__ v, const bf16_t* __restrict__ a,
     const bf16_t* __restrict__ b, const float* __restrict__ ckpt, const bf16_t* __restrict__ dy,
@@ -146,270 +148,318 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
     const long NN = (long)NK * NK;
     const long ncp = ckpt_count(Tn);
     const int nchunk = (Tn + CH - 1) / CH;
-    const bool consumer = wv < 4;
-    const int cw = wv;      // consumer: value-row block / key strip
-    const int pw = wv - 4;  // producer index
+    const bool consumer = wv < 8;
+    const bool hside = wv < 4;  // consumer: owner of H (else the S0 side)
+    const int cw = wv & 3;      // consumer: value-row block / key strip
+    const int pw = wv - 8;      // producer index
     int i_own = 16 * cw + r16;
     int j_own = 16 * cw + r16;
     const int lane0 = lane;
     const long rstride = (long)H * NK;  // between consecutive tokens of one head
 
-    // ---------------- producer (lane: token r16, keys 32 hf + 8q + e) ----------------
-    float gq[2][8];  // cumulative log-decay, phase 0 -> 1
     // processing index xx -> chunk nchunk-1-xx: byte offset of its first row, valid length
     auto chunk_off = [&](int xx) { return (uint32_t)(((long)(bb * Tn + (nchunk - 1 - xx) * CH) * H + h) * NK * 2); };
     auto chunk_len = [&](int xx) { return min(CH, Tn - (nchunk - 1 - xx) * CH); };
     const uint32_t tbytes = (uint32_t)((long)gridDim.x * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
-    uint32_t voff[2];  // this lane's LDS DMA offsets
-    dma_lane_offsets(voff, rstride, lane);
-    const bf16_t* const rsrc_src[5] = {r, w, k, a, b};
-
-    // ---------------- consumer ----------------
-    // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e]; the next chunk's saved state in the same layout
-    f32x4_t Ht[4], S0n[4];
-    float carry = 0.f;  // dlogd carry for key j_own
-    auto load_state = [&](int cc) {
-#pragma unroll
-        for (int tj = 0; tj < 4; tj++) {
-            const float4 s = *reinterpret_cast<const float4*>(ckpt + (bh * ncp + cc) * NN + (long)i_own * NK + 16 * tj + 4 * q);
-            S0n[tj] = f32x4_t{s.x, s.y, s.z, s.w};
-        }
+    const float* const ckh = ckpt + bh * ncp * NN;                       // this head's saved states
+    // byte offset for the 8-byte row piece of a D-layout tile of chunk cc: lane (q, 4m + jj)
+    // stores row 4q + jj, columns 16 cw + 4m .. +3 (rows past the chunk's end: dropped)
+    auto piece_off = [&](int cc) {
+        const int tr = 4 * q + (lane & 3);
+        return tr < min(CH, Tn - cc * CH)
+                   ? (uint32_t)((((long)(bb * Tn + cc * CH + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
+                   : OUT_OF_RANGE;
     };
-    if (consumer) {
-        f32x4_t STt[4];
+    // this side's part of dlogd_t = carry + sum_{s>=t} z_s + sum_{s>t} t2_s over the
+    // chunk (t = 4q + e), times fw_t = d w_t / d logd_t
+    auto dlogd_part = [&](const float (&z)[4], const float (&t2)[4], const float (&fw)[4], float& carry, float (&gw)[4]) {
+        float tot = 0.f;
 #pragma unroll
-        for (int tj = 0; tj < 4; tj++) {
-            const long off = (long)i_own * NK + 16 * tj + 4 * q;
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (dsT) x = *reinterpret_cast<const float4*>(dsT + bh * NN + off);
-            Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
-            const float4 s = *reinterpret_cast<const float4*>(ckpt + (bh * ncp + ncp - 1) * NN + off);
-            STt[tj] = f32x4_t{s.x, s.y, s.z, s.w};
+        for (int e = 0; e < 4; e++) tot += z[e] + t2[e];
+        const float s1 = __shfl(tot, (lane & 15) + 16), s2 = __shfl(tot, (lane & 15) + 32),
+                    s3 = __shfl(tot, (lane & 15) + 48), s0 = __shfl(tot, lane & 15);
+        float run = carry + (q < 1 ? s1 : 0.f) + (q < 2 ? s2 : 0.f) + (q < 3 ? s3 : 0.f);
+#pragma unroll
+        for (int e = 3; e >= 0; e--) {
+            run += z[e];
+            gw[e] = run * fw[e];
+            run += t2[e];
         }
-        load_state(nchunk - 1);
-        // carry_j = sum_i dsT[i][j] S_T[i][j]: 16 rows per lane group, then the 4 waves in order
-        float* part = reinterpret_cast<float*>(&sm.Hx[0][0]);
-#pragma unroll
-        for (int tj = 0; tj < 4; tj++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float p = Ht[tj][e] * STt[tj][e];
-#pragma unroll
-                for (int off = 1; off < 16; off <<= 1) p += __shfl_xor(p, off, 16);
-                if (r16 == 0) part[cw * NK + 16 * tj + 4 * q + e] = p;
-            }
-        // consumers load nothing else before use: drain, so the tick loop never
-        // waits on the (in-order) memory counter for earlier stores
-        vm_wait0();
-    } else if (pw < nchunk) {
-        // the first chunk of each producer; only processing index 0 can be partial,
-        // and its V, dY go into its slot here too so the loop only ever runs DMA
-#pragma unroll
-        for (int ts = 0; ts < 5; ts++)
-            stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(pw), voff, rstride,
-                        chunk_len(pw), lane);
-        if (pw == 0) {
-            stage_plane(sm.slot[0].V, dma_rsrc(v, tbytes), v, chunk_off(0), voff, rstride, chunk_len(0), lane);
-            stage_plane(sm.slot[0].dY, dma_rsrc(dy, tbytes), dy, chunk_off(0), voff, rstride, chunk_len(0), lane);
-        }
-    }
-    lds_barrier();
-    if (consumer) {
-        const float* part = reinterpret_cast<const float*>(&sm.Hx[0][0]);
-        carry = part[j_own] + part[NK + j_own] + part[2 * NK + j_own] + part[3 * NK + j_own];
-    }
-    lds_barrier();
-
-    // Producer work for chunk x (processing order) in phase ph, split into the part
-    // done while consumers run stage B (part 0) and the part done during stage C.
-    f32x4_t Aab, AabT, Aak, Brb, Brk, M2;  // phase 2, part 0 -> part 1
-    auto produce = [&](int x, int ph, int part) {
-        Slot& S = sm.slot[x % NPROD];
-        const Plane* raw = sm.raw[pw];
-        if (ph == 0) {
-            if (part == 0) {
-                // ---- phase 0: log-decays and their cumulative sum ----
-                vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
-                const int L = chunk_len(x);
-#pragma unroll
-                for (int hf = 0; hf < 2; hf++) {
-                    const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        float ld = log_decay(bf_el8(wr, e));
-                        if (L < CH) ld = r16 < L ? ld : 0.f;
-                        gq[hf][e] = row_prefix_sum(ld);
-                    }
-                }
-            }
-        } else if (ph == 1) {
-            // ---- phase 1: scaled operands, g and e^{gL} into the slot (keys 0-31 in
-            //      part 0, 32-63 in part 1); then V, dY of this chunk and the inputs of
-            //      this producer's next chunk by LDS DMA ----
-            auto half = [&](auto hfc) {
-                constexpr int hf = decltype(hfc)::value;
-                const int c8 = 32 * hf + 8 * q;
-                const uint4 rr = ld16_sw<SwDma>(raw[0], r16, c8), kk = ld16_sw<SwDma>(raw[2], r16, c8);
-                const uint4 aa = ld16_sw<SwDma>(raw[3], r16, c8), bv = ld16_sw<SwDma>(raw[4], r16, c8);
-                float at[8], rt[8], bbv[8], kbv[8], el[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float eg = __expf(gq[hf][e]), eng = __expf(-gq[hf][e]);
-                    at[e] = bf_el8(aa, e) * row_prev(eg, 1.f);
-                    rt[e] = bf_el8(rr, e) * eg;
-                    bbv[e] = bf_el8(bv, e) * eng;
-                    kbv[e] = bf_el8(kk, e) * eng;
-                    el[e] = row_last(eg);
-                }
-                uint4 hh, ll;
-                pack8(at, hh, ll);
-                st16_sw<SwLane>(S.At[0], r16, c8, hh);
-                st16_sw<SwLane>(S.At[1], r16, c8, ll);
-                pack8(rt, hh, ll);
-                st16_sw<SwLane>(S.Rt[0], r16, c8, hh);
-                st16_sw<SwLane>(S.Rt[1], r16, c8, ll);
-                pack8(bbv, hh, ll);
-                st16_sw<SwLane>(S.Bb[0], r16, c8, hh);
-                st16_sw<SwLane>(S.Bb[1], r16, c8, ll);
-                pack8(kbv, hh, ll);
-                st16_sw<SwLane>(S.Kb[0], r16, c8, hh);
-                st16_sw<SwLane>(S.Kb[1], r16, c8, ll);
-                float* gp_ = &S.g[r16 * LDG + 32 * hf + 8 * q];
-                *reinterpret_cast<float4*>(gp_) = make_float4(gq[hf][0], gq[hf][1], gq[hf][2], gq[hf][3]);
-                *reinterpret_cast<float4*>(gp_ + 4) = make_float4(gq[hf][4], gq[hf][5], gq[hf][6], gq[hf][7]);
-                if (r16 == 0) {
-                    *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q]) = make_float4(el[0], el[1], el[2], el[3]);
-                    *reinterpret_cast<float4*>(&S.egL[32 * hf + 8 * q + 4]) = make_float4(el[4], el[5], el[6], el[7]);
-                }
-            };
-            if (part == 0) {
-                half(std::integral_constant<int, 0>{});
-            } else {
-                half(std::integral_constant<int, 1>{});
-                if (x > 0) {  // (chunk 0's V, dY were staged before the loop)
-                    dma_plane(S.V, dma_rsrc(v, tbytes), chunk_off(x), voff);
-                    dma_plane(S.dY, dma_rsrc(dy, tbytes), chunk_off(x), voff);
-                }
-                wave_lds_fence();  // staging reads done before the DMA overwrites it
-                if (x + NPROD < nchunk) {
-#pragma unroll
-                    for (int ts = 0; ts < 5; ts++)
-                        dma_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
-                }
-            }
-        } else if (part == 0) {
-            // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
-            // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
-            if (x + NPROD < nchunk) vm_wait10();
-            else vm_wait0();
-            auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
-#pragma unroll
-                for (int hf = 0; hf < 2; hf++) {
-                    xh[hf] = ld16_sw<SwLane>(pl2[0], r16, 32 * hf + 8 * q);
-                    xl[hf] = ld16_sw<SwLane>(pl2[1], r16, 32 * hf + 8 * q);
-                }
-            };
-            {
-                uint4 ath[2], atl[2], xh[2], xl[2];
-                rd(S.At, ath, atl);
-                rd(S.Bb, xh, xl);
-                Aab = mm_keys8(ath, atl, xh, xl);
-                AabT = mm_keys8(xh, xl, ath, atl);
-                rd(S.Kb, xh, xl);
-                Aak = mm_keys8(ath, atl, xh, xl);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            {
-                uint4 rth[2], rtl[2], xh[2], xl[2];
-                rd(S.Rt, rth, rtl);
-                rd(S.Bb, xh, xl);
-                Brb = mm_keys8(rth, rtl, xh, xl);
-                rd(S.Kb, xh, xl);
-                Brk = mm_keys8(rth, rtl, xh, xl);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            {
-                uint4 vv[2], yy[2];
-#pragma unroll
-                for (int hf = 0; hf < 2; hf++) {
-                    vv[hf] = ld16_sw<SwDma>(S.V, r16, 32 * hf + 8 * q);
-                    yy[hf] = ld16_sw<SwDma>(S.dY, r16, 32 * hf + 8 * q);
-                }
-                M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
-                const int rw = 4 * q + e;
-                if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;  // [t][s]: s < t
-                if (rw >= r16) AabT[e] = 0.f;               // [s][t]: s < t
-                if (r16 > rw) Brb[e] = 0.f, Brk[e] = 0.f;   // [t][s]: s <= t
-                if (r16 < rw) M2[e] = 0.f;                  // [t][s]: s >= t
-            }
-            f32x4_t Ti, TiT;
-            tri_inverse(Aab, AabT, lane, Ti, TiT);
-            put_mat(S.Ti, Ti, lane);
-            put_mat(S.Aak, Aak, lane);
-            put_mat(S.Brb, Brb, lane);
-            put_mat(S.Brk, Brk, lane);
-            put_mat(S.M2, M2, lane);
-        }
+        carry += ((s0 + s1) + s2) + s3;
     };
-
-    for (int n = -NPROD; n < nchunk; n++) {
+    // the per-lane quantities of stage C that depend on the slot only:
+    // [A~; R~] and [B-; K-] strips as K=32 B operands, g_t and g_{t-1} (t = 4q + e)
+    struct Strip {
+        uint4 arh, arl, bkh, bkl;
+        float gv[4], gp[4], fw[4];
+    };
+    auto strip = [&](const Slot& S) {
+        Strip st;
+        st.arh = cat(ldtr_sw<SwLane>(S.At[0], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Rt[0], 0, 16 * cw, lane));
+        st.arl = cat(ldtr_sw<SwLane>(S.At[1], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Rt[1], 0, 16 * cw, lane));
+        st.bkh = cat(ldtr_sw<SwLane>(S.Bb[0], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[0], 0, 16 * cw, lane));
+        st.bkl = cat(ldtr_sw<SwLane>(S.Bb[1], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[1], 0, 16 * cw, lane));
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 4 * q + e;
+            st.gv[e] = S.g[t * LDG + j_own];
+            st.gp[e] = t > 0 ? S.g[(t - 1) * LDG + j_own] : 0.f;
+            const float sg = (st.gp[e] - st.gv[e]) * (1.f / DECAY_SCALE);  // sigmoid(w_t)
+            st.fw[e] = -DECAY_SCALE * sg * (1.f - sg);
+        }
+        return st;
+    };
+    auto new_tick = [&]() {  // lane-derived values, recomputed so they are not held across the loop
         lane = opaque(lane0);
         q = lane >> 4;
         r16 = lane & 15;
         i_own = 16 * cw + r16;
         j_own = i_own;
-        // the chunk a producer works on at tick n (x = pw mod 3, so slot x % 3 is its
-        // own) and its phase; prologue ticks have no chunk for some producers
-        const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
-        const int ph = n + NPROD - x;
-        const bool pact = !consumer && x >= 0 && x < nchunk;
-        if (pact) produce(x, ph, 0);
-        // ================= consumers, stage B (chunk n, rows i_own) =================
-        if (consumer && n >= 0) {
-            const Slot& S = sm.slot[n % NPROD];
-            const int c = nchunk - 1 - n, t0 = c * CH, L = min(CH, Tn - t0);
-            f32x4_t S0r[4], Hp[4];
+    };
+
+    // The three roles run separate tick loops with the same barriers, so that
+    // registers and memory-counter waits are allocated per role.
+    if (!consumer) {
+        // ======================= producers (lane: token r16, keys 32 hf + 8q + e) =======================
+        float gq[2][8];  // cumulative log-decay, phase 0 -> 1
+        // scaled operands of one key half (lane: token r16, keys 32 hf + 8q + e), split
+        auto operands = [&](const Plane* raw, const float (&g)[8], int hf, uint4 (&o)[8]) {
+            const int c8 = 32 * hf + 8 * q;
+            const uint4 rr = ld16_sw<SwDma>(raw[0], r16, c8), kk = ld16_sw<SwDma>(raw[2], r16, c8);
+            const uint4 aa = ld16_sw<SwDma>(raw[3], r16, c8), bv = ld16_sw<SwDma>(raw[4], r16, c8);
+            float at[8], rt[8], bbv[8], kbv[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float eg = __expf(g[e]), eng = __expf(-g[e]);
+                at[e] = bf_el8(aa, e) * row_prev(eg, 1.f);
+                rt[e] = bf_el8(rr, e) * eg;
+                bbv[e] = bf_el8(bv, e) * eng;
+                kbv[e] = bf_el8(kk, e) * eng;
+            }
+            pack8(at, o[0], o[1]);
+            pack8(rt, o[2], o[3]);
+            pack8(bbv, o[4], o[5]);
+            pack8(kbv, o[6], o[7]);
+        };
+        auto put_operands = [&](Slot& S, int hf, const uint4 (&o)[8]) {
+            const int c8 = 32 * hf + 8 * q;
+            st16_sw<SwLane>(S.At[0], r16, c8, o[0]);
+            st16_sw<SwLane>(S.At[1], r16, c8, o[1]);
+            st16_sw<SwLane>(S.Rt[0], r16, c8, o[2]);
+            st16_sw<SwLane>(S.Rt[1], r16, c8, o[3]);
+            st16_sw<SwLane>(S.Bb[0], r16, c8, o[4]);
+            st16_sw<SwLane>(S.Bb[1], r16, c8, o[5]);
+            st16_sw<SwLane>(S.Kb[0], r16, c8, o[6]);
+            st16_sw<SwLane>(S.Kb[1], r16, c8, o[7]);
+            float* gp_ = &S.g[r16 * LDG + c8];
+            const float* g = gq[hf];
+            *reinterpret_cast<float4*>(gp_) = make_float4(g[0], g[1], g[2], g[3]);
+            *reinterpret_cast<float4*>(gp_ + 4) = make_float4(g[4], g[5], g[6], g[7]);
+            if (r16 == CH - 1) {  // e^{gL}: the last token's e^{g} (padded steps repeat g_L)
+                *reinterpret_cast<float4*>(&S.egL[c8]) = make_float4(__expf(g[0]), __expf(g[1]), __expf(g[2]), __expf(g[3]));
+                *reinterpret_cast<float4*>(&S.egL[c8 + 4]) = make_float4(__expf(g[4]), __expf(g[5]), __expf(g[6]), __expf(g[7]));
+            }
+        };
+        uint32_t voff[2];  // this lane's LDS DMA offsets
+        dma_lane_offsets(voff, rstride, lane);
+        const bf16_t* const rsrc_src[5] = {r, w, k, a, b};
+        if (pw < nchunk) {
+            // the first chunk of each producer; only processing index 0 can be partial,
+            // and its V, dY go into its slot here too so the loop only ever runs DMA
+#pragma unroll
+            for (int ts = 0; ts < 5; ts++)
+                stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(pw), voff, rstride,
+                            chunk_len(pw), lane);
+            if (pw == 0) {
+                stage_plane(sm.slot[0].V, dma_rsrc(v, tbytes), v, chunk_off(0), voff, rstride, chunk_len(0), lane);
+                stage_plane(sm.slot[0].dY, dma_rsrc(dy, tbytes), dy, chunk_off(0), voff, rstride, chunk_len(0), lane);
+            }
+        }
+        lds_barrier();
+        lds_barrier();
+        // Producer work for chunk x (processing order) in phase ph, split into the part
+        // done while consumers run stage B (part 0) and the part done during stage C.
+        f32x4_t Aab, AabT, Aak, Brb, Brk, M2;  // phase 2, part 0 -> part 1
+        auto produce = [&](int x, int ph, int part) {
+            Slot& S = sm.slot[x % NPROD];
+            const Plane* raw = sm.raw[pw];
+            if (ph == 0) {
+                if (part == 0) {
+                    // ---- phase 0: log-decays and their cumulative sum ----
+                    vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
+                    const int L = chunk_len(x);
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) {
+                        const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            float ld = log_decay(bf_el8(wr, e));
+                            if (L < CH) ld = r16 < L ? ld : 0.f;
+                            gq[hf][e] = row_prefix_sum(ld);
+                        }
+                    }
+                }
+            } else if (ph == 1) {
+                // ---- phase 1: the slot's A~, R~, B-, K-, g and e^{gL} (keys 0-31 in part 0,
+                //      32-63 in part 1); then V, dY of this chunk and the inputs of this
+                //      producer's next chunk by LDS DMA ----
+                if (part == 0) {
+                    uint4 o[8];
+                    operands(raw, gq[0], 0, o);
+                    put_operands(S, 0, o);
+                } else {
+                    uint4 o[8];
+                    operands(raw, gq[1], 1, o);
+                    put_operands(S, 1, o);
+                    dma_lane_offsets(voff, rstride, lane);
+                    if (x > 0) {  // (chunk 0's V, dY were staged before the loop)
+                        dma_plane(S.V, dma_rsrc(v, tbytes), chunk_off(x), voff);
+                        dma_plane(S.dY, dma_rsrc(dy, tbytes), chunk_off(x), voff);
+                    }
+                    wave_lds_fence();  // staging reads done before the DMA overwrites it
+                    if (x + NPROD < nchunk) {
+#pragma unroll
+                        for (int ts = 0; ts < 5; ts++)
+                            dma_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
+                    }
+                }
+            } else if (part == 0) {
+                // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
+                // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
+                if (x + NPROD < nchunk) vm_wait10();
+                else vm_wait0();
+                auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) {
+                        xh[hf] = ld16_sw<SwLane>(pl2[0], r16, 32 * hf + 8 * q);
+                        xl[hf] = ld16_sw<SwLane>(pl2[1], r16, 32 * hf + 8 * q);
+                    }
+                };
+                {
+                    uint4 ath[2], atl[2], xh[2], xl[2];
+                    rd(S.At, ath, atl);
+                    rd(S.Bb, xh, xl);
+                    Aab = mm_keys8(ath, atl, xh, xl);
+                    AabT = mm_keys8(xh, xl, ath, atl);
+                    rd(S.Kb, xh, xl);
+                    Aak = mm_keys8(ath, atl, xh, xl);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                {
+                    uint4 rth[2], rtl[2], xh[2], xl[2];
+                    rd(S.Rt, rth, rtl);
+                    rd(S.Bb, xh, xl);
+                    Brb = mm_keys8(rth, rtl, xh, xl);
+                    rd(S.Kb, xh, xl);
+                    Brk = mm_keys8(rth, rtl, xh, xl);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                {
+                    uint4 vv[2], yy[2];
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) {
+                        vv[hf] = ld16_sw<SwDma>(S.V, r16, 32 * hf + 8 * q);
+                        yy[hf] = ld16_sw<SwDma>(S.dY, r16, 32 * hf + 8 * q);
+                    }
+                    M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
+                    const int rw = 4 * q + e;
+                    if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;  // [t][s]: s < t
+                    if (rw >= r16) AabT[e] = 0.f;               // [s][t]: s < t
+                    if (r16 > rw) Brb[e] = 0.f, Brk[e] = 0.f;   // [t][s]: s <= t
+                    if (r16 < rw) M2[e] = 0.f;                  // [t][s]: s >= t
+                }
+                f32x4_t Ti, TiT;
+                tri_inverse(Aab, AabT, lane, Ti, TiT);
+                put_mat(S.Ti, Ti, lane);
+                put_mat(S.Aak, Aak, lane);
+                put_mat(S.Brb, Brb, lane);
+                put_mat(S.Brk, Brk, lane);
+                put_mat(S.M2, M2, lane);
+            }
+        };
+
+        for (int n = -NPROD; n < nchunk; n++) {
+            new_tick();
+            // the chunk this producer works on at tick n (x = pw mod 3, so slot x % 3 is
+            // its own) and its phase; prologue and final ticks have no chunk for some
+            const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
+            const int ph = n + NPROD - x;
+            const bool pact = x >= 0 && x < nchunk;
+            if (pact) produce(x, ph, 0);
+            lds_barrier();
+            if (pact) produce(x, ph, 1);
+            lds_barrier();
+        }
+    } else if (hside) {
+        // ======================= H side: rows i_own of H and dV; key strip j_own: dK, dB =======================
+        f32x4_t Ht[4];      // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e] (H' within a tick)
+        float carry = 0.f;  // this side's part of the dlogd carry for key j_own
+        {
+            f32x4_t STt[4];
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
-                S0r[tj] = S0n[tj];
-                const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
-                Hp[tj] = Ht[tj] * f32x4_t{el.x, el.y, el.z, el.w};
+                const long off = (long)i_own * NK + 16 * tj + 4 * q;
+                float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (dsT) x = *reinterpret_cast<const float4*>(dsT + bh * NN + off);
+                Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
+                const float4 st = *reinterpret_cast<const float4*>(ckh + (ncp - 1) * NN + off);
+                STt[tj] = f32x4_t{st.x, st.y, st.z, st.w};
             }
-            const uint2 vfr = ldtr_sw<SwDma>(S.V, 0, 16 * cw, lane);   // V[s = 4q+e][i_own]
-            const uint2 dyf = ldtr_sw<SwDma>(S.dY, 0, 16 * cw, lane);  // dY[s = 4q+e][i_own]
-            // X1 = A~ S0^T + Aak V ; X2 = B- H'^T + Brb^T dY ; dV0 = K- H'^T + Brk^T dY
-            f32x4_t x1 = zero4(), x2 = zero4(), dv0 = zero4();
+            // carry_j = sum_i dsT[i][j] S_T[i][j]: 16 rows per lane group, then the 4 waves in order
+            float* part = reinterpret_cast<float*>(&sm.Hx[0][0]);
 #pragma unroll
-            for (int s = 0; s < 2; s++) {
-                float hv[8], sv[8];
+            for (int tj = 0; tj < 4; tj++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    hv[e] = Hp[2 * s][e];
-                    hv[4 + e] = Hp[2 * s + 1][e];
-                    sv[e] = S0r[2 * s][e];
-                    sv[4 + e] = S0r[2 * s + 1][e];
+                    float p = Ht[tj][e] * STt[tj][e];
+#pragma unroll
+                    for (int off = 1; off < 16; off <<= 1) p += __shfl_xor(p, off, 16);
+                    if (r16 == 0) part[cw * NK + 16 * tj + 4 * q + e] = p;
                 }
-                uint4 hbh, hbl, sbh, sbl;
+            vm_wait0();  // nothing is loaded in the loop: the counter then only tracks stores
+        }
+        lds_barrier();
+        {
+            const float* part = reinterpret_cast<const float*>(&sm.Hx[0][0]);
+            carry = part[j_own] + part[NK + j_own] + part[2 * NK + j_own] + part[3 * NK + j_own];
+        }
+        lds_barrier();
+        for (int n = -NPROD; n < 0; n++) {
+            lds_barrier();
+            lds_barrier();
+        }
+        for (int n = 0; n < nchunk; n++) {
+            new_tick();
+            Slot& S = sm.slot[n % NPROD];
+            const int c = nchunk - 1 - n;
+            // ---- stage B: X2 = B- H'^T + Brb^T dY ; Q = Ti^T X2 ; publish H' and Q^T rows ----
+            const uint2 dyf = ldtr_sw<SwDma>(S.dY, 0, 16 * cw, lane);  // dY[s = 4q+e][i_own]
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++) {
+                const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
+                Ht[tj] = Ht[tj] * f32x4_t{el.x, el.y, el.z, el.w};  // H' = H diag(e^{gL})
+            }
+            f32x4_t x2 = zero4(), dv0 = zero4();  // dv0 = K- H'^T (the rest of dV in stage C)
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                float hv[8];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    hv[e] = Ht[2 * s][e];
+                    hv[4 + e] = Ht[2 * s + 1][e];
+                }
+                uint4 hbh, hbl;
                 pack8(hv, hbh, hbl);
-                pack8(sv, sbh, sbl);
-                // the halves are this lane's 4-key pieces of H' and S0 (tiles 2s, 2s+1):
-                // publish them for stage C now (no second split)
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
                     const int col = 16 * (2 * s + u) + 4 * q;
                     st8_sw<SwLane>(sm.Hx[0], i_own, col, u ? make_uint2(hbh.z, hbh.w) : make_uint2(hbh.x, hbh.y));
                     st8_sw<SwLane>(sm.Hx[1], i_own, col, u ? make_uint2(hbl.z, hbl.w) : make_uint2(hbl.x, hbl.y));
-                    st8_sw<SwLane>(sm.S0x[0], i_own, col, u ? make_uint2(sbh.z, sbh.w) : make_uint2(sbh.x, sbh.y));
-                    st8_sw<SwLane>(sm.S0x[1], i_own, col, u ? make_uint2(sbl.z, sbl.w) : make_uint2(sbl.x, sbl.y));
                 }
-                const uint4 ah = fragp_sw<SwLane>(S.At[0], r16, 32 * s, lane), al = fragp_sw<SwLane>(S.At[1], r16, 32 * s, lane);
-                x1 = mma32(x1, ah, sbh);
-                x1 = mma32(x1, ah, sbl);
-                x1 = mma32(x1, al, sbh);
                 const uint4 bh_ = fragp_sw<SwLane>(S.Bb[0], r16, 32 * s, lane), bl_ = fragp_sw<SwLane>(S.Bb[1], r16, 32 * s, lane);
                 x2 = mma32(x2, bh_, hbh);
                 x2 = mma32(x2, bh_, hbl);
@@ -419,178 +469,238 @@ __global__ __launch_bounds__(448) void chunk_backward_bf16(
                 dv0 = mma32(dv0, kh, hbl);
                 dv0 = mma32(dv0, kl, hbh);
             }
+            Pk pq;  // Q for rows i_own, as the B operand [t][i]
             {
-                f32x4_t c1 = zero4(), c2 = zero4(), c3 = zero4();
-                const Pk aak = mat_n(S.Aak, lane), brbT = mat_t(S.Brb, lane), brkT = mat_t(S.Brk, lane);
-                c1 = mma16(c1, aak.h, vfr);
-                c1 = mma16(c1, aak.l, vfr);
-                c2 = mma16(c2, brbT.h, dyf);
+                const Pk brbT = mat_t(S.Brb, lane);
+                f32x4_t c2 = mma16(zero4(), brbT.h, dyf);
                 c2 = mma16(c2, brbT.l, dyf);
-                c3 = mma16(c3, brkT.h, dyf);
-                c3 = mma16(c3, brkT.l, dyf);
-                x1 += c1;
-                x2 += c2;
-                dv0 += c3;
+                pq = pk(mm16s(mat_t(S.Ti, lane), pk(x2 + c2)));  // Q = Ti^T X2
+                st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
+                st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
             }
-            const f32x4_t sa = mm16s(mat_n(S.Ti, lane), pk(x1));   // SA = Ti X1
-            const f32x4_t qq = mm16s(mat_t(S.Ti, lane), pk(x2));   // Q  = Ti^T X2
-            const Pk pq = pk(qq), psa = pk(sa);
-            const f32x4_t dvv = dv0 + mm16s(mat_t(S.Aak, lane), pq);
-            // publish this block's rows for stage C
-            st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
-            st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
-            st8(&sm.SAT[0][pl16(i_own, 4 * q)], psa.h);
-            st8(&sm.SAT[1][pl16(i_own, 4 * q)], psa.l);
+            lds_barrier();
+            // ---- stage C: key strip j_own of dK, dB (all value rows, fixed order); dV rows i_own; new H ----
+            const Strip st = strip(S);
+            f32x4_t xm = zero4(), m1T = zero4(), n1T = zero4(), gK = zero4(), gB = zero4();
+            {
+                f32x4_t cn = zero4(), cb = zero4();
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);   // V[t][i], exact
+                    const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);  // dY[t][i], exact
+                    const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
+                    const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
+                    const uint4 hh = rows_tr_sw(sm.Hx[0], s, 16 * cw, lane), hl = rows_tr_sw(sm.Hx[1], s, 16 * cw, lane);
+                    xm = mma32(xm, ya, sh);  // dY SA^T        [t][s]
+                    xm = mma32(xm, ya, sl);
+                    m1T = mma32(m1T, qh, va);  // Q V^T = M1^T  [s][t]
+                    m1T = mma32(m1T, ql, va);
+                    n1T = mma32(n1T, qh, sh);  // Q SA^T = N1^T [s][t]
+                    n1T = mma32(n1T, qh, sl);
+                    cn = mma32(cn, ql, sh);
+                    gK = mma32(gK, va, hh);  // V H'
+                    gK = mma32(gK, va, hl);
+                    gB = mma32(gB, sh, hh);  // SA H'
+                    gB = mma32(gB, sh, hl);
+                    cb = mma32(cb, sl, hh);
+                }
+                n1T += cn;
+                gB += cb;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
+                const int rw = 4 * q + e;
+                if (r16 > rw) xm[e] = 0.f;                  // XM[t][s]: keep s <= t
+                if (rw <= r16) m1T[e] = 0.f, n1T[e] = 0.f;  // M1^T[s][t], N1^T[s][t]: keep s > t
+            }
+            const Pk m2n = mat_n(S.M2, lane), pm1 = pk(m1T), pn1 = pk(n1T), pxm = pk(xm);
+            const f32x4_t cK = mm32s(cat(pm1.h, m2n.h), cat(pm1.l, m2n.l), st.arh, st.arl);  // [triu_s(M1) | triu(M2)]
+            const f32x4_t cB = mm32s(cat(pn1.h, pxm.h), cat(pn1.l, pxm.l), st.arh, st.arl);  // [triu_s(N1) | triu(SA dY^T)]
+            float gk_[4], gb_[4], z[4], t2[4], gw_[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float uK = gK[e] + cK[e], uB = gB[e] + cB[e];
+                const float eng = __expf(-st.gv[e]);
+                gk_[e] = eng * uK;
+                gb_[e] = eng * uB;
+                const float Bb_ = bf_el8(st.bkh, e) + bf_el8(st.bkl, e);
+                const float Kb_ = bf_el8(st.bkh, 4 + e) + bf_el8(st.bkl, 4 + e);
+                z[e] = -(Bb_ * uB + Kb_ * uK);
+                t2[e] = 0.f;
+            }
+            const uint32_t o = piece_off(c);
+            store8(dk, tbytes, o, quad_rows_bf16(f32x4_t{gk_[0], gk_[1], gk_[2], gk_[3]}, lane));
+            store8(db, tbytes, o, quad_rows_bf16(f32x4_t{gb_[0], gb_[1], gb_[2], gb_[3]}, lane));
+            dlogd_part(z, t2, st.fw, carry, gw_);
+            *reinterpret_cast<float4*>(&sm.dlp[n & 1][cw][4 * lane]) = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
+            {  // dV = K- H'^T + Brk^T dY + Aak^T Q
+                const Pk brkT = mat_t(S.Brk, lane);
+                f32x4_t c3 = mma16(zero4(), brkT.h, dyf);
+                c3 = mma16(c3, brkT.l, dyf);
+                const f32x4_t dvv = dv0 + c3 + mm16s(mat_t(S.Aak, lane), pq);
+                store8(dv, tbytes, o, quad_rows_bf16(dvv, lane));
+            }
             // H_0^T = H'^T + [A~^T R~^T] [Q; dY]
             const uint4 bhi = cat(pq.h, dyf), blo = cat(pq.l, make_uint2(0, 0));
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
                 const uint4 ah = cat(ldtr_sw<SwLane>(S.At[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[0], 0, 16 * tj, lane));
                 const uint4 al = cat(ldtr_sw<SwLane>(S.At[1], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[1], 0, 16 * tj, lane));
-                f32x4_t acc = mma32(Hp[tj], ah, bhi);
+                f32x4_t acc = mma32(Ht[tj], ah, bhi);
                 f32x4_t c1 = mma32(zero4(), ah, blo);
                 c1 = mma32(c1, al, bhi);
                 Ht[tj] = acc + c1;
             }
-            {  // lane (q, 4m + jj) stores row 4q + jj, values 16c + 4m .. +3
-                const int tr = 4 * q + (lane & 3);
-                const uint32_t o = tr < L ? (uint32_t)((((long)(bb * Tn + t0 + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
-                                          : OUT_OF_RANGE;
-                store8(dv, tbytes, o, quad_rows_bf16(dvv, lane));
-            }
+            lds_barrier();
         }
-        lds_barrier();
-        if (consumer) {
-            // ================= consumers, stage C (chunk n, key strip j_own) =================
-            if (n >= 0) {
-                Slot& S = sm.slot[n % NPROD];
-                const int c = nchunk - 1 - n, t0 = c * CH, L = min(CH, Tn - t0);
-                if (c > 0) load_state(c - 1);  // saved state of the next chunk processed
-                // contractions over all value rows i (each fragment read once)
-                f32x4_t m1 = zero4(), n1 = zero4(), xm = zero4(), gK = zero4(), gB = zero4(), gR = zero4(), gA = zero4();
-                {
-                    f32x4_t c1 = zero4(), c2 = zero4(), c3 = zero4();
-#pragma unroll
-                    for (int s = 0; s < 2; s++) {
-                        const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);    // V[t][i], exact
-                        const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);   // dY[t][i], exact
-                        const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
-                        const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
-                        const uint4 hh = rows_tr_sw(sm.Hx[0], s, 16 * cw, lane), hl = rows_tr_sw(sm.Hx[1], s, 16 * cw, lane);
-                        const uint4 oh = rows_tr_sw(sm.S0x[0], s, 16 * cw, lane), ol = rows_tr_sw(sm.S0x[1], s, 16 * cw, lane);
-                        m1 = mma32(m1, va, qh);   // V Q^T
-                        m1 = mma32(m1, va, ql);
-                        gK = mma32(gK, va, hh);   // V H'
-                        gK = mma32(gK, va, hl);
-                        xm = mma32(xm, ya, sh);   // dY SA^T
-                        xm = mma32(xm, ya, sl);
-                        gR = mma32(gR, ya, oh);   // dY S0
-                        gR = mma32(gR, ya, ol);
-                        n1 = mma32(n1, sh, qh);   // SA Q^T
-                        n1 = mma32(n1, sh, ql);
-                        c1 = mma32(c1, sl, qh);
-                        gB = mma32(gB, sh, hh);   // SA H'
-                        gB = mma32(gB, sh, hl);
-                        c2 = mma32(c2, sl, hh);
-                        gA = mma32(gA, qh, oh);   // Q S0
-                        gA = mma32(gA, qh, ol);
-                        c3 = mma32(c3, ql, oh);
-                    }
-                    n1 += c1;
-                    gB += c2;
-                    gA += c3;
-                }
-#pragma unroll
-                for (int e = 0; e < 4; e++) {  // D layout: row t = 4q+e, column s = r16
-                    const int t = 4 * q + e;
-                    if (r16 <= t) m1[e] = 0.f, n1[e] = 0.f;  // keep s > t
-                    if (r16 > t) xm[e] = 0.f;                // keep s <= t
-                }
-                // [A~; R~] and [B-; K-] strips as K=32 B operands (also their values in D layout)
-                const uint4 arh = cat(ldtr_sw<SwLane>(S.At[0], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Rt[0], 0, 16 * cw, lane));
-                const uint4 arl = cat(ldtr_sw<SwLane>(S.At[1], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Rt[1], 0, 16 * cw, lane));
-                const uint4 bkh = cat(ldtr_sw<SwLane>(S.Bb[0], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[0], 0, 16 * cw, lane));
-                const uint4 bkl = cat(ldtr_sw<SwLane>(S.Bb[1], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[1], 0, 16 * cw, lane));
-                // the 16x16 masked products go through this wave's scratch matrix (in the
-                // slot's Ti/Aak/Brb/Brk area, dead after stage B) to get both orientations
-                Mat& P = cw == 0 ? S.Ti : cw == 1 ? S.Aak : cw == 2 ? S.Brb : S.Brk;
-                const Pk m2n = mat_n(S.M2, lane), m2t = mat_t(S.M2, lane);
-                put_mat(P, m1, lane);
-                wave_lds_fence();
-                const Pk m1n = mat_n(P, lane), m1t = mat_t(P, lane);
-                wave_lds_fence();
-                const f32x4_t cK = mm32s(cat(m1n.h, m2n.h), cat(m1n.l, m2n.l), arh, arl);  // [triu_s(M1) | triu(M2)]
-                put_mat(P, xm, lane);
-                wave_lds_fence();
-                const Pk xmn = mat_n(P, lane), xmt = mat_t(P, lane);
-                wave_lds_fence();
-                const f32x4_t cR = mm32s(cat(xmn.h, m2t.h), cat(xmn.l, m2t.l), bkh, bkl);  // [tril(dY SA^T) | tril(dY V^T)]
-                put_mat(P, n1, lane);
-                wave_lds_fence();
-                const Pk n1n = mat_n(P, lane), n1t = mat_t(P, lane);
-                const f32x4_t cB = mm32s(cat(n1n.h, xmt.h), cat(n1n.l, xmt.l), arh, arl);  // [triu_s(N1) | triu(SA dY^T)]
-                const f32x4_t cA = mm32s(cat(n1t.h, m1t.h), cat(n1t.l, m1t.l), bkh, bkl);  // [tril_s(Q SA^T) | tril_s(Q V^T)]
-                float gk_[4], gb_[4], gr_[4], ga_[4], gw_[4], z[4], t2[4], fw[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int t = 4 * q + e;
-                    const float gv = S.g[t * LDG + j_own];
-                    const float gp = t > 0 ? S.g[(t - 1) * LDG + j_own] : 0.f;
-                    const float uK = gK[e] + cK[e], uB = gB[e] + cB[e], uR = gR[e] + cR[e], uA = gA[e] + cA[e];
-                    const float eng = __expf(-gv);
-                    gk_[e] = eng * uK;
-                    gb_[e] = eng * uB;
-                    gr_[e] = __expf(gv) * uR;
-                    ga_[e] = __expf(gp) * uA;
-                    const float At_ = bf_el8(arh, e) + bf_el8(arl, e);
-                    const float Rt_ = bf_el8(arh, 4 + e) + bf_el8(arl, 4 + e);
-                    const float Bb_ = bf_el8(bkh, e) + bf_el8(bkl, e);
-                    const float Kb_ = bf_el8(bkh, 4 + e) + bf_el8(bkl, 4 + e);
-                    z[e] = Rt_ * uR - Bb_ * uB - Kb_ * uK;
-                    t2[e] = At_ * uA;
-                    const float sg = (gp - gv) * (1.f / DECAY_SCALE);  // sigmoid(w_t)
-                    fw[e] = -DECAY_SCALE * sg * (1.f - sg);
-                }
-                // dlogd_t = carry + sum_{s>=t} z_s + sum_{s>t} t2_s over the chunk (t = 4q + e)
-                float tot = 0.f;
-#pragma unroll
-                for (int e = 0; e < 4; e++) tot += z[e] + t2[e];
-                const float s1 = __shfl(tot, (lane & 15) + 16), s2 = __shfl(tot, (lane & 15) + 32),
-                            s3 = __shfl(tot, (lane & 15) + 48), s0 = __shfl(tot, lane & 15);
-                float run = carry + (q < 1 ? s1 : 0.f) + (q < 2 ? s2 : 0.f) + (q < 3 ? s3 : 0.f);
-#pragma unroll
-                for (int e = 3; e >= 0; e--) {
-                    run += z[e];
-                    gw_[e] = run * fw[e];
-                    run += t2[e];
-                }
-                carry += ((s0 + s1) + s2) + s3;
-                // lane (q, 4m + jj) stores row 4q + jj, keys 16c + 4m .. +3 of each gradient
-                const int tr = 4 * q + (lane & 3);
-                const uint32_t o = tr < L ? (uint32_t)((((long)(bb * Tn + t0 + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
-                                          : OUT_OF_RANGE;
-                store8(dk, tbytes, o, quad_rows_bf16(f32x4_t{gk_[0], gk_[1], gk_[2], gk_[3]}, lane));
-                store8(db, tbytes, o, quad_rows_bf16(f32x4_t{gb_[0], gb_[1], gb_[2], gb_[3]}, lane));
-                store8(dr, tbytes, o, quad_rows_bf16(f32x4_t{gr_[0], gr_[1], gr_[2], gr_[3]}, lane));
-                store8(da, tbytes, o, quad_rows_bf16(f32x4_t{ga_[0], ga_[1], ga_[2], ga_[3]}, lane));
-                store8(dw, tbytes, o, quad_rows_bf16(f32x4_t{gw_[0], gw_[1], gw_[2], gw_[3]}, lane));
-            }
-        } else {
-            // ================= producers, second part of the tick's phase =================
-            if (pact) produce(x, ph, 1);
-        }
-        lds_barrier();
-    }
-    if (consumer) {
 #pragma unroll
         for (int tj = 0; tj < 4; tj++)
             *reinterpret_cast<float4*>(ds0 + bh * NN + (long)i_own * NK + 16 * tj + 4 * q) =
                 make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+    } else {
+        // ======================= S side: rows i_own of S0; key strip j_own: dR, dA, dw =======================
+        // the next chunk's saved state as rows (same layout as Ht) and as the key strip,
+        // S0s[m] = S0[32(m/8) + 16((m/4)%2) + 4q + m%4][j_own], loaded a tick ahead
+        f32x4_t S0n[4];
+        float S0s[16];
+        float carry = 0.f;  // this side's part of the dlogd carry for key j_own
+        // buffer loads from this head's saved states: one lane offset, the rest in
+        // scalar and immediate offsets (no per-load address arithmetic)
+        const __amdgpu_buffer_rsrc_t ckr = make_rsrc(ckh, (uint32_t)(ncp * NN * 4));
+        auto load_rows = [&](int cc) {
+            const uint32_t vo = (uint32_t)((i_own * NK + 4 * q) * 4), so = (uint32_t)(cc * NN * 4);
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++)
+                S0n[tj] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ckr, vo + 64 * tj, so, 0));
+        };
+        auto load_strip = [&](int cc) {
+            const uint32_t vo = (uint32_t)((4 * q * NK + j_own) * 4);
+#pragma unroll
+            for (int m = 0; m < 16; m++)
+                S0s[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    ckr, vo + (m & 3) * NK * 4, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0));
+        };
+        // dw of chunk cc = this side's part + the H side's part
+        auto store_dw = [&](int cc, float4 gs, float4 gh) {
+            store8(dw, tbytes, piece_off(cc), quad_rows_bf16(f32x4_t{gs.x + gh.x, gs.y + gh.y, gs.z + gh.z, gs.w + gh.w}, lane));
+        };
+        load_rows(nchunk - 1);
+        load_strip(nchunk - 1);
+        vm_wait0();
+        lds_barrier();
+        lds_barrier();
+        for (int n = -NPROD; n < 0; n++) {
+            lds_barrier();
+            lds_barrier();
+        }
+        for (int n = 0; n < nchunk; n++) {
+            new_tick();
+            Slot& S = sm.slot[n % NPROD];
+            const int c = nchunk - 1 - n;
+            // ---- stage B: X1 = A~ S0^T + Aak V ; SA = Ti X1 ; publish SA^T rows ----
+            {
+                const uint2 vfr = ldtr_sw<SwDma>(S.V, 0, 16 * cw, lane);  // V[s = 4q+e][i_own]
+                f32x4_t x1 = zero4();
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    float sv[8];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        sv[e] = S0n[2 * s][e];
+                        sv[4 + e] = S0n[2 * s + 1][e];
+                    }
+                    uint4 sbh, sbl;
+                    pack8(sv, sbh, sbl);
+                    const uint4 ah = fragp_sw<SwLane>(S.At[0], r16, 32 * s, lane), al = fragp_sw<SwLane>(S.At[1], r16, 32 * s, lane);
+                    x1 = mma32(x1, ah, sbh);
+                    x1 = mma32(x1, ah, sbl);
+                    x1 = mma32(x1, al, sbh);
+                }
+                const Pk aak = mat_n(S.Aak, lane);
+                f32x4_t c1 = mma16(zero4(), aak.h, vfr);
+                c1 = mma16(c1, aak.l, vfr);
+                const Pk psa = pk(mm16s(mat_n(S.Ti, lane), pk(x1 + c1)));  // SA = Ti X1
+                st8(&sm.SAT[0][pl16(i_own, 4 * q)], psa.h);
+                st8(&sm.SAT[1][pl16(i_own, 4 * q)], psa.l);
+            }
+            lds_barrier();
+            // ---- stage C: key strip j_own of dR, dA, dw; dV rows i_own ----
+            const Strip st = strip(S);
+            uint4 oh[2], ol[2];  // this chunk's saved-state strip (loaded a tick ago)
+#pragma unroll
+            for (int s = 0; s < 2; s++) pack8(&S0s[8 * s], oh[s], ol[s]);
+            // the next chunk's state, a tick ahead: strip, then rows.  The memory counter is
+            // in order, so this strip must be consumed before they are issued (or using it
+            // would wait for them too): the asm pins that order.
+            asm volatile("" ::"v"(__builtin_bit_cast(i32x4_t, oh[0])), "v"(__builtin_bit_cast(i32x4_t, oh[1])),
+                         "v"(__builtin_bit_cast(i32x4_t, ol[0])), "v"(__builtin_bit_cast(i32x4_t, ol[1]))
+                         : "memory");
+            load_strip(max(c - 1, 0));  // (unconditional, like every memory operation of the loop,
+            load_rows(max(c - 1, 0));   // so the compiler's waits count a fixed sequence)
+            f32x4_t m1 = zero4(), xmT = zero4(), n1 = zero4(), gR = zero4(), gA = zero4();
+            {
+                f32x4_t cn = zero4(), ca = zero4();
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);
+                    const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);
+                    const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
+                    const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
+                    m1 = mma32(m1, va, qh);  // V Q^T = M1     [t][s]
+                    m1 = mma32(m1, va, ql);
+                    xmT = mma32(xmT, sh, ya);  // SA dY^T = XM^T [s][t]
+                    xmT = mma32(xmT, sl, ya);
+                    n1 = mma32(n1, sh, qh);  // SA Q^T = N1    [t][s]
+                    n1 = mma32(n1, sh, ql);
+                    cn = mma32(cn, sl, qh);
+                    gR = mma32(gR, ya, oh[s]);  // dY S0
+                    gR = mma32(gR, ya, ol[s]);
+                    gA = mma32(gA, qh, oh[s]);  // Q S0
+                    gA = mma32(gA, qh, ol[s]);
+                    ca = mma32(ca, ql, oh[s]);
+                }
+                n1 += cn;
+                gA += ca;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
+                const int rw = 4 * q + e;
+                if (r16 <= rw) m1[e] = 0.f, n1[e] = 0.f;  // M1[t][s], N1[t][s]: keep s > t
+                if (rw > r16) xmT[e] = 0.f;               // XM^T[s][t]: keep s <= t
+            }
+            const Pk m2t = mat_t(S.M2, lane), pm1 = pk(m1), pn1 = pk(n1), pxm = pk(xmT);
+            const f32x4_t cR = mm32s(cat(pxm.h, m2t.h), cat(pxm.l, m2t.l), st.bkh, st.bkl);  // [tril(dY SA^T) | tril(dY V^T)]
+            const f32x4_t cA = mm32s(cat(pn1.h, pm1.h), cat(pn1.l, pm1.l), st.bkh, st.bkl);  // [tril_s(Q SA^T) | tril_s(Q V^T)]
+            float gr_[4], ga_[4], z[4], t2[4], gw_[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float uR = gR[e] + cR[e], uA = gA[e] + cA[e];
+                gr_[e] = __expf(st.gv[e]) * uR;
+                ga_[e] = __expf(st.gp[e]) * uA;
+                const float At_ = bf_el8(st.arh, e) + bf_el8(st.arl, e);
+                const float Rt_ = bf_el8(st.arh, 4 + e) + bf_el8(st.arl, 4 + e);
+                z[e] = Rt_ * uR;
+                t2[e] = At_ * uA;
+            }
+            const uint32_t o = piece_off(c);
+            store8(dr, tbytes, o, quad_rows_bf16(f32x4_t{gr_[0], gr_[1], gr_[2], gr_[3]}, lane));
+            store8(da, tbytes, o, quad_rows_bf16(f32x4_t{ga_[0], ga_[1], ga_[2], ga_[3]}, lane));
+            dlogd_part(z, t2, st.fw, carry, gw_);
+            // the previous chunk's dw: the H side published its part a tick ago (at n = 0
+            // chunk c + 1 does not exist and every row of the store falls outside the tensor)
+            float4* const mine = reinterpret_cast<float4*>(&sm.dls[cw][4 * lane]);
+            store_dw(c + 1, *mine, *reinterpret_cast<const float4*>(&sm.dlp[(n + 1) & 1][cw][4 * lane]));
+            *mine = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
+            lds_barrier();
+        }
+        // the last chunk's dw
+        store_dw(0, *reinterpret_cast<const float4*>(&sm.dls[cw][4 * lane]),
+                 *reinterpret_cast<const float4*>(&sm.dlp[(nchunk - 1) & 1][cw][4 * lane]));
     }
 }
 
 void launch_chunk_backward(const Bwd& p) {
-    hipLaunchKernelGGL(chunk_backward_bf16, dim3(p.B * p.H), dim3(448), 0, p.stream, p.T, p.H,
+    hipLaunchKernelGGL(chunk_backward_bf16, dim3(p.B * p.H), dim3(704), 0, p.stream, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
                        (const bf16_t*)p.a, (const bf16_t*)p.b, p.ckpt, (const bf16_t*)p.dy, p.dsT,
                        (bf16_t*)p.dr, (bf16_t*)p.dw, (bf16_t*)p.dk, (bf16_t*)p.dv, (bf16_t*)p.da,
