@@ -201,8 +201,10 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
         vm_wait0();
     }
 
-    for (int n = -NPROD; n < nchunk; n++) {
-        if (producer) {
+    // The two roles run separate tick loops with the same barriers, so that
+    // registers and memory-counter waits are allocated per role.
+    if (producer) {
+        for (int n = -NPROD; n < nchunk; n++) {
             // the chunk this producer works on at tick n (x = pw mod 4), and its phase
             const int x = n + 1 + ((pw - n - 1) & 3);
             const int ph = n + NPROD - x;
@@ -302,7 +304,11 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                     else vm_wait0();
                 }
             }
-        } else if (n >= 0) {
+            lds_barrier();
+        }
+    } else {
+        for (int n = -NPROD; n < 0; n++) lds_barrier();
+        for (int n = 0; n < nchunk; n++) {
             // ---------------- consumer: rows i_own through chunk n ----------------
             const Slot& S = sm.slot[n % NSLOT];
             const int t0 = n * CH, L = min(CH, Tn - t0);
@@ -363,10 +369,8 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                     *reinterpret_cast<float4*>(ckpt + (bh * ncp + n + 1) * NN + (long)i_own * NK + 16 * tj + 4 * q) =
                         make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
             }
+            lds_barrier();
         }
-        lds_barrier();
-    }
-    if (!producer) {
 #pragma unroll
         for (int tj = 0; tj < 4; tj++)
             *reinterpret_cast<float4*>(sT + bh * NN + (long)i_own * NK + 16 * tj + 4 * q) =
