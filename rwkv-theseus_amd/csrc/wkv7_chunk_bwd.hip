@@ -74,6 +74,7 @@ struct BwdLds {
     float dlp[2][4][64 * 4];                     // H side's dw part of a chunk, per key strip (D layout)
     float dls[4][64 * 4];                        // S side's dw part of the previous chunk
     Plane raw[NPROD][5];                         // producer input staging: r, w, k, a, b
+    uint32_t csync;                              // consumers' mid-tick rendezvous counter
 };
 static_assert(sizeof(BwdLds) <= 160 * 1024, "backward LDS budget");
 
@@ -97,6 +98,20 @@ __device__ __forceinline__ Pk mat_t(const Mat& m, int lane) {  // A operand of M
 }
 __device__ __forceinline__ Pk mat_n(const Mat& m, int lane) {  // A operand of M
     return Pk{ldtr16(m[0], 0, lane), ldtr16(m[1], 0, lane)};
+}
+// The consumer waves' mid-tick rendezvous (their exchange planes written before,
+// read after): each of the 8 counts itself in on an LDS counter and waits for the
+// tick's total.  The producers do not take part, so their work is not cut in two
+// by it.  The wait is bounded (a wave that never arrives cannot hang the kernel).
+constexpr int NCONS = 8;
+__device__ __forceinline__ void consumer_sync(uint32_t* cnt, uint32_t target) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are done
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int i = 0; i < (1 << 22); i++) {
+        if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
 }
 // split-precision K=32 product (both operands split)
 __device__ __forceinline__ f32x4_t mm32s(uint4 ah, uint4 al, uint4 bh, uint4 bl) {
@@ -217,8 +232,11 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         j_own = i_own;
     };
 
-    // The three roles run separate tick loops with the same barriers, so that
-    // registers and memory-counter waits are allocated per role.
+    if (tid == 0) sm.csync = 0;  // (visible after the prologue's barriers)
+
+    // The three roles run separate tick loops with the same barriers (one per tick;
+    // the consumers also meet mid-tick on csync), so that registers and
+    // memory-counter waits are allocated per role.
     if (!consumer) {
         // ======================= producers (lane: token r16, keys 32 hf + 8q + e) =======================
         float gq[2][8];  // cumulative log-decay, phase 0 -> 1
@@ -277,8 +295,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         }
         lds_barrier();
         lds_barrier();
-        // Producer work for chunk x (processing order) in phase ph, split into the part
-        // done while consumers run stage B (part 0) and the part done during stage C.
+        // Producer work for chunk x (processing order) in phase ph, in two parts (the
+        // second part of a phase depends on DMA or on registers set in the first).
         f32x4_t Aab, AabT, Aak, Brb, Brk, M2;  // phase 2, part 0 -> part 1
         auto produce = [&](int x, int ph, int part) {
             Slot& S = sm.slot[x % NPROD];
@@ -389,9 +407,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
             const int ph = n + NPROD - x;
             const bool pact = x >= 0 && x < nchunk;
-            if (pact) produce(x, ph, 0);
-            lds_barrier();
-            if (pact) produce(x, ph, 1);
+            if (pact) {
+                produce(x, ph, 0);
+                produce(x, ph, 1);
+            }
             lds_barrier();
         }
     } else if (hside) {
@@ -428,10 +447,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             carry = part[j_own] + part[NK + j_own] + part[2 * NK + j_own] + part[3 * NK + j_own];
         }
         lds_barrier();
-        for (int n = -NPROD; n < 0; n++) {
-            lds_barrier();
-            lds_barrier();
-        }
+        for (int n = -NPROD; n < 0; n++) lds_barrier();
         for (int n = 0; n < nchunk; n++) {
             new_tick();
             Slot& S = sm.slot[n % NPROD];
@@ -478,7 +494,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
                 st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
             }
-            lds_barrier();
+            consumer_sync(&sm.csync, NCONS * (n + 1));
             // ---- stage C: key strip j_own of dK, dB (all value rows, fixed order); dV rows i_own; new H ----
             const Strip st = strip(S);
             f32x4_t xm = zero4(), m1T = zero4(), n1T = zero4(), gK = zero4(), gB = zero4();
@@ -589,10 +605,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         vm_wait0();
         lds_barrier();
         lds_barrier();
-        for (int n = -NPROD; n < 0; n++) {
-            lds_barrier();
-            lds_barrier();
-        }
+        for (int n = -NPROD; n < 0; n++) lds_barrier();
         for (int n = 0; n < nchunk; n++) {
             new_tick();
             Slot& S = sm.slot[n % NPROD];
@@ -623,7 +636,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 st8(&sm.SAT[0][pl16(i_own, 4 * q)], psa.h);
                 st8(&sm.SAT[1][pl16(i_own, 4 * q)], psa.l);
             }
-            lds_barrier();
+            consumer_sync(&sm.csync, NCONS * (n + 1));
             // ---- stage C: key strip j_own of dR, dA, dw; dV rows i_own ----
             const Strip st = strip(S);
             uint4 oh[2], ol[2];  // this chunk's saved-state strip (loaded a tick ago)
