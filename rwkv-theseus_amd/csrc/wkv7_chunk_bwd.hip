@@ -115,10 +115,12 @@ __device__ __forceinline__ void consumer_sync(uint32_t* cnt, uint32_t target) {
 }
 // split-precision K=32 product (both operands split)
 __device__ __forceinline__ f32x4_t mm32s(uint4 ah, uint4 al, uint4 bh, uint4 bl) {
-    const f32x4_t acc = mma32(zero4(), ah, bh);
-    f32x4_t c = mma32(zero4(), ah, bl);
-    c = mma32(c, al, bh);
-    return acc + c;
+    // one accumulator chain: no VALU adds (the VALU, not the matrix pipe, is the busier)
+    return mma32(mma32(mma32(zero4(), ah, bh), ah, bl), al, bh);
+}
+// acc + A B for packed tiles (split precision), one accumulator chain
+__device__ __forceinline__ f32x4_t mm16s_acc(f32x4_t acc, const Pk& A, const Pk& B) {
+    return mma16(mma16(mma16(acc, A.h, B.h), A.h, B.l), A.l, B.h);
 }
 // X Y^T over 64 keys, both in the K=32 operand layout (x[hf] = X[t][32hf + 8q ..])
 __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&xl)[2], const uint4 (&yh)[2],
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
         for (int n = 0; n < nchunk; n++) {
-            new_tick();
+            // (lane-derived addresses may stay in registers on this side)
             Slot& S = sm.slot[n % NPROD];
             const int c = nchunk - 1 - n;
             // ---- stage B: X2 = B- H'^T + Brb^T dY ; Q = Ti^T X2 ; publish H' and Q^T rows ----
@@ -490,7 +492,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const Pk brbT = mat_t(S.Brb, lane);
                 f32x4_t c2 = mma16(zero4(), brbT.h, dyf);
                 c2 = mma16(c2, brbT.l, dyf);
-                pq = pk(mm16s(mat_t(S.Ti, lane), pk(x2 + c2)));  // Q = Ti^T X2
+                pq = pk(mm16s_acc(zero4(), mat_t(S.Ti, lane), pk(x2 + c2)));  // Q = Ti^T X2
                 st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
                 st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
             }
@@ -499,7 +501,6 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const Strip st = strip(S);
             f32x4_t xm = zero4(), m1T = zero4(), n1T = zero4(), gK = zero4(), gB = zero4();
             {
-                f32x4_t cn = zero4(), cb = zero4();
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
                     const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);   // V[t][i], exact
@@ -513,15 +514,13 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     m1T = mma32(m1T, ql, va);
                     n1T = mma32(n1T, qh, sh);  // Q SA^T = N1^T [s][t]
                     n1T = mma32(n1T, qh, sl);
-                    cn = mma32(cn, ql, sh);
+                    n1T = mma32(n1T, ql, sh);
                     gK = mma32(gK, va, hh);  // V H'
                     gK = mma32(gK, va, hl);
                     gB = mma32(gB, sh, hh);  // SA H'
                     gB = mma32(gB, sh, hl);
-                    cb = mma32(cb, sl, hh);
+                    gB = mma32(gB, sl, hh);
                 }
-                n1T += cn;
-                gB += cb;
             }
 #pragma unroll
             for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
@@ -551,9 +550,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             *reinterpret_cast<float4*>(&sm.dlp[n & 1][cw][4 * lane]) = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
             {  // dV = K- H'^T + Brk^T dY + Aak^T Q
                 const Pk brkT = mat_t(S.Brk, lane);
-                f32x4_t c3 = mma16(zero4(), brkT.h, dyf);
-                c3 = mma16(c3, brkT.l, dyf);
-                const f32x4_t dvv = dv0 + c3 + mm16s(mat_t(S.Aak, lane), pq);
+                const f32x4_t c3 = mm16s_acc(mma16(mma16(zero4(), brkT.h, dyf), brkT.l, dyf), mat_t(S.Aak, lane), pq);
+                const f32x4_t dvv = dv0 + c3;
                 store8(dv, tbytes, o, quad_rows_bf16(dvv, lane));
             }
             // H_0^T = H'^T + [A~^T R~^T] [Q; dY]
@@ -562,10 +560,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             for (int tj = 0; tj < 4; tj++) {
                 const uint4 ah = cat(ldtr_sw<SwLane>(S.At[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[0], 0, 16 * tj, lane));
                 const uint4 al = cat(ldtr_sw<SwLane>(S.At[1], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[1], 0, 16 * tj, lane));
-                f32x4_t acc = mma32(Ht[tj], ah, bhi);
-                f32x4_t c1 = mma32(zero4(), ah, blo);
-                c1 = mma32(c1, al, bhi);
-                Ht[tj] = acc + c1;
+                Ht[tj] = mma32(mma32(mma32(Ht[tj], ah, bhi), ah, blo), al, bhi);
             }
             lds_barrier();
         }
@@ -632,7 +627,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const Pk aak = mat_n(S.Aak, lane);
                 f32x4_t c1 = mma16(zero4(), aak.h, vfr);
                 c1 = mma16(c1, aak.l, vfr);
-                const Pk psa = pk(mm16s(mat_n(S.Ti, lane), pk(x1 + c1)));  // SA = Ti X1
+                const Pk psa = pk(mm16s_acc(zero4(), mat_n(S.Ti, lane), pk(x1 + c1)));  // SA = Ti X1
                 st8(&sm.SAT[0][pl16(i_own, 4 * q)], psa.h);
                 st8(&sm.SAT[1][pl16(i_own, 4 * q)], psa.l);
             }
@@ -652,7 +647,6 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             load_rows(max(c - 1, 0));   // so the compiler's waits count a fixed sequence)
             f32x4_t m1 = zero4(), xmT = zero4(), n1 = zero4(), gR = zero4(), gA = zero4();
             {
-                f32x4_t cn = zero4(), ca = zero4();
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
                     const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);
@@ -665,15 +659,13 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     xmT = mma32(xmT, sl, ya);
                     n1 = mma32(n1, sh, qh);  // SA Q^T = N1    [t][s]
                     n1 = mma32(n1, sh, ql);
-                    cn = mma32(cn, sl, qh);
+                    n1 = mma32(n1, sl, qh);
                     gR = mma32(gR, ya, oh[s]);  // dY S0
                     gR = mma32(gR, ya, ol[s]);
                     gA = mma32(gA, qh, oh[s]);  // Q S0
                     gA = mma32(gA, qh, ol[s]);
-                    ca = mma32(ca, ql, oh[s]);
+                    gA = mma32(gA, ql, oh[s]);
                 }
-                n1 += cn;
-                gA += ca;
             }
 #pragma unroll
             for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
