@@ -602,7 +602,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
         for (int n = 0; n < nchunk; n++) {
-            new_tick();
+            // (lane-derived addresses may stay in registers on this side)
             Slot& S = sm.slot[n % NPROD];
             const int c = nchunk - 1 - n;
             // ---- stage B: X1 = A~ S0^T + Aak V ; SA = Ti X1 ; publish SA^T rows ----
