@@ -125,14 +125,14 @@ __device__ __forceinline__ f32x4_t mm16s_acc(f32x4_t acc, const Pk& A, const Pk&
 // X Y^T over 64 keys, both in the K=32 operand layout (x[hf] = X[t][32hf + 8q ..])
 __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&xl)[2], const uint4 (&yh)[2],
                                             const uint4 (&yl)[2]) {
-    f32x4_t acc = zero4(), c1 = zero4(), c2 = zero4();
+    f32x4_t acc = zero4();  // one accumulator chain: no VALU adds
 #pragma unroll
     for (int s = 0; s < 2; s++) {
         acc = mma32(acc, xh[s], yh[s]);
-        c1 = mma32(c1, xh[s], yl[s]);
-        c2 = mma32(c2, xl[s], yh[s]);
+        acc = mma32(acc, xh[s], yl[s]);
+        acc = mma32(acc, xl[s], yh[s]);
     }
-    return acc + c1 + c2;
+    return acc;
 }
 // permuted K=32 fragments over the rows of a [64][*] plane (k = 32s + 4q + e, 32s + 16 + 4q + e)
 __device__ __forceinline__ uint4 rows_tr(const uint16_t* x, int s, int lane) {  // [64][16] plane

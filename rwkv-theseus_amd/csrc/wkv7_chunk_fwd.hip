@@ -85,14 +85,14 @@ __device__ __forceinline__ float bf_el8(uint4 u, int e) {
 // (x[hf] = X[t = l%16][32 hf + 8q .. +7], split into hi / lo)
 __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&xl)[2], const uint4 (&yh)[2],
                                             const uint4 (&yl)[2]) {
-    f32x4_t acc = zero4(), c1 = zero4(), c2 = zero4();
+    f32x4_t acc = zero4();  // one accumulator chain: no VALU adds
 #pragma unroll
     for (int s = 0; s < 2; s++) {
         acc = mma32(acc, xh[s], yh[s]);
-        c1 = mma32(c1, xh[s], yl[s]);
-        c2 = mma32(c2, xl[s], yh[s]);
+        acc = mma32(acc, xh[s], yl[s]);
+        acc = mma32(acc, xl[s], yh[s]);
     }
-    return acc + c1 + c2;
+    return acc;
 }
 }  // namespace
 
@@ -351,11 +351,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 const uint4 ah = cat(ldtr_sw<SwLane>(S.Bh[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Kh[0], 0, 16 * tj, lane));
                 const uint4 al = cat(ldtr_sw<SwLane>(S.Bh[1], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Kh[1], 0, 16 * tj, lane));
                 const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
-                f32x4_t acc = St[tj] * f32x4_t{el.x, el.y, el.z, el.w};
-                acc = mma32(acc, ah, bhi);
-                f32x4_t c1 = mma32(zero4(), ah, blo);
-                c1 = mma32(c1, al, bhi);
-                St[tj] = acc + c1;
+                St[tj] = mma32(mma32(mma32(St[tj] * f32x4_t{el.x, el.y, el.z, el.w}, ah, bhi), ah, blo), al, bhi);
             }
             {  // lane (q, 4m + jj) stores row 4q + jj, values 16c + 4m .. +3 (rows past the end dropped)
                 const int tr = 4 * q + (lane & 3);

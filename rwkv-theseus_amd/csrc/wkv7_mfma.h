@@ -283,10 +283,8 @@ __device__ __forceinline__ Pk pk(const f32x4_t& x) {
 }
 // split-precision product of packed tiles: A = packed D-layout of X^T, B = of Y
 __device__ __forceinline__ f32x4_t mm16s(const Pk& A, const Pk& B) {
-    const f32x4_t acc = mma16(zero4(), A.h, B.h);
-    f32x4_t c = mma16(zero4(), A.h, B.l);
-    c = mma16(c, A.l, B.h);
-    return acc + c;
+    // one accumulator chain: no VALU adds (per SIMD the VALU is the busier pipe)
+    return mma16(mma16(mma16(zero4(), A.h, B.h), A.h, B.l), A.l, B.h);
 }
 // (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8) for a strictly lower
 // triangular 16x16 L (L^16 = 0), from L and L^T in D layout; returns the
