@@ -61,8 +61,14 @@ const char* theseus_wkv7_error_string(int status);
 int theseus_wkv7_checkpoint_interval(void);
 long long theseus_wkv7_checkpoint_count(int T);
 
-/* Bytes of device workspace theseus_wkv7_backward needs for these sizes and
- * dtype (0 when the chunked kernels run: they need none). */
+/* Bytes of device workspace theseus_wkv7_forward / theseus_wkv7_backward
+ * need for these sizes and dtype on the current device (0 when none).  The
+ * chunked kernels use it when B*H heads outnumber the device's CUs: heads are
+ * then cut between workgroups, which hand the carried state over through it;
+ * the step-serial backward replays each 16-step segment into it.  Contents
+ * need not be initialised (each call clears what it uses, on its stream), and
+ * a workspace must not be shared by calls that may run at the same time. */
+size_t theseus_wkv7_forward_workspace_size(int B, int T, int H, int N, int dtype);
 size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtype);
 
 /* Forward recurrence.  Replaces wkv_forward (kernels/wkv7_state.cpp:16-25)
@@ -72,7 +78,8 @@ size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtyp
 int theseus_wkv7_forward(int B, int T, int H, int N, int dtype,
                          const void* r, const void* w, const void* k, const void* v,
                          const void* a, const void* b, const float* s0,
-                         void* y, float* sT, float* ckpt, hipStream_t stream);
+                         void* y, float* sT, float* ckpt, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
 
 /* Backward (adjoint) pass.  Replaces wkv_backward (kernels/wkv7_state.cpp:26-37)
  * and launch_backward (kernels/wkv7_state.cu:87-92).  ckpt is the buffer the

@@ -16,7 +16,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 
 int check_dims(int B, int T, int H, int N, int dtype) {
     if (B < 1 || H < 1 || T < 1 || N < 2 || N > 128) return THESEUS_WKV7_ERR_SHAPE;
@@ -44,18 +44,36 @@ static bool chunk_ok(int B, int T, int H, int N, int dtype) {
     return N == 64 && dtype == THESEUS_WKV7_BF16 && (long long)B * T * H * N * 2 < (1ll << 31) && !force_seq();
 }
 
+// CUs of the current device, which the chunked kernels' schedule spreads the
+// heads over (one workgroup each).  THESEUS_WKV7_CUS=<n> plans for n instead
+// (the tests use it to cut heads at small sizes).
+static int cu_count() {
+    if (const char* e = getenv("THESEUS_WKV7_CUS")) {
+        const int n = atoi(e);
+        if (n > 0) return n;
+    }
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+        n = 1;  // (cutting no head is always correct)
+    return n;
+}
+
 void launch_forward(const Fwd& p) {
-    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_forward(p);
+    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_forward(p, cu_count());
     else launch_seq_forward(p);
 }
 void launch_backward(const Bwd& p) {
-    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_backward(p);
+    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_backward(p, cu_count());
     else launch_seq_backward(p);
 }
-// The chunked backward needs no workspace; the step-serial one replays each
-// 16-step segment into it.
+// The chunked kernels' handoffs; the step-serial backward replays each
+// 16-step segment into its workspace (its forward needs none).
+size_t forward_workspace(int B, int T, int H, int N, int dtype) {
+    return chunk_ok(B, T, H, N, dtype) ? chunk_forward_workspace(B, T, H, cu_count()) : 0;
+}
 size_t backward_workspace(int B, int T, int H, int N, int dtype) {
-    return chunk_ok(B, T, H, N, dtype) ? 0 : seq_backward_workspace(B, H, N);
+    return chunk_ok(B, T, H, N, dtype) ? chunk_backward_workspace(B, T, H, cu_count()) : seq_backward_workspace(B, H, N);
 }
 
 }  // namespace wkv7
@@ -82,6 +100,11 @@ long long theseus_wkv7_checkpoint_count(int T) {
     return T < 1 ? 0 : (long long)(T + wkv7::kCkptInterval - 1) / wkv7::kCkptInterval + 1;
 }
 
+size_t theseus_wkv7_forward_workspace_size(int B, int T, int H, int N, int dtype) {
+    if (check_dims(B, T, H, N, dtype) != THESEUS_WKV7_OK) return 0;
+    return wkv7::forward_workspace(B, T, H, N, dtype);
+}
+
 size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtype) {
     if (check_dims(B, T, H, N, dtype) != THESEUS_WKV7_OK) return 0;
     return wkv7::backward_workspace(B, T, H, N, dtype);
@@ -89,10 +112,13 @@ size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtyp
 
 int theseus_wkv7_forward(int B, int T, int H, int N, int dtype, const void* r, const void* w,
                          const void* k, const void* v, const void* a, const void* b,
-                         const float* s0, void* y, float* sT, float* ckpt, hipStream_t stream) {
+                         const float* s0, void* y, float* sT, float* ckpt, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
     if (int e = check_dims(B, T, H, N, dtype)) return e;
     if (!r || !w || !k || !v || !a || !b || !s0 || !y || !sT) return THESEUS_WKV7_ERR_NULL;
-    wkv7::Fwd p{B, T, H, N, dtype, r, w, k, v, a, b, s0, y, sT, ckpt, stream};
+    const size_t need = wkv7::forward_workspace(B, T, H, N, dtype);
+    if (workspace_bytes < need || (need && !workspace)) return THESEUS_WKV7_ERR_WORKSPACE;
+    wkv7::Fwd p{B, T, H, N, dtype, r, w, k, v, a, b, s0, y, sT, ckpt, workspace, stream};
     wkv7::launch_forward(p);
     return launch_status();
 }

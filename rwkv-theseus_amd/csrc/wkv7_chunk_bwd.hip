@@ -40,6 +40,7 @@
 //    matrix with ds_read_b64_tr_b16.
 #include "wkv7_launch.h"
 #include "wkv7_io.h"
+#include "wkv7_sched.h"
 
 namespace wkv7 {
 namespace {
@@ -67,16 +68,24 @@ struct Slot {
     float g[CH * LDG];                 // cumulative log-decay [t][j]
     float egL[NK];
 };
+// The consumers' exchange planes come first: LDS instructions reach 64 KB past
+// their address register, so planes at fixed offsets below that share one
+// lane-offset register per access pattern (and the slots are addressed from a
+// per-tick base).
 struct BwdLds {
-    Slot slot[NPROD];
     uint16_t Hx[2][NK * NK];                     // H' [i][j] (swizzled)
     uint16_t QT[2][NK * LDQ], SAT[2][NK * LDQ];  // Q^T, SA^T [i][t]
     float dlp[2][4][64 * 4];                     // H side's dw part of a chunk, per key strip (D layout)
     float dls[4][64 * 4];                        // S side's dw part of the previous chunk
+    Slot slot[NPROD];
     Plane raw[NPROD][5];                         // producer input staging: r, w, k, a, b
     uint32_t csync;                              // consumers' mid-tick rendezvous counter
 };
 static_assert(sizeof(BwdLds) <= 160 * 1024, "backward LDS budget");
+// 16-byte LDS accesses and DMA rows need 16-byte aligned planes
+static_assert(offsetof(BwdLds, slot) % 256 == 0 && sizeof(Slot) % 16 == 0 && offsetof(BwdLds, raw) % 16 == 0 &&
+                  offsetof(Slot, g) % 16 == 0 && offsetof(Slot, egL) % 16 == 0 && offsetof(BwdLds, dlp) % 16 == 0,
+              "backward LDS alignment");
 
 __device__ __forceinline__ void st8(uint16_t* p, uint2 v) { *reinterpret_cast<uint2*>(p) = v; }
 __device__ __forceinline__ float lo_bf(uint32_t u) { return __uint_as_float(u << 16); }
@@ -152,19 +161,20 @@ __device__ __forceinline__ int opaque(int x) {
 }  // namespace
 
 __global__ __launch_bounds__(704) void chunk_backward_bf16(
-    int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
+    Sched sc, int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ k, const bf16_t* __restrict__ v, const bf16_t* __restrict__ a,
     const bf16_t* __restrict__ b, const float* __restrict__ ckpt, const bf16_t* __restrict__ dy,
     const float* __restrict__ dsT, bf16_t* __restrict__ dr, bf16_t* __restrict__ dw,
     bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, bf16_t* __restrict__ da,
-    bf16_t* __restrict__ db, float* __restrict__ ds0) {
+    bf16_t* __restrict__ db, float* __restrict__ ds0, uint32_t* __restrict__ flags, float* __restrict__ hand) {
     __shared__ BwdLds sm;
-    const int bh = blockIdx.x, bb = bh / H, h = bh % H;
+    const int m = machine_of_block(sc), nstream = stream_len(sc, m);
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     int lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
+    const long NH = NN + 2 * NK;  // handoff per boundary: H (dL/dS), then the two sides' dlogd carries
     const long ncp = ckpt_count(Tn);
-    const int nchunk = (Tn + CH - 1) / CH;
+    const int nchunk = sc.n;
     const bool consumer = wv < 8;
     const bool hside = wv < 4;  // consumer: owner of H (else the S0 side)
     const int cw = wv & 3;      // consumer: value-row block / key strip
@@ -174,14 +184,22 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
     const int lane0 = lane;
     const long rstride = (long)H * NK;  // between consecutive tokens of one head
 
-    // processing index xx -> chunk nchunk-1-xx: byte offset of its first row, valid length
-    auto chunk_off = [&](int xx) { return (uint32_t)(((long)(bb * Tn + (nchunk - 1 - xx) * CH) * H + h) * NK * 2); };
-    auto chunk_len = [&](int xx) { return min(CH, Tn - (nchunk - 1 - xx) * CH); };
-    const uint32_t tbytes = (uint32_t)((long)gridDim.x * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
-    const float* const ckh = ckpt + bh * ncp * NN;                       // this head's saved states
-    // byte offset for the 8-byte row piece of a D-layout tile of chunk cc: lane (q, 4m + jj)
-    // stores row 4q + jj, columns 16 cw + 4m .. +3 (rows past the chunk's end: dropped)
-    auto piece_off = [&](int cc) {
+    // stream index x -> (head, chunk): step s of a head is its chunk nchunk-1-s
+    auto chunk_at = [&](int x) {
+        const int2 js = stream_at(sc, m, x);
+        return make_int2(js.x, nchunk - 1 - js.y);
+    };
+    // byte offset of the chunk's first row, its valid length
+    auto chunk_off = [&](int x) {
+        const int2 jc = chunk_at(x);
+        const int bb = jc.x / H, h = jc.x - bb * H;
+        return (uint32_t)(((long)(bb * Tn + jc.y * CH) * H + h) * NK * 2);
+    };
+    auto chunk_len = [&](int x) { return min(CH, Tn - chunk_at(x).y * CH); };
+    const uint32_t tbytes = (uint32_t)((long)sc.J * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
+    // byte offset for the 8-byte row piece of a D-layout tile of chunk cc of head (bb, h):
+    // lane (q, 4m + jj) stores row 4q + jj, columns 16 cw + 4m .. +3 (rows past the end: dropped)
+    auto piece_off = [&](int bb, int h, int cc) {
         const int tr = 4 * q + (lane & 3);
         return tr < min(CH, Tn - cc * CH)
                    ? (uint32_t)((((long)(bb * Tn + cc * CH + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
@@ -283,9 +301,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         uint32_t voff[2];  // this lane's LDS DMA offsets
         dma_lane_offsets(voff, rstride, lane);
         const bf16_t* const rsrc_src[5] = {r, w, k, a, b};
-        if (pw < nchunk) {
-            // the first chunk of each producer; only processing index 0 can be partial,
-            // and its V, dY go into its slot here too so the loop only ever runs DMA
+        if (pw < nstream) {
+            // the first chunk of each producer; stream index 0's V, dY go into its slot here too
 #pragma unroll
             for (int ts = 0; ts < 5; ts++)
                 stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(pw), voff, rstride,
@@ -332,21 +349,25 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     operands(raw, gq[1], 1, o);
                     put_operands(S, 1, o);
                     dma_lane_offsets(voff, rstride, lane);
-                    if (x > 0) {  // (chunk 0's V, dY were staged before the loop)
-                        dma_plane(S.V, dma_rsrc(v, tbytes), chunk_off(x), voff);
-                        dma_plane(S.dY, dma_rsrc(dy, tbytes), chunk_off(x), voff);
+                    if (x > 0) {  // (stream index 0's V, dY were staged before the loop)
+                        const uint32_t o = chunk_off(x);
+                        const int L = chunk_len(x);
+                        stage_plane(S.V, dma_rsrc(v, tbytes), v, o, voff, rstride, L, lane);
+                        stage_plane(S.dY, dma_rsrc(dy, tbytes), dy, o, voff, rstride, L, lane);
                     }
                     wave_lds_fence();  // staging reads done before the DMA overwrites it
-                    if (x + NPROD < nchunk) {
+                    if (x + NPROD < nstream) {
+                        const uint32_t o = chunk_off(x + NPROD);
+                        const int L = chunk_len(x + NPROD);
 #pragma unroll
                         for (int ts = 0; ts < 5; ts++)
-                            dma_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), chunk_off(x + NPROD), voff);
+                            stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], o, voff, rstride, L, lane);
                     }
                 }
             } else if (part == 0) {
                 // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
                 // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
-                if (x + NPROD < nchunk) vm_wait10();
+                if (x + NPROD < nstream) vm_wait10();
                 else vm_wait0();
                 auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
 #pragma unroll
@@ -402,13 +423,13 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             }
         };
 
-        for (int n = -NPROD; n < nchunk; n++) {
+        for (int n = -NPROD; n < nstream; n++) {
             new_tick();
             // the chunk this producer works on at tick n (x = pw mod 3, so slot x % 3 is
             // its own) and its phase; prologue and final ticks have no chunk for some
             const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
             const int ph = n + NPROD - x;
-            const bool pact = x >= 0 && x < nchunk;
+            const bool pact = x >= 0 && x < nstream;
             if (pact) {
                 produce(x, ph, 0);
                 produce(x, ph, 1);
@@ -419,41 +440,35 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         // ======================= H side: rows i_own of H and dV; key strip j_own: dK, dB =======================
         f32x4_t Ht[4];      // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e] (H' within a tick)
         float carry = 0.f;  // this side's part of the dlogd carry for key j_own
-        {
-            f32x4_t STt[4];
-#pragma unroll
-            for (int tj = 0; tj < 4; tj++) {
-                const long off = (long)i_own * NK + 16 * tj + 4 * q;
-                float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (dsT) x = *reinterpret_cast<const float4*>(dsT + bh * NN + off);
-                Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
-                const float4 st = *reinterpret_cast<const float4*>(ckh + (ncp - 1) * NN + off);
-                STt[tj] = f32x4_t{st.x, st.y, st.z, st.w};
-            }
-            // carry_j = sum_i dsT[i][j] S_T[i][j]: 16 rows per lane group, then the 4 waves in order
-            float* part = reinterpret_cast<float*>(&sm.Hx[0][0]);
-#pragma unroll
-            for (int tj = 0; tj < 4; tj++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float p = Ht[tj][e] * STt[tj][e];
-#pragma unroll
-                    for (int off = 1; off < 16; off <<= 1) p += __shfl_xor(p, off, 16);
-                    if (r16 == 0) part[cw * NK + 16 * tj + 4 * q + e] = p;
-                }
-            vm_wait0();  // nothing is loaded in the loop: the counter then only tracks stores
-        }
         lds_barrier();
-        {
-            const float* part = reinterpret_cast<const float*>(&sm.Hx[0][0]);
-            carry = part[j_own] + part[NK + j_own] + part[2 * NK + j_own] + part[3 * NK + j_own];
-        }
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
-        for (int n = 0; n < nchunk; n++) {
+        // one piece (a head's chunks on this workgroup) after another; tick n counts the stream
+        const int jlast = (m * sc.L + nstream - 1) / sc.n;
+        int n = 0;
+        for (int j = m * sc.L / sc.n; j <= jlast; j++) {
+          const Seg sg = seg_of(sc, m, j);
+          const int bb = j / H, h = j - bb * H;
+          {  // H at the piece's start: dsT (zero if absent) at the head's end, else the handoff
+             // of boundary m + 1 with this side's carry (the S side starts the head's carry).
+             // (Lane offsets at piece boundaries come from an opaque lane, so that they are
+             // not kept in registers across the tick loop.)
+            const int ln = opaque(lane0), row = 16 * cw + (ln & 15), col = 4 * (ln >> 4);
+            const float* src = sg.fresh ? (dsT ? dsT + (long)j * NN : nullptr) : hand + (m + 1) * NH;
+            const bool ok = sg.fresh || handoff_wait(flags + m + 1, NCONS);
+            const float bad = ok ? 1.f : __builtin_nanf("");
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++) {
+                float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (src) x = *reinterpret_cast<const float4*>(src + row * NK + 16 * tj + col);
+                Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w} * bad;
+            }
+            carry = sg.fresh ? 0.f : hand[(m + 1) * NH + NN + row];
+          }
+          for (int kk = 0; kk < sg.count; kk++, n++) {
             // (lane-derived addresses may stay in registers on this side)
             Slot& S = sm.slot[n % NPROD];
-            const int c = nchunk - 1 - n;
+            const int c = nchunk - 1 - (sg.step0 + kk);
             // ---- stage B: X2 = B- H'^T + Brb^T dY ; Q = Ti^T X2 ; publish H' and Q^T rows ----
             const uint2 dyf = ldtr_sw<SwDma>(S.dY, 0, 16 * cw, lane);  // dY[s = 4q+e][i_own]
 #pragma unroll
@@ -543,7 +558,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 z[e] = -(Bb_ * uB + Kb_ * uK);
                 t2[e] = 0.f;
             }
-            const uint32_t o = piece_off(c);
+            const uint32_t o = piece_off(bb, h, c);
             store8(dk, tbytes, o, quad_rows_bf16(f32x4_t{gk_[0], gk_[1], gk_[2], gk_[3]}, lane));
             store8(db, tbytes, o, quad_rows_bf16(f32x4_t{gb_[0], gb_[1], gb_[2], gb_[3]}, lane));
             dlogd_part(z, t2, st.fw, carry, gw_);
@@ -563,11 +578,20 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 Ht[tj] = mma32(mma32(mma32(Ht[tj], ah, bhi), ah, blo), al, bhi);
             }
             lds_barrier();
-        }
+          }
+          {  // ds0 at the head's start, or the handoff at boundary m (H and this side's carry)
+            const int ln = opaque(lane0), row = 16 * cw + (ln & 15), col = 4 * (ln >> 4);
+            float* const dst = sg.handoff ? hand + m * NH : ds0 + (long)j * NN;
 #pragma unroll
-        for (int tj = 0; tj < 4; tj++)
-            *reinterpret_cast<float4*>(ds0 + bh * NN + (long)i_own * NK + 16 * tj + 4 * q) =
-                make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+            for (int tj = 0; tj < 4; tj++)
+                *reinterpret_cast<float4*>(dst + row * NK + 16 * tj + col) =
+                    make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+            if (sg.handoff) {
+                if (col == 0) dst[NN + row] = carry;
+                handoff_signal(flags + m);
+            }
+          }
+        }
     } else {
         // ======================= S side: rows i_own of S0; key strip j_own: dR, dA, dw =======================
         // the next chunk's saved state as rows (same layout as Ht) and as the key strip,
@@ -575,36 +599,70 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         f32x4_t S0n[4];
         float S0s[16];
         float carry = 0.f;  // this side's part of the dlogd carry for key j_own
-        // buffer loads from this head's saved states: one lane offset, the rest in
+        // buffer loads from a head's saved states: one lane offset, the rest in
         // scalar and immediate offsets (no per-load address arithmetic)
-        const __amdgpu_buffer_rsrc_t ckr = make_rsrc(ckh, (uint32_t)(ncp * NN * 4));
-        auto load_rows = [&](int cc) {
+        auto ck_rsrc = [&](int j) { return make_rsrc(ckpt + (long)j * ncp * NN, (uint32_t)(ncp * NN * 4)); };
+        auto load_rows = [&](__amdgpu_buffer_rsrc_t ckr, int cc) {
             const uint32_t vo = (uint32_t)((i_own * NK + 4 * q) * 4), so = (uint32_t)(cc * NN * 4);
 #pragma unroll
             for (int tj = 0; tj < 4; tj++)
                 S0n[tj] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ckr, vo + 64 * tj, so, 0));
         };
-        auto load_strip = [&](int cc) {
+        auto load_strip = [&](__amdgpu_buffer_rsrc_t ckr, int cc) {
             const uint32_t vo = (uint32_t)((4 * q * NK + j_own) * 4);
 #pragma unroll
             for (int m = 0; m < 16; m++)
                 S0s[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
                     ckr, vo + (m & 3) * NK * 4, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0));
         };
-        // dw of chunk cc = this side's part + the H side's part
-        auto store_dw = [&](int cc, float4 gs, float4 gh) {
-            store8(dw, tbytes, piece_off(cc), quad_rows_bf16(f32x4_t{gs.x + gh.x, gs.y + gh.y, gs.z + gh.z, gs.w + gh.w}, lane));
+        // dw of a chunk (piece offset o) = this side's part + the H side's part
+        auto store_dw = [&](uint32_t o, float4 gs, float4 gh) {
+            store8(dw, tbytes, o, quad_rows_bf16(f32x4_t{gs.x + gh.x, gs.y + gh.y, gs.z + gh.z, gs.w + gh.w}, lane));
         };
-        load_rows(nchunk - 1);
-        load_strip(nchunk - 1);
+        {
+            const int2 jc = chunk_at(0);
+            load_rows(ck_rsrc(jc.x), jc.y);
+            load_strip(ck_rsrc(jc.x), jc.y);
+        }
         vm_wait0();
         lds_barrier();
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
-        for (int n = 0; n < nchunk; n++) {
+        uint32_t o_prev = OUT_OF_RANGE;  // the previous tick's chunk (its dw is completed a tick late)
+        const int jlast = (m * sc.L + nstream - 1) / sc.n;
+        int n = 0;
+        for (int j = m * sc.L / sc.n; j <= jlast; j++) {
+          const Seg sg = seg_of(sc, m, j);
+          const int bb = j / H, h = j - bb * H;
+          {  // (lane offsets at piece boundaries from an opaque lane: none held across the tick loop)
+            const int ln = opaque(lane0), key = 16 * cw + (ln & 15);
+            if (sg.fresh) {
+                // the head's carry starts at colsum(dsT o S_T) (key j_own): 16 rows per lane group
+                float p = 0.f;
+                if (dsT) {
+                    const float* d = dsT + (long)j * NN + key;
+                    const float* st = ckpt + ((long)j * ncp + ncp - 1) * NN + key;
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        const int row = 16 * (u >> 2) + 4 * (ln >> 4) + (u & 3);
+                        p += d[row * NK] * st[row * NK];
+                    }
+                    p += __shfl_xor(p, 16);
+                    p += __shfl_xor(p, 32);
+                }
+                carry = p;
+            } else {  // this side's carry from the handoff of boundary m + 1
+                const bool ok = handoff_wait(flags + m + 1, NCONS);
+                carry = ok ? hand[(m + 1) * NH + NN + NK + key] : __builtin_nanf("");
+            }
+          }
+          // the chunk after this piece's last: the next piece's first (or a repeat at the end)
+          const int jn = j < jlast ? j + 1 : j;
+          const int cn = j < jlast ? nchunk - 1 - seg_of(sc, m, j + 1).step0 : nchunk - 1 - (sg.step0 + sg.count - 1);
+          for (int kk = 0; kk < sg.count; kk++, n++) {
             // (lane-derived addresses may stay in registers on this side)
             Slot& S = sm.slot[n % NPROD];
-            const int c = nchunk - 1 - n;
+            const int c = nchunk - 1 - (sg.step0 + kk);
             // ---- stage B: X1 = A~ S0^T + Aak V ; SA = Ti X1 ; publish SA^T rows ----
             {
                 const uint2 vfr = ldtr_sw<SwDma>(S.V, 0, 16 * cw, lane);  // V[s = 4q+e][i_own]
@@ -643,8 +701,13 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             asm volatile("" ::"v"(__builtin_bit_cast(i32x4_t, oh[0])), "v"(__builtin_bit_cast(i32x4_t, oh[1])),
                          "v"(__builtin_bit_cast(i32x4_t, ol[0])), "v"(__builtin_bit_cast(i32x4_t, ol[1]))
                          : "memory");
-            load_strip(max(c - 1, 0));  // (unconditional, like every memory operation of the loop,
-            load_rows(max(c - 1, 0));   // so the compiler's waits count a fixed sequence)
+            {  // (unconditional, like every memory operation of the loop, so the compiler's
+               // waits count a fixed sequence)
+                const bool last = kk + 1 == sg.count;
+                const __amdgpu_buffer_rsrc_t ckr = ck_rsrc(last ? jn : j);
+                load_strip(ckr, last ? cn : c - 1);
+                load_rows(ckr, last ? cn : c - 1);
+            }
             f32x4_t m1 = zero4(), xmT = zero4(), n1 = zero4(), gR = zero4(), gA = zero4();
             {
 #pragma unroll
@@ -687,29 +750,47 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 z[e] = Rt_ * uR;
                 t2[e] = At_ * uA;
             }
-            const uint32_t o = piece_off(c);
+            const uint32_t o = piece_off(bb, h, c);
             store8(dr, tbytes, o, quad_rows_bf16(f32x4_t{gr_[0], gr_[1], gr_[2], gr_[3]}, lane));
             store8(da, tbytes, o, quad_rows_bf16(f32x4_t{ga_[0], ga_[1], ga_[2], ga_[3]}, lane));
             dlogd_part(z, t2, st.fw, carry, gw_);
-            // the previous chunk's dw: the H side published its part a tick ago (at n = 0
-            // chunk c + 1 does not exist and every row of the store falls outside the tensor)
+            // the previous tick's dw: the H side published its part a tick ago (at n = 0
+            // there is none and the store's offset lies outside the tensor)
             float4* const mine = reinterpret_cast<float4*>(&sm.dls[cw][4 * lane]);
-            store_dw(c + 1, *mine, *reinterpret_cast<const float4*>(&sm.dlp[(n + 1) & 1][cw][4 * lane]));
+            store_dw(o_prev, *mine, *reinterpret_cast<const float4*>(&sm.dlp[(n + 1) & 1][cw][4 * lane]));
             *mine = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
+            o_prev = o;
             lds_barrier();
+          }
+          if (sg.handoff) {  // this side's carry at boundary m
+              const int ln = opaque(lane0);
+              if (ln < 16) hand[m * NH + NN + NK + 16 * cw + ln] = carry;
+              handoff_signal(flags + m);
+          }
         }
         // the last chunk's dw
-        store_dw(0, *reinterpret_cast<const float4*>(&sm.dls[cw][4 * lane]),
-                 *reinterpret_cast<const float4*>(&sm.dlp[(nchunk - 1) & 1][cw][4 * lane]));
+        store_dw(o_prev, *reinterpret_cast<const float4*>(&sm.dls[cw][4 * lane]),
+                 *reinterpret_cast<const float4*>(&sm.dlp[(nstream - 1) & 1][cw][4 * lane]));
     }
 }
 
-void launch_chunk_backward(const Bwd& p) {
-    hipLaunchKernelGGL(chunk_backward_bf16, dim3(p.B * p.H), dim3(704), 0, p.stream, p.T, p.H,
+size_t chunk_backward_workspace(int B, int T, int H, int cus) {
+    return sched_workspace(plan_schedule(B * H, (T + CH - 1) / CH, cus), NK * NK + 2 * NK);
+}
+void launch_chunk_backward(const Bwd& p, int cus) {
+    const Sched sc = plan_schedule(p.B * p.H, (p.T + CH - 1) / CH, cus);
+    uint32_t* flags = nullptr;
+    float* hand = nullptr;
+    if (sched_cuts(sc)) {
+        flags = static_cast<uint32_t*>(p.ws);
+        hand = reinterpret_cast<float*>(static_cast<char*>(p.ws) + sched_flag_bytes(sc));
+        hipLaunchKernelGGL(clear_words, dim3(1), dim3(256), 0, p.stream, flags, sc.G);
+    }
+    hipLaunchKernelGGL(chunk_backward_bf16, dim3(sc.G), dim3(704), 0, p.stream, sc, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
                        (const bf16_t*)p.a, (const bf16_t*)p.b, p.ckpt, (const bf16_t*)p.dy, p.dsT,
                        (bf16_t*)p.dr, (bf16_t*)p.dw, (bf16_t*)p.dk, (bf16_t*)p.dv, (bf16_t*)p.da,
-                       (bf16_t*)p.db, p.ds0);
+                       (bf16_t*)p.db, p.ds0, flags, hand);
 }
 
 }  // namespace wkv7

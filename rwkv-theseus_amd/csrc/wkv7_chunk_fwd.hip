@@ -14,9 +14,12 @@
 // which is the step recurrence of theseus/wkv7.py:16-28 rewritten in the
 // WY / diagonal-plus-low-rank chunk form (exact in exact arithmetic).
 //
-// Mapping: one 512-lane workgroup per (b,h), two roles, lock-step "ticks"
-// that each end in one LDS barrier (no global-memory fence, so prefetches stay
-// in flight across it).
+// Mapping: 512-lane workgroups, one per CU, each running a stream of chunks
+// (b,h heads one after another, the first and last possibly cut pieces of a
+// head shared with another workgroup: wkv7_sched.h), two roles, lock-step
+// "ticks" that each end in one LDS barrier (no global-memory fence, so
+// prefetches stay in flight across it).  The producers' pipeline runs on across
+// head boundaries; only the consumers see them (initial and final state).
 //  * Producers (waves 0-3).  Everything above that does not involve the
 //    state depends only on the chunk's inputs, so producer p builds the
 //    operands of chunks p, p+4, p+8, ... alone -- no barrier inside -- in four
@@ -36,6 +39,7 @@
 //    chunk x-5).
 #include "wkv7_launch.h"
 #include "wkv7_io.h"
+#include "wkv7_sched.h"
 
 namespace wkv7 {
 namespace {
@@ -97,23 +101,27 @@ __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&
 }  // namespace
 
 __global__ __launch_bounds__(512) void chunk_forward_bf16(
-    int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
+    Sched sc, int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ k, const bf16_t* __restrict__ v, const bf16_t* __restrict__ a,
     const bf16_t* __restrict__ b, const float* __restrict__ s0, bf16_t* __restrict__ y,
-    float* __restrict__ sT, float* __restrict__ ckpt) {
+    float* __restrict__ sT, float* __restrict__ ckpt, uint32_t* __restrict__ flags, float* __restrict__ hand) {
     __shared__ FwdLds sm;
-    const int bh = blockIdx.x, bb = bh / H, h = bh % H;
+    const int m = machine_of_block(sc), nstream = stream_len(sc, m);
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
     const long ncp = ckpt_count(Tn);
-    const int nchunk = (Tn + CH - 1) / CH;
     const bool producer = wv < NPROD;
     const int pw = wv, cw = wv - NPROD;
-    const long rstride = (long)H * NK;                                  // between consecutive tokens of one head
-    const uint32_t tbytes = (uint32_t)((long)gridDim.x * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
-    auto chunk_off = [&](int cc) { return (uint32_t)(((long)(bb * Tn + cc * CH) * H + h) * NK * 2); };
-    auto chunk_len = [&](int cc) { return min(CH, Tn - cc * CH); };
+    const long rstride = (long)H * NK;                              // between consecutive tokens of one head
+    const uint32_t tbytes = (uint32_t)((long)sc.J * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
+    // stream index -> byte offset of the chunk's first row, its valid length
+    auto chunk_off = [&](int x) {
+        const int2 jc = stream_at(sc, m, x);
+        const int bb = jc.x / H, h = jc.x - bb * H;
+        return (uint32_t)(((long)(bb * Tn + jc.y * CH) * H + h) * NK * 2);
+    };
+    auto chunk_len = [&](int x) { return min(CH, Tn - stream_at(sc, m, x).y * CH); };
 
     // ---------------- producer state ----------------
     uint32_t voff[2];  // this lane's LDS DMA offsets
@@ -181,34 +189,23 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     const int i_own = 16 * cw + r16;
     f32x4_t St[4];
     if (producer) {
-        // this producer's first chunk (only the last chunk of the sequence can be partial)
-        if (pw < nchunk) {
+        // this producer's first chunk
+        if (pw < nstream) {
 #pragma unroll
             for (int ts = 0; ts < 5; ts++)
                 stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(pw), voff, rstride,
                             chunk_len(pw), lane);
         }
-    } else {
-#pragma unroll
-        for (int tj = 0; tj < 4; tj++) {
-            const long off = bh * NN + (long)i_own * NK + 16 * tj + 4 * q;
-            const float4 x = *reinterpret_cast<const float4*>(s0 + off);
-            St[tj] = f32x4_t{x.x, x.y, x.z, x.w};
-            if (ckpt) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + (long)i_own * NK + 16 * tj + 4 * q) = x;
-        }
-        // nothing else is loaded by consumers: drain here so the tick loop never
-        // waits on the (in-order) memory counter, which also counts its stores
-        vm_wait0();
     }
 
     // The two roles run separate tick loops with the same barriers, so that
     // registers and memory-counter waits are allocated per role.
     if (producer) {
-        for (int n = -NPROD; n < nchunk; n++) {
+        for (int n = -NPROD; n < nstream; n++) {
             // the chunk this producer works on at tick n (x = pw mod 4), and its phase
             const int x = n + 1 + ((pw - n - 1) & 3);
             const int ph = n + NPROD - x;
-            if (x >= 0 && x < nchunk) {  // (prologue ticks have no chunk for some producers)
+            if (x >= 0 && x < nstream) {  // (prologue ticks have no chunk for some producers)
                 Slot& S = sm.slot[x % NSLOT];
                 Plane* raw = sm.raw[pw];
                 if (ph == 0) {
@@ -258,7 +255,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                         BrkT = mm_keys8(kbh, kbl, rth, rtl);
                     }
                     wave_lds_fence();  // staging reads done before the DMA overwrites them
-                    if (x + NPROD < nchunk) {
+                    if (x + NPROD < nstream) {
 #pragma unroll
                         for (int ts = 0; ts < 5; ts++)
                             stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(x + NPROD),
@@ -300,7 +297,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                         st8_sw<SwLane>(S.P2[1], r16, 16 * tj + 4 * q, p2.l);
                     }
                     // V (phase 0) was followed only by the 10 staging DMA ops of phase 2
-                    if (x + NPROD < nchunk) vm_wait10();
+                    if (x + NPROD < nstream) vm_wait10();
                     else vm_wait0();
                 }
             }
@@ -308,10 +305,34 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
         }
     } else {
         for (int n = -NPROD; n < 0; n++) lds_barrier();
-        for (int n = 0; n < nchunk; n++) {
-            // ---------------- consumer: rows i_own through chunk n ----------------
+        // one segment (a head's piece) after another; tick n counts the stream
+        const int jlast = (m * sc.L + nstream - 1) / sc.n;
+        int n = 0;
+        for (int j = m * sc.L / sc.n; j <= jlast; j++) {
+          const Seg sg = seg_of(sc, m, j);
+          const int bb = j / H, h = j - bb * H;
+          const long bh = j;
+          {  // the initial state: s0 at the head's start, else the handoff of boundary m + 1
+            const float* src = s0 + bh * NN;
+            bool ok = true;
+            if (!sg.fresh) {
+                ok = handoff_wait(flags + m + 1, 4);
+                src = hand + (m + 1) * NN;
+            }
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++) {
+                const long off = (long)i_own * NK + 16 * tj + 4 * q;
+                float4 x = *reinterpret_cast<const float4*>(src + off);
+                if (!ok) x = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+                St[tj] = f32x4_t{x.x, x.y, x.z, x.w};
+                if (ckpt && sg.fresh) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + off) = x;
+            }
+          }
+          for (int kk = 0; kk < sg.count; kk++, n++) {
+            // ---------------- consumer: rows i_own through chunk c of head j ----------------
             const Slot& S = sm.slot[n % NSLOT];
-            const int t0 = n * CH, L = min(CH, Tn - t0);
+            const int c = sg.step0 + kk;
+            const int t0 = c * CH, L = min(CH, Tn - t0);
             f32x4_t sa = zero4(), yy = zero4();
 #pragma unroll
             for (int s = 0; s < 2; s++) {  // K = 64 over keys in two permuted K=32 steps
@@ -362,22 +383,37 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             if (ckpt) {
 #pragma unroll
                 for (int tj = 0; tj < 4; tj++)
-                    *reinterpret_cast<float4*>(ckpt + (bh * ncp + n + 1) * NN + (long)i_own * NK + 16 * tj + 4 * q) =
+                    *reinterpret_cast<float4*>(ckpt + (bh * ncp + c + 1) * NN + (long)i_own * NK + 16 * tj + 4 * q) =
                         make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
             }
             lds_barrier();
-        }
+          }
+          // the final state, or the handoff at boundary m
+          float* const dst = sg.handoff ? hand + m * NN : sT + bh * NN;
 #pragma unroll
-        for (int tj = 0; tj < 4; tj++)
-            *reinterpret_cast<float4*>(sT + bh * NN + (long)i_own * NK + 16 * tj + 4 * q) =
-                make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+          for (int tj = 0; tj < 4; tj++)
+              *reinterpret_cast<float4*>(dst + (long)i_own * NK + 16 * tj + 4 * q) =
+                  make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+          if (sg.handoff) handoff_signal(flags + m);
+        }
     }
 }
 
-void launch_chunk_forward(const Fwd& p) {
-    hipLaunchKernelGGL(chunk_forward_bf16, dim3(p.B * p.H), dim3(512), 0, p.stream, p.T, p.H,
+size_t chunk_forward_workspace(int B, int T, int H, int cus) {
+    return sched_workspace(plan_schedule(B * H, (T + CH - 1) / CH, cus), NK * NK);
+}
+void launch_chunk_forward(const Fwd& p, int cus) {
+    const Sched sc = plan_schedule(p.B * p.H, (p.T + CH - 1) / CH, cus);
+    uint32_t* flags = nullptr;
+    float* hand = nullptr;
+    if (sched_cuts(sc)) {
+        flags = static_cast<uint32_t*>(p.ws);
+        hand = reinterpret_cast<float*>(static_cast<char*>(p.ws) + sched_flag_bytes(sc));
+        hipLaunchKernelGGL(clear_words, dim3(1), dim3(256), 0, p.stream, flags, sc.G);
+    }
+    hipLaunchKernelGGL(chunk_forward_bf16, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
-                       (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, p.ckpt);
+                       (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, p.ckpt, flags, hand);
 }
 
 }  // namespace wkv7

@@ -16,6 +16,7 @@ struct Fwd {
     void* y;
     float* sT;
     float* ckpt;  // may be null
+    void* ws;     // workspace (the chunked kernels' handoffs)
     hipStream_t stream;
 };
 
@@ -43,13 +44,17 @@ void launch_seq_forward(const Fwd& p);
 void launch_seq_backward(const Bwd& p);
 size_t seq_backward_workspace(int B, int H, int N);
 void launch_decode(const Dec& p);
-void launch_chunk_forward(const Fwd& p);   // bf16, N == 64
-void launch_chunk_backward(const Bwd& p);  // bf16, N == 64
+// bf16, N == 64; `cus` = CUs the schedule spreads the heads over
+void launch_chunk_forward(const Fwd& p, int cus);
+void launch_chunk_backward(const Bwd& p, int cus);
+size_t chunk_forward_workspace(int B, int T, int H, int cus);
+size_t chunk_backward_workspace(int B, int T, int H, int cus);
 
 // Family dispatch (wkv7_capi.cpp): the chunked MFMA kernels when they cover
 // the call, else the step-serial ones.
 void launch_forward(const Fwd& p);
 void launch_backward(const Bwd& p);
+size_t forward_workspace(int B, int T, int H, int N, int dtype);
 size_t backward_workspace(int B, int T, int H, int N, int dtype);
 
 }  // namespace wkv7

@@ -1,0 +1,107 @@
+// Load-balanced schedule of the chunked WKV7 kernels over the CUs.
+//
+// A job is one (b, h) head: n chunks that must be processed in order (forward:
+// chunk 0 first; backward: chunk n-1 first).  The kernels keep one workgroup
+// per CU (their LDS use admits no second), so J > CUs jobs of one workgroup
+// each would run in ceil(J / CUs) rounds, the last one mostly idle (320 heads on
+// 256 CUs: two rounds for 1.25 rounds of work).
+//
+// Instead the J*n (job, chunk) units are laid end to end, job after job, and
+// "machine" m owns the global positions [m L, (m+1) L) with
+// L = max(n, ceil(J n / CUs)) (wrap-around, McNaughton's rule).  A job that
+// crosses the boundary m L is cut in two and rotated: its FIRST steps are the
+// positions at the start of machine m, its LAST steps the positions at the end
+// of machine m-1.  Machine m runs its first piece at local times [0, e) and
+// hands the job's carried state over at step e; machine m-1 reaches that job's
+// last piece at local time L - (n - e) >= e, so with machines moving at equal
+// speed the handoff is ready L - n ticks before it is needed.  Every machine
+// holds at most two cut pieces (one at each end), whole jobs in between.
+//
+// Machine m runs as workgroup G-1-m, so a waiting piece's workgroup has a
+// higher index than the one it waits on: workgroups are dispatched in index
+// order, so the awaited workgroup is already running (or done) whenever a
+// waiter spins, whatever the number of CUs free.  The wait is bounded all the
+// same (a missing handoff poisons the state with NaN instead of hanging).
+//
+// Handoffs go through a caller workspace: one 32-bit counter per boundary
+// (zeroed by clear_words on the same stream before the kernel) and the carried
+// state.  Every consumer wave of the handing workgroup stores its part,
+// releases it at agent scope and counts itself in; the waiting waves acquire
+// once the count is complete.
+#pragma once
+
+#include "wkv7_common.h"
+
+namespace wkv7 {
+
+struct Sched {
+    int J;  // jobs (B*H)
+    int n;  // chunks per job
+    int L;  // positions per machine
+    int G;  // machines = workgroups
+};
+
+__host__ __device__ inline Sched plan_schedule(int J, int n, int cus) {
+    const long total = (long)J * n, per = (total + cus - 1) / cus;
+    const int L = (int)(per > n ? per : n);
+    return Sched{J, n, L, (int)((total + L - 1) / L)};
+}
+// some job is cut in two (L a multiple of n places whole jobs only)
+__host__ __device__ inline bool sched_cuts(const Sched& s) { return s.L % s.n != 0; }
+// workspace: the boundary counters (256-byte aligned), then `per` floats per boundary
+__host__ __device__ inline size_t sched_flag_bytes(const Sched& s) { return ((size_t)s.G * 4 + 255) / 256 * 256; }
+__host__ __device__ inline size_t sched_workspace(const Sched& s, size_t per) {
+    return sched_cuts(s) ? sched_flag_bytes(s) + (size_t)s.G * per * 4 : 0;
+}
+
+// One job's piece on one machine: steps [step0, step0 + count) of job `job`.
+struct Seg {
+    int job, step0, count;
+    bool fresh;    // starts the job (else it continues from the handoff at boundary m + 1)
+    bool handoff;  // hands the job over at boundary m (else it ends the job)
+};
+__device__ __forceinline__ Seg seg_of(const Sched& s, int m, int j) {
+    const int p0 = m * s.L, p1 = min(p0 + s.L, s.J * s.n), j0 = j * s.n;
+    const int lo = max(j0, p0), hi = min(j0 + s.n, p1);
+    Seg g;
+    g.job = j;
+    g.count = hi - lo;
+    g.handoff = lo > j0;                 // the job began at the end of machine m - 1: first steps here
+    g.fresh = g.handoff || hi == j0 + s.n;  // else: the job runs on into machine m + 1, last steps here
+    g.step0 = g.fresh ? 0 : s.n - g.count;
+    return g;
+}
+// stream index x of machine m -> (job, step)
+__device__ __forceinline__ int2 stream_at(const Sched& s, int m, int x) {
+    const int p = m * s.L + x, j = p / s.n;
+    const Seg g = seg_of(s, m, j);
+    return make_int2(j, g.step0 + p - max(j * s.n, m * s.L));
+}
+__device__ __forceinline__ int stream_len(const Sched& s, int m) { return min(s.L, s.J * s.n - m * s.L); }
+__device__ __forceinline__ int machine_of_block(const Sched& s) { return s.G - 1 - (int)blockIdx.x; }
+
+// This wave's handoff stores are done and visible at agent scope: count it in.
+__device__ __forceinline__ void handoff_signal(uint32_t* cnt) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait (bounded, about a second) until `target` waves have counted in, then
+// acquire their stores.  Returns false on time-out.
+__device__ __forceinline__ bool handoff_wait(const uint32_t* cnt, uint32_t target) {
+    for (int i = 0; i < (1 << 21); i++) {
+        if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            return true;
+        }
+        __builtin_amdgcn_s_sleep(8);
+    }
+    return false;
+}
+
+// zero `n` 32-bit words (the boundary counters; a kernel, not a memset, so the
+// sequence may be captured into a graph)
+__global__ static void clear_words(uint32_t* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+}  // namespace wkv7

@@ -79,9 +79,10 @@ class Extension:
         lib.theseus_wkv7_checkpoint_interval.restype = i32
         lib.theseus_wkv7_checkpoint_count.argtypes = [i32]
         lib.theseus_wkv7_checkpoint_count.restype = ctypes.c_longlong
-        lib.theseus_wkv7_backward_workspace_size.argtypes = [i32] * 5
-        lib.theseus_wkv7_backward_workspace_size.restype = sz
-        lib.theseus_wkv7_forward.argtypes = [i32] * 5 + [vp] * 10 + [vp]
+        for fn in (lib.theseus_wkv7_forward_workspace_size, lib.theseus_wkv7_backward_workspace_size):
+            fn.argtypes = [i32] * 5
+            fn.restype = sz
+        lib.theseus_wkv7_forward.argtypes = [i32] * 5 + [vp] * 10 + [vp, sz, vp]
         lib.theseus_wkv7_forward.restype = i32
         lib.theseus_wkv7_backward.argtypes = [i32] * 5 + [vp] * 16 + [vp, sz, vp]
         lib.theseus_wkv7_backward.restype = i32
@@ -130,10 +131,13 @@ class Extension:
                                     dtype=torch.float32, device=r.device)
             else:
                 saved = torch.empty((0,), dtype=torch.float32, device=r.device)
+            dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
+            ws_bytes = int(self.lib.theseus_wkv7_forward_workspace_size(B, T, H, N, dt))
+            ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=r.device)
             status = self.lib.theseus_wkv7_forward(
-                B, T, H, N, _BF16 if r.dtype == torch.bfloat16 else _FP32,
-                *map(_ptr, (r, w, k, v, a, b, s0, y, end)),
-                _ptr(saved) if save_history else ctypes.c_void_p(0), _stream(r.device))
+                B, T, H, N, dt, *map(_ptr, (r, w, k, v, a, b, s0, y, end)),
+                _ptr(saved) if save_history else ctypes.c_void_p(0), _ptr(ws),
+                ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)
         return [y, end, saved]
 

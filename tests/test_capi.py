@@ -49,7 +49,7 @@ def declared_arity(header=HEADER):
 def test_ctypes_bindings_match_header_arity():
     ext = W.extension()
     arity = declared_arity()
-    assert arity["theseus_wkv7_forward"] == 16 and arity["theseus_wkv7_backward"] == 24
+    assert arity["theseus_wkv7_forward"] == 18 and arity["theseus_wkv7_backward"] == 24
     for name, n in arity.items():
         fn = getattr(ext.lib, name)
         bound = len(fn.argtypes) if fn.argtypes is not None else 0
@@ -69,7 +69,7 @@ def test_timemix_abi_exported_and_bound_with_header_arity():
 
 def test_host_queries():
     ext = W.extension()
-    assert ext.abi_version == 1
+    assert ext.abi_version == 2
     assert ext.checkpoint_interval == 16
     lib = ext.lib
     assert ext.checkpoint_count(1) == 2
@@ -82,8 +82,43 @@ def test_host_queries():
     assert lib.theseus_wkv7_error_string(2) == b"expected BF16 or FP32"
     assert lib.theseus_wkv7_error_string(99) == b"unknown status"
     assert lib.theseus_wkv7_backward_workspace_size(1, 0, 1, 64, 0) == 0  # invalid T
-    assert lib.theseus_wkv7_backward_workspace_size(2, 32, 3, 64, 0) == 0  # chunked: none
+    assert lib.theseus_wkv7_forward_workspace_size(1, 0, 1, 64, 0) == 0
     assert lib.theseus_wkv7_backward_workspace_size(2, 32, 3, 64, 1) > 0   # step-serial replay
+    assert lib.theseus_wkv7_forward_workspace_size(2, 32, 3, 64, 1) == 0
+
+
+def test_schedule_workspace_follows_the_cu_count(monkeypatch):
+    """Chunked kernels: a workspace only when heads are cut between workgroups.
+
+    With c CUs, J = B*H heads of n chunks go L = max(n, ceil(J n / c)) to a
+    workgroup; a head is cut when L is not a multiple of n, and then every one
+    of the G = ceil(J n / L) workgroups has a 256-byte-aligned counter block
+    plus a handoff of N*N floats (forward) or N*N + 2N floats (backward).
+    """
+    lib = W.extension().lib
+    N = 64
+
+    def expect(B, T, H, cus, per):
+        n = -(-T // 16)
+        J = B * H
+        L = max(n, -(-J * n // cus))
+        if L % n == 0:
+            return 0
+        G = -(-J * n // L)
+        return -(-4 * G // 256) * 256 + G * per * 4
+
+    for B, T, H, cus in [(2, 32, 3, 6), (2, 32, 3, 5), (1, 100, 6, 4), (4, 2048, 80, 256),
+                         (4, 2048, 64, 256), (4, 2048, 80, 255), (1, 16, 7, 3), (3, 33, 5, 1)]:
+        monkeypatch.setenv("THESEUS_WKV7_CUS", str(cus))
+        f = lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0)
+        b = lib.theseus_wkv7_backward_workspace_size(B, T, H, N, 0)
+        assert f == expect(B, T, H, cus, N * N), (B, T, H, cus)
+        assert b == expect(B, T, H, cus, N * N + 2 * N), (B, T, H, cus)
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    # config 2: 320 heads of 128 chunks on 256 CUs -> L = 160, G = 256, cut
+    assert lib.theseus_wkv7_forward_workspace_size(4, 2048, 80, 64, 0) == 1024 + 256 * 4096 * 4
+    # 256 heads: one each, nothing cut
+    assert lib.theseus_wkv7_backward_workspace_size(4, 2048, 64, 64, 0) == 0
 
 
 @pytest.mark.parametrize("B,T,H,N,dtype,code", [
@@ -92,7 +127,7 @@ def test_host_queries():
 def test_c_abi_rejects_bad_arguments_without_launching(B, T, H, N, dtype, code):
     lib = W.extension().lib
     null = ctypes.c_void_p(0)
-    status = lib.theseus_wkv7_forward(B, T, H, N, dtype, *([null] * 10), null)
+    status = lib.theseus_wkv7_forward(B, T, H, N, dtype, *([null] * 11), 0, null)
     assert status == code
     status = lib.theseus_wkv7_backward(B, T, H, N, dtype, *([null] * 17), 0, null)
     assert status == code

@@ -202,6 +202,43 @@ def test_chunked_and_step_serial_families_agree(T, monkeypatch):
         assert rl < 5e-3, (name, rl)
 
 
+# -- the load-balanced schedule: heads cut between workgroups ---------------------------
+def _ext_fwd_bwd(inp):
+    ext = W.extension()
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
+    y, end, saved = ext.forward(*xs, s0, True)
+    grads = ext.backward(*xs, saved, inp["dy"].cuda(), inp["dsT"].cuda())
+    y_ng, end_ng, _ = ext.forward(*xs, s0, False)  # no saved states: handoffs through the workspace only
+    torch.cuda.synchronize()
+    return [y, end, saved] + list(grads) + [y_ng, end_ng]
+
+
+@pytest.mark.parametrize("B,T,H", [(2, 100, 3), (3, 33, 2), (1, 256, 5), (2, 16, 7)])
+def test_cut_schedule_is_bitwise_the_uncut_one(B, T, H, monkeypatch):
+    """THESEUS_WKV7_CUS=c plans the chunked kernels for c CUs: B*H heads of
+    ceil(T/16) chunks are spread over the workgroups and heads are cut between
+    two of them, which hand the fp32 state (and, backward, dL/dS and the decay
+    carries) over exactly.  Every output must equal the one-head-per-workgroup
+    run bit for bit -- partial chunks (T % 16 != 0) then fall mid-stream."""
+    print(f"  cut schedule B={B} T={T} H={H}", flush=True)
+    inp = wkv7_inputs(B, T, H, 64, seed=700 + T + H, dtype=torch.bfloat16, s0_std=0.1, with_dsT=True)
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "100000")  # one head per workgroup: nothing cut
+    base = _ext_fwd_bwd(inp)
+    names = ["y", "sT", "saved"] + NAMES[2:] + ["y_nograd", "sT_nograd"]
+    for cus in (1, 2, 3, 4, 5, 7):
+        monkeypatch.setenv("THESEUS_WKV7_CUS", str(cus))
+        got = _ext_fwd_bwd(inp)
+        for name, g, b in zip(names, got, base):
+            assert torch.equal(g, b), (cus, name, (g.float() - b.float()).abs().max().item())
+
+
+def test_cut_schedule_against_oracle(monkeypatch):
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "5")
+    _parity(2, 100, 3, 64, torch.bfloat16, seed=777)
+    _parity(3, 33, 2, 64, torch.bfloat16, seed=778)
+
+
 # -- operator semantics ----------------------------------------------------------------
 def test_backward_is_deterministic_and_dend_none_is_zero():
     inp = wkv7_inputs(2, 70, 3, 64, seed=5, dtype=torch.bfloat16, s0_std=0.1)
