@@ -454,16 +454,24 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
              // (Lane offsets at piece boundaries come from an opaque lane, so that they are
              // not kept in registers across the tick loop.)
             const int ln = opaque(lane0), row = 16 * cw + (ln & 15), col = 4 * (ln >> 4);
-            const float* src = sg.fresh ? (dsT ? dsT + (long)j * NN : nullptr) : hand + (m + 1) * NH;
-            const bool ok = sg.fresh || handoff_wait(flags + m + 1, NCONS);
-            const float bad = ok ? 1.f : __builtin_nanf("");
+            if (sg.fresh) {
 #pragma unroll
-            for (int tj = 0; tj < 4; tj++) {
-                float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (src) x = *reinterpret_cast<const float4*>(src + row * NK + 16 * tj + col);
-                Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w} * bad;
+                for (int tj = 0; tj < 4; tj++) {
+                    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (dsT) x = *reinterpret_cast<const float4*>(dsT + (long)j * NN + row * NK + 16 * tj + col);
+                    Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
+                }
+                carry = 0.f;
+            } else {
+                const float bad = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");
+                const float* src = hand + (m + 1) * NH;
+#pragma unroll
+                for (int tj = 0; tj < 4; tj++) {
+                    const float4 x = handoff_get4(src + row * NK + 16 * tj + col);
+                    Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w} * bad;
+                }
+                carry = handoff_get(src + NN + row) * bad;
             }
-            carry = sg.fresh ? 0.f : hand[(m + 1) * NH + NN + row];
           }
           for (int kk = 0; kk < sg.count; kk++, n++) {
             // (lane-derived addresses may stay in registers on this side)
@@ -581,14 +589,18 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
           }
           {  // ds0 at the head's start, or the handoff at boundary m (H and this side's carry)
             const int ln = opaque(lane0), row = 16 * cw + (ln & 15), col = 4 * (ln >> 4);
-            float* const dst = sg.handoff ? hand + m * NH : ds0 + (long)j * NN;
-#pragma unroll
-            for (int tj = 0; tj < 4; tj++)
-                *reinterpret_cast<float4*>(dst + row * NK + 16 * tj + col) =
-                    make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
             if (sg.handoff) {
-                if (col == 0) dst[NN + row] = carry;
+                float* const dst = hand + m * NH;
+#pragma unroll
+                for (int tj = 0; tj < 4; tj++)
+                    handoff_put4(dst + row * NK + 16 * tj + col, Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+                if (col == 0) handoff_put(dst + NN + row, carry);
                 handoff_signal(flags + m);
+            } else {
+#pragma unroll
+                for (int tj = 0; tj < 4; tj++)
+                    *reinterpret_cast<float4*>(ds0 + (long)j * NN + row * NK + 16 * tj + col) =
+                        make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
             }
           }
         }
@@ -652,8 +664,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 }
                 carry = p;
             } else {  // this side's carry from the handoff of boundary m + 1
-                const bool ok = handoff_wait(flags + m + 1, NCONS);
-                carry = ok ? hand[(m + 1) * NH + NN + NK + key] : __builtin_nanf("");
+                const float bad = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");
+                carry = handoff_get(hand + (m + 1) * NH + NN + NK + key) * bad;
             }
           }
           // the chunk after this piece's last: the next piece's first (or a repeat at the end)
@@ -764,7 +776,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
           }
           if (sg.handoff) {  // this side's carry at boundary m
               const int ln = opaque(lane0);
-              if (ln < 16) hand[m * NH + NN + NK + 16 * cw + ln] = carry;
+              if (ln < 16) handoff_put(hand + m * NH + NN + NK + 16 * cw + ln, carry);
               handoff_signal(flags + m);
           }
         }

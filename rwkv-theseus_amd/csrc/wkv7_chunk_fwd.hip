@@ -312,20 +312,20 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
           const Seg sg = seg_of(sc, m, j);
           const int bb = j / H, h = j - bb * H;
           const long bh = j;
-          {  // the initial state: s0 at the head's start, else the handoff of boundary m + 1
-            const float* src = s0 + bh * NN;
-            bool ok = true;
-            if (!sg.fresh) {
-                ok = handoff_wait(flags + m + 1, 4);
-                src = hand + (m + 1) * NN;
-            }
+          if (sg.fresh) {  // the initial state: s0 at the head's start ...
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
                 const long off = (long)i_own * NK + 16 * tj + 4 * q;
-                float4 x = *reinterpret_cast<const float4*>(src + off);
-                if (!ok) x = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+                const float4 x = *reinterpret_cast<const float4*>(s0 + bh * NN + off);
                 St[tj] = f32x4_t{x.x, x.y, x.z, x.w};
-                if (ckpt && sg.fresh) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + off) = x;
+                if (ckpt) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + off) = x;
+            }
+          } else {  // ... else the handoff of boundary m + 1
+            const float bad = handoff_wait(flags + m + 1, 4) ? 1.f : __builtin_nanf("");
+#pragma unroll
+            for (int tj = 0; tj < 4; tj++) {
+                const float4 x = handoff_get4(hand + (m + 1) * NN + (long)i_own * NK + 16 * tj + 4 * q);
+                St[tj] = f32x4_t{x.x, x.y, x.z, x.w} * bad;
             }
           }
           for (int kk = 0; kk < sg.count; kk++, n++) {
@@ -389,11 +389,12 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             lds_barrier();
           }
           // the final state, or the handoff at boundary m
-          float* const dst = sg.handoff ? hand + m * NN : sT + bh * NN;
 #pragma unroll
-          for (int tj = 0; tj < 4; tj++)
-              *reinterpret_cast<float4*>(dst + (long)i_own * NK + 16 * tj + 4 * q) =
-                  make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+          for (int tj = 0; tj < 4; tj++) {
+              const long off = (long)i_own * NK + 16 * tj + 4 * q;
+              if (sg.handoff) handoff_put4(hand + m * NN + off, St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+              else *reinterpret_cast<float4*>(sT + bh * NN + off) = make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+          }
           if (sg.handoff) handoff_signal(flags + m);
         }
     }
