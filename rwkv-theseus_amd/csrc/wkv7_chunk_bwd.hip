@@ -189,13 +189,11 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         const int2 js = stream_at(sc, m, x);
         return make_int2(js.x, nchunk - 1 - js.y);
     };
-    // byte offset of the chunk's first row, its valid length
-    auto chunk_off = [&](int x) {
-        const int2 jc = chunk_at(x);
-        const int bb = jc.x / H, h = jc.x - bb * H;
-        return (uint32_t)(((long)(bb * Tn + jc.y * CH) * H + h) * NK * 2);
+    // stream position (cursor) -> byte offset of the chunk's first row, its valid length
+    auto chunk_off = [&](const Cursor& cu) {
+        return (uint32_t)(((long)(cu.bb * Tn + (nchunk - 1 - cu.step) * CH) * H + cu.h) * NK * 2);
     };
-    auto chunk_len = [&](int x) { return min(CH, Tn - chunk_at(x).y * CH); };
+    auto chunk_len = [&](const Cursor& cu) { return min(CH, Tn - (nchunk - 1 - cu.step) * CH); };
     const uint32_t tbytes = (uint32_t)((long)sc.J * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
     // byte offset for the 8-byte row piece of a D-layout tile of chunk cc of head (bb, h):
     // lane (q, 4m + jj) stores row 4q + jj, columns 16 cw + 4m .. +3 (rows past the end: dropped)
@@ -301,15 +299,17 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         uint32_t voff[2];  // this lane's LDS DMA offsets
         dma_lane_offsets(voff, rstride, lane);
         const bf16_t* const rsrc_src[5] = {r, w, k, a, b};
+        // this producer's current chunk (stream index x = pw mod 3) and its next
+        Cursor cx = cursor_at(sc, m, pw, H), cy = cursor_at(sc, m, pw + NPROD, H);
         if (pw < nstream) {
             // the first chunk of each producer; stream index 0's V, dY go into its slot here too
 #pragma unroll
             for (int ts = 0; ts < 5; ts++)
-                stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(pw), voff, rstride,
-                            chunk_len(pw), lane);
+                stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], chunk_off(cx), voff, rstride,
+                            chunk_len(cx), lane);
             if (pw == 0) {
-                stage_plane(sm.slot[0].V, dma_rsrc(v, tbytes), v, chunk_off(0), voff, rstride, chunk_len(0), lane);
-                stage_plane(sm.slot[0].dY, dma_rsrc(dy, tbytes), dy, chunk_off(0), voff, rstride, chunk_len(0), lane);
+                stage_plane(sm.slot[0].V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride, chunk_len(cx), lane);
+                stage_plane(sm.slot[0].dY, dma_rsrc(dy, tbytes), dy, chunk_off(cx), voff, rstride, chunk_len(cx), lane);
             }
         }
         lds_barrier();
@@ -324,7 +324,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 if (part == 0) {
                     // ---- phase 0: log-decays and their cumulative sum ----
                     vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
-                    const int L = chunk_len(x);
+                    const int L = chunk_len(cx);
 #pragma unroll
                     for (int hf = 0; hf < 2; hf++) {
                         const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
@@ -350,15 +350,15 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     put_operands(S, 1, o);
                     dma_lane_offsets(voff, rstride, lane);
                     if (x > 0) {  // (stream index 0's V, dY were staged before the loop)
-                        const uint32_t o = chunk_off(x);
-                        const int L = chunk_len(x);
+                        const uint32_t o = chunk_off(cx);
+                        const int L = chunk_len(cx);
                         stage_plane(S.V, dma_rsrc(v, tbytes), v, o, voff, rstride, L, lane);
                         stage_plane(S.dY, dma_rsrc(dy, tbytes), dy, o, voff, rstride, L, lane);
                     }
                     wave_lds_fence();  // staging reads done before the DMA overwrites it
                     if (x + NPROD < nstream) {
-                        const uint32_t o = chunk_off(x + NPROD);
-                        const int L = chunk_len(x + NPROD);
+                        const uint32_t o = chunk_off(cy);
+                        const int L = chunk_len(cy);
 #pragma unroll
                         for (int ts = 0; ts < 5; ts++)
                             stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], o, voff, rstride, L, lane);
@@ -430,6 +430,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
             const int ph = n + NPROD - x;
             const bool pact = x >= 0 && x < nstream;
+            if (ph == 0 && x > pw) {  // on to the next chunk
+                cx = cy;
+                cursor_advance(cy, sc, m, NPROD, H);
+            }
             if (pact) {
                 produce(x, ph, 0);
                 produce(x, ph, 1);

@@ -115,18 +115,18 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     const int pw = wv, cw = wv - NPROD;
     const long rstride = (long)H * NK;                              // between consecutive tokens of one head
     const uint32_t tbytes = (uint32_t)((long)sc.J * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
-    // stream index -> byte offset of the chunk's first row, its valid length
-    auto chunk_off = [&](int x) {
-        const int2 jc = stream_at(sc, m, x);
-        const int bb = jc.x / H, h = jc.x - bb * H;
-        return (uint32_t)(((long)(bb * Tn + jc.y * CH) * H + h) * NK * 2);
+    // stream position (cursor) -> byte offset of the chunk's first row, its valid length
+    auto chunk_off = [&](const Cursor& cu) {
+        return (uint32_t)(((long)(cu.bb * Tn + cu.step * CH) * H + cu.h) * NK * 2);
     };
-    auto chunk_len = [&](int x) { return min(CH, Tn - stream_at(sc, m, x).y * CH); };
+    auto chunk_len = [&](const Cursor& cu) { return min(CH, Tn - cu.step * CH); };
 
     // ---------------- producer state ----------------
     uint32_t voff[2];  // this lane's LDS DMA offsets
     dma_lane_offsets(voff, rstride, lane);
     const bf16_t* const src5[5] = {r, w, k, a, b};
+    // this producer's current chunk (stream index x = pw mod 4) and its next
+    Cursor cx = cursor_at(sc, m, pw, H), cy = cursor_at(sc, m, pw + NPROD, H);
     float g1[8];  // cumulative log-decay, keys 32 + 8q + e (phase 0 -> 1)
     Pk pTiT, pB;  // Ti^T, Brb^T packed (phase 2 -> 3)
 
@@ -193,8 +193,8 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
         if (pw < nstream) {
 #pragma unroll
             for (int ts = 0; ts < 5; ts++)
-                stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(pw), voff, rstride,
-                            chunk_len(pw), lane);
+                stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(cx), voff, rstride,
+                            chunk_len(cx), lane);
         }
     }
 
@@ -205,6 +205,10 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             // the chunk this producer works on at tick n (x = pw mod 4), and its phase
             const int x = n + 1 + ((pw - n - 1) & 3);
             const int ph = n + NPROD - x;
+            if (ph == 0 && x > pw) {  // on to the next chunk
+                cx = cy;
+                cursor_advance(cy, sc, m, NPROD, H);
+            }
             if (x >= 0 && x < nstream) {  // (prologue ticks have no chunk for some producers)
                 Slot& S = sm.slot[x % NSLOT];
                 Plane* raw = sm.raw[pw];
@@ -212,8 +216,8 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                     // ---- phase 0: log-decays and their cumulative sum; V by LDS DMA;
                     //      the operands of keys 0-31 ----
                     vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
-                    stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(x), voff, rstride, chunk_len(x), lane);
-                    const int L = chunk_len(x);
+                    const int L = chunk_len(cx);
+                    stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride, L, lane);
                     float g0[8];
 #pragma unroll
                     for (int hf = 0; hf < 2; hf++) {
@@ -258,8 +262,8 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                     if (x + NPROD < nstream) {
 #pragma unroll
                         for (int ts = 0; ts < 5; ts++)
-                            stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(x + NPROD),
-                                        voff, rstride, chunk_len(x + NPROD), lane);
+                            stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(cy),
+                                        voff, rstride, chunk_len(cy), lane);
                     }
 #pragma unroll
                     for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16

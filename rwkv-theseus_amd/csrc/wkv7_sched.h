@@ -89,6 +89,31 @@ __device__ __forceinline__ int2 stream_at(const Sched& s, int m, int x) {
 __device__ __forceinline__ int stream_len(const Sched& s, int m) { return min(s.L, s.J * s.n - m * s.L); }
 __device__ __forceinline__ int machine_of_block(const Sched& s) { return s.G - 1 - (int)blockIdx.x; }
 
+// A stream position as (job j = bb H + h, offset r = p - j n within the job's n
+// positions, and the job's step there), advanced without division: a producer
+// wave visits every NPROD-th position and keeps a cursor on its current chunk
+// and one on its next.
+struct Cursor {
+    int j, r, bb, h, step;
+};
+// the step of job j at offset r within it on machine m (as stream_at)
+__device__ __forceinline__ int step_of(const Sched& s, int m, int j, int r) {
+    return seg_of(s, m, j).step0 + r - max(0, m * s.L - j * s.n);
+}
+__device__ __forceinline__ Cursor cursor_at(const Sched& s, int m, int x, int H) {
+    const int p = m * s.L + x, j = p / s.n, r = p - j * s.n;
+    return Cursor{j, r, j / H, j % H, step_of(s, m, j, r)};
+}
+__device__ __forceinline__ void cursor_advance(Cursor& c, const Sched& s, int m, int k, int H) {
+    c.r += k;
+    while (c.r >= s.n) {
+        c.r -= s.n;
+        c.j++;
+        if (++c.h == H) c.h = 0, c.bb++;
+    }
+    c.step = step_of(s, m, c.j, c.r);
+}
+
 // handoff words: agent-scope atomic stores / loads only
 __device__ __forceinline__ void handoff_put(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
