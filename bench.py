@@ -139,8 +139,8 @@ def cpu_baseline(B, H, N, T_slice, seed, budget_s=12.0, T_total=2048):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-slice", type=int, default=256, help="T of each CPU baseline slice (0: skip)")
     ap.add_argument("--timemix-unfused", action="store_true",
