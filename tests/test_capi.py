@@ -133,6 +133,22 @@ def test_c_abi_rejects_bad_arguments_without_launching(B, T, H, N, dtype, code):
     assert status == code
 
 
+def test_c_abi_rejects_a_small_workspace_without_launching(monkeypatch):
+    """With heads cut between workgroups the chunked kernels need the workspace;
+    a smaller one is refused before anything is enqueued (THESEUS_WKV7_ERR_WORKSPACE)."""
+    lib = W.extension().lib
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "5")
+    B, T, H, N = 2, 100, 3, 64
+    need_f = lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0)
+    need_b = lib.theseus_wkv7_backward_workspace_size(B, T, H, N, 0)
+    assert need_f > 0 and need_b > 0
+    p = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    null = ctypes.c_void_p(0)
+    assert lib.theseus_wkv7_forward(B, T, H, N, 0, *([p] * 9), null, p, need_f - 1, null) == 4
+    assert lib.theseus_wkv7_forward(B, T, H, N, 0, *([p] * 9), null, null, need_f, null) == 4
+    assert lib.theseus_wkv7_backward(B, T, H, N, 0, *([p] * 8), null, *([p] * 7), p, need_b - 1, null) == 4
+
+
 def test_backend_errors_match_reference():
     x = torch.zeros(1, 2, 1, 4)
     s = torch.zeros(1, 1, 4, 4)
