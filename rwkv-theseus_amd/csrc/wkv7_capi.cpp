@@ -60,7 +60,11 @@ static int cu_count() {
 }
 
 void launch_forward(const Fwd& p) {
-    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_forward(p, cu_count());
+    if (p.T == 1 && !p.ckpt && !force_seq()) {
+        // one step without saved states (the serving step through the operator):
+        // the single-step kernel, s0 -> sT
+        launch_decode(Dec{p.B, p.H, p.N, p.dtype, p.r, p.w, p.k, p.v, p.a, p.b, p.s0, p.sT, p.y, p.stream});
+    } else if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_forward(p, cu_count());
     else launch_seq_forward(p);
 }
 void launch_backward(const Bwd& p) {
@@ -145,7 +149,7 @@ int theseus_wkv7_decode_step(int B, int H, int N, int dtype, const void* r, cons
                              float* state, void* y, hipStream_t stream) {
     if (int e = check_dims(B, 1, H, N, dtype)) return e;
     if (!r || !w || !k || !v || !a || !b || !state || !y) return THESEUS_WKV7_ERR_NULL;
-    wkv7::Dec p{B, H, N, dtype, r, w, k, v, a, b, state, y, stream};
+    wkv7::Dec p{B, H, N, dtype, r, w, k, v, a, b, state, state, y, stream};
     wkv7::launch_decode(p);
     return launch_status();
 }

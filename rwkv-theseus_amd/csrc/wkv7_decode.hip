@@ -1,5 +1,7 @@
-// Single-step (T = 1) WKV7 update with the fp32 state read and written in
-// place -- the serving step.  HBM-bound: per (b,h) it moves 2*N*N*4 bytes of
+// Single-step (T = 1) WKV7 update -- the serving step: the fp32 state is read
+// from s_in and the new state written to s_out, which may be the same buffer
+// (in place: each lane reads its state elements before it writes them, and no
+// lane touches another's).  HBM-bound: per (b,h) it moves 2*N*N*4 bytes of
 // state and 7*N token values.
 //
 // One 256-lane workgroup per (b,h).  Each value row is handled by a 16-lane
@@ -14,12 +16,13 @@ template <typename T, int VEC, int NP>
 __global__ __launch_bounds__(256) void decode_step(
     int H, int N, const T* __restrict__ r, const T* __restrict__ w, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ a, const T* __restrict__ b,
-    float* __restrict__ state, T* __restrict__ y) {
+    const float* s_in, float* s_out, T* __restrict__ y) {
     constexpr int MM = (NP + 16 * VEC - 1) / (16 * VEC);  // key groups per lane
     const int bh = blockIdx.x;
     const int l16 = threadIdx.x & 15, grp = threadIdx.x >> 4;
     const long o = (long)bh * N;  // token vectors of this (b,h): T = 1
-    float* S = state + (long)bh * N * N;
+    const float* S = s_in + (long)bh * N * N;
+    float* So = s_out + (long)bh * N * N;
 
     float kr[MM][VEC], kd[MM][VEC], kk[MM][VEC], ka[MM][VEC], kb[MM][VEC];
 #pragma unroll
@@ -79,12 +82,12 @@ __global__ __launch_bounds__(256) void decode_step(
             const int j0 = VEC * (l16 + 16 * m);
             if constexpr (VEC == 4) {
                 if (row && j0 < N)
-                    *reinterpret_cast<float4*>(S + (long)i * N + j0) =
+                    *reinterpret_cast<float4*>(So + (long)i * N + j0) =
                         make_float4(s[m][0], s[m][1], s[m][2], s[m][3]);
             } else {
 #pragma unroll
                 for (int e = 0; e < VEC; e++)
-                    if (row && j0 + e < N) S[(long)i * N + j0 + e] = s[m][e];
+                    if (row && j0 + e < N) So[(long)i * N + j0 + e] = s[m][e];
             }
         }
     }
@@ -102,13 +105,13 @@ static void decode_t(const Dec& p) {
     if (p.N % 4 == 0) {
         if (p.N <= 64)
             hipLaunchKernelGGL((decode_step<T, 4, 64>), grid, block, 0, p.stream, p.H, p.N, (const T*)p.r,
-                               (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state, (T*)p.y);
+                               (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state_in, p.state, (T*)p.y);
         else
             hipLaunchKernelGGL((decode_step<T, 4, 128>), grid, block, 0, p.stream, p.H, p.N, (const T*)p.r,
-                               (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state, (T*)p.y);
+                               (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state_in, p.state, (T*)p.y);
     } else {
         hipLaunchKernelGGL((decode_step<T, 1, 128>), grid, block, 0, p.stream, p.H, p.N, (const T*)p.r,
-                           (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state, (T*)p.y);
+                           (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state_in, p.state, (T*)p.y);
     }
 }
 

@@ -35,7 +35,8 @@ struct Bwd {
 struct Dec {
     int B, H, N, dtype;
     const void *r, *w, *k, *v, *a, *b;
-    float* state;
+    const float* state_in;  // read; may equal state
+    float* state;           // written
     void* y;
     hipStream_t stream;
 };

@@ -208,6 +208,47 @@ def test_cuda_inference_chunking_and_current_stream():
 
 
 @gpu
+def test_cuda_token_by_token_decode_matches_one_call():
+    """Serving: the reference's Runner steps each TimeMix one token at a time with the
+    carried {"shift", "wkv"} state (theseus/hf_model.py:96-108); on backend="cuda" every
+    such step is a T=1 no-grad call, which runs the single-step kernel."""
+    torch.manual_seed(5)
+    model = TimeMix(256, 2, 6, head_size=64, backend="cuda").cuda().to(torch.bfloat16)
+    torch.nn.init.normal_(model.output.weight, std=.02)
+    x = torch.randn(2, 24, 256, device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        full, final = model(x)
+        state, outs = None, []
+        for t in range(x.shape[1]):
+            y, state = model(x[:, t:t + 1], state)
+            outs.append(y)
+    torch.testing.assert_close(torch.cat(outs, 1), full, atol=.006, rtol=.025)
+    torch.testing.assert_close(state["wkv"], final["wkv"], atol=.0005, rtol=.02)
+    assert torch.equal(state["shift"], final["shift"])
+
+
+@gpu
+def test_state_resumes_across_backends():
+    """The carried state has the reference's format ({"shift": [B,C] in x's dtype,
+    "wkv": [B,H,value,key] fp32}, theseus/checkpoint.py:100-102, the export's
+    state_layout "B,H,value,key"): a prefix run on the reference backend (CPU, fp32)
+    resumes on the HIP backend and matches the reference continuing itself."""
+    torch.manual_seed(6)
+    ref = TimeMix(128, 1, 4, head_size=64, backend="reference")
+    torch.nn.init.normal_(ref.output.weight, std=.05)
+    dev = TimeMix(128, 1, 4, head_size=64, backend="cuda").cuda()
+    dev.load_state_dict(ref.state_dict())
+    x = torch.randn(2, 20, 128)
+    _, st = ref(x[:, :12])
+    y_ref, st_ref = ref(x[:, 12:], st)
+    assert set(st) == {"shift", "wkv"} and st["wkv"].shape == (2, 2, 64, 64) and st["wkv"].dtype == torch.float32
+    with torch.no_grad():
+        y_dev, st_dev = dev(x[:, 12:].cuda(), {k: v.cuda() for k, v in st.items()})
+    assert rel_l2(y_dev.cpu(), y_ref.detach()) < 2e-3
+    assert rel_l2(st_dev["wkv"].cpu(), st_ref["wkv"].detach()) < 2e-3
+
+
+@gpu
 def test_cuda_fp32_optimizer_states_and_learning():
     model = TimeMix(128, 3, 8, head_size=64, backend="cuda").cuda()
     optimizer = torch.optim.AdamW(model.parameters(), lr=.003)

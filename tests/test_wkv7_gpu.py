@@ -184,6 +184,33 @@ def test_config4_decode_full_size():
     _check("sT", state[:2], s_ref, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N", [64, 8])
+def test_single_step_forward_runs_the_serving_step(dtype, N):
+    """A T=1 forward without saved states (the no-grad step TimeMix makes while
+    serving, theseus/wkv7.py:67-69) runs the single-step kernel out of place:
+    s0 is left untouched, and y, sT equal the in-place decode step bit for bit and
+    the float64 oracle; the chunked T=1 path (with saved states) agrees."""
+    B, H = 3, 4
+    inp = wkv7_inputs(B, 1, H, N, seed=4100 + N, dtype=dtype, s0_std=0.1)
+    ext = W.extension()
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
+    s0_copy = s0.clone()
+    y, end, saved = ext.forward(*xs, s0, False)
+    state = s0.clone()
+    y_dec = W.decode_step_(*xs, state)
+    y_hist, end_hist, _ = ext.forward(*xs, s0, True)
+    torch.cuda.synchronize()
+    assert saved.numel() == 0 and torch.equal(s0, s0_copy)
+    assert torch.equal(y, y_dec) and torch.equal(end, state)
+    y_ref, s_ref = O.forward(*(inp[n].double().numpy() for n in "rwkvab"), inp["s0"].double().numpy())
+    _check("y", y, y_ref, dtype)
+    _check("sT", end, s_ref, dtype)
+    torch.testing.assert_close(end, end_hist, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(y.float(), y_hist.float(), atol=2e-2, rtol=1e-2)
+
+
 # -- the two kernel families agree ----------------------------------------------------
 @pytest.mark.parametrize("T", [1, 15, 16, 17, 100, 512])
 def test_chunked_and_step_serial_families_agree(T, monkeypatch):
