@@ -21,6 +21,7 @@ boundary is never detached by this operator; callers detach (wkv7.py:5).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from functools import lru_cache
 from pathlib import Path
@@ -56,6 +57,17 @@ def reference(r, w, k, v, a, b, state):
 
 def _ptr(x):
     return ctypes.c_void_p(x.data_ptr()) if x is not None else ctypes.c_void_p(0)
+
+
+def _on(device):
+    """The device guard of kernels/wkv7_state.cpp:17,27 (a no-op when it is already current)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
+
+
+def _workspace(nbytes, device):
+    return (torch.empty((nbytes,), dtype=torch.uint8, device=device), nbytes) if nbytes else (None, 0)
 
 
 def _stream(device):
@@ -123,7 +135,7 @@ class Extension:
             raise RuntimeError("s0 must be contiguous CUDA FP32")
         if tuple(s0.shape) != (B, H, N, N):
             raise RuntimeError("invalid s0 shape")
-        with torch.cuda.device(r.device):
+        with _on(r.device):
             y = torch.empty_like(r)
             end = torch.empty_like(s0)
             if save_history:
@@ -132,8 +144,7 @@ class Extension:
             else:
                 saved = torch.empty((0,), dtype=torch.float32, device=r.device)
             dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
-            ws_bytes = int(self.lib.theseus_wkv7_forward_workspace_size(B, T, H, N, dt))
-            ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=r.device)
+            ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_forward_workspace_size(B, T, H, N, dt)), r.device)
             status = self.lib.theseus_wkv7_forward(
                 B, T, H, N, dt, *map(_ptr, (r, w, k, v, a, b, s0, y, end)),
                 _ptr(saved) if save_history else ctypes.c_void_p(0), _ptr(ws),
@@ -153,12 +164,11 @@ class Extension:
                                      and dend.is_contiguous()
                                      and tuple(dend.shape) == (B, H, N, N)):
             raise RuntimeError("invalid dend")
-        with torch.cuda.device(r.device):
+        with _on(r.device):
             grads = [torch.empty_like(r) for _ in range(6)]
             ds0 = torch.empty((B, H, N, N), dtype=torch.float32, device=r.device)
             dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
-            ws_bytes = int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N, dt))
-            ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=r.device)
+            ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N, dt)), r.device)
             status = self.lib.theseus_wkv7_backward(
                 B, T, H, N, dt,
                 *map(_ptr, (r, w, k, v, a, b, saved, dy, dend, *grads, ds0, ws)),
@@ -178,7 +188,7 @@ class Extension:
         if not (state.device == r.device and state.dtype == torch.float32
                 and state.is_contiguous() and tuple(state.shape) == (B, H, N, N)):
             raise RuntimeError("invalid state")
-        with torch.cuda.device(r.device):
+        with _on(r.device):
             y = torch.empty_like(r)
             status = self.lib.theseus_wkv7_decode_step(
                 B, H, N, _BF16 if r.dtype == torch.bfloat16 else _FP32,
