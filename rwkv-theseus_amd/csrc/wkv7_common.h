@@ -47,4 +47,19 @@ __device__ __forceinline__ float log_decay(float w) { return -DECAY_SCALE * sigm
 
 __host__ __device__ constexpr inline long ckpt_count(int T) { return (T + CKPT - 1) / CKPT + 1; }
 
+// Sum over each 16-lane row of the wave, left in every lane of the row: DPP
+// exchanges (quad_perm 1,0,3,2 and 2,3,0,1, then row_half_mirror and row_mirror),
+// so the data stays in the VALU (no LDS permute).  Fixed order: deterministic.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp_move<0xb1>(x);
+    x += dpp_move<0x4e>(x);
+    x += dpp_move<0x141>(x);
+    x += dpp_move<0x140>(x);
+    return x;
+}
+
 }  // namespace wkv7
