@@ -21,23 +21,27 @@
 // equal the step adjoint of kernels/wkv7_state.cu:52-78 (checked against it on
 // the CPU oracle in float64).
 //
-// Mapping: one 448-lane workgroup per (b,h), chunks in reverse, lock-step
-// ticks of two LDS barriers (no global-memory fence).
-//  * Producers (waves 4-6) build everything that depends only on a chunk's
-//    inputs -- A~, R~, B-, K-, g, e^{gL}, Ti, Aak, Brb, Brk, V dY^T -- one
+// Mapping: 704-lane workgroups, one per CU, each running a stream of chunks
+// (b,h heads one after another, chunks of a head in reverse; the first and last
+// pieces of a head may be shared with another workgroup: wkv7_sched.h), in
+// lock-step ticks that end in one LDS barrier (no global-memory fence).
+//  * Producers (waves 8-10) build everything that depends only on a chunk's
+//    inputs -- A~, R~, B-, K-, g, e^{gL}, Ti, Aak, Brb, Brk, triu(V dY^T) -- one
 //    chunk each, in three phases over the three ticks before it is consumed,
-//    into a 3-slot LDS ring (as the forward's producers do).  Their inputs
-//    arrive by LDS DMA (global_load_lds_dwordx4) two ticks ahead, so no
-//    prefetch registers are held across ticks.  Each phase is split in two
-//    parts, one run beside each consumer stage, so the producers' work spans
-//    the whole tick.
-//  * Consumers (waves 0-3).  Stage B: wave c owns value rows 16c..16c+15 of H
-//    in registers and computes SA, Q, dV and the new H for them; it publishes
-//    H', S0, Q^T and SA^T rows.  Barrier.  Stage C: wave c produces the key
-//    strip 16c..16c+15 of dK, dB, dR, dA and dw, contracting over all value
-//    rows in a fixed order (deterministic; the reference accumulates with fp32
-//    atomics, cu:68-72), reading the other orientation of every exchanged
-//    matrix with ds_read_b64_tr_b16.
+//    into a 3-slot LDS ring.  Their inputs arrive by LDS DMA two ticks ahead, so
+//    no prefetch registers are held across ticks.  Each phase is split in two
+//    parts (the second depends on DMA or on the first's registers).
+//  * Consumers, 8 waves in two sides.  The H side (waves 0-3: wave c owns value
+//    rows 16c..16c+15 of H = dL/dS in registers) forms H', Q and the first part
+//    of dV in stage B and publishes H' and Q^T rows; the S side (waves 4-7, the
+//    same rows of the saved state S0, loaded a tick ahead) forms SA and
+//    publishes SA^T rows.  The eight meet on an LDS counter (the producers do
+//    not take part); in stage C wave c of each side produces key strip
+//    16c..16c+15 of its gradients (H side dK, dB; S side dR, dA, dw) contracting
+//    over all value rows in a fixed order (deterministic; the reference
+//    accumulates with fp32 atomics, cu:68-72), reading the other orientation of
+//    each exchanged matrix with ds_read_b64_tr_b16; the H side also finishes dV
+//    and advances H to the previous chunk.
 #include "wkv7_launch.h"
 #include "wkv7_io.h"
 #include "wkv7_sched.h"
@@ -209,16 +213,23 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         float tot = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; e++) tot += z[e] + t2[e];
-        const float s1 = __shfl(tot, (lane & 15) + 16), s2 = __shfl(tot, (lane & 15) + 32),
-                    s3 = __shfl(tot, (lane & 15) + 48), s0 = __shfl(tot, lane & 15);
-        float run = carry + (q < 1 ? s1 : 0.f) + (q < 2 ? s2 : 0.f) + (q < 3 ? s3 : 0.f);
+        // the other lane groups' totals s_q' (same column) by row swaps in the VALU (gfx950
+        // permlane16/32_swap, layout checked with an in-bounds probe): od = s of the odd row
+        // of this lane's row pair, lo / hi = s0 + s1 / s2 + s3 in every lane
+        const uint32_t tb = __float_as_uint(tot);
+        const auto p16 = __builtin_amdgcn_permlane16_swap(tb, tb, false, false);
+        const float ev = __uint_as_float(p16[0]), od = __uint_as_float(p16[1]);
+        const uint32_t pb = __float_as_uint(ev + od);
+        const auto p32 = __builtin_amdgcn_permlane32_swap(pb, pb, false, false);
+        const float lo = __uint_as_float(p32[0]), hi = __uint_as_float(p32[1]);
+        float run = carry + ((q & 1) ? 0.f : od) + (q < 2 ? hi : 0.f);  // + sum over groups after q
 #pragma unroll
         for (int e = 3; e >= 0; e--) {
             run += z[e];
             gw[e] = run * fw[e];
             run += t2[e];
         }
-        carry += ((s0 + s1) + s2) + s3;
+        carry += lo + hi;
     };
     // the per-lane quantities of stage C that depend on the slot only:
     // [A~; R~] and [B-; K-] strips as K=32 B operands, g_t and g_{t-1} (t = 4q + e)
