@@ -260,6 +260,42 @@ def test_cut_schedule_is_bitwise_the_uncut_one(B, T, H, monkeypatch):
             assert torch.equal(g, b), (cus, name, (g.float() - b.float()).abs().max().item())
 
 
+def test_cut_schedules_on_concurrent_streams(monkeypatch):
+    """Calls on different streams, each with its own workspace, may overlap on the
+    device: their handoff counters and states never meet, so each matches the
+    same call made alone, bit for bit."""
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "3")
+    inps = [wkv7_inputs(2, 100, 3, 64, seed=901, dtype=torch.bfloat16, s0_std=0.1, with_dsT=True),
+            wkv7_inputs(3, 65, 2, 64, seed=902, dtype=torch.bfloat16, s0_std=0.1, with_dsT=True)]
+    alone = [_ext_fwd_bwd(inp) for inp in inps]
+    streams = [torch.cuda.Stream() for _ in inps]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    together = []
+    for _ in range(3):
+        outs = [None, None]
+        for i in (0, 1):
+            with torch.cuda.stream(streams[i]):
+                outs[i] = _ext_fwd_bwd_async(inps[i])
+        torch.cuda.synchronize()
+        together.append(outs)
+    for outs in together:
+        for got, ref in zip(outs, alone):
+            for g, r in zip(got, ref):
+                assert torch.equal(g, r)
+
+
+def _ext_fwd_bwd_async(inp):
+    """_ext_fwd_bwd without the final synchronisation (runs on the current stream)."""
+    ext = W.extension()
+    xs = [inp[n].cuda(non_blocking=False) for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
+    y, end, saved = ext.forward(*xs, s0, True)
+    grads = ext.backward(*xs, saved, inp["dy"].cuda(), inp["dsT"].cuda())
+    y_ng, end_ng, _ = ext.forward(*xs, s0, False)
+    return [y, end, saved] + list(grads) + [y_ng, end_ng]
+
+
 def test_cut_schedule_against_oracle(monkeypatch):
     monkeypatch.setenv("THESEUS_WKV7_CUS", "5")
     _parity(2, 100, 3, 64, torch.bfloat16, seed=777)
