@@ -79,7 +79,7 @@ struct Slot {
 struct BwdLds {
     uint16_t Hx[2][NK * NK];                     // H' [i][j] (swizzled)
     uint16_t QT[2][NK * LDQ], SAT[2][NK * LDQ];  // Q^T, SA^T [i][t]
-    float dlp[2][4][64 * 4];                     // H side's dw part of a chunk, per key strip (D layout)
+    float dlp[2][4][64 * 4];                     // H side's dlogd part (fw not applied), per key strip
     float dls[4][64 * 4];                        // S side's dw part of the previous chunk
     Slot slot[NPROD];
     Plane raw[NPROD][5];                         // producer input staging: r, w, k, a, b
@@ -232,7 +232,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         carry += lo + hi;
     };
     // the per-lane quantities of stage C that depend on the slot only:
-    // [A~; R~] and [B-; K-] strips as K=32 B operands, g_t and g_{t-1} (t = 4q + e)
+    // [A~; R~] and [B-; K-] strips as K=32 B operands, g_t (t = 4q + e); the S side
+    // also needs g_{t-1} and fw_t = d w_t / d logd_t (strip_fw)
     struct Strip {
         uint4 arh, arl, bkh, bkl;
         float gv[4], gp[4], fw[4];
@@ -244,14 +245,17 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         st.bkh = cat(ldtr_sw<SwLane>(S.Bb[0], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[0], 0, 16 * cw, lane));
         st.bkl = cat(ldtr_sw<SwLane>(S.Bb[1], 0, 16 * cw, lane), ldtr_sw<SwLane>(S.Kb[1], 0, 16 * cw, lane));
 #pragma unroll
+        for (int e = 0; e < 4; e++) st.gv[e] = S.g[(4 * q + e) * LDG + j_own];
+        return st;
+    };
+    auto strip_fw = [&](const Slot& S, Strip& st) {
+#pragma unroll
         for (int e = 0; e < 4; e++) {
             const int t = 4 * q + e;
-            st.gv[e] = S.g[t * LDG + j_own];
             st.gp[e] = t > 0 ? S.g[(t - 1) * LDG + j_own] : 0.f;
             const float sg = (st.gp[e] - st.gv[e]) * (1.f / DECAY_SCALE);  // sigmoid(w_t)
             st.fw[e] = -DECAY_SCALE * sg * (1.f - sg);
         }
-        return st;
     };
     auto new_tick = [&]() {  // lane-derived values, recomputed so they are not held across the loop
         lane = opaque(lane0);
@@ -584,7 +588,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const uint32_t o = piece_off(bb, h, c);
             store8(dk, tbytes, o, quad_rows_bf16(f32x4_t{gk_[0], gk_[1], gk_[2], gk_[3]}, lane));
             store8(db, tbytes, o, quad_rows_bf16(f32x4_t{gb_[0], gb_[1], gb_[2], gb_[3]}, lane));
-            dlogd_part(z, t2, st.fw, carry, gw_);
+            {  // this side's part of dlogd, unscaled (the S side multiplies the sum by fw)
+                const float one[4] = {1.f, 1.f, 1.f, 1.f};
+                dlogd_part(z, t2, one, carry, gw_);
+            }
             *reinterpret_cast<float4*>(&sm.dlp[n & 1][cw][4 * lane]) = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
             {  // dV = K- H'^T + Brk^T dY + Aak^T Q
                 const Pk brkT = mat_t(S.Brk, lane);
@@ -643,9 +650,13 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     ckr, vo + (m & 3) * NK * 4, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0));
         };
         // dw of a chunk (piece offset o) = this side's part + the H side's part
-        auto store_dw = [&](uint32_t o, float4 gs, float4 gh) {
-            store8(dw, tbytes, o, quad_rows_bf16(f32x4_t{gs.x + gh.x, gs.y + gh.y, gs.z + gh.z, gs.w + gh.w}, lane));
+        // (gs: this side's part, scaled by fw; gh: the H side's, unscaled; f: that chunk's fw)
+        auto store_dw = [&](uint32_t o, float4 gs, float4 gh, const float (&f)[4]) {
+            store8(dw, tbytes, o,
+                   quad_rows_bf16(f32x4_t{gs.x + gh.x * f[0], gs.y + gh.y * f[1], gs.z + gh.z * f[2], gs.w + gh.w * f[3]},
+                                  lane));
         };
+        float fwp[4] = {0.f, 0.f, 0.f, 0.f};  // fw of the previous tick's chunk
         {
             const int2 jc = chunk_at(0);
             load_rows(ck_rsrc(jc.x), jc.y);
@@ -718,7 +729,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             }
             consumer_sync(&sm.csync, NCONS * (n + 1));
             // ---- stage C: key strip j_own of dR, dA, dw; dV rows i_own ----
-            const Strip st = strip(S);
+            Strip st = strip(S);
+            strip_fw(S, st);
             uint4 oh[2], ol[2];  // this chunk's saved-state strip (loaded a tick ago)
 #pragma unroll
             for (int s = 0; s < 2; s++) pack8(&S0s[8 * s], oh[s], ol[s]);
@@ -784,8 +796,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             // the previous tick's dw: the H side published its part a tick ago (at n = 0
             // there is none and the store's offset lies outside the tensor)
             float4* const mine = reinterpret_cast<float4*>(&sm.dls[cw][4 * lane]);
-            store_dw(o_prev, *mine, *reinterpret_cast<const float4*>(&sm.dlp[(n + 1) & 1][cw][4 * lane]));
+            store_dw(o_prev, *mine, *reinterpret_cast<const float4*>(&sm.dlp[(n + 1) & 1][cw][4 * lane]), fwp);
             *mine = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) fwp[e] = st.fw[e];
             o_prev = o;
             lds_barrier();
           }
@@ -797,7 +811,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         }
         // the last chunk's dw
         store_dw(o_prev, *reinterpret_cast<const float4*>(&sm.dls[cw][4 * lane]),
-                 *reinterpret_cast<const float4*>(&sm.dlp[(nstream - 1) & 1][cw][4 * lane]));
+                 *reinterpret_cast<const float4*>(&sm.dlp[(nstream - 1) & 1][cw][4 * lane]), fwp);
     }
 }
 
