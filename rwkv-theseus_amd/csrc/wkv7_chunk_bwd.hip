@@ -79,8 +79,7 @@ struct Slot {
 struct BwdLds {
     uint16_t Hx[2][NK * NK];                     // H' [i][j] (swizzled)
     uint16_t QT[2][NK * LDQ], SAT[2][NK * LDQ];  // Q^T, SA^T [i][t]
-    float dlp[2][4][64 * 4];                     // H side's dlogd part (fw not applied), per key strip
-    float dls[4][64 * 4];                        // S side's dw part of the previous chunk
+    float dlp[2][4][64 * 4];                     // H side's dlogd terms z_t of a chunk, per key strip
     Slot slot[NPROD];
     Plane raw[NPROD][5];                         // producer input staging: r, w, k, a, b
     uint32_t csync;                              // consumers' mid-tick rendezvous counter
@@ -176,7 +175,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     int lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
-    const long NH = NN + 2 * NK;  // handoff per boundary: H (dL/dS), then the two sides' dlogd carries
+    const long NH = NN + NK;  // handoff per boundary: H (dL/dS), then the dlogd carry
     const long ncp = ckpt_count(Tn);
     const int nchunk = sc.n;
     const bool consumer = wv < 8;
@@ -207,8 +206,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                    ? (uint32_t)((((long)(bb * Tn + cc * CH + tr) * H + h) * NK + 16 * cw + 4 * (r16 >> 2)) * 2)
                    : OUT_OF_RANGE;
     };
-    // this side's part of dlogd_t = carry + sum_{s>=t} z_s + sum_{s>t} t2_s over the
-    // chunk (t = 4q + e), times fw_t = d w_t / d logd_t
+    // dw of a chunk: dlogd_t = carry + sum_{s>=t} z_s + sum_{s>t} t2_s over the chunk
+    // (t = 4q + e), times fw_t = d w_t / d logd_t; the carry moves on to the chunk before
     auto dlogd_part = [&](const float (&z)[4], const float (&t2)[4], const float (&fw)[4], float& carry, float (&gw)[4]) {
         float tot = 0.f;
 #pragma unroll
@@ -457,8 +456,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         }
     } else if (hside) {
         // ======================= H side: rows i_own of H and dV; key strip j_own: dK, dB =======================
-        f32x4_t Ht[4];      // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e] (H' within a tick)
-        float carry = 0.f;  // this side's part of the dlogd carry for key j_own
+        f32x4_t Ht[4];  // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e] (H' within a tick)
         lds_barrier();
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
@@ -469,9 +467,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
           const Seg sg = seg_of(sc, m, j);
           const int bb = j / H, h = j - bb * H;
           {  // H at the piece's start: dsT (zero if absent) at the head's end, else the handoff
-             // of boundary m + 1 with this side's carry (the S side starts the head's carry).
-             // (Lane offsets at piece boundaries come from an opaque lane, so that they are
-             // not kept in registers across the tick loop.)
+             // of boundary m + 1.  (Lane offsets at piece boundaries come from an opaque
+             // lane, so that they are not kept in registers across the tick loop.)
             const int ln = opaque(lane0), row = 16 * cw + (ln & 15), col = 4 * (ln >> 4);
             if (sg.fresh) {
 #pragma unroll
@@ -480,7 +477,6 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     if (dsT) x = *reinterpret_cast<const float4*>(dsT + (long)j * NN + row * NK + 16 * tj + col);
                     Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
                 }
-                carry = 0.f;
             } else {
                 const float bad = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");
                 const float* src = hand + (m + 1) * NH;
@@ -489,7 +485,6 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     const float4 x = handoff_get4(src + row * NK + 16 * tj + col);
                     Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w} * bad;
                 }
-                carry = handoff_get(src + NN + row) * bad;
             }
           }
           for (int kk = 0; kk < sg.count; kk++, n++) {
@@ -573,7 +568,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const Pk m2n = mat_n(S.M2, lane), pm1 = pk(m1T), pn1 = pk(n1T), pxm = pk(xm);
             const f32x4_t cK = mm32s(cat(pm1.h, m2n.h), cat(pm1.l, m2n.l), st.arh, st.arl);  // [triu_s(M1) | triu(M2)]
             const f32x4_t cB = mm32s(cat(pn1.h, pxm.h), cat(pn1.l, pxm.l), st.arh, st.arl);  // [triu_s(N1) | triu(SA dY^T)]
-            float gk_[4], gb_[4], z[4], t2[4], gw_[4];
+            float gk_[4], gb_[4], z[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float uK = gK[e] + cK[e], uB = gB[e] + cB[e];
@@ -582,17 +577,13 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 gb_[e] = eng * uB;
                 const float Bb_ = bf_el8(st.bkh, e) + bf_el8(st.bkl, e);
                 const float Kb_ = bf_el8(st.bkh, 4 + e) + bf_el8(st.bkl, 4 + e);
-                z[e] = -(Bb_ * uB + Kb_ * uK);
-                t2[e] = 0.f;
+                z[e] = -(Bb_ * uB + Kb_ * uK);  // -(b dB + k dK) before e^{-g}: this side's dlogd terms
             }
             const uint32_t o = piece_off(bb, h, c);
             store8(dk, tbytes, o, quad_rows_bf16(f32x4_t{gk_[0], gk_[1], gk_[2], gk_[3]}, lane));
             store8(db, tbytes, o, quad_rows_bf16(f32x4_t{gb_[0], gb_[1], gb_[2], gb_[3]}, lane));
-            {  // this side's part of dlogd, unscaled (the S side multiplies the sum by fw)
-                const float one[4] = {1.f, 1.f, 1.f, 1.f};
-                dlogd_part(z, t2, one, carry, gw_);
-            }
-            *reinterpret_cast<float4*>(&sm.dlp[n & 1][cw][4 * lane]) = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
+            // (the S side forms dw from both sides' terms a tick later)
+            *reinterpret_cast<float4*>(&sm.dlp[n & 1][cw][4 * lane]) = make_float4(z[0], z[1], z[2], z[3]);
             {  // dV = K- H'^T + Brk^T dY + Aak^T Q
                 const Pk brkT = mat_t(S.Brk, lane);
                 const f32x4_t c3 = mm16s_acc(mma16(mma16(zero4(), brkT.h, dyf), brkT.l, dyf), mat_t(S.Aak, lane), pq);
@@ -609,14 +600,13 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             }
             lds_barrier();
           }
-          {  // ds0 at the head's start, or the handoff at boundary m (H and this side's carry)
+          {  // ds0 at the head's start, or the handoff of H at boundary m
             const int ln = opaque(lane0), row = 16 * cw + (ln & 15), col = 4 * (ln >> 4);
             if (sg.handoff) {
                 float* const dst = hand + m * NH;
 #pragma unroll
                 for (int tj = 0; tj < 4; tj++)
                     handoff_put4(dst + row * NK + 16 * tj + col, Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
-                if (col == 0) handoff_put(dst + NN + row, carry);
                 handoff_signal(flags + m);
             } else {
 #pragma unroll
@@ -632,7 +622,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         // S0s[m] = S0[32(m/8) + 16((m/4)%2) + 4q + m%4][j_own], loaded a tick ahead
         f32x4_t S0n[4];
         float S0s[16];
-        float carry = 0.f;  // this side's part of the dlogd carry for key j_own
+        float carry = 0.f;  // the dlogd carry for key j_own
         // buffer loads from a head's saved states: one lane offset, the rest in
         // scalar and immediate offsets (no per-load address arithmetic)
         auto ck_rsrc = [&](int j) { return make_rsrc(ckpt + (long)j * ncp * NN, (uint32_t)(ncp * NN * 4)); };
@@ -649,14 +639,23 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 S0s[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
                     ckr, vo + (m & 3) * NK * 4, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0));
         };
-        // dw of a chunk (piece offset o) = this side's part + the H side's part
-        // (gs: this side's part, scaled by fw; gh: the H side's, unscaled; f: that chunk's fw)
-        auto store_dw = [&](uint32_t o, float4 gs, float4 gh, const float (&f)[4]) {
-            store8(dw, tbytes, o,
-                   quad_rows_bf16(f32x4_t{gs.x + gh.x * f[0], gs.y + gh.y * f[1], gs.z + gh.z * f[2], gs.w + gh.w * f[3]},
-                                  lane));
+        // The previous tick's chunk (stream index np) is completed a tick late, once the H
+        // side's dlogd terms of it are published: this side's terms zp, tp, its fw and its
+        // piece offset are held over, the carry then moves on to it.
+        float zp[4], tp[4], fwp[4];
+        uint32_t o_prev = OUT_OF_RANGE;
+        auto flush = [&](int np) {
+            const float4 zh = *reinterpret_cast<const float4*>(&sm.dlp[np & 1][cw][4 * lane]);
+            const float zz[4] = {zp[0] + zh.x, zp[1] + zh.y, zp[2] + zh.z, zp[3] + zh.w};
+            float gw[4];
+            dlogd_part(zz, tp, fwp, carry, gw);
+            store8(dw, tbytes, o_prev, quad_rows_bf16(f32x4_t{gw[0], gw[1], gw[2], gw[3]}, lane));
         };
-        float fwp[4] = {0.f, 0.f, 0.f, 0.f};  // fw of the previous tick's chunk
+        auto hand_carry = [&]() {  // the carry at boundary m (after the start piece's last chunk)
+            const int ln = opaque(lane0);
+            if (ln < 16) handoff_put(hand + m * NH + NN + 16 * cw + ln, carry);
+            handoff_signal(flags + m);
+        };
         {
             const int2 jc = chunk_at(0);
             load_rows(ck_rsrc(jc.x), jc.y);
@@ -666,12 +665,17 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         lds_barrier();
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
-        uint32_t o_prev = OUT_OF_RANGE;  // the previous tick's chunk (its dw is completed a tick late)
         const int jlast = (m * sc.L + nstream - 1) / sc.n;
         int n = 0;
+        bool hand_prev = false;  // the previous piece hands its carry over at boundary m
         for (int j = m * sc.L / sc.n; j <= jlast; j++) {
           const Seg sg = seg_of(sc, m, j);
           const int bb = j / H, h = j - bb * H;
+          if (n > 0) {  // the previous piece's last chunk, with that piece's carry
+              flush(n - 1);
+              if (hand_prev) hand_carry();
+          }
+          hand_prev = sg.handoff;
           {  // (lane offsets at piece boundaries from an opaque lane: none held across the tick loop)
             const int ln = opaque(lane0), key = 16 * cw + (ln & 15);
             if (sg.fresh) {
@@ -689,9 +693,9 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     p += __shfl_xor(p, 32);
                 }
                 carry = p;
-            } else {  // this side's carry from the handoff of boundary m + 1
+            } else {  // the carry from the handoff of boundary m + 1
                 const float bad = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");
-                carry = handoff_get(hand + (m + 1) * NH + NN + NK + key) * bad;
+                carry = handoff_get(hand + (m + 1) * NH + NN + key) * bad;
             }
           }
           // the chunk after this piece's last: the next piece's first (or a repeat at the end)
@@ -778,7 +782,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const Pk m2t = mat_t(S.M2, lane), pm1 = pk(m1), pn1 = pk(n1), pxm = pk(xmT);
             const f32x4_t cR = mm32s(cat(pxm.h, m2t.h), cat(pxm.l, m2t.l), st.bkh, st.bkl);  // [tril(dY SA^T) | tril(dY V^T)]
             const f32x4_t cA = mm32s(cat(pn1.h, pm1.h), cat(pn1.l, pm1.l), st.bkh, st.bkl);  // [tril_s(Q SA^T) | tril_s(Q V^T)]
-            float gr_[4], ga_[4], z[4], t2[4], gw_[4];
+            float gr_[4], ga_[4], z[4], t2[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float uR = gR[e] + cR[e], uA = gA[e] + cA[e];
@@ -792,31 +796,21 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const uint32_t o = piece_off(bb, h, c);
             store8(dr, tbytes, o, quad_rows_bf16(f32x4_t{gr_[0], gr_[1], gr_[2], gr_[3]}, lane));
             store8(da, tbytes, o, quad_rows_bf16(f32x4_t{ga_[0], ga_[1], ga_[2], ga_[3]}, lane));
-            dlogd_part(z, t2, st.fw, carry, gw_);
-            // the previous tick's dw: the H side published its part a tick ago (at n = 0
-            // there is none and the store's offset lies outside the tensor)
-            float4* const mine = reinterpret_cast<float4*>(&sm.dls[cw][4 * lane]);
-            store_dw(o_prev, *mine, *reinterpret_cast<const float4*>(&sm.dlp[(n + 1) & 1][cw][4 * lane]), fwp);
-            *mine = make_float4(gw_[0], gw_[1], gw_[2], gw_[3]);
+            if (kk > 0) flush(n - 1);  // the previous chunk of this piece (same carry)
 #pragma unroll
-            for (int e = 0; e < 4; e++) fwp[e] = st.fw[e];
+            for (int e = 0; e < 4; e++) zp[e] = z[e], tp[e] = t2[e], fwp[e] = st.fw[e];
             o_prev = o;
             lds_barrier();
           }
-          if (sg.handoff) {  // this side's carry at boundary m
-              const int ln = opaque(lane0);
-              if (ln < 16) handoff_put(hand + m * NH + NN + NK + 16 * cw + ln, carry);
-              handoff_signal(flags + m);
-          }
         }
-        // the last chunk's dw
-        store_dw(o_prev, *reinterpret_cast<const float4*>(&sm.dls[cw][4 * lane]),
-                 *reinterpret_cast<const float4*>(&sm.dlp[(nstream - 1) & 1][cw][4 * lane]), fwp);
+        // the last chunk (a machine's last piece never hands over; a lone start piece does)
+        flush(nstream - 1);
+        if (hand_prev) hand_carry();
     }
 }
 
 size_t chunk_backward_workspace(int B, int T, int H, int cus) {
-    return sched_workspace(plan_schedule(B * H, (T + CH - 1) / CH, cus), NK * NK + 2 * NK);
+    return sched_workspace(plan_schedule(B * H, (T + CH - 1) / CH, cus), NK * NK + NK);
 }
 void launch_chunk_backward(const Bwd& p, int cus) {
     const Sched sc = plan_schedule(p.B * p.H, (p.T + CH - 1) / CH, cus);

@@ -93,7 +93,8 @@ def test_schedule_workspace_follows_the_cu_count(monkeypatch):
     With c CUs, J = B*H heads of n chunks go L = max(n, ceil(J n / c)) to a
     workgroup; a head is cut when L is not a multiple of n, and then every one
     of the G = ceil(J n / L) workgroups has a 256-byte-aligned counter block
-    plus a handoff of N*N floats (forward) or N*N + 2N floats (backward).
+    plus a handoff of N*N floats (forward: the state) or N*N + N floats (backward:
+    dL/dS and the decay-gradient carry).
     """
     lib = W.extension().lib
     N = 64
@@ -113,7 +114,7 @@ def test_schedule_workspace_follows_the_cu_count(monkeypatch):
         f = lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0)
         b = lib.theseus_wkv7_backward_workspace_size(B, T, H, N, 0)
         assert f == expect(B, T, H, cus, N * N), (B, T, H, cus)
-        assert b == expect(B, T, H, cus, N * N + 2 * N), (B, T, H, cus)
+        assert b == expect(B, T, H, cus, N * N + N), (B, T, H, cus)
     monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
     # config 2: 320 heads of 128 chunks on 256 CUs -> L = 160, G = 256, cut
     assert lib.theseus_wkv7_forward_workspace_size(4, 2048, 80, 64, 0) == 1024 + 256 * 4096 * 4
