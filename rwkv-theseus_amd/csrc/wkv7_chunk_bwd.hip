@@ -731,8 +731,9 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 st8(&sm.SAT[0][pl16(i_own, 4 * q)], psa.h);
                 st8(&sm.SAT[1][pl16(i_own, 4 * q)], psa.l);
             }
-            consumer_sync(&sm.csync, NCONS * (n + 1));
-            // ---- stage C: key strip j_own of dR, dA, dw; dV rows i_own ----
+            // ---- still before the rendezvous (this side's stage B is the shorter): the work
+            //      of stage C that needs nothing published this tick ----
+            if (kk > 0) flush(n - 1);  // the previous chunk of this piece (same carry)
             Strip st = strip(S);
             strip_fw(S, st);
             uint4 oh[2], ol[2];  // this chunk's saved-state strip (loaded a tick ago)
@@ -751,7 +752,15 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 load_strip(ckr, last ? cn : c - 1);
                 load_rows(ckr, last ? cn : c - 1);
             }
-            f32x4_t m1 = zero4(), xmT = zero4(), n1 = zero4(), gR = zero4(), gA = zero4();
+            f32x4_t gR = zero4();
+#pragma unroll
+            for (int s = 0; s < 2; s++) {  // dY S0
+                const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);
+                gR = mma32(mma32(gR, ya, oh[s]), ya, ol[s]);
+            }
+            consumer_sync(&sm.csync, NCONS * (n + 1));
+            // ---- stage C: key strip j_own of dR, dA and this chunk's dlogd terms ----
+            f32x4_t m1 = zero4(), xmT = zero4(), n1 = zero4(), gA = zero4();
             {
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
@@ -766,8 +775,6 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     n1 = mma32(n1, sh, qh);  // SA Q^T = N1    [t][s]
                     n1 = mma32(n1, sh, ql);
                     n1 = mma32(n1, sl, qh);
-                    gR = mma32(gR, ya, oh[s]);  // dY S0
-                    gR = mma32(gR, ya, ol[s]);
                     gA = mma32(gA, qh, oh[s]);  // Q S0
                     gA = mma32(gA, qh, ol[s]);
                     gA = mma32(gA, ql, oh[s]);
@@ -796,7 +803,6 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const uint32_t o = piece_off(bb, h, c);
             store8(dr, tbytes, o, quad_rows_bf16(f32x4_t{gr_[0], gr_[1], gr_[2], gr_[3]}, lane));
             store8(da, tbytes, o, quad_rows_bf16(f32x4_t{ga_[0], ga_[1], ga_[2], ga_[3]}, lane));
-            if (kk > 0) flush(n - 1);  // the previous chunk of this piece (same carry)
 #pragma unroll
             for (int e = 0; e < 4; e++) zp[e] = z[e], tp[e] = t2[e], fwp[e] = st.fw[e];
             o_prev = o;
