@@ -328,132 +328,130 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         }
         lds_barrier();
         lds_barrier();
-        // Producer work for chunk x (processing order) in phase ph, in two parts (the
-        // second part of a phase depends on DMA or on registers set in the first).
-        f32x4_t Aab, AabT, Aak, Brb, Brk, M2;  // phase 2, part 0 -> part 1
-        auto produce = [&](int x, int ph, int part) {
-            Slot& S = sm.slot[x % NPROD];
+        // Producer pw's chunks are x = pw, pw + 3, ... (slot x % 3 = pw is its own); phase
+        // ph of chunk x runs at tick x - 3 + ph, while the consumers work on chunk x - 3 + ph.
+        // Phase 0 may not write the slot (the consumers read it at that tick), so the
+        // first key half's operands wait in registers until phase 1.
+        auto phase0 = [&](uint4 (&o0)[8]) {
+            // ---- log-decays, their cumulative sum; key half 0's operands ----
+            vm_wait0();  // this chunk's inputs (LDS DMA issued in the previous chunk's phase 1)
             const Plane* raw = sm.raw[pw];
-            if (ph == 0) {
-                if (part == 0) {
-                    // ---- phase 0: log-decays and their cumulative sum ----
-                    vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
-                    const int L = chunk_len(cx);
+            const int L = chunk_len(cx);
 #pragma unroll
-                    for (int hf = 0; hf < 2; hf++) {
-                        const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
+            for (int hf = 0; hf < 2; hf++) {
+                const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
 #pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            float ld = log_decay(bf_el8(wr, e));
-                            if (L < CH) ld = r16 < L ? ld : 0.f;
-                            gq[hf][e] = row_prefix_sum(ld);
-                        }
-                    }
+                for (int e = 0; e < 8; e++) {
+                    float ld = log_decay(bf_el8(wr, e));
+                    if (L < CH) ld = r16 < L ? ld : 0.f;
+                    gq[hf][e] = row_prefix_sum(ld);
                 }
-            } else if (ph == 1) {
-                // ---- phase 1: the slot's A~, R~, B-, K-, g and e^{gL} (keys 0-31 in part 0,
-                //      32-63 in part 1); then V, dY of this chunk and the inputs of this
-                //      producer's next chunk by LDS DMA ----
-                if (part == 0) {
-                    uint4 o[8];
-                    operands(raw, gq[0], 0, o);
-                    put_operands(S, 0, o);
-                } else {
-                    uint4 o[8];
-                    operands(raw, gq[1], 1, o);
-                    put_operands(S, 1, o);
-                    dma_lane_offsets(voff, rstride, lane);
-                    if (x > 0) {  // (stream index 0's V, dY were staged before the loop)
-                        const uint32_t o = chunk_off(cx);
-                        const int L = chunk_len(cx);
-                        stage_plane(S.V, dma_rsrc(v, tbytes), v, o, voff, rstride, L, lane);
-                        stage_plane(S.dY, dma_rsrc(dy, tbytes), dy, o, voff, rstride, L, lane);
-                    }
-                    wave_lds_fence();  // staging reads done before the DMA overwrites it
-                    if (x + NPROD < nstream) {
-                        const uint32_t o = chunk_off(cy);
-                        const int L = chunk_len(cy);
+            }
+            operands(raw, gq[0], 0, o0);
+        };
+        auto phase1 = [&](int x, const uint4 (&o0)[8]) {
+            // ---- the slot's A~, R~, B-, K-, g and e^{gL}; then V, dY of this chunk and the
+            //      inputs of this producer's next chunk by LDS DMA ----
+            Slot& S = sm.slot[pw];
+            const Plane* raw = sm.raw[pw];
+            put_operands(S, 0, o0);
+            uint4 o[8];
+            operands(raw, gq[1], 1, o);
+            put_operands(S, 1, o);
+            dma_lane_offsets(voff, rstride, lane);
+            if (x > 0) {  // (stream index 0's V, dY were staged before the loop)
+                const uint32_t off = chunk_off(cx);
+                const int L = chunk_len(cx);
+                stage_plane(S.V, dma_rsrc(v, tbytes), v, off, voff, rstride, L, lane);
+                stage_plane(S.dY, dma_rsrc(dy, tbytes), dy, off, voff, rstride, L, lane);
+            }
+            wave_lds_fence();  // staging reads done before the DMA overwrites it
+            if (x + NPROD < nstream) {
+                const uint32_t off = chunk_off(cy);
+                const int L = chunk_len(cy);
 #pragma unroll
-                        for (int ts = 0; ts < 5; ts++)
-                            stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], o, voff, rstride, L, lane);
-                    }
-                }
-            } else if (part == 0) {
-                // ---- phase 2: chunk matrices over keys / value rows, triangular inverse ----
-                // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
-                if (x + NPROD < nstream) vm_wait10();
-                else vm_wait0();
-                auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
-#pragma unroll
-                    for (int hf = 0; hf < 2; hf++) {
-                        xh[hf] = ld16_sw<SwLane>(pl2[0], r16, 32 * hf + 8 * q);
-                        xl[hf] = ld16_sw<SwLane>(pl2[1], r16, 32 * hf + 8 * q);
-                    }
-                };
-                {
-                    uint4 ath[2], atl[2], xh[2], xl[2];
-                    rd(S.At, ath, atl);
-                    rd(S.Bb, xh, xl);
-                    Aab = mm_keys8(ath, atl, xh, xl);
-                    AabT = mm_keys8(xh, xl, ath, atl);
-                    rd(S.Kb, xh, xl);
-                    Aak = mm_keys8(ath, atl, xh, xl);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                {
-                    uint4 rth[2], rtl[2], xh[2], xl[2];
-                    rd(S.Rt, rth, rtl);
-                    rd(S.Bb, xh, xl);
-                    Brb = mm_keys8(rth, rtl, xh, xl);
-                    rd(S.Kb, xh, xl);
-                    Brk = mm_keys8(rth, rtl, xh, xl);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                {
-                    uint4 vv[2], yy[2];
-#pragma unroll
-                    for (int hf = 0; hf < 2; hf++) {
-                        vv[hf] = ld16_sw<SwDma>(S.V, r16, 32 * hf + 8 * q);
-                        yy[hf] = ld16_sw<SwDma>(S.dY, r16, 32 * hf + 8 * q);
-                    }
-                    M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
-                    const int rw = 4 * q + e;
-                    if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;  // [t][s]: s < t
-                    if (rw >= r16) AabT[e] = 0.f;               // [s][t]: s < t
-                    if (r16 > rw) Brb[e] = 0.f, Brk[e] = 0.f;   // [t][s]: s <= t
-                    if (r16 < rw) M2[e] = 0.f;                  // [t][s]: s >= t
-                }
-                f32x4_t Ti, TiT;
-                tri_inverse(Aab, AabT, lane, Ti, TiT);
-                put_mat(S.Ti, Ti, lane);
-                put_mat(S.Aak, Aak, lane);
-                put_mat(S.Brb, Brb, lane);
-                put_mat(S.Brk, Brk, lane);
-                put_mat(S.M2, M2, lane);
+                for (int ts = 0; ts < 5; ts++)
+                    stage_plane(sm.raw[pw][ts], dma_rsrc(rsrc_src[ts], tbytes), rsrc_src[ts], off, voff, rstride, L, lane);
             }
         };
+        auto phase2 = [&](int x) {
+            // ---- chunk matrices over keys / value rows, triangular inverse ----
+            Slot& S = sm.slot[pw];
+            // V, dY of this chunk: the 10 staging DMA ops issued after them may still run
+            if (x + NPROD < nstream) vm_wait10();
+            else vm_wait0();
+            auto rd = [&](const Plane (&pl2)[2], uint4 (&xh)[2], uint4 (&xl)[2]) {
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    xh[hf] = ld16_sw<SwLane>(pl2[0], r16, 32 * hf + 8 * q);
+                    xl[hf] = ld16_sw<SwLane>(pl2[1], r16, 32 * hf + 8 * q);
+                }
+            };
+            f32x4_t Aab, AabT, Aak, Brb, Brk, M2;
+            {
+                uint4 ath[2], atl[2], xh[2], xl[2];
+                rd(S.At, ath, atl);
+                rd(S.Bb, xh, xl);
+                Aab = mm_keys8(ath, atl, xh, xl);
+                AabT = mm_keys8(xh, xl, ath, atl);
+                rd(S.Kb, xh, xl);
+                Aak = mm_keys8(ath, atl, xh, xl);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            {
+                uint4 rth[2], rtl[2], xh[2], xl[2];
+                rd(S.Rt, rth, rtl);
+                rd(S.Bb, xh, xl);
+                Brb = mm_keys8(rth, rtl, xh, xl);
+                rd(S.Kb, xh, xl);
+                Brk = mm_keys8(rth, rtl, xh, xl);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            {
+                uint4 vv[2], yy[2];
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    vv[hf] = ld16_sw<SwDma>(S.V, r16, 32 * hf + 8 * q);
+                    yy[hf] = ld16_sw<SwDma>(S.dY, r16, 32 * hf + 8 * q);
+                }
+                M2 = mma32(mma32(zero4(), vv[0], yy[0]), vv[1], yy[1]);  // V dY^T (exact operands)
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
+                const int rw = 4 * q + e;
+                if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;  // [t][s]: s < t
+                if (rw >= r16) AabT[e] = 0.f;               // [s][t]: s < t
+                if (r16 > rw) Brb[e] = 0.f, Brk[e] = 0.f;   // [t][s]: s <= t
+                if (r16 < rw) M2[e] = 0.f;                  // [t][s]: s >= t
+            }
+            f32x4_t Ti, TiT;
+            tri_inverse(Aab, AabT, lane, Ti, TiT);
+            put_mat(S.Ti, Ti, lane);
+            put_mat(S.Aak, Aak, lane);
+            put_mat(S.Brb, Brb, lane);
+            put_mat(S.Brk, Brk, lane);
+            put_mat(S.M2, M2, lane);
+        };
 
-        for (int n = -NPROD; n < nstream; n++) {
-            new_tick();
-            // the chunk this producer works on at tick n (x = pw mod 3, so slot x % 3 is
-            // its own) and its phase; prologue and final ticks have no chunk for some
-            const int x = n + 1 + ((pw - n - 1) % NPROD + NPROD) % NPROD;
-            const int ph = n + NPROD - x;
-            const bool pact = x >= 0 && x < nstream;
-            if (ph == 0 && x > pw) {  // on to the next chunk
+        int n = -NPROD;
+        for (; n < pw - NPROD; n++) lds_barrier();  // (ticks before this producer's first chunk)
+        for (int x = pw; x < nstream; x += NPROD, n += NPROD) {
+            if (x > pw) {  // on to the next chunk
                 cx = cy;
                 cursor_advance(cy, sc, m, NPROD, H);
             }
-            if (pact) {
-                produce(x, ph, 0);
-                produce(x, ph, 1);
-            }
+            uint4 o0[8];
+            new_tick();
+            phase0(o0);
+            lds_barrier();
+            new_tick();
+            phase1(x, o0);
+            lds_barrier();
+            new_tick();
+            phase2(x);
             lds_barrier();
         }
+        for (; n < nstream; n++) lds_barrier();  // (ticks after its last chunk)
     } else if (hside) {
         // ======================= H side: rows i_own of H and dV; key strip j_own: dK, dB =======================
         f32x4_t Ht[4];  // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e] (H' within a tick)
