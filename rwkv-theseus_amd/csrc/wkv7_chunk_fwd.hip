@@ -127,7 +127,6 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     const bf16_t* const src5[5] = {r, w, k, a, b};
     // this producer's current chunk (stream index x = pw mod 4) and its next
     Cursor cx = cursor_at(sc, m, pw, H), cy = cursor_at(sc, m, pw + NPROD, H);
-    float g1[8];  // cumulative log-decay, keys 32 + 8q + e (phase 0 -> 1)
     Pk pTiT, pB;  // Ti^T, Brb^T packed (phase 2 -> 3)
 
     // scaled operands of one key half from the staged inputs and g: written to
@@ -201,112 +200,116 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     // The two roles run separate tick loops with the same barriers, so that
     // registers and memory-counter waits are allocated per role.
     if (producer) {
-        for (int n = -NPROD; n < nstream; n++) {
-            // the chunk this producer works on at tick n (x = pw mod 4), and its phase
-            const int x = n + 1 + ((pw - n - 1) & 3);
-            const int ph = n + NPROD - x;
-            if (ph == 0 && x > pw) {  // on to the next chunk
+        // Producer pw's chunks are x = pw, pw + 4, ...; phase ph of chunk x runs at tick
+        // x - 4 + ph, so each iteration below is four consecutive ticks.
+        int n = -NPROD;
+        for (; n < pw - NPROD; n++) lds_barrier();  // (ticks before this producer's first chunk)
+        for (int x = pw; x < nstream; x += NPROD, n += NPROD) {
+            if (x > pw) {  // on to the next chunk
                 cx = cy;
                 cursor_advance(cy, sc, m, NPROD, H);
             }
-            if (x >= 0 && x < nstream) {  // (prologue ticks have no chunk for some producers)
-                Slot& S = sm.slot[x % NSLOT];
-                Plane* raw = sm.raw[pw];
-                if (ph == 0) {
-                    // ---- phase 0: log-decays and their cumulative sum; V by LDS DMA;
-                    //      the operands of keys 0-31 ----
-                    vm_wait0();  // this chunk's inputs (LDS DMA issued two ticks ago)
-                    const int L = chunk_len(cx);
-                    stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride, L, lane);
-                    float g0[8];
+            Slot& S = sm.slot[x % NSLOT];
+            Plane* raw = sm.raw[pw];
+            const int L = chunk_len(cx);
+            // cumulative log-decay of keys 32 hf + 8q + e (lane: token r16)
+            auto decay_scan = [&](int hf, float (&g)[8]) {
+                const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float ld = log_decay(bf_el8(wr, e));
+                    if (L < CH) ld = r16 < L ? ld : 0.f;  // padded steps keep the state
+                    g[e] = row_prefix_sum(ld);
+                }
+            };
+            {   // ---- phase 0: V by LDS DMA; keys 0-31: decays and operands ----
+                vm_wait0();  // this chunk's inputs (LDS DMA issued in the previous chunk's phase 2)
+                stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride, L, lane);
+                float g0[8];
+                decay_scan(0, g0);
+                operands(S, raw, g0, 0);
+            }
+            lds_barrier();
+            {   // ---- phase 1: keys 32-63: decays and operands ----
+                float g1[8];
+                decay_scan(1, g1);
+                operands(S, raw, g1, 1);
+            }
+            lds_barrier();
+            f32x4_t Aak, BrkT;  // phase 2 -> 3
+            {   // ---- phase 2: the chunk matrices over the keys, triangular inverse; then
+                //      this producer's next chunk by LDS DMA ----
+                f32x4_t Aab, AabT, BrbT;
+                {
+                    uint4 ath[2], atl[2], rth[2], rtl[2], bbh[2], bbl[2], kbh[2], kbl[2];
 #pragma unroll
                     for (int hf = 0; hf < 2; hf++) {
-                        const uint4 wr = ld16_sw<SwDma>(raw[1], r16, 32 * hf + 8 * q);
-#pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            float ld = log_decay(bf_el8(wr, e));
-                            if (L < CH) ld = r16 < L ? ld : 0.f;  // padded steps keep the state
-                            const float gv = row_prefix_sum(ld);
-                            if (hf) g1[e] = gv; else g0[e] = gv;
-                        }
+                        const int c8 = 32 * hf + 8 * q;
+                        ath[hf] = ld16_sw<SwLane>(S.P[0], r16, c8);
+                        atl[hf] = ld16_sw<SwLane>(S.P[1], r16, c8);
+                        rth[hf] = ld16_sw<SwLane>(S.P2[0], r16, c8);
+                        rtl[hf] = ld16_sw<SwLane>(S.P2[1], r16, c8);
+                        bbh[hf] = ld16_sw<SwDma>(raw[0], r16, c8);
+                        bbl[hf] = ld16_sw<SwDma>(raw[2], r16, c8);
+                        kbh[hf] = ld16_sw<SwDma>(raw[3], r16, c8);
+                        kbl[hf] = ld16_sw<SwDma>(raw[4], r16, c8);
                     }
-                    operands(S, raw, g0, 0);
-                } else if (ph == 1) {
-                    // ---- phase 1: the operands of keys 32-63 ----
-                    operands(S, raw, g1, 1);
-                } else if (ph == 2) {
-                    // ---- phase 2: the chunk matrices over the keys, triangular inverse,
-                    //      Q' = Ti Aak, Q2; then this producer's next chunk ----
-                    f32x4_t Aab, AabT, Aak, BrbT, BrkT;
-                    {
-                        uint4 ath[2], atl[2], rth[2], rtl[2], bbh[2], bbl[2], kbh[2], kbl[2];
-#pragma unroll
-                        for (int hf = 0; hf < 2; hf++) {
-                            const int c8 = 32 * hf + 8 * q;
-                            ath[hf] = ld16_sw<SwLane>(S.P[0], r16, c8);
-                            atl[hf] = ld16_sw<SwLane>(S.P[1], r16, c8);
-                            rth[hf] = ld16_sw<SwLane>(S.P2[0], r16, c8);
-                            rtl[hf] = ld16_sw<SwLane>(S.P2[1], r16, c8);
-                            bbh[hf] = ld16_sw<SwDma>(raw[0], r16, c8);
-                            bbl[hf] = ld16_sw<SwDma>(raw[2], r16, c8);
-                            kbh[hf] = ld16_sw<SwDma>(raw[3], r16, c8);
-                            kbl[hf] = ld16_sw<SwDma>(raw[4], r16, c8);
-                        }
-                        Aab = mm_keys8(ath, atl, bbh, bbl);
-                        AabT = mm_keys8(bbh, bbl, ath, atl);
-                        Aak = mm_keys8(ath, atl, kbh, kbl);
-                        BrbT = mm_keys8(bbh, bbl, rth, rtl);
-                        BrkT = mm_keys8(kbh, kbl, rth, rtl);
-                    }
-                    wave_lds_fence();  // staging reads done before the DMA overwrites them
-                    if (x + NPROD < nstream) {
-#pragma unroll
-                        for (int ts = 0; ts < 5; ts++)
-                            stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(cy),
-                                        voff, rstride, chunk_len(cy), lane);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
-                        const int rw = 4 * q + e;
-                        if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;   // [t][s]: s < t
-                        if (rw >= r16) AabT[e] = 0.f;                // [s][t]: s < t
-                        if (rw > r16) BrbT[e] = 0.f, BrkT[e] = 0.f;  // [s][t]: s <= t
-                    }
-                    f32x4_t Ti, TiT;
-                    tri_inverse(Aab, AabT, lane, Ti, TiT);
-                    pTiT = pk(TiT);
-                    pB = pk(BrbT);
-                    // Q' (D layout [t][s]) stored as Q'^T [s][t]
-                    const Pk pq1 = pk(mm16s(pTiT, pk(Aak)));
-                    st8(&S.Q1T[0][pl16(r16, 4 * q)], pq1.h);
-                    st8(&S.Q1T[1][pl16(r16, 4 * q)], pq1.l);
-                    // Q2^T = Brk^T + Q'^T Brb^T  (lane: Q2[t = r16][s = 4q + e])
-                    const Pk q2 = pk(BrkT + mm16s(pq1, pB));
-                    st8(&S.Q2[0][pl16(r16, 4 * q)], q2.h);
-                    st8(&S.Q2[1][pl16(r16, 4 * q)], q2.l);
-                } else {
-                    // ---- phase 3: P = Ti A~, P2^T = R~^T + P^T Brb^T (R~ read from the P2
-                    //      plane first); then V has landed ----
-                    p_tiles(S, 0, 4);
-#pragma unroll
-                    for (int tj = 0; tj < 4; tj++) {
-                        const uint2 hh = ld8_sw<SwLane>(S.P2[0], r16, 16 * tj + 4 * q);
-                        const uint2 ll = ld8_sw<SwLane>(S.P2[1], r16, 16 * tj + 4 * q);
-                        f32x4_t rt;
-#pragma unroll
-                        for (int e = 0; e < 4; e++) rt[e] = bf_el(hh, e) + bf_el(ll, e);
-                        const Pk pp = {ldtr_sw<SwLane>(S.P[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.P[1], 0, 16 * tj, lane)};
-                        const Pk p2 = pk(rt + mm16s(pp, pB));
-                        st8_sw<SwLane>(S.P2[0], r16, 16 * tj + 4 * q, p2.h);
-                        st8_sw<SwLane>(S.P2[1], r16, 16 * tj + 4 * q, p2.l);
-                    }
-                    // V (phase 0) was followed only by the 10 staging DMA ops of phase 2
-                    if (x + NPROD < nstream) vm_wait10();
-                    else vm_wait0();
+                    Aab = mm_keys8(ath, atl, bbh, bbl);
+                    AabT = mm_keys8(bbh, bbl, ath, atl);
+                    Aak = mm_keys8(ath, atl, kbh, kbl);
+                    BrbT = mm_keys8(bbh, bbl, rth, rtl);
+                    BrkT = mm_keys8(kbh, kbl, rth, rtl);
                 }
+                wave_lds_fence();  // staging reads done before the DMA overwrites them
+                if (x + NPROD < nstream) {
+#pragma unroll
+                    for (int ts = 0; ts < 5; ts++)
+                        stage_plane(sm.raw[pw][ts], dma_rsrc(src5[ts], tbytes), src5[ts], chunk_off(cy), voff,
+                                    rstride, chunk_len(cy), lane);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
+                    const int rw = 4 * q + e;
+                    if (r16 >= rw) Aab[e] = 0.f, Aak[e] = 0.f;   // [t][s]: s < t
+                    if (rw >= r16) AabT[e] = 0.f;                // [s][t]: s < t
+                    if (rw > r16) BrbT[e] = 0.f, BrkT[e] = 0.f;  // [s][t]: s <= t
+                }
+                f32x4_t Ti, TiT;
+                tri_inverse(Aab, AabT, lane, Ti, TiT);
+                pTiT = pk(TiT);
+                pB = pk(BrbT);
+            }
+            lds_barrier();
+            {   // ---- phase 3: Q' = Ti Aak, Q2; P = Ti A~, P2^T = R~^T + P^T Brb^T (R~ read
+                //      from the P2 plane first); then V has landed ----
+                // Q' (D layout [t][s]) stored as Q'^T [s][t]
+                const Pk pq1 = pk(mm16s(pTiT, pk(Aak)));
+                st8(&S.Q1T[0][pl16(r16, 4 * q)], pq1.h);
+                st8(&S.Q1T[1][pl16(r16, 4 * q)], pq1.l);
+                // Q2^T = Brk^T + Q'^T Brb^T  (lane: Q2[t = r16][s = 4q + e])
+                const Pk q2 = pk(BrkT + mm16s(pq1, pB));
+                st8(&S.Q2[0][pl16(r16, 4 * q)], q2.h);
+                st8(&S.Q2[1][pl16(r16, 4 * q)], q2.l);
+                p_tiles(S, 0, 4);
+#pragma unroll
+                for (int tj = 0; tj < 4; tj++) {
+                    const uint2 hh = ld8_sw<SwLane>(S.P2[0], r16, 16 * tj + 4 * q);
+                    const uint2 ll = ld8_sw<SwLane>(S.P2[1], r16, 16 * tj + 4 * q);
+                    f32x4_t rt;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) rt[e] = bf_el(hh, e) + bf_el(ll, e);
+                    const Pk pp = {ldtr_sw<SwLane>(S.P[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.P[1], 0, 16 * tj, lane)};
+                    const Pk p2 = pk(rt + mm16s(pp, pB));
+                    st8_sw<SwLane>(S.P2[0], r16, 16 * tj + 4 * q, p2.h);
+                    st8_sw<SwLane>(S.P2[1], r16, 16 * tj + 4 * q, p2.l);
+                }
+                // V (phase 0) was followed only by the 10 staging DMA ops of phase 2
+                if (x + NPROD < nstream) vm_wait10();
+                else vm_wait0();
             }
             lds_barrier();
         }
+        for (; n < nstream; n++) lds_barrier();  // (ticks after its last chunk)
     } else {
         for (int n = -NPROD; n < 0; n++) lds_barrier();
         // one segment (a head's piece) after another; tick n counts the stream
