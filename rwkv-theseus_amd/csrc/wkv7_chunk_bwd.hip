@@ -29,8 +29,10 @@
 //    inputs -- A~, R~, B-, K-, g, e^{gL}, Ti, Aak, Brb, Brk, triu(V dY^T) -- one
 //    chunk each, in three phases over the three ticks before it is consumed,
 //    into a 3-slot LDS ring.  Their inputs arrive by LDS DMA two ticks ahead, so
-//    no prefetch registers are held across ticks.  Each phase is split in two
-//    parts (the second depends on DMA or on the first's registers).
+//    no prefetch registers are held across ticks.  Each producer runs one
+//    chunk's three phases in sequence; phase 0 may not write the slot (the
+//    consumers still read it in that tick), so the operands of the first 32
+//    keys it computes wait in registers until phase 1.
 //  * Consumers, 8 waves in two sides.  The H side (waves 0-3: wave c owns value
 //    rows 16c..16c+15 of H = dL/dS in registers) forms H', Q and the first part
 //    of dV in stage B and publishes H' and Q^T rows; the S side (waves 4-7, the

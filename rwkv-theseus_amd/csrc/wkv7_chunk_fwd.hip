@@ -23,10 +23,11 @@
 //  * Producers (waves 0-3).  Everything above that does not involve the
 //    state depends only on the chunk's inputs, so producer p builds the
 //    operands of chunks p, p+4, p+8, ... alone -- no barrier inside -- in four
-//    phases spread over the four ticks before the chunk is consumed; at any
-//    tick the four producers are in four different phases, each phase about a
-//    quarter of the work.  A chunk's inputs arrive by LDS DMA three ticks
-//    ahead into the producer's staging planes (no prefetch registers).  A lane
+//    phases over the four ticks before the chunk is consumed (one loop
+//    iteration per chunk); at any tick the four producers are in four different
+//    phases, each phase about a quarter of the work.  A chunk's inputs arrive
+//    by LDS DMA two ticks ahead into the producer's staging planes (no
+//    prefetch registers).  A lane
 //    holds one token and 8 keys of a 32-key half (X[t = l%16][32 hf + 8q + e],
 //    the K=32 operand layout), so the decay cumsum over tokens is a 16-lane
 //    DPP scan, the key contractions (Aab, ...) take the operands straight from
@@ -36,7 +37,9 @@
 //    state in registers (value rows never interact) and advances them by one
 //    chunk per tick from the operands the producers left in a 5-slot LDS ring
 //    (chunk x in slot x % 5, free from tick x-4 since its last reader was
-//    chunk x-5).
+//    chunk x-5).  Their outputs leave in whole 128-byte rows: y through LDS,
+//    stored a tick late by all four waves, and each wave's saved-state rows
+//    regrouped eight at a time.
 #include "wkv7_launch.h"
 #include "wkv7_io.h"
 #include "wkv7_sched.h"
