@@ -82,6 +82,7 @@ struct BwdLds {
     uint16_t Hx[2][NK * NK];                     // H' [i][j] (swizzled)
     uint16_t QT[2][NK * LDQ], SAT[2][NK * LDQ];  // Q^T, SA^T [i][t]
     float dlp[2][4][64 * 4];                     // H side's dlogd terms z_t of a chunk, per key strip
+    Mat Mq[3];                                   // a tick's masked XM, M1^T and N1 (split), formed once
     Slot slot[NPROD];
     Plane raw[NPROD][5];                         // producer input staging: r, w, k, a, b
     uint32_t csync;                              // consumers' mid-tick rendezvous counter
@@ -533,25 +534,47 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
                 st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
             }
-            consumer_sync(&sm.csync, NCONS * (n + 1));
+            consumer_sync(&sm.csync, NCONS * (2 * n + 1));
             // ---- stage C: key strip j_own of dK, dB (all value rows, fixed order); dV rows i_own; new H ----
             const Strip st = strip(S);
-            f32x4_t xm = zero4(), m1T = zero4(), n1T = zero4(), gK = zero4(), gB = zero4();
+            // The masked 16x16 products XM = dY SA^T (keep s <= t), M1^T = Q V^T and N1 = SA Q^T
+            // (keep s > t) are the same for all eight consumer waves: one wave forms each (this
+            // side's waves 3 and 1, the S side's wave 2), publishes it split (Mq), and every
+            // wave reads it back, in the orientation it needs, after a second rendezvous.
+            if (cw == 3) {
+                f32x4_t xm = zero4();
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);  // dY[t][i], exact
+                    const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
+                    xm = mma32(xm, ya, sh);  // dY SA^T        [t][s]
+                    xm = mma32(xm, ya, sl);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++)  // D layout: row 4q+e, column r16
+                    if (r16 > 4 * q + e) xm[e] = 0.f;  // XM[t][s]: keep s <= t
+                put_mat(sm.Mq[0], xm, lane);
+            } else if (cw == 1) {
+                f32x4_t m1T = zero4();
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);  // V[t][i], exact
+                    const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
+                    m1T = mma32(m1T, qh, va);  // Q V^T = M1^T  [s][t]
+                    m1T = mma32(m1T, ql, va);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (4 * q + e <= r16) m1T[e] = 0.f;  // M1^T[s][t]: keep s > t
+                put_mat(sm.Mq[1], m1T, lane);
+            }
+            f32x4_t gK = zero4(), gB = zero4();
             {
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
                     const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);   // V[t][i], exact
-                    const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);  // dY[t][i], exact
-                    const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
                     const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
                     const uint4 hh = rows_tr_sw(sm.Hx[0], s, 16 * cw, lane), hl = rows_tr_sw(sm.Hx[1], s, 16 * cw, lane);
-                    xm = mma32(xm, ya, sh);  // dY SA^T        [t][s]
-                    xm = mma32(xm, ya, sl);
-                    m1T = mma32(m1T, qh, va);  // Q V^T = M1^T  [s][t]
-                    m1T = mma32(m1T, ql, va);
-                    n1T = mma32(n1T, qh, sh);  // Q SA^T = N1^T [s][t]
-                    n1T = mma32(n1T, qh, sl);
-                    n1T = mma32(n1T, ql, sh);
                     gK = mma32(gK, va, hh);  // V H'
                     gK = mma32(gK, va, hl);
                     gB = mma32(gB, sh, hh);  // SA H'
@@ -559,13 +582,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     gB = mma32(gB, sl, hh);
                 }
             }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
-                const int rw = 4 * q + e;
-                if (r16 > rw) xm[e] = 0.f;                  // XM[t][s]: keep s <= t
-                if (rw <= r16) m1T[e] = 0.f, n1T[e] = 0.f;  // M1^T[s][t], N1^T[s][t]: keep s > t
-            }
-            const Pk m2n = mat_n(S.M2, lane), pm1 = pk(m1T), pn1 = pk(n1T), pxm = pk(xm);
+            consumer_sync(&sm.csync, NCONS * (2 * n + 2));
+            // (put_mat of a D tile of M: mat_t reads the A operand of M^T, mat_n that of M)
+            const Pk m2n = mat_n(S.M2, lane), pm1 = mat_t(sm.Mq[1], lane), pn1 = mat_n(sm.Mq[2], lane),
+                     pxm = mat_t(sm.Mq[0], lane);
             const f32x4_t cK = mm32s(cat(pm1.h, m2n.h), cat(pm1.l, m2n.l), st.arh, st.arl);  // [triu_s(M1) | triu(M2)]
             const f32x4_t cB = mm32s(cat(pn1.h, pxm.h), cat(pn1.l, pxm.l), st.arh, st.arl);  // [triu_s(N1) | triu(SA dY^T)]
             float gk_[4], gb_[4], z[4];
@@ -758,35 +778,37 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);
                 gR = mma32(mma32(gR, ya, oh[s]), ya, ol[s]);
             }
-            consumer_sync(&sm.csync, NCONS * (n + 1));
-            // ---- stage C: key strip j_own of dR, dA and this chunk's dlogd terms ----
-            f32x4_t m1 = zero4(), xmT = zero4(), n1 = zero4(), gA = zero4();
-            {
+            consumer_sync(&sm.csync, NCONS * (2 * n + 1));
+            // ---- stage C: key strip j_own of dR, dA and this chunk's dlogd terms (this side's
+            //      wave 2 forms N1 for all eight consumer waves; XM and M1^T come from the H side) ----
+            if (cw == 2) {
+                f32x4_t n1 = zero4();
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
-                    const uint4 va = fragp_sw<SwDma>(S.V, r16, 32 * s, lane);
-                    const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);
                     const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
                     const uint4 sh = rows_tr(sm.SAT[0], s, lane), sl = rows_tr(sm.SAT[1], s, lane);
-                    m1 = mma32(m1, va, qh);  // V Q^T = M1     [t][s]
-                    m1 = mma32(m1, va, ql);
-                    xmT = mma32(xmT, sh, ya);  // SA dY^T = XM^T [s][t]
-                    xmT = mma32(xmT, sl, ya);
                     n1 = mma32(n1, sh, qh);  // SA Q^T = N1    [t][s]
                     n1 = mma32(n1, sh, ql);
                     n1 = mma32(n1, sl, qh);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++)  // D layout: row 4q+e, column r16
+                    if (r16 <= 4 * q + e) n1[e] = 0.f;  // N1[t][s]: keep s > t
+                put_mat(sm.Mq[2], n1, lane);
+            }
+            f32x4_t gA = zero4();
+            {
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const uint4 qh = rows_tr(sm.QT[0], s, lane), ql = rows_tr(sm.QT[1], s, lane);
                     gA = mma32(gA, qh, oh[s]);  // Q S0
                     gA = mma32(gA, qh, ol[s]);
                     gA = mma32(gA, ql, oh[s]);
                 }
             }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {  // D layout: row 4q+e, column r16
-                const int rw = 4 * q + e;
-                if (r16 <= rw) m1[e] = 0.f, n1[e] = 0.f;  // M1[t][s], N1[t][s]: keep s > t
-                if (rw > r16) xmT[e] = 0.f;               // XM^T[s][t]: keep s <= t
-            }
-            const Pk m2t = mat_t(S.M2, lane), pm1 = pk(m1), pn1 = pk(n1), pxm = pk(xmT);
+            consumer_sync(&sm.csync, NCONS * (2 * n + 2));
+            const Pk m2t = mat_t(S.M2, lane), pm1 = mat_n(sm.Mq[1], lane), pn1 = mat_t(sm.Mq[2], lane),
+                     pxm = mat_n(sm.Mq[0], lane);
             const f32x4_t cR = mm32s(cat(pxm.h, m2t.h), cat(pxm.l, m2t.l), st.bkh, st.bkl);  // [tril(dY SA^T) | tril(dY V^T)]
             const f32x4_t cA = mm32s(cat(pn1.h, pm1.h), cat(pn1.l, pm1.l), st.bkh, st.bkl);  // [tril_s(Q SA^T) | tril_s(Q V^T)]
             float gr_[4], ga_[4], z[4], t2[4];
