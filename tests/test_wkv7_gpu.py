@@ -119,6 +119,36 @@ def test_config2_nonzero_dsT_reduced_length():
     _parity(4, 256, 80, 64, torch.bfloat16, seed=20262, s0_std=0.1, with_dsT=True)
 
 
+@pytest.mark.parametrize("mode", ["wide", "max_decay", "no_decay"])
+@pytest.mark.parametrize("N", [64, 32])
+def test_decays_at_the_ends_of_their_range(mode, N):
+    """The decay exp(-e^{-1/2} sigmoid(w)) at its limits, on the chunked (N=64) and the
+    step-serial (N=32) kernels: w ~ N(0, 8^2) saturates sigmoid both ways in about a third
+    of the elements; w = +30 gives every step the strongest decay (inside a 16-step chunk
+    the e^{-g} scalings reach e^{9.7}); w = -30 gives no decay at all.
+
+    Every output meets the usual bars, except that with every step at the strongest decay
+    the exact dw is ~1e-13 everywhere (sigmoid'(30) = 9e-14), which makes its rel-L2
+    ill-conditioned; there dw is held to the elementwise bar only.  (The chunked backward
+    recovers sigmoid(w) from differences of fp32 cumulative log-decays, so its dw carries an
+    absolute error of at most ~5e-7 |dL/dlog d|.)"""
+    B, T, H = 2, 80, 3
+    inp = wkv7_inputs(B, T, H, N, seed=4242 + N, dtype=torch.bfloat16, s0_std=0.1, with_dsT=True)
+    w = inp["w"].float()
+    w = {"wide": 8.0 * w, "max_decay": torch.full_like(w, 30.0), "no_decay": torch.full_like(w, -30.0)}[mode]
+    inp["w"] = w.to(torch.bfloat16).contiguous()
+    print(f"  case decays={mode} B={B} T={T} H={H} N={N}", flush=True)
+    got = _gpu_fwd_bwd(inp, torch.bfloat16, inp["dsT"])
+    ref = _oracle(inp, inp["dsT"])
+    for name, g, r in zip(NAMES, got, ref):
+        if mode == "max_decay" and name == "dw":
+            err = np.abs(g.detach().float().cpu().numpy().astype(np.float64) - r)
+            print(f"    dw   max_abs={err.max():.2e} (|ref| <= {np.abs(r).max():.1e})", flush=True)
+            assert np.all(err <= MAX_ABS + 2.0 ** -7 * np.abs(r))
+            continue
+        _check(name, g, r, torch.bfloat16)
+
+
 # -- config 1: chunked calls with carried state == one unchunked call ------------------
 def test_config1_chunked_equals_unchunked():
     inp = wkv7_inputs(1, 4096, 80, 64, seed=20261, dtype=torch.bfloat16)
