@@ -23,8 +23,8 @@ constexpr int TB = 64;   // tokens per block for the parameter-gradient partials
 struct V8 {
     float x[8];
 };
-__device__ __forceinline__ V8 ld_bf8(const uint16_t* p) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
+__device__ __forceinline__ uint4 ld_raw8(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ V8 cvt_bf8(uint4 u) {
     V8 r;
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -34,6 +34,7 @@ __device__ __forceinline__ V8 ld_bf8(const uint16_t* p) {
     }
     return r;
 }
+__device__ __forceinline__ V8 ld_bf8(const uint16_t* p) { return cvt_bf8(ld_raw8(p)); }
 __device__ __forceinline__ V8 ld_f8(const float* p) {
     const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
     return V8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
@@ -86,7 +87,24 @@ __global__ __launch_bounds__(256) void shift_lerp_fwd(long M, int T, int C, cons
     }
 }
 
-// grid (ceil(C/512), ceil(M/TB)), 64 lanes, 8 channels per lane
+// grid (ceil(C/256), ceil(M/TB)), 64 lanes, 4 channels per lane (8-byte rows pieces, so
+// that a group's loads fit in registers with two waves per SIMD).  A wave walks its TB
+// tokens in order (the parameter-gradient partials are sums over them), UG tokens at a
+// time: all loads of a group -- the six gradient rows of tokens m+1 .. m+UG (token m's
+// are carried over) and the x rows of m .. m+UG-1 (x[m-1] is carried) -- are issued
+// before any is used, so a group costs one memory latency instead of one per token.
+constexpr int UG = 4;
+struct V4 {
+    float x[4];
+};
+__device__ __forceinline__ uint2 ld_raw4(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+__device__ __forceinline__ V4 cvt_bf4(uint2 u) {
+    return V4{{bf16_to_f32((uint16_t)(u.x & 0xffffu)), bf16_to_f32((uint16_t)(u.x >> 16)),
+               bf16_to_f32((uint16_t)(u.y & 0xffffu)), bf16_to_f32((uint16_t)(u.y >> 16))}};
+}
+__device__ __forceinline__ void st_bf4(uint16_t* p, const V4& v) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(f32x2_to_bf16x2(v.x[0], v.x[1]), f32x2_to_bf16x2(v.x[2], v.x[3]));
+}
 __global__ __launch_bounds__(64) void shift_lerp_bwd(long M, int T, int C, const uint16_t* d0,
                                                      const uint16_t* d1, const uint16_t* d2,
                                                      const uint16_t* d3, const uint16_t* d4,
@@ -94,58 +112,70 @@ __global__ __launch_bounds__(64) void shift_lerp_bwd(long M, int T, int C, const
                                                      const uint16_t* __restrict__ st,
                                                      const float* __restrict__ coef, uint16_t* dx,
                                                      uint16_t* dshift, float* __restrict__ part) {
-    const int c = (blockIdx.x * 64 + threadIdx.x) * 8;
+    const int c = (blockIdx.x * 64 + threadIdx.x) * 4;
     if (c >= C) return;
     const long m0 = (long)blockIdx.y * TB, m1 = min(M, m0 + TB);
     const uint16_t* dn[6] = {d0, d1, d2, d3, d4, d5};
-    V8 cf[6];
+    V4 cf[6];
 #pragma unroll
-    for (int n = 0; n < 6; n++) cf[n] = ld_f8(coef + n * C + c);
-    float acc[6][8];
+    for (int n = 0; n < 6; n++) {
+        const float4 f = *reinterpret_cast<const float4*>(coef + n * C + c);
+        cf[n] = V4{{f.x, f.y, f.z, f.w}};
+    }
+    float acc[6][4];
 #pragma unroll
     for (int n = 0; n < 6; n++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[n][e] = 0.f;
-    V8 cur[6];
+        for (int e = 0; e < 4; e++) acc[n][e] = 0.f;
+    const uint2 zero = make_uint2(0, 0);
+    uint2 dcur[6];  // gradient rows of the group's first token
 #pragma unroll
-    for (int n = 0; n < 6; n++) cur[n] = ld_bf8(dn[n] + m0 * C + c);
-    for (long m = m0; m < m1; m++) {
-        const int t = (int)(m % T), b = (int)(m / T);
-        V8 nxt[6];
-        const bool has_next = m + 1 < M;
+    for (int n = 0; n < 6; n++) dcur[n] = ld_raw4(dn[n] + m0 * C + c);
+    uint2 xprev = (m0 % T) > 0 ? ld_raw4(x + (m0 - 1) * C + c) : ld_raw4(st + (m0 / T) * C + c);
+    for (long m = m0; m < m1; m += UG) {
+        uint2 dr[UG][6], xr[UG];
 #pragma unroll
-        for (int n = 0; n < 6; n++) {
-            if (has_next) nxt[n] = ld_bf8(dn[n] + (m + 1) * C + c);
-            else
+        for (int u = 0; u < UG; u++) {
+            const long row = m + 1 + u;  // (the last token's successor may lie past m1)
 #pragma unroll
-                for (int e = 0; e < 8; e++) nxt[n].x[e] = 0.f;
+            for (int n = 0; n < 6; n++) dr[u][n] = row < M ? ld_raw4(dn[n] + row * C + c) : zero;
+            xr[u] = m + u < m1 ? ld_raw4(x + (m + u) * C + c) : zero;
         }
-        const V8 xv = ld_bf8(x + m * C + c);
-        const V8 pv = t > 0 ? ld_bf8(x + (m - 1) * C + c) : ld_bf8(st + (long)b * C + c);
-        V8 gx, gs;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float delta = round_bf16(pv.x[e] - xv.x[e]);
-            float dsum = 0.f, dc = 0.f, nx = 0.f;
+        for (int u = 0; u < UG; u++) {
+            const long mm = m + u;
+            if (mm < m1) {
+                const int t = (int)(mm % T), b = (int)(mm / T);
+                const V4 xv = cvt_bf4(xr[u]);
+                const V4 pv = cvt_bf4(t > 0 ? (u == 0 ? xprev : xr[u - 1]) : ld_raw4(st + (long)b * C + c));
+                V4 gx, gs;
 #pragma unroll
-            for (int n = 0; n < 6; n++) {
-                dsum += cur[n].x[e];
-                dc += cur[n].x[e] * cf[n].x[e];
-                nx += nxt[n].x[e] * cf[n].x[e];
-                acc[n][e] += cur[n].x[e] * delta;
+                for (int e = 0; e < 4; e++) {
+                    const float delta = round_bf16(pv.x[e] - xv.x[e]);
+                    float dsum = 0.f, dc = 0.f, nx = 0.f;
+#pragma unroll
+                    for (int n = 0; n < 6; n++) {
+                        const float cu = cvt_bf4(u == 0 ? dcur[n] : dr[u - 1][n]).x[e];
+                        dsum += cu;
+                        dc += cu * cf[n].x[e];
+                        nx += cvt_bf4(dr[u][n]).x[e] * cf[n].x[e];
+                        acc[n][e] += cu * delta;
+                    }
+                    gx.x[e] = dsum - dc + (t + 1 < T ? nx : 0.f);
+                    gs.x[e] = dc;
+                }
+                st_bf4(dx + mm * C + c, gx);
+                if (t == 0) st_bf4(dshift + (long)b * C + c, gs);
             }
-            gx.x[e] = dsum - dc + (t + 1 < T ? nx : 0.f);
-            gs.x[e] = dc;
         }
-        st_bf8(dx + m * C + c, gx);
-        if (t == 0) st_bf8(dshift + (long)b * C + c, gs);
+        xprev = xr[UG - 1];
 #pragma unroll
-        for (int n = 0; n < 6; n++) cur[n] = nxt[n];
+        for (int n = 0; n < 6; n++) dcur[n] = dr[UG - 1][n];
     }
     float* pb = part + (long)blockIdx.y * 6 * C;
 #pragma unroll
-    for (int n = 0; n < 6; n++) st_f8(pb + n * C + c, V8{{acc[n][0], acc[n][1], acc[n][2], acc[n][3], acc[n][4],
-                                                         acc[n][5], acc[n][6], acc[n][7]}});
+    for (int n = 0; n < 6; n++)
+        *reinterpret_cast<float4*>(pb + n * C + c) = make_float4(acc[n][0], acc[n][1], acc[n][2], acc[n][3]);
 }
 
 // part is [nblk][P][C]; outs[p][c] = sum_b part[b][p][c], summed in block order
@@ -156,8 +186,17 @@ __global__ __launch_bounds__(256) void reduce_blocks(const float* __restrict__ p
                                                      Outs outs) {
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= P * C) return;
+    const long stride = (long)P * C;
     float s = 0.f;
-    for (int b = 0; b < nblk; b++) s += part[(long)b * P * C + j];
+    int b = 0;
+    for (; b + 16 <= nblk; b += 16) {  // 16 loads in flight, summed in block order
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = part[(b + u) * stride + j];
+#pragma unroll
+        for (int u = 0; u < 16; u++) s += v[u];
+    }
+    for (; b < nblk; b++) s += part[b * stride + j];
     outs.p[j / C][j % C] = s;
 }
 
@@ -449,7 +488,7 @@ int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const 
     if (!ws || ws_bytes < theseus_tm_shift_lerp_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
     const long M = (long)B * T;
     const int nb = (int)nblk_t(B, T);
-    hipLaunchKernelGGL(tmix::shift_lerp_bwd, dim3((C + 511) / 512, nb), dim3(64), 0, stream, M, T, C,
+    hipLaunchKernelGGL(tmix::shift_lerp_bwd, dim3((C + 255) / 256, nb), dim3(64), 0, stream, M, T, C,
                        (const uint16_t*)dm[0], (const uint16_t*)dm[1], (const uint16_t*)dm[2],
                        (const uint16_t*)dm[3], (const uint16_t*)dm[4], (const uint16_t*)dm[5],
                        (const uint16_t*)x, (const uint16_t*)st, coef, (uint16_t*)dx, (uint16_t*)dshift, ws);
