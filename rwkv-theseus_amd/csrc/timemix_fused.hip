@@ -60,6 +60,9 @@ __device__ __forceinline__ float sum8(float x) {  // over the 8 lanes of a head 
 }
 
 // ---------------------------------------------------------------- shift-lerp
+// Thread: 8 channels of SLT consecutive tokens (the six coefficient vectors loaded once,
+// all x rows issued before use, x[t-1] taken from the previous token's registers).
+constexpr int SLT = 8;
 __global__ __launch_bounds__(256) void shift_lerp_fwd(long M, int T, int C, const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ st,
                                                       const float* __restrict__ coef, uint16_t* o0,
@@ -67,23 +70,36 @@ __global__ __launch_bounds__(256) void shift_lerp_fwd(long M, int T, int C, cons
                                                       uint16_t* o4, uint16_t* o5) {
     const long gid = (long)blockIdx.x * 256 + threadIdx.x;
     const int cv = C / 8;
-    if (gid >= M * cv) return;
-    const long m = gid / cv;
+    const long ng = (M + SLT - 1) / SLT;
+    if (gid >= ng * cv) return;
+    const long m0 = gid / cv * SLT, m1 = min(M, m0 + SLT);
     const int c = (int)(gid % cv) * 8;
-    const int t = (int)(m % T), b = (int)(m / T);
-    const V8 xv = ld_bf8(x + m * C + c);
-    const V8 pv = t > 0 ? ld_bf8(x + (m - 1) * C + c) : ld_bf8(st + (long)b * C + c);
+    uint4 xr[SLT];
+#pragma unroll
+    for (int u = 0; u < SLT; u++) xr[u] = m0 + u < m1 ? ld_raw8(x + (m0 + u) * C + c) : make_uint4(0, 0, 0, 0);
+    const uint4 prev0 = (m0 % T) > 0 ? ld_raw8(x + (m0 - 1) * C + c) : ld_raw8(st + (m0 / T) * C + c);
+    V8 cf[6];
+#pragma unroll
+    for (int n = 0; n < 6; n++) cf[n] = ld_f8(coef + n * C + c);
     uint16_t* outs[6] = {o0, o1, o2, o3, o4, o5};
-    float d[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) d[e] = round_bf16(pv.x[e] - xv.x[e]);  // delta is a bf16 tensor
+    for (int u = 0; u < SLT; u++) {
+        const long m = m0 + u;
+        if (m < m1) {
+            const int t = (int)(m % T), b = (int)(m / T);
+            const V8 xv = cvt_bf8(xr[u]);
+            const V8 pv = cvt_bf8(t > 0 ? (u == 0 ? prev0 : xr[u - 1]) : ld_raw8(st + (long)b * C + c));
+            float d[8];
 #pragma unroll
-    for (int n = 0; n < 6; n++) {
-        const V8 cf = ld_f8(coef + n * C + c);
-        V8 o;
+            for (int e = 0; e < 8; e++) d[e] = round_bf16(pv.x[e] - xv.x[e]);  // delta is a bf16 tensor
 #pragma unroll
-        for (int e = 0; e < 8; e++) o.x[e] = xv.x[e] + d[e] * cf.x[e];
-        st_bf8(outs[n] + m * C + c, o);
+            for (int n = 0; n < 6; n++) {
+                V8 o;
+#pragma unroll
+                for (int e = 0; e < 8; e++) o.x[e] = xv.x[e] + d[e] * cf[n].x[e];
+                st_bf8(outs[n] + m * C + c, o);
+            }
+        }
     }
 }
 
@@ -467,7 +483,7 @@ int theseus_tm_shift_lerp_fwd(int B, int T, int C, const void* x, const void* st
     if (!x || !st || !coef || !out) return THESEUS_WKV7_ERR_NULL;
     for (int n = 0; n < 6; n++)
         if (!out[n]) return THESEUS_WKV7_ERR_NULL;
-    const long M = (long)B * T, total = M * (C / 8);
+    const long M = (long)B * T, total = (M + tmix::SLT - 1) / tmix::SLT * (C / 8);
     hipLaunchKernelGGL(tmix::shift_lerp_fwd, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, M, T, C,
                        (const uint16_t*)x, (const uint16_t*)st, coef, (uint16_t*)out[0], (uint16_t*)out[1],
                        (uint16_t*)out[2], (uint16_t*)out[3], (uint16_t*)out[4], (uint16_t*)out[5]);
