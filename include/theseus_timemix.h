@@ -9,7 +9,8 @@
  * parameters are float32 [C] (r_k is [H,N] = [C]).  Parameter gradients are
  * reduced over B*T in a fixed order through a caller-provided float32 workspace
  * (theseus_tm_*_workspace gives its size), then written to [C] outputs.
- * Head size N must be 64 (8 lanes x 8 channels per head row).  All calls are
+ * Head size N must be 64 (8 lanes x 8 channels per head row), and B*T at most
+ * 65535 * 64 tokens (status 1, THESEUS_WKV7_ERR_SHAPE, otherwise).  All calls are
  * asynchronous on `stream`; status codes are those of theseus_wkv7.h.
  */
 #ifndef THESEUS_TIMEMIX_H

@@ -469,6 +469,8 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
 namespace {
 int tm_check(int B, int T, int C) {
     if (B < 1 || T < 1 || C < tmix::HN || C % tmix::HN) return THESEUS_WKV7_ERR_SHAPE;
+    // token blocks run along the grid's y dimension (at most 65535 blocks)
+    if ((long)B * T > 65535L * tmix::TB) return THESEUS_WKV7_ERR_SHAPE;
     return THESEUS_WKV7_OK;
 }
 int tm_status() { return hipGetLastError() == hipSuccess ? THESEUS_WKV7_OK : THESEUS_WKV7_ERR_LAUNCH; }

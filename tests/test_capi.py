@@ -67,6 +67,23 @@ def test_timemix_abi_exported_and_bound_with_header_arity():
         assert fn.argtypes is not None and len(fn.argtypes) == n, (name, n)
 
 
+def test_timemix_abi_rejects_shapes_before_launching():
+    """Every fused TimeMix entry point checks B, T, C first (status 1, nothing enqueued):
+    C must be a positive multiple of 64, and B*T may not exceed 65535 blocks of 64 tokens
+    along the grid's y dimension.  Null pointers are never reached."""
+    from theseus import fused
+    lib = fused._lib()
+    names = ["theseus_tm_shift_lerp_fwd", "theseus_tm_shift_lerp_bwd", "theseus_tm_kk_fwd",
+             "theseus_tm_kk_bwd", "theseus_tm_gn_fwd", "theseus_tm_gn_bwd"]
+    for B, T, C in [(1 << 16, 1 << 13, 64), (65535, 65, 64), (1, 4, 96), (0, 4, 64), (1, 0, 64)]:
+        for name in names:
+            fn = getattr(lib, name)
+            rest = [0.0 if t is ctypes.c_float else 0 if t is ctypes.c_size_t else None for t in fn.argtypes[3:]]
+            assert fn(B, T, C, *rest) == 1, (name, B, T, C)
+    # exactly 65535 blocks of 64 tokens passes the shape check and stops at the null pointers
+    assert lib.theseus_tm_shift_lerp_fwd(65535, 64, 64, None, None, None, None, None) not in (0, 1)
+
+
 def test_host_queries():
     ext = W.extension()
     assert ext.abi_version == 2
