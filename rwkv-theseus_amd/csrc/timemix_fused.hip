@@ -19,6 +19,7 @@ using namespace wkv7;
 
 constexpr int HN = 64;   // head size handled here
 constexpr int TB = 64;   // tokens per block for the parameter-gradient partials
+constexpr int HG = 8;    // heads per block of the kk / GroupNorm backward kernels
 
 struct V8 {
     float x[8];
@@ -257,7 +258,7 @@ __global__ __launch_bounds__(256) void kk_fwd(long rows, int H, int C, const uin
     }
 }
 
-// grid (H, ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
+// grid (ceil(H/HG), ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
 __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16_t* __restrict__ dkw,
                                               const uint16_t* __restrict__ daw,
                                               const uint16_t* __restrict__ dbw, const uint16_t* __restrict__ k,
@@ -265,13 +266,16 @@ __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16
                                               const float* __restrict__ kap, uint16_t* dk, float* da,
                                               float* __restrict__ part) {
     __shared__ float red[2][32][HN + 1];
-    const int h = blockIdx.x, rs = threadIdx.x >> 3, sub = threadIdx.x & 7;
-    const int c = h * HN + 8 * sub;
+    // 32 rows = 4 tokens x HG consecutive heads, so a wave reads whole 1 KB runs of a token
+    const int rs = threadIdx.x >> 3, sub = threadIdx.x & 7, hh = rs % HG, tt = rs / HG;
+    const int h = blockIdx.x * HG + hh;
+    const bool hok = h < H;
+    const int c = (hok ? h : 0) * HN + 8 * sub;
     const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c);
     float acc_kk[8] = {}, acc_ka[8] = {};
-    for (int it = 0; it < TB / 32; it++) {
-        const long m = (long)blockIdx.y * TB + it * 32 + rs;
-        const bool ok = m < M;
+    for (int it = 0; it < TB / 4; it++) {
+        const long m = (long)blockIdx.y * TB + it * 4 + tt;
+        const bool ok = hok && m < M;
         const long o = m * C + c;
         V8 kv{}, av{}, gw{}, ga{}, gb{};
         if (ok) {
@@ -319,11 +323,13 @@ __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16
         red[1][rs][8 * sub + e] = acc_ka[e];
     }
     __syncthreads();
-    if (threadIdx.x < 2 * HN) {
-        const int p = threadIdx.x / HN, n = threadIdx.x % HN;
-        float s = 0.f;
-        for (int i = 0; i < 32; i++) s += red[p][i][n];
-        part[((long)blockIdx.y * 2 + p) * C + h * HN + n] = s;
+    for (int q = threadIdx.x; q < 2 * HG * HN; q += 256) {  // sum the 4 token rows of each head
+        const int p = q / (HG * HN), hq = (q / HN) % HG, n = q % HN, hd = blockIdx.x * HG + hq;
+        if (hd < H) {
+            float s = 0.f;
+            for (int i = 0; i < 32 / HG; i++) s += red[p][i * HG + hq][n];
+            part[((long)blockIdx.y * 2 + p) * C + hd * HN + n] = s;
+        }
     }
 }
 
@@ -370,7 +376,7 @@ __global__ __launch_bounds__(256) void gn_fwd(long rows, int H, int C, const uin
     if (ok) st_bf8(out + o, ov);
 }
 
-// grid (H, ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
+// grid (ceil(H/HG), ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
 __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16_t* __restrict__ dout,
                                               const uint16_t* __restrict__ y, const uint16_t* __restrict__ r,
                                               const uint16_t* __restrict__ k, const float* __restrict__ a,
@@ -380,13 +386,16 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
                                               float eps, uint16_t* dy, uint16_t* dr, uint16_t* dk,
                                               uint16_t* dv, uint16_t* dg, float* da, float* __restrict__ part) {
     __shared__ float red[4][32][HN + 1];
-    const int h = blockIdx.x, rs = threadIdx.x >> 3, sub = threadIdx.x & 7;
-    const int c = h * HN + 8 * sub;
+    // 32 rows = 4 tokens x HG consecutive heads, as kk_bwd
+    const int rs = threadIdx.x >> 3, sub = threadIdx.x & 7, hh = rs % HG, tt = rs / HG;
+    const int h = blockIdx.x * HG + hh;
+    const bool hok = h < H;
+    const int c = (hok ? h : 0) * HN + 8 * sub;
     const V8 ka = ld_f8(kap + c), rk = ld_f8(rkp + c), lw = ld_f8(lwp + c), lb = ld_f8(lbp + c);
     float acc[4][8] = {};  // dr_k, dln_w, dln_b, dk_a
-    for (int it = 0; it < TB / 32; it++) {
-        const long m = (long)blockIdx.y * TB + it * 32 + rs;
-        const bool ok = m < M;
+    for (int it = 0; it < TB / 4; it++) {
+        const long m = (long)blockIdx.y * TB + it * 4 + tt;
+        const bool ok = hok && m < M;
         const long o = m * C + c;
         V8 yv{}, rv{}, kv{}, av{}, vv{}, gv{}, go{};
         if (ok) {
@@ -455,11 +464,13 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
 #pragma unroll
         for (int e = 0; e < 8; e++) red[p][rs][8 * sub + e] = acc[p][e];
     __syncthreads();
-    {
-        const int p = threadIdx.x / HN, n = threadIdx.x % HN;  // 256 = 4 x 64
-        float s = 0.f;
-        for (int i = 0; i < 32; i++) s += red[p][i][n];
-        part[((long)blockIdx.y * 4 + p) * C + h * HN + n] = s;
+    for (int q = threadIdx.x; q < 4 * HG * HN; q += 256) {  // sum the 4 token rows of each head
+        const int p = q / (HG * HN), hq = (q / HN) % HG, n = q % HN, hd = blockIdx.x * HG + hq;
+        if (hd < H) {
+            float s = 0.f;
+            for (int i = 0; i < 32 / HG; i++) s += red[p][i * HG + hq][n];
+            part[((long)blockIdx.y * 4 + p) * C + hd * HN + n] = s;
+        }
     }
 }
 
@@ -538,7 +549,7 @@ int theseus_tm_kk_bwd(int B, int T, int C, const void* dkw, const void* daw, con
         return THESEUS_WKV7_ERR_NULL;
     if (!ws || ws_bytes < theseus_tm_kk_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
     const int H = C / tmix::HN, nb = (int)nblk_t(B, T);
-    hipLaunchKernelGGL(tmix::kk_bwd, dim3(H, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dkw,
+    hipLaunchKernelGGL(tmix::kk_bwd, dim3((H + tmix::HG - 1) / tmix::HG, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dkw,
                        (const uint16_t*)daw, (const uint16_t*)dbw, (const uint16_t*)k, a, k_k, k_a,
                        (uint16_t*)dk, da, ws);
     tmix::Outs o2{{dk_k, dk_a, nullptr, nullptr, nullptr, nullptr}};
@@ -574,7 +585,7 @@ int theseus_tm_gn_bwd(int B, int T, int C, const void* dout, const void* y, cons
         return THESEUS_WKV7_ERR_NULL;
     if (!ws || ws_bytes < theseus_tm_gn_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
     const int H = C / tmix::HN, nb = (int)nblk_t(B, T);
-    hipLaunchKernelGGL(tmix::gn_bwd, dim3(H, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dout,
+    hipLaunchKernelGGL(tmix::gn_bwd, dim3((H + tmix::HG - 1) / tmix::HG, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dout,
                        (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, a, k_a, (const uint16_t*)v,
                        (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)dy, (uint16_t*)dr, (uint16_t*)dk,
                        (uint16_t*)dv, (uint16_t*)dg, da, ws);
