@@ -11,6 +11,18 @@ events on the stream the kernels run on; ``cpu_baseline`` times the
 reference's PyTorch op sequence (float32, autograd) on the host cores over a
 bounded slice of the same workload.
 
+Counted traffic (``roofline.traffic``, ``hbm_frac_counted``) is not measured in
+this run: it is the per-launch FETCH_SIZE + WRITE_SIZE of committed rocprofv3
+--pmc runs (profiles/wkv7_<config>_traffic.json, source named in the line).  At
+config 2 it is the algorithmic bytes plus the saved states the config mandates
+(a state every 16 steps, written by the forward and read by the backward,
+0.676 GB each way), 3.075 GB per step: even at the full 8 TB/s a step takes
+0.384 ms, which caps the algorithmic fraction near 55 %.
+
+Other configurations (``--config``): c1 = 8 chained T=512 forward calls without
+saved states (state carried), B=1, H=80; c4 = 256 in-place decode steps at
+B=64, with one fused T=256 forward timed beside them; c3 = the TimeMix layer.
+
 Algorithmic bytes (compulsory contract I/O; E = H*N, S_l = H*N*N*4 bytes):
   forward  = B*T*E*2*7  + 2*B*S_l   (r,w,k,v,a,b in, y out; s0 in, sT out)
   backward = B*T*E*2*13 + 3*B*S_l   (r..b, dy in; six grads out; s0, dsT in, ds0 out)
@@ -192,12 +204,21 @@ def main():
         def one_step():
             for t in range(T):
                 ext.decode_step(*steps_in[t], state)
-    else:
+    elif args.config == "c2":
         def one_step():
             y, end, saved = ext.forward(*xs, s0, True)
-            if args.config == "c1":
-                return
             ext.backward(*xs, saved, dy, None)
+    else:
+        # c1: 8 consecutive T=512 calls with the state carried, no saved states (no-grad path)
+        NSPLIT = 8
+        Tc = T // NSPLIT
+        pieces = [[x[:, i * Tc:(i + 1) * Tc].contiguous() for x in xs] for i in range(NSPLIT)]
+
+        def one_step():
+            st = s0
+            for pc in pieces:
+                _, st, _ = ext.forward(*pc, st, False)
+            return st
 
     for _ in range(args.warmup):
         one_step()
@@ -224,6 +245,28 @@ def main():
         e1.record(stream)
         torch.cuda.synchronize()
         kern["decode"] = (e0.elapsed_time(e1) / T, alg_bytes(B, 1, H, N, "decode"))
+        # the same T tokens as one fused forward (no saved states)
+        fused_ms = []
+        for _ in range(max(3, min(args.steps, 10))):
+            a0, a1 = ev(), ev()
+            a0.record(stream)
+            ext.forward(*xs, s0, False)
+            a1.record(stream)
+            torch.cuda.synchronize()
+            fused_ms.append(a0.elapsed_time(a1))
+        t256_ms = sum(fused_ms) / len(fused_ms)
+    elif args.config == "c1":
+        call_ms = []
+        for _ in range(max(3, min(args.steps, 10))):
+            st = s0
+            for pc in pieces:
+                a0, a1 = ev(), ev()
+                a0.record(stream)
+                _, st, _ = ext.forward(*pc, st, False)
+                a1.record(stream)
+                torch.cuda.synchronize()
+                call_ms.append(a0.elapsed_time(a1))
+        kern["fwd"] = (sum(call_ms) / len(call_ms), alg_bytes(B, Tc, H, N, "fwd"))
     else:
         fwd_ms, bwd_ms = [], []
         for _ in range(max(3, min(args.steps, 10))):
@@ -231,37 +274,42 @@ def main():
             a0.record(stream)
             y, end, saved = ext.forward(*xs, s0, True)
             a1.record(stream)
-            if args.config != "c1":
-                ext.backward(*xs, saved, dy, None)
+            ext.backward(*xs, saved, dy, None)
             a2.record(stream)
             torch.cuda.synchronize()
             fwd_ms.append(a0.elapsed_time(a1))
             bwd_ms.append(a1.elapsed_time(a2))
         kern["fwd"] = (sum(fwd_ms) / len(fwd_ms), alg_bytes(B, T, H, N, "fwd"))
-        if args.config != "c1":
-            kern["bwd"] = (sum(bwd_ms) / len(bwd_ms), alg_bytes(B, T, H, N, "bwd"))
+        kern["bwd"] = (sum(bwd_ms) / len(bwd_ms), alg_bytes(B, T, H, N, "bwd"))
     dom = max(kern, key=lambda k: kern[k][0])
     dom_ms, dom_bytes = kern[dom]
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
 
     if args.config == "c4":
         step_bytes = alg_bytes(B, 1, H, N, "decode") * T
+    elif args.config == "c1":
+        step_bytes = alg_bytes(B, Tc, H, N, "fwd") * NSPLIT
     else:
-        step_bytes = alg_bytes(B, T, H, N, "fwd") + (0 if args.config == "c1" else alg_bytes(B, T, H, N, "bwd"))
+        step_bytes = alg_bytes(B, T, H, N, "fwd") + alg_bytes(B, T, H, N, "bwd")
     step_gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    traffic = None  # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC runs
+    # HBM bytes per launch, from committed rocprofv3 --pmc runs (FETCH_SIZE and WRITE_SIZE,
+    # calibrated against a copy kernel): not measured in this run
+    traffic, traffic_src, counted = None, None, None
     tf = ROOT / "profiles" / f"wkv7_{args.config}_traffic.json"
     if tf.exists():
         rec = json.loads(tf.read_text())
         if (rec.get("B"), rec.get("T"), rec.get("H"), rec.get("N")) == (B, T, H, N):
             traffic = rec["bytes_per_launch"].get(dom)
+            traffic_src = f"committed rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE: {rec['source']}"
+            if all(k in rec["bytes_per_launch"] for k in kern):
+                counted = sum(rec["bytes_per_launch"][k] for k in kern)
 
     cpu = None
     if args.cpu_slice and args.config == "c2":
         cpu = cpu_baseline(B, H, N, args.cpu_slice, cfg["seed"])
 
-    workload = {"c2": "wkv7_fwd_bwd", "c1": "wkv7_fwd", "c4": "wkv7_decode"}[args.config]
+    workload = {"c2": "wkv7_fwd_bwd", "c1": "wkv7_fwd_8x512_chained", "c4": "wkv7_decode"}[args.config]
     line = {
         "metric": METRIC if args.config == "c2" else f"WKV7 {workload} tokens/s ({args.config})",
         "value": round(value, 1),
@@ -283,9 +331,24 @@ def main():
         "kernel_ms": {k: round(v[0], 4) for k, v in kern.items()},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "alg_bytes_per_launch": dom_bytes},
+                     "traffic_source": traffic_src, "alg_bytes_per_launch": dom_bytes,
+                     "frac_counted": (round(traffic / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
+                                      if traffic else None)},
         "cpu_baseline": cpu,
     }
+    if counted:
+        # the whole step on counted bytes, and the algorithmic fraction a step could reach at
+        # the full 8 TB/s with these bytes (the saved-state traffic the config mandates)
+        line["hbm_frac_counted"] = round(counted / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
+        line["alg_frac_cap_at_peak"] = round(step_bytes / counted, 4)
+    if args.config == "c1":
+        line["config"].update(calls=NSPLIT, T_per_call=Tc, saved_states=False)
+        line["call_ms"] = round(kern["fwd"][0], 4)
+    if args.config == "c4":
+        line["config"].update(steps_per_call=1, saved_states=False)
+        line["decode_step_ms"] = round(kern["decode"][0], 4)
+        line["fused_t256_forward_ms"] = round(t256_ms, 4)
+        line["decode_over_fused_t256"] = round(kern["decode"][0] * T / t256_ms, 2)
     print(json.dumps(line), flush=True)
 
 

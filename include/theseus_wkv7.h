@@ -47,11 +47,29 @@ enum theseus_wkv7_status {
     THESEUS_WKV7_ERR_LAUNCH = 5      /* hipGetLastError reported a failure          */
 };
 
+/* Kernel family a call of these sizes runs on (theseus_wkv7_kernel_family). */
+enum theseus_wkv7_family {
+    THESEUS_WKV7_FAMILY_CHUNKED = 0,    /* chunked MFMA kernels (bf16, N = 64)              */
+    THESEUS_WKV7_FAMILY_FORCED = 1,     /* step-serial: THESEUS_WKV7_FAMILY=seq is set       */
+    THESEUS_WKV7_FAMILY_FP32 = 2,       /* step-serial: fp32 token tensors                   */
+    THESEUS_WKV7_FAMILY_HEAD_SIZE = 3,  /* step-serial: N != 64                              */
+    THESEUS_WKV7_FAMILY_SIZE = 4        /* step-serial: a token tensor >= 2 GiB or one head's
+                                           saved states >= 4 GiB (32-bit buffer offsets)     */
+};
+
 /* ABI version of this header; bumped on any incompatible change. */
 int theseus_wkv7_abi_version(void);
 
 /* Static message for a status code (never NULL). */
 const char* theseus_wkv7_error_string(int status);
+
+/* Which kernel family theseus_wkv7_forward / _backward use for these sizes
+ * (a theseus_wkv7_family value), or minus a status code for invalid sizes.
+ * The step-serial kernels are exact but run one step at a time (config 2:
+ * ~0.12 M tokens/s against ~9 M on the chunked kernels); callers can warn or
+ * refuse when a call would fall back to them.  No counterpart in the
+ * reference (its kernel is step-serial for every call, kernels/wkv7_state.cu:81-92). */
+int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype);
 
 /* Steps between saved states (16); the saved-state tensor of a T-step
  * forward holds theseus_wkv7_checkpoint_count(T) states

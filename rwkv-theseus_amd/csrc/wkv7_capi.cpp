@@ -38,11 +38,20 @@ static bool force_seq() {
     const char* e = getenv("THESEUS_WKV7_FAMILY");
     return e && strcmp(e, "seq") == 0;
 }
-// The chunked kernels cover bf16, N = 64, and token tensors under 2 GiB (the
-// backward addresses them with 32-bit buffer offsets).
-static bool chunk_ok(int B, int T, int H, int N, int dtype) {
-    return N == 64 && dtype == THESEUS_WKV7_BF16 && (long long)B * T * H * N * 2 < (1ll << 31) && !force_seq();
+// Why the chunked kernels do not cover a call (0: they do).  They need bf16,
+// N = 64, token tensors under 2 GiB and one head's saved states under 4 GiB:
+// both are addressed with 32-bit buffer offsets (the token tensors' range
+// check also drops rows past a partial chunk, so the limit is 2^31).
+int chunk_refusal(int B, int T, int H, int N, int dtype) {
+    if (force_seq()) return THESEUS_WKV7_FAMILY_FORCED;
+    if (dtype != THESEUS_WKV7_BF16) return THESEUS_WKV7_FAMILY_FP32;
+    if (N != 64) return THESEUS_WKV7_FAMILY_HEAD_SIZE;
+    if ((long long)B * T * H * N * 2 >= (1ll << 31) ||
+        ((long long)(T + kCkptInterval - 1) / kCkptInterval + 1) * N * N * 4 >= (1ll << 32))
+        return THESEUS_WKV7_FAMILY_SIZE;
+    return 0;
 }
+static bool chunk_ok(int B, int T, int H, int N, int dtype) { return chunk_refusal(B, T, H, N, dtype) == 0; }
 
 // CUs of the current device, which the chunked kernels' schedule spreads the
 // heads over (one workgroup each).  THESEUS_WKV7_CUS=<n> plans for n instead
@@ -96,6 +105,11 @@ const char* theseus_wkv7_error_string(int status) {
         case THESEUS_WKV7_ERR_LAUNCH: return "HIP kernel launch failed";
         default: return "unknown status";
     }
+}
+
+int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype) {
+    if (int e = check_dims(B, T, H, N, dtype)) return -e;
+    return wkv7::chunk_refusal(B, T, H, N, dtype);
 }
 
 int theseus_wkv7_checkpoint_interval(void) { return wkv7::kCkptInterval; }

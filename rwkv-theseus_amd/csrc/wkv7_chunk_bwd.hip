@@ -117,16 +117,30 @@ __device__ __forceinline__ Pk mat_n(const Mat& m, int lane) {  // A operand of M
 // The consumer waves' mid-tick rendezvous (their exchange planes written before,
 // read after): each of the 8 counts itself in on an LDS counter and waits for the
 // tick's total.  The producers do not take part, so their work is not cut in two
-// by it.  The wait is bounded (a wave that never arrives cannot hang the kernel).
+// by it.  The wait is bounded (a wave that never arrives cannot hang the kernel);
+// it returns false on time-out, and the waves then write NaN in place of every
+// gradient from that tick on (the `bad` flag below), so a broken rendezvous can
+// never pass for a result.  The count is read through readfirstlane, so the
+// outcome is wave-uniform and the poisoning is a scalar branch.
 constexpr int NCONS = 8;
-__device__ __forceinline__ void consumer_sync(uint32_t* cnt, uint32_t target) {
+__device__ __forceinline__ bool consumer_sync(uint32_t* cnt, uint32_t target) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are done
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    bool ok = false;
     for (int i = 0; i < (1 << 22); i++) {
-        if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        if (__builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) >= target) {
+            ok = true;
+            break;
+        }
         __builtin_amdgcn_s_sleep(1);
     }
     asm volatile("" ::: "memory");
+    return ok;
+}
+__device__ __forceinline__ f32x4_t nan4() {
+    const float x = __builtin_nanf("");
+    return f32x4_t{x, x, x, x};
 }
 // split-precision K=32 product (both operands split)
 __device__ __forceinline__ f32x4_t mm32s(uint4 ah, uint4 al, uint4 bh, uint4 bl) {
@@ -458,6 +472,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
     } else if (hside) {
         // ======================= H side: rows i_own of H and dV; key strip j_own: dK, dB =======================
         f32x4_t Ht[4];  // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e] (H' within a tick)
+        bool bad = false;  // a rendezvous timed out: every later output is NaN
         lds_barrier();
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
@@ -479,12 +494,12 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
                 }
             } else {
-                const float bad = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");
+                const float hw = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");  // NaN: time-out
                 const float* src = hand + (m + 1) * NH;
 #pragma unroll
                 for (int tj = 0; tj < 4; tj++) {
                     const float4 x = handoff_get4(src + row * NK + 16 * tj + col);
-                    Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w} * bad;
+                    Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w} * hw;
                 }
             }
           }
@@ -534,7 +549,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
                 st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
             }
-            consumer_sync(&sm.csync, NCONS * (2 * n + 1));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 1));
             // ---- stage C: key strip j_own of dK, dB (all value rows, fixed order); dV rows i_own; new H ----
             const Strip st = strip(S);
             // The masked 16x16 products XM = dY SA^T (keep s <= t), M1^T = Q V^T and N1 = SA Q^T
@@ -582,7 +597,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     gB = mma32(gB, sl, hh);
                 }
             }
-            consumer_sync(&sm.csync, NCONS * (2 * n + 2));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 2));
             // (put_mat of a D tile of M: mat_t reads the A operand of M^T, mat_n that of M)
             const Pk m2n = mat_n(S.M2, lane), pm1 = mat_t(sm.Mq[1], lane), pn1 = mat_n(sm.Mq[2], lane),
                      pxm = mat_t(sm.Mq[0], lane);
@@ -599,6 +614,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const float Kb_ = bf_el8(st.bkh, 4 + e) + bf_el8(st.bkl, 4 + e);
                 z[e] = -(Bb_ * uB + Kb_ * uK);  // -(b dB + k dK) before e^{-g}: this side's dlogd terms
             }
+            if (__builtin_expect(bad, false)) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) gk_[e] = gb_[e] = z[e] = __builtin_nanf("");
+            }
             const uint32_t o = piece_off(bb, h, c);
             store8(dk, tbytes, o, quad_rows_bf16(f32x4_t{gk_[0], gk_[1], gk_[2], gk_[3]}, lane));
             store8(db, tbytes, o, quad_rows_bf16(f32x4_t{gb_[0], gb_[1], gb_[2], gb_[3]}, lane));
@@ -607,7 +626,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             {  // dV = K- H'^T + Brk^T dY + Aak^T Q
                 const Pk brkT = mat_t(S.Brk, lane);
                 const f32x4_t c3 = mm16s_acc(mma16(mma16(zero4(), brkT.h, dyf), brkT.l, dyf), mat_t(S.Aak, lane), pq);
-                const f32x4_t dvv = dv0 + c3;
+                const f32x4_t dvv = __builtin_expect(bad, false) ? nan4() : dv0 + c3;
                 store8(dv, tbytes, o, quad_rows_bf16(dvv, lane));
             }
             // H_0^T = H'^T + [A~^T R~^T] [Q; dY]
@@ -617,6 +636,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const uint4 ah = cat(ldtr_sw<SwLane>(S.At[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[0], 0, 16 * tj, lane));
                 const uint4 al = cat(ldtr_sw<SwLane>(S.At[1], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Rt[1], 0, 16 * tj, lane));
                 Ht[tj] = mma32(mma32(mma32(Ht[tj], ah, bhi), ah, blo), al, bhi);
+            }
+            if (__builtin_expect(bad, false)) {
+#pragma unroll
+                for (int tj = 0; tj < 4; tj++) Ht[tj] = nan4();
             }
             lds_barrier();
           }
@@ -643,6 +666,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         f32x4_t S0n[4];
         float S0s[16];
         float carry = 0.f;  // the dlogd carry for key j_own
+        bool bad = false;   // a rendezvous timed out: every later output is NaN
         // buffer loads from a head's saved states: one lane offset, the rest in
         // scalar and immediate offsets (no per-load address arithmetic)
         auto ck_rsrc = [&](int j) { return make_rsrc(ckpt + (long)j * ncp * NN, (uint32_t)(ncp * NN * 4)); };
@@ -714,8 +738,8 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 }
                 carry = p;
             } else {  // the carry from the handoff of boundary m + 1
-                const float bad = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");
-                carry = handoff_get(hand + (m + 1) * NH + NN + key) * bad;
+                const float hw = handoff_wait(flags + m + 1, NCONS) ? 1.f : __builtin_nanf("");  // NaN: time-out
+                carry = handoff_get(hand + (m + 1) * NH + NN + key) * hw;
             }
           }
           // the chunk after this piece's last: the next piece's first (or a repeat at the end)
@@ -778,7 +802,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);
                 gR = mma32(mma32(gR, ya, oh[s]), ya, ol[s]);
             }
-            consumer_sync(&sm.csync, NCONS * (2 * n + 1));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 1));
             // ---- stage C: key strip j_own of dR, dA and this chunk's dlogd terms (this side's
             //      wave 2 forms N1 for all eight consumer waves; XM and M1^T come from the H side) ----
             if (cw == 2) {
@@ -806,7 +830,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     gA = mma32(gA, ql, oh[s]);
                 }
             }
-            consumer_sync(&sm.csync, NCONS * (2 * n + 2));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 2));
             const Pk m2t = mat_t(S.M2, lane), pm1 = mat_n(sm.Mq[1], lane), pn1 = mat_t(sm.Mq[2], lane),
                      pxm = mat_n(sm.Mq[0], lane);
             const f32x4_t cR = mm32s(cat(pxm.h, m2t.h), cat(pxm.l, m2t.l), st.bkh, st.bkl);  // [tril(dY SA^T) | tril(dY V^T)]
@@ -821,6 +845,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const float Rt_ = bf_el8(st.arh, 4 + e) + bf_el8(st.arl, 4 + e);
                 z[e] = Rt_ * uR;
                 t2[e] = At_ * uA;
+            }
+            if (__builtin_expect(bad, false)) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) gr_[e] = ga_[e] = z[e] = t2[e] = __builtin_nanf("");
             }
             const uint32_t o = piece_off(bb, h, c);
             store8(dr, tbytes, o, quad_rows_bf16(f32x4_t{gr_[0], gr_[1], gr_[2], gr_[3]}, lane));

@@ -53,9 +53,15 @@ def _lib():
     return lib if _ready else None
 
 
+# The fused kernels' grids index token blocks of 64 in blockIdx.y (at most 65535).
+MAX_TOKENS = 65535 * 64
+
+
 def available(x, head_size):
-    """True when the fused kernels cover this call: bf16 CUDA activations, N = 64."""
-    return x.dtype == torch.bfloat16 and head_size == 64 and x.shape[-1] % 64 == 0 and _lib() is not None
+    """True when the fused kernels cover this call: bf16 CUDA activations, N = 64, and
+    B*T within the kernels' grid (longer inputs take the torch op sequence)."""
+    return (x.dtype == torch.bfloat16 and head_size == 64 and x.shape[-1] % 64 == 0
+            and x.shape[0] * x.shape[1] <= MAX_TOKENS and _lib() is not None)
 
 
 def _p(t):

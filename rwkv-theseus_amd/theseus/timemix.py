@@ -14,6 +14,14 @@ modulation that produces the WKV operands (:78-80), and the fp32 GroupNorm +
 r*k*r_k bonus + gate (:83-88).  Projections and LoRAs stay torch GEMMs
 (hipBLASLt).  ``backend="reference"`` runs the reference's torch op sequence
 for all of it.
+
+Credit: the parameter schema and the initialisation formulas are those of
+RWKV-LM-V7's RWKV_Tmix_x070 and generate_init_weight (RWKV-Vibe/RWKV-LM-V7,
+src/model.py at commit 665472dab30952de9379a3a3a01eaa3453f1ad4e, Apache-2.0),
+as adapted by the reference (theseus/timemix.py:1-10: independent blocks with
+no cross-layer v_first, explicit shift/WKV state, fp32 normalisation).  They
+are kept as the module's contract (state dicts, seeds and exports depend on
+them), under that licence.
 """
 from __future__ import annotations
 
@@ -24,6 +32,28 @@ from torch import nn
 from torch.nn import functional as F
 
 from .wkv7 import wkv7
+
+
+def _group_norm(x, groups, weight, bias, eps):
+    """F.group_norm(x, groups, weight, bias, eps) for x [M, C], written out (mean, biased
+    variance, affine) so that its backward is plain elementwise autograd.
+
+    Used for GPU tensors: torch 2.10+rocm7.0's group_norm backward returns wrong weight
+    and bias gradients (relative error ~1) once x has about 1024 rows or more (measured
+    against float64 on the CPU: M=1024..8192 rows at 4..80 groups), which would silently
+    mistrain ln_x.  Same arithmetic as the reference's call (theseus/timemix.py:84)."""
+    M, C = x.shape
+    xg = x.reshape(M, groups, C // groups)
+    mean = xg.mean(-1, keepdim=True)
+    var = (xg - mean).square().mean(-1, keepdim=True)
+    return ((xg - mean) * torch.rsqrt(var + eps)).reshape(M, C) * weight + bias
+
+
+def _shift_lerp_ops(x, shift, coefs):
+    """The reference's token-shift lerp as torch ops (theseus/timemix.py:70-71): the six
+    mixes x + (x[t-1] - x) * coef, with x[-1] = the carried shift."""
+    delta = torch.cat([shift.unsqueeze(1), x[:, :-1]], 1) - x
+    return [(x + delta * c).to(x.dtype) for c in coefs]
 
 
 class TimeMix(nn.Module):
@@ -94,8 +124,8 @@ class TimeMix(nn.Module):
             mixed = dict(zip("rwkvag", fused.shift_lerp(
                 x, state["shift"], [getattr(self, "x_" + n) for n in "rwkvag"])))
         else:
-            delta = torch.cat([state["shift"].unsqueeze(1), x[:, :-1]], 1) - x
-            mixed = {n: (x + delta * getattr(self, "x_" + n)).to(x.dtype) for n in "rwkvag"}
+            mixed = dict(zip("rwkvag", _shift_lerp_ops(
+                x, state["shift"], [getattr(self, "x_" + n) for n in "rwkvag"])))
         r = self.receptance(mixed["r"])
         w = self.w0 + torch.tanh(mixed["w"] @ self.w1) @ self.w2
         k, v = self.key(mixed["k"]), self.value(mixed["v"])
@@ -120,9 +150,10 @@ class TimeMix(nn.Module):
         else:
             # norms in fp32 with autocast off, cast back for the output projection
             with torch.autocast(x.device.type, enabled=False):
-                yn = F.group_norm(y.float().reshape(B * T, self.width), self.heads,
-                                  self.ln_x.weight.float(), self.ln_x.bias.float(),
-                                  self.ln_x.eps).reshape(B, T, self.width)
+                gn = _group_norm if y.is_cuda else F.group_norm
+                yn = gn(y.float().reshape(B * T, self.width), self.heads,
+                        self.ln_x.weight.float(), self.ln_x.bias.float(),
+                        self.ln_x.eps).reshape(B, T, self.width)
                 bonus = ((r.float().reshape(shape) * kmod.float().reshape(shape) * self.r_k)
                          .sum(-1, keepdim=True) * v.float().reshape(shape)).reshape(B, T, self.width)
                 out = ((yn + bonus) * g.float()).to(x.dtype)

@@ -23,6 +23,8 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import os
+import warnings
 from functools import lru_cache
 from pathlib import Path
 
@@ -32,6 +34,14 @@ DECAY_SCALE = 0.6065306597126334  # e^{-1/2} (theseus/wkv7.py:19)
 LIB_PATH = Path(__file__).resolve().parent / "libtheseus_wkv7.so"
 
 _BF16, _FP32 = 0, 1
+
+# theseus_wkv7_family codes (include/theseus_wkv7.h) -> why the step-serial kernels run
+_FAMILY_FORCED = 1
+_FALLBACK_REASON = {
+    2: "float32 token tensors",
+    3: "a head size other than 64",
+    4: "a token tensor of 2 GiB or more, or one head's saved states of 4 GiB or more",
+}
 
 
 def reference(r, w, k, v, a, b, state):
@@ -100,12 +110,32 @@ class Extension:
         lib.theseus_wkv7_backward.restype = i32
         lib.theseus_wkv7_decode_step.argtypes = [i32] * 4 + [vp] * 8 + [vp]
         lib.theseus_wkv7_decode_step.restype = i32
+        lib.theseus_wkv7_kernel_family.argtypes = [i32] * 5
+        lib.theseus_wkv7_kernel_family.restype = i32
         self.abi_version = lib.theseus_wkv7_abi_version()
         self.checkpoint_interval = lib.theseus_wkv7_checkpoint_interval()
 
     # -- helpers ---------------------------------------------------------
     def checkpoint_count(self, T):
         return int(self.lib.theseus_wkv7_checkpoint_count(T))
+
+    def kernel_family(self, B, T, H, N, dtype):
+        """theseus_wkv7_family code of a call (0: chunked MFMA kernels)."""
+        return int(self.lib.theseus_wkv7_kernel_family(B, T, H, N, dtype))
+
+    def _warn_fallback(self, B, T, H, N, dt):
+        """Say so when a call runs on the step-serial kernels (exact, but one step at a
+        time: ~75x slower than the chunked kernels at config 2).  THESEUS_WKV7_STRICT=1
+        turns the warning into an error; THESEUS_WKV7_FAMILY=seq (an explicit request)
+        is silent."""
+        reason = _FALLBACK_REASON.get(self.kernel_family(B, T, H, N, dt))
+        if reason is None:
+            return
+        msg = (f"theseus_wkv7: {reason} -> the step-serial kernels run this call "
+               f"(B={B} T={T} H={H} N={N}); only bf16 with N=64 uses the chunked MFMA kernels")
+        if os.environ.get("THESEUS_WKV7_STRICT", "") == "1":
+            raise RuntimeError(msg)
+        warnings.warn(msg, RuntimeWarning, stacklevel=4)
 
     def _raise(self, status):
         if status:
@@ -144,6 +174,8 @@ class Extension:
             else:
                 saved = torch.empty((0,), dtype=torch.float32, device=r.device)
             dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
+            if T > 1 or save_history:  # (a T=1 step without saved states runs the single-step kernel)
+                self._warn_fallback(B, T, H, N, dt)
             ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_forward_workspace_size(B, T, H, N, dt)), r.device)
             status = self.lib.theseus_wkv7_forward(
                 B, T, H, N, dt, *map(_ptr, (r, w, k, v, a, b, s0, y, end)),
@@ -168,6 +200,7 @@ class Extension:
             grads = [torch.empty_like(r) for _ in range(6)]
             ds0 = torch.empty((B, H, N, N), dtype=torch.float32, device=r.device)
             dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
+            self._warn_fallback(B, T, H, N, dt)
             ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N, dt)), r.device)
             status = self.lib.theseus_wkv7_backward(
                 B, T, H, N, dt,

@@ -194,3 +194,61 @@ def test_reference_backend_on_cpu_matches_oracle():
     yo, sTo = O.forward(*(inp[n].numpy() for n in "rwkvab"), inp["s0"].numpy())
     np.testing.assert_allclose(y.numpy(), yo, atol=1e-4, rtol=1e-4)
     np.testing.assert_allclose(sT.numpy(), sTo, atol=1e-4, rtol=1e-4)
+
+
+def test_kernel_family_dispatch_predicate(monkeypatch):
+    """theseus_wkv7_kernel_family: the chunked MFMA kernels (0) cover bf16 with N = 64 only
+    while both 32-bit buffer ranges hold: every [B,T,H,64] token tensor under 2 GiB and one
+    head's saved states (ceil(T/16)+1 states of 16 KiB) under 4 GiB.  Anything else runs on
+    the step-serial kernels, with the reason as the code."""
+    monkeypatch.delenv("THESEUS_WKV7_FAMILY", raising=False)
+    lib = W.extension().lib
+    fam = lib.theseus_wkv7_kernel_family
+    assert fam(4, 2048, 80, 64, 0) == 0
+    assert fam(4, 2048, 80, 64, 1) == 2   # fp32
+    assert fam(4, 2048, 80, 32, 0) == 3   # head size
+    # token tensors: B*T*H*64*2 bytes must stay below 2^31
+    assert fam(1, (1 << 21) - 1, 8, 64, 0) == 0
+    assert fam(1, 1 << 21, 8, 64, 0) == 4
+    # saved states of one head: (ceil(T/16) + 1) * 64 * 64 * 4 bytes must stay below 2^32,
+    # i.e. ceil(T/16) + 1 < 262144 -- reached long before 2 GiB of tokens when B*H is small
+    t_max = 16 * (262144 - 2)
+    assert fam(1, t_max, 1, 64, 0) == 0
+    assert fam(1, t_max + 1, 1, 64, 0) == 4
+    assert fam(1, 0, 1, 64, 0) == -1      # invalid sizes: minus the status code
+    assert fam(1, 4, 1, 64, 9) == -2
+    monkeypatch.setenv("THESEUS_WKV7_FAMILY", "seq")
+    assert fam(4, 2048, 80, 64, 0) == 1
+
+
+def test_step_serial_fallback_warns_and_strict_mode_refuses(monkeypatch):
+    monkeypatch.delenv("THESEUS_WKV7_FAMILY", raising=False)
+    ext = W.extension()
+    with pytest.warns(RuntimeWarning, match="float32 token tensors"):
+        ext._warn_fallback(1, 32, 2, 64, 1)
+    with pytest.warns(RuntimeWarning, match="head size other than 64"):
+        ext._warn_fallback(1, 32, 2, 8, 0)
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        ext._warn_fallback(1, 32, 2, 64, 0)  # chunked: silent
+        monkeypatch.setenv("THESEUS_WKV7_FAMILY", "seq")
+        ext._warn_fallback(1, 32, 2, 64, 0)  # an explicit request: silent
+    monkeypatch.delenv("THESEUS_WKV7_FAMILY")
+    monkeypatch.setenv("THESEUS_WKV7_STRICT", "1")
+    with pytest.raises(RuntimeError, match="step-serial kernels"):
+        ext._warn_fallback(1, 32, 2, 64, 1)
+
+
+def test_fused_timemix_covers_only_what_its_grid_addresses():
+    """Above 65535 token blocks of 64 the fused kernels refuse the shape; TimeMix must then
+    take the reference's torch op sequence instead of raising."""
+    from theseus import fused
+    lim = 65535 * 64
+    assert fused.MAX_TOKENS == lim
+    ok = torch.empty((1, lim, 128), dtype=torch.bfloat16, device="meta")
+    big = torch.empty((1, lim + 1, 128), dtype=torch.bfloat16, device="meta")
+    two = torch.empty((2, lim // 2 + 1, 128), dtype=torch.bfloat16, device="meta")
+    assert fused.available(ok, 64)
+    assert not fused.available(big, 64) and not fused.available(two, 64)
+    assert not fused.available(ok.float(), 64) and not fused.available(ok, 32)

@@ -87,11 +87,20 @@ def _torch_mix(x, shift, coefs):
     return [(x + delta * c).to(x.dtype) for c in coefs]
 
 
+# Op-level sizes: one partial token block at C=256 (4 heads); 19 heads (more than one
+# 8-head group of the backward kernels and a partial last group) over 1203 tokens (18 token
+# blocks of 64 plus a 51-token tail, so the fixed-order parameter-gradient reductions run
+# over many blocks); and config 3's own size (B=2, T=4096, C=5120: 80 heads, 128 blocks).
+OP_SIZES = [pytest.param(3, 37, 4, id="C256"), pytest.param(3, 401, 19, id="C1216-ragged"),
+            pytest.param(2, 4096, 80, id="config3")]
+
+
 @gpu
-def test_fused_shift_lerp_matches_torch():
+@pytest.mark.parametrize("B,T,H", OP_SIZES)
+def test_fused_shift_lerp_matches_torch(B, T, H):
     from theseus import fused
     torch.manual_seed(1)
-    B, T, C = 3, 37, 256
+    C = 64 * H
     x = torch.randn(B, T, C, device="cuda", dtype=torch.bfloat16, requires_grad=True)
     sh = torch.randn(B, C, device="cuda", dtype=torch.bfloat16, requires_grad=True)
     coefs = [torch.rand(1, 1, C, device="cuda", requires_grad=True) for _ in range(6)]
@@ -118,11 +127,32 @@ def test_fused_shift_lerp_matches_torch():
         assert e_fused < 5e-3 and e_fused <= 1.5 * e_ref + 1e-4
 
 
+def _kk_gn_chain(leaves, B, T, H, N, out_dtype):
+    """The reference's op chains around the recurrence (theseus/timemix.py:78-80, 83-88):
+    the WKV operands k*(1+(a-1)k_a), -kk, kk*a and the GroupNorm/bonus/gate output."""
+    k, a, k_k, k_a, r, v, g, y, r_k, ln_w, ln_b = leaves
+    C = H * N
+    f = torch.float64 if out_dtype == torch.float64 else torch.float32
+    shape = (B, T, H, N)
+    kk = F.normalize((k.to(f) * k_k).reshape(shape), dim=-1, eps=1e-12)
+    kmod = k * (1 + (a - 1) * k_a)
+    ops = [z.reshape(shape).to(out_dtype) for z in (kmod, -kk, kk * a.reshape(shape))]
+    yn = F.group_norm(y.to(f).reshape(B * T, C), H, ln_w, ln_b, 64e-5).reshape(B, T, C)
+    bonus = ((r.to(f).reshape(shape) * kmod.to(f).reshape(shape) * r_k).sum(-1, keepdim=True)
+             * v.to(f).reshape(shape)).reshape(B, T, C)
+    return ops + [((yn + bonus) * g.to(f)).to(out_dtype)]
+
+
 @gpu
-def test_fused_kk_and_gn_match_torch():
+@pytest.mark.parametrize("B,T,H", OP_SIZES)
+def test_fused_kk_and_gn_match_torch(B, T, H):
+    """The fused kk/k-mod and GroupNorm/bonus/gate kernels against the same op chain in
+    float64 on the CPU (outputs and all 11 input gradients at rel-L2 5e-3).  The torch
+    chain on the GPU (bf16/fp32, as TimeMix runs it unfused) is measured against the same
+    float64 truth and printed beside it."""
     from theseus import fused
     torch.manual_seed(2)
-    B, T, H, N = 2, 29, 4, 64
+    N = 64
     C = H * N
     bf = torch.bfloat16
     mk = lambda *s, dt=bf: torch.randn(*s, device="cuda", dtype=dt)  # noqa: E731
@@ -137,29 +167,30 @@ def test_fused_kk_and_gn_match_torch():
     ln_b = (.1 * torch.randn(C, device="cuda")).requires_grad_()
     leaves = [k, a, k_k, k_a, r, v, g, y, r_k, ln_w, ln_b]
     refl = [t.detach().clone().requires_grad_() for t in leaves]
+    truthl = [t.detach().cpu().double().requires_grad_() for t in leaves]
 
     kw, aw, bw, km = fused.kk_kmod(k, a, k_k, k_a, N, bf)
     out = fused.gn_bonus_gate(y, r, km, v, g, r_k, ln_w, ln_b, 64e-5, bf)
-
-    kR, aR, kkR, kaR, rR, vR, gR, yR, rkR, lwR, lbR = refl
-    shape = (B, T, H, N)
-    kk = F.normalize((kR.float() * kkR).reshape(shape), dim=-1, eps=1e-12)
-    kmod = kR * (1 + (aR - 1) * kaR)
-    refs = [z.reshape(shape).to(bf) for z in (kmod, -kk, kk * aR.reshape(shape))]
-    yn = F.group_norm(yR.float().reshape(B * T, C), H, lwR, lbR, 64e-5).reshape(B, T, C)
-    bonus = ((rR.float().reshape(shape) * kmod.float().reshape(shape) * rkR).sum(-1, keepdim=True)
-             * vR.float().reshape(shape)).reshape(B, T, C)
-    outR = ((yn + bonus) * gR.float()).to(bf)
-    for o, rr in zip((kw, aw, bw, out), (*refs, outR)):
-        assert rel_l2(o.float().cpu(), rr.float().cpu()) < 5e-3
-    gs = [torch.randn_like(t) for t in (kw, aw, bw, out)]
-    torch.autograd.backward((kw, aw, bw, out), gs)
-    torch.autograd.backward((*refs, outR), gs)
-    names = ["k", "a", "k_k", "k_a", "r", "v", "g", "y", "r_k", "ln_w", "ln_b"]
-    for n, t, tr in zip(names, leaves, refl):
-        e = rel_l2(t.grad.float().cpu(), tr.grad.float().cpu())
-        print(f"    grad {n}: rel_l2 {e:.2e}", flush=True)
+    got = (kw, aw, bw, out)
+    refs = _kk_gn_chain(refl, B, T, H, N, bf)
+    truth = _kk_gn_chain(truthl, B, T, H, N, torch.float64)
+    for n, o, rr, tt in zip(("kw", "aw", "bw", "out"), got, refs, truth):
+        e, e_ref = rel_l2(o.float().cpu(), tt.detach()), rel_l2(rr.float().cpu(), tt.detach())
+        print(f"    {n}: rel_l2 vs fp64 {e:.2e} (torch GPU chain {e_ref:.2e})", flush=True)
         assert e < 5e-3, (n, e)
+    gs = [torch.randn_like(t) for t in got]
+    torch.autograd.backward(got, gs)
+    torch.autograd.backward(refs, gs)
+    torch.autograd.backward(truth, [gg.cpu().double() for gg in gs])
+    names = ["k", "a", "k_k", "k_a", "r", "v", "g", "y", "r_k", "ln_w", "ln_b"]
+    bad = []
+    for n, t, tr, tt in zip(names, leaves, refl, truthl):
+        e = rel_l2(t.grad.float().cpu(), tt.grad)
+        e_ref = rel_l2(tr.grad.float().cpu(), tt.grad)
+        print(f"    grad {n}: rel_l2 vs fp64 {e:.2e} (torch GPU chain {e_ref:.2e})", flush=True)
+        if not e < 5e-3:
+            bad.append((n, e))
+    assert not bad, bad
 
 
 @gpu
@@ -268,3 +299,21 @@ def test_cuda_fp32_optimizer_states_and_learning():
     for param, state in optimizer.state.items():
         assert param.dtype == param.grad.dtype == torch.float32
         assert state["exp_avg"].dtype == state["exp_avg_sq"].dtype == torch.float32
+
+
+def test_explicit_group_norm_is_torch_group_norm():
+    """The unfused GPU path's GroupNorm (written out, because torch's ROCm group_norm backward
+    returns wrong weight/bias gradients at >= ~1024 rows) is the same function as
+    F.group_norm: values and all three gradients, float64 on the CPU."""
+    from theseus.timemix import _group_norm
+    torch.manual_seed(4)
+    M, G, C = 1500, 6, 6 * 16
+    x = torch.randn(M, C, dtype=torch.float64, requires_grad=True)
+    w = (1 + .1 * torch.randn(C, dtype=torch.float64)).requires_grad_()
+    b = (.1 * torch.randn(C, dtype=torch.float64)).requires_grad_()
+    go = torch.randn(M, C, dtype=torch.float64)
+    ours = torch.autograd.grad(_group_norm(x, G, w, b, 64e-5), (x, w, b), go)
+    ref = F.group_norm(x, G, w, b, 64e-5)
+    torch.testing.assert_close(_group_norm(x, G, w, b, 64e-5), ref, rtol=1e-12, atol=1e-12)
+    for g1, g2 in zip(ours, torch.autograd.grad(ref, (x, w, b), go)):
+        torch.testing.assert_close(g1, g2, rtol=1e-10, atol=1e-10)
