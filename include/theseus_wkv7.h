@@ -23,7 +23,9 @@
  * nothing was enqueued (argument errors) or that the launch failed
  * (THESEUS_WKV7_ERR_LAUNCH, checked with hipGetLastError like
  * C10_CUDA_KERNEL_LAUNCH_CHECK at kernels/wkv7_state.cpp:24,36).  The library
- * keeps no mutable global state, so calls are reentrant.
+ * keeps no mutable global state, so calls are reentrant -- except
+ * theseus_wkv7_forward_noalloc, whose calls on one device share a static
+ * device scratch array (see its declaration).
  */
 #ifndef THESEUS_WKV7_H
 #define THESEUS_WKV7_H
@@ -44,7 +46,9 @@ enum theseus_wkv7_status {
     THESEUS_WKV7_ERR_DTYPE = 2,      /* dtype is not BF16/FP32 (cpp:13)             */
     THESEUS_WKV7_ERR_NULL = 3,       /* a required pointer is NULL                  */
     THESEUS_WKV7_ERR_WORKSPACE = 4,  /* workspace smaller than required             */
-    THESEUS_WKV7_ERR_LAUNCH = 5      /* hipGetLastError reported a failure          */
+    THESEUS_WKV7_ERR_LAUNCH = 5,     /* hipGetLastError reported a failure          */
+    THESEUS_WKV7_ERR_SCRATCH = 6     /* theseus_wkv7_forward_noalloc: these sizes need
+                                        more than THESEUS_WKV7_NOALLOC_SCRATCH_BYTES    */
 };
 
 /* Kernel family a call of these sizes runs on (theseus_wkv7_kernel_family). */
@@ -120,6 +124,29 @@ int theseus_wkv7_decode_step(int B, int H, int N, int dtype,
                              const void* r, const void* w, const void* k, const void* v,
                              const void* a, const void* b, float* state, void* y,
                              hipStream_t stream);
+
+/* Bytes of the library's static device scratch array, which
+ * theseus_wkv7_forward_noalloc uses in place of a caller workspace.  8 MiB
+ * holds the forward's handoffs for up to ~500 workgroups (a call needs
+ * theseus_wkv7_forward_workspace_size bytes: 4.2 MB at most on 256 CUs). */
+#define THESEUS_WKV7_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* theseus_wkv7_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, whose
+ * forward allocates its outputs and history itself (kernels/wkv7_state.cpp:16-25).
+ * Same arguments, kernels and results as theseus_wkv7_forward (bitwise), minus
+ * workspace/workspace_bytes: the chunked kernels' handoffs go through a static
+ * device array of THESEUS_WKV7_NOALLOC_SCRATCH_BYTES that the library owns (one
+ * per device, held until the process ends).  Calls whose sizes need more
+ * return THESEUS_WKV7_ERR_SCRATCH without enqueuing anything.  The call
+ * allocates nothing (no hipMalloc/hipFree).  All calls on one device share
+ * that array: calls that may run at the same time on one device (different
+ * streams) race and must be serialised by the caller. */
+int theseus_wkv7_forward_noalloc(int B, int T, int H, int N, int dtype,
+                                 const void* r, const void* w, const void* k, const void* v,
+                                 const void* a, const void* b, const float* s0,
+                                 void* y, float* sT, float* ckpt, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -103,6 +103,9 @@ const char* theseus_wkv7_error_string(int status) {
         case THESEUS_WKV7_ERR_NULL: return "null pointer argument";
         case THESEUS_WKV7_ERR_WORKSPACE: return "workspace too small";
         case THESEUS_WKV7_ERR_LAUNCH: return "HIP kernel launch failed";
+        case THESEUS_WKV7_ERR_SCRATCH:
+            return "sizes need more handoff scratch than the library's static array holds "
+                   "(THESEUS_WKV7_NOALLOC_SCRATCH_BYTES); use theseus_wkv7_forward with a workspace";
         default: return "unknown status";
     }
 }

@@ -110,6 +110,9 @@ class Extension:
         lib.theseus_wkv7_backward.restype = i32
         lib.theseus_wkv7_decode_step.argtypes = [i32] * 4 + [vp] * 8 + [vp]
         lib.theseus_wkv7_decode_step.restype = i32
+        # forward without a workspace argument (static device scratch; allocates nothing)
+        lib.theseus_wkv7_forward_noalloc.argtypes = [i32] * 5 + [vp] * 10 + [vp]
+        lib.theseus_wkv7_forward_noalloc.restype = i32
         lib.theseus_wkv7_kernel_family.argtypes = [i32] * 5
         lib.theseus_wkv7_kernel_family.restype = i32
         self.abi_version = lib.theseus_wkv7_abi_version()
