@@ -21,7 +21,10 @@ config 2 it is the algorithmic bytes plus the saved states the config mandates
 
 Other configurations (``--config``): c1 = 8 chained T=512 forward calls without
 saved states (state carried), B=1, H=80; c4 = 256 in-place decode steps at
-B=64, with one fused T=256 forward timed beside them; c3 = the TimeMix layer.
+B=64, with one fused T=256 forward timed beside them; c3 = the TimeMix layer;
+c4tm = config 4 through a whole TimeMix layer (C=5120, bf16 serving weights): 256
+tokens per step, served out of place (the reference's T=1 forward), in place
+(TimeMix.step_) and as a captured HIP graph of the in-place step (the timed one).
 
 Algorithmic bytes (compulsory contract I/O; E = H*N, S_l = H*N*N*4 bytes):
   forward  = B*T*E*2*7  + 2*B*S_l   (r,w,k,v,a,b in, y out; s0 in, sT out)
@@ -47,6 +50,7 @@ CONFIGS = {
     "c1": dict(B=1, T=4096, H=80, N=64, s0_std=0.0, seed=20261),
     "c4": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
     "c3": dict(B=2, T=4096, H=80, N=64, s0_std=0.0, seed=20263),
+    "c4tm": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
 }
 
 
@@ -107,6 +111,78 @@ def bench_timemix(args, cfg):
         "roofline": {"kernel": "layer (GEMM-dominated)", "bound": "mfma", "achieved": round(tflops, 1),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None}}),
         flush=True)
+
+
+def bench_serving(args, cfg):
+    """Config 4 through a TimeMix layer: B=64 lanes, 256 consecutive tokens, one per call,
+    C=5120 (H=80, N=64), bf16 weights as the reference's install() loads a layer for
+    inference (hf_model.py:147-148), weights N(0,0.02), x ~ N(0,1).  Three ways of serving
+    a token: the out-of-place T=1 forward (what the reference's Runner calls), the in-place
+    TimeMix.step_, and a HIP graph of step_ (theseus.serving.CapturedStep) -- the timed
+    step replays the graph 256 times.  Per-token HBM bytes: the layer's bf16 weights once
+    plus the fp32 WKV state read and written (2*B*S_l) plus activations."""
+    import torch
+    from theseus.serving import CapturedStep, serving_state
+    from theseus.timemix import TimeMix
+
+    B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
+    C = H * N
+    torch.manual_seed(cfg["seed"])
+    m = TimeMix(C, 3, 8, head_size=N, backend="cuda")
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if p.dim() == 2 and name != "r_k":
+                p.normal_(0, .02)
+    m = m.cuda().to(torch.bfloat16).eval()
+    x = torch.randn(B, T, C, device="cuda", dtype=torch.bfloat16)
+    toks = [x[:, t:t + 1].contiguous() for t in range(T)]
+    st0 = m.initial_state(x)
+    st_ip = serving_state(st0)
+    graph = CapturedStep(m, serving_state(st0), toks[0], autocast=None)
+
+    def run(mode):
+        if mode == "out_of_place":
+            st = st0
+            for t in range(T):
+                _, st = m(toks[t], st)
+        elif mode == "in_place":
+            for t in range(T):
+                m.step_(toks[t], st_ip)
+        else:
+            for t in range(T):
+                graph(toks[t])
+
+    per_token = {}
+    with torch.no_grad():
+        for mode in ("out_of_place", "in_place", "graph"):
+            for _ in range(max(1, args.warmup // 5)):
+                run(mode)
+            torch.cuda.synchronize()
+            n = max(1, args.steps // 10) if mode != "graph" else max(1, args.steps // 5)
+            t0 = time.perf_counter()
+            for _ in range(n):
+                run(mode)
+            torch.cuda.synchronize()
+            per_token[mode] = (time.perf_counter() - t0) * 1e3 / (n * T)
+    ms_tok = per_token["graph"]
+    weight_bytes = sum(p.numel() * p.element_size() for p in m.parameters())
+    state_bytes = 2 * B * H * N * N * 4
+    act_bytes = B * C * 2 * 8  # x in, out, and the mixes / WKV operands that stay small at T=1
+    step_bytes = weight_bytes + state_bytes + act_bytes
+    gbps = step_bytes / (ms_tok * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "TimeMix serving step tokens/s (config 4 through the layer, C=5120, B=64)",
+        "value": round(B / (ms_tok * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": max(1, args.steps // 5), "warmup": max(1, args.warmup // 5),
+        "ms_per_step": round(ms_tok * T, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "timemix_serving_step", "B": B, "tokens_per_step": T, "C": C, "H": H,
+                   "N": N, "weights": "bf16", "state_dtype": "fp32"},
+        "ms_per_token": {k: round(v, 4) for k, v in per_token.items()},
+        "roofline": {"kernel": "whole serving step (graph replay)", "bound": "hbm",
+                     "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "alg_bytes_per_launch": step_bytes}}), flush=True)
 
 
 def alg_bytes(B, T, H, N, which):
@@ -186,6 +262,9 @@ def main():
     if args.config == "c3":
         torch.cuda.set_device(0)
         return bench_timemix(args, cfg)
+    if args.config == "c4tm":
+        torch.cuda.set_device(0)
+        return bench_serving(args, cfg)
     B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

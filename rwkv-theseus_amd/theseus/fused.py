@@ -19,6 +19,7 @@ in the parameter's dtype.
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
@@ -77,8 +78,38 @@ def _check(status):
         raise RuntimeError("theseus_timemix: " + extension().lib.theseus_wkv7_error_string(status).decode())
 
 
+# float32 copies of parameters kept in another dtype (bf16 serving weights) and the
+# stacked shift-lerp coefficients, reused while every source tensor is unchanged (same
+# version counter and storage), so a serving step does not convert its parameters again
+# on every token.  Never filled while a stream is being captured into a graph: a copy
+# made under capture holds its values only once the graph has run.
+_derived = {}  # id(first source) -> {slot: (ids of the sources, their stamps, value)}
+
+
+def _cached(slot, srcs, make):
+    ids = tuple(id(t) for t in srcs)
+    stamp = tuple((t._version, t.data_ptr()) for t in srcs)
+    slots = _derived.get(ids[0])
+    hit = slots.get(slot) if slots is not None else None
+    if hit is not None and hit[0] == ids and hit[1] == stamp:
+        return hit[2]
+    out = make()
+    if not (out.is_cuda and torch.cuda.is_current_stream_capturing()):
+        if slots is None:
+            slots = _derived[ids[0]] = {}
+            weakref.finalize(srcs[0], _derived.pop, ids[0], None)  # forget it with its source
+        slots[slot] = (ids, stamp, out)
+    return out
+
+
 def _vec(p, C):
-    return p.detach().reshape(C).float().contiguous()
+    if p.dtype == torch.float32:
+        return p.detach().reshape(C).contiguous()
+    return _cached("vec", (p,), lambda: p.detach().reshape(C).float().contiguous())
+
+
+def _coef_matrix(coefs, C):
+    return _cached("coefs", tuple(coefs), lambda: torch.stack([_vec(c, C) for c in coefs]).contiguous())
 
 
 class _ShiftLerp(torch.autograd.Function):
@@ -87,7 +118,7 @@ class _ShiftLerp(torch.autograd.Function):
         B, T, C = x.shape
         x = x.contiguous()
         shift = shift.to(x.dtype).contiguous()
-        cf = torch.stack([_vec(c, C) for c in coefs]).contiguous()
+        cf = _coef_matrix(coefs, C)
         outs = [torch.empty_like(x) for _ in range(6)]
         arr = (ctypes.c_void_p * 6)(*[o.data_ptr() for o in outs])
         with torch.cuda.device(x.device):

@@ -31,7 +31,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from .wkv7 import wkv7
+from .wkv7 import decode_step_, wkv7
 
 
 def _group_norm(x, groups, weight, bias, eps):
@@ -116,6 +116,40 @@ class TimeMix(nn.Module):
         """x [B,T,C] -> (out [B,T,C] in x.dtype, {"shift": x[:, -1], "wkv": end state})."""
         if state is None:
             state = self.initial_state(x)
+        return self._run(x, state, inplace=False)
+
+    def step_(self, x, state):
+        """Serving step that carries ``state`` in place: x [B,1,C] -> out [B,1,C].
+
+        Same value as ``forward(x, state)[0]``, but the WKV state goes through the
+        single-step kernel in place (theseus_wkv7_decode_step) and ``state["shift"]`` is
+        overwritten with x[:, -1], so no new state is allocated per token and the state
+        tensors keep their addresses (which lets a caller capture the step into a HIP
+        graph, ``theseus.serving.CapturedStep``).  The reference's serving path calls
+        ``forward`` with T=1 and gets a new state back each token (theseus/hf_model.py:104-106,
+        kernels/wkv7_state.cpp:21); ``forward`` keeps doing that, since callers such as
+        ``isolated_state`` (hf_model.py:240-252) hold on to earlier state objects.
+        Needs backend="cuda", CUDA tensors, T == 1, no autograd, and ``state`` as
+        ``initial_state``/``forward`` make it (shift [B,C] in x's dtype, wkv [B,H,N,N] fp32,
+        both contiguous)."""
+        if self.backend != "cuda" or not x.is_cuda:
+            raise ValueError("step_ needs backend='cuda' and CUDA tensors")
+        if x.dim() != 3 or x.shape[1] != 1:
+            raise ValueError("step_ takes one token per call: x [B,1,C]")
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            raise RuntimeError("step_ updates the state in place and has no backward; call it under "
+                               "torch.no_grad() (or use forward for training)")
+        B, H, N = x.shape[0], self.heads, self.head_size
+        sh, wkv = state["shift"], state["wkv"]
+        if not (sh.shape == (B, self.width) and sh.dtype == x.dtype and sh.is_contiguous()
+                and sh.device == x.device):
+            raise ValueError("state['shift'] must be a contiguous [B,C] tensor of x's dtype and device")
+        if not (wkv.shape == (B, H, N, N) and wkv.dtype == torch.float32 and wkv.is_contiguous()
+                and wkv.device == x.device):
+            raise ValueError("state['wkv'] must be a contiguous [B,H,N,N] float32 tensor on x's device")
+        return self._run(x, state, inplace=True)[0]
+
+    def _run(self, x, state, inplace):
         B, T, _ = x.shape
         shape = (B, T, self.heads, self.head_size)
         fused_ok = self._fused(x)
@@ -142,7 +176,10 @@ class TimeMix(nn.Module):
             args = [z.reshape(shape).to(r.dtype).contiguous()
                     for z in (r, w, k, v, -kk, kk * a.reshape(shape))]
             kmod = k
-        y, end = wkv7(*args, state["wkv"], backend=self.backend)
+        if inplace:
+            y, end = decode_step_(*args, state["wkv"]), state["wkv"]
+        else:
+            y, end = wkv7(*args, state["wkv"], backend=self.backend)
         if fused_ok:
             from . import fused
             out = fused.gn_bonus_gate(y, r, kmod, v, g, self.r_k, self.ln_x.weight, self.ln_x.bias,
@@ -157,7 +194,11 @@ class TimeMix(nn.Module):
                 bonus = ((r.float().reshape(shape) * kmod.float().reshape(shape) * self.r_k)
                          .sum(-1, keepdim=True) * v.float().reshape(shape)).reshape(B, T, self.width)
                 out = ((yn + bonus) * g.float()).to(x.dtype)
-        return self.output(out).to(x.dtype), {"shift": x[:, -1], "wkv": end}
+        out = self.output(out).to(x.dtype)
+        if inplace:
+            state["shift"].copy_(x[:, -1])
+            return out, state
+        return out, {"shift": x[:, -1], "wkv": end}
 
 
 def detach_state(state):
