@@ -24,7 +24,10 @@ saved states (state carried), B=1, H=80; c4 = 256 in-place decode steps at
 B=64, with one fused T=256 forward timed beside them; c3 = the TimeMix layer;
 c4tm = config 4 through a whole TimeMix layer (C=5120, bf16 serving weights): 256
 tokens per step, served out of place (the reference's T=1 forward), in place
-(TimeMix.step_) and as a captured HIP graph of the in-place step (the timed one).
+(TimeMix.step_) and as a captured HIP graph of the in-place step (the timed one);
+optim = the optimizer step after backward over one C=5120 TimeMix layer's 112 M
+float32 parameters (gradient scale, clip_grad_norm_, AdamW), fused
+(theseus.optim.FusedAdamW) against the reference's torch sequence.
 
 Algorithmic bytes (compulsory contract I/O; E = H*N, S_l = H*N*N*4 bytes):
   forward  = B*T*E*2*7  + 2*B*S_l   (r,w,k,v,a,b in, y out; s0 in, sT out)
@@ -51,6 +54,7 @@ CONFIGS = {
     "c4": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
     "c3": dict(B=2, T=4096, H=80, N=64, s0_std=0.0, seed=20263),
     "c4tm": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
+    "optim": dict(B=0, T=0, H=80, N=64, s0_std=0.0, seed=20265),
 }
 
 
@@ -185,6 +189,78 @@ def bench_serving(args, cfg):
                      "alg_bytes_per_launch": step_bytes}}), flush=True)
 
 
+def bench_optim(args, cfg):
+    """The step after backward (train.py:202-208) over a C=5120 TimeMix layer's parameter
+    schema (112,460,800 float32 parameters in 23 tensors, theseus/stage.py:36-42 groups),
+    gradients ~N(0, 1e-4) with scale 0.5 and clip norm 1.0 (so the clip is active).  One
+    step of FusedAdamW.step_after_backward against the reference's p.grad.mul_ loop +
+    clip_grad_norm_(error_if_nonfinite=True) + torch.optim.AdamW(fused=True).step(), each
+    timed with HIP events on the current stream.  Algorithmic bytes per parameter: read
+    param, grad and both moments, write param and moments (28 B)."""
+    import torch
+    from theseus.optim import FusedAdamW
+    from theseus.timemix import TimeMix
+
+    C = cfg["H"] * cfg["N"]
+    with torch.device("meta"):
+        shapes = [p.shape for p in TimeMix(C, 3, 8, head_size=cfg["N"], backend="cuda").parameters()]
+    gen = torch.Generator(device="cuda").manual_seed(cfg["seed"])
+
+    def make():
+        ps = [torch.nn.Parameter(torch.randn(sh, generator=gen, device="cuda") * .02) for sh in shapes]
+        return ps, [p for p in ps if p.ndim == 2], [p for p in ps if p.ndim != 2]
+
+    ours_p, od, on = make()
+    ref_p, rd, rn = make()
+    ours = FusedAdamW([{"params": od, "weight_decay": .1}, {"params": on, "weight_decay": 0.}], lr=1e-4,
+                      betas=(.9, .95), eps=1e-8)
+    ref = torch.optim.AdamW([{"params": rd, "weight_decay": .1}, {"params": rn, "weight_decay": 0.}], lr=1e-4,
+                            betas=(.9, .95), eps=1e-8, fused=True)
+    grads = [torch.randn(sh, generator=gen, device="cuda") * 1e-4 for sh in shapes]
+    for p, q, g in zip(ours_p, ref_p, grads):
+        p.grad, q.grad = g, g.clone()
+    n_param = sum(p.numel() for p in ours_p)
+    stream = torch.cuda.current_stream()
+
+    def ours_step():
+        ours.step_after_backward(grad_scale=.5, max_norm=1.0, error_if_nonfinite=True)
+
+    def ref_step():
+        for p in ref_p:
+            p.grad.mul_(.5)
+        torch.nn.utils.clip_grad_norm_(ref_p, 1.0, error_if_nonfinite=True)
+        ref.step()
+
+    times = {}
+    for name, fn in (("fused", ours_step), ("reference_torch", ref_step)):
+        for _ in range(max(2, args.warmup)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times[name] = e0.elapsed_time(e1) / args.steps
+    ms = times["fused"]
+    alg = 28 * n_param
+    gbps = alg / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "optimizer step after backward, parameters/s (one C=5120 TimeMix layer, fp32 AdamW + clip)",
+        "value": round(n_param / (ms * 1e-3), 1), "unit": "parameters/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": max(2, args.warmup), "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "adamw_clip_step", "parameters": n_param, "tensors": len(shapes),
+                   "grad_scale": .5, "max_norm": 1.0},
+        "ms_per_step_by_impl": {k: round(v, 4) for k, v in times.items()},
+        "speedup_vs_reference_torch": round(times["reference_torch"] / ms, 3),
+        "roofline": {"kernel": "fused step (3 launches)", "bound": "hbm", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": 32 * n_param, "traffic_source": "by construction: gradients read twice",
+                     "alg_bytes_per_launch": alg}}), flush=True)
+
+
 def alg_bytes(B, T, H, N, which):
     E, Sl = H * N, H * N * N * 4
     if which == "fwd":
@@ -265,6 +341,9 @@ def main():
     if args.config == "c4tm":
         torch.cuda.set_device(0)
         return bench_serving(args, cfg)
+    if args.config == "optim":
+        torch.cuda.set_device(0)
+        return bench_optim(args, cfg)
     B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
