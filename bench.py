@@ -27,7 +27,10 @@ tokens per step, served out of place (the reference's T=1 forward), in place
 (TimeMix.step_) and as a captured HIP graph of the in-place step (the timed one);
 optim = the optimizer step after backward over one C=5120 TimeMix layer's 112 M
 float32 parameters (gradient scale, clip_grad_norm_, AdamW), fused
-(theseus.optim.FusedAdamW) against the reference's torch sequence.
+(theseus.optim.FusedAdamW) against the reference's torch sequence; gdn = the teacher's
+gated delta rule (Qwen3.5 GDN geometry: 32 value heads, K = V = 128) through the WKV7
+kernels' exp-decay mode (theseus.gdn), forward and forward+backward, against
+transformers' torch_chunk_gated_delta_rule on the same GPU.
 
 Algorithmic bytes (compulsory contract I/O; E = H*N, S_l = H*N*N*4 bytes):
   forward  = B*T*E*2*7  + 2*B*S_l   (r,w,k,v,a,b in, y out; s0 in, sT out)
@@ -55,6 +58,7 @@ CONFIGS = {
     "c3": dict(B=2, T=4096, H=80, N=64, s0_std=0.0, seed=20263),
     "c4tm": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
     "optim": dict(B=0, T=0, H=80, N=64, s0_std=0.0, seed=20265),
+    "gdn": dict(B=1, T=2048, H=32, N=128, s0_std=0.0, seed=20266),
 }
 
 
@@ -261,6 +265,72 @@ def bench_optim(args, cfg):
                      "alg_bytes_per_launch": alg}}), flush=True)
 
 
+def bench_gdn(args, cfg):
+    """GDN forward (no grad) and forward+backward at B=1, T=2048, H=32, K=V=128, bf16 q/k/v
+    with the layers' in-kernel q/k L2 norm, through theseus.gdn (the WKV7 step-serial
+    kernels in exp-decay mode, N=128), beside transformers' torch_chunk_gated_delta_rule
+    (its torch fallback, the function the reference's teacher runs without FLA)."""
+    import inspect
+
+    import torch
+    from theseus import gdn
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as M
+
+    B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
+    g = torch.Generator(device="cuda").manual_seed(cfg["seed"])
+    q, k, v = (torch.randn(B, T, H, N, generator=g, device="cuda").to(torch.bfloat16) for _ in range(3))
+    gg = -torch.exp(torch.randn(B, T, H, generator=g, device="cuda"))
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g, device="cuda"))
+    s0 = .1 * torch.randn(B, H, N, N, generator=g, device="cuda")
+    hf_chunk = inspect.unwrap(M.torch_chunk_gated_delta_rule)
+
+    def timed(fn, n):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    def ours_fwd():
+        with torch.no_grad():
+            gdn.chunk_gated_delta_rule(q, k, v, gg, beta, initial_state=s0, output_final_state=True,
+                                       use_qk_l2norm_in_kernel=True)
+
+    xs = [t.detach().clone().requires_grad_() for t in (q, k, v, gg, beta, s0)]
+
+    def ours_fwd_bwd():
+        o, st = gdn.chunk_gated_delta_rule(*xs[:5], initial_state=xs[5], output_final_state=True,
+                                           use_qk_l2norm_in_kernel=True)
+        (o.float().sum() + st.sum()).backward()
+
+    def hf_fwd():
+        with torch.no_grad():
+            hf_chunk(q, k, v, gg, beta, initial_state=s0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+
+    n = max(2, args.steps // 10)
+    ms = {"ours_fwd": timed(ours_fwd, n), "ours_fwd_bwd": timed(ours_fwd_bwd, n),
+          "transformers_torch_chunk_fwd": timed(hf_fwd, max(1, n // 2))}
+    # compulsory bytes of the forward: q, k, v in (bf16), g, beta in (fp32), out (bf16),
+    # state in and out (fp32)
+    fwd_bytes = B * T * H * N * 2 * 4 + B * T * H * 4 * 2 + 2 * B * H * N * N * 4
+    gbps = fwd_bytes / (ms["ours_fwd"] * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "GDN (gated delta rule) forward tokens/s, Qwen3.5 GDN geometry (H=32, K=V=128)",
+        "value": round(B * T / (ms["ours_fwd"] * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": n,
+        "warmup": 2, "ms_per_step": round(ms["ours_fwd"], 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 I/O, fp32 compute", "data": "synthetic",
+        "config": {"workload": "gdn_forward", "B": B, "T": T, "H": H, "K": N, "V": N,
+                   "kernels": "step-serial WKV7, exp decay, key-value states"},
+        "ms_by_impl": {k2: round(v2, 4) for k2, v2 in ms.items()},
+        "speedup_vs_transformers_torch_chunk": round(ms["transformers_torch_chunk_fwd"] / ms["ours_fwd"], 2),
+        "roofline": {"kernel": "forward", "bound": "latency (step-serial)", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "alg_bytes_per_launch": fwd_bytes}}), flush=True)
+
+
 def alg_bytes(B, T, H, N, which):
     E, Sl = H * N, H * N * N * 4
     if which == "fwd":
@@ -344,6 +414,9 @@ def main():
     if args.config == "optim":
         torch.cuda.set_device(0)
         return bench_optim(args, cfg)
+    if args.config == "gdn":
+        torch.cuda.set_device(0)
+        return bench_gdn(args, cfg)
     B, T, H, N = cfg["B"], cfg["T"], cfg["H"], cfg["N"]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -47,8 +47,20 @@ enum theseus_wkv7_status {
     THESEUS_WKV7_ERR_NULL = 3,       /* a required pointer is NULL                  */
     THESEUS_WKV7_ERR_WORKSPACE = 4,  /* workspace smaller than required             */
     THESEUS_WKV7_ERR_LAUNCH = 5,     /* hipGetLastError reported a failure          */
-    THESEUS_WKV7_ERR_SCRATCH = 6     /* theseus_wkv7_forward_noalloc: these sizes need
+    THESEUS_WKV7_ERR_SCRATCH = 6,    /* theseus_wkv7_forward_noalloc: these sizes need
                                         more than THESEUS_WKV7_NOALLOC_SCRATCH_BYTES    */
+    THESEUS_WKV7_ERR_FLAGS = 7       /* flags other than theseus_wkv7_flags bits        */
+};
+
+/* Options of the *_ex entry points (0 = the reference's operator). */
+enum theseus_wkv7_flags {
+    /* d = exp(w) with no clamp or sigmoid instead of exp(-e^{-1/2} sigmoid(w)): the
+     * decay of the GDN teacher layers, w = g ("wkv_decay_operation",
+     * convert_qwen2rwkv_lightning.py:383-384); dw is then dL/d(log d). */
+    THESEUS_WKV7_DECAY_EXP = 1,
+    /* s0, sT, dsT and ds0 are [B,H,key,value] (GDN's "B,Hv,K,V", :382) instead of
+     * [B,H,value,key]; saved states keep the library's own layout. */
+    THESEUS_WKV7_STATE_KEY_VALUE = 2
 };
 
 /* Kernel family a call of these sizes runs on (theseus_wkv7_kernel_family). */
@@ -57,8 +69,10 @@ enum theseus_wkv7_family {
     THESEUS_WKV7_FAMILY_FORCED = 1,     /* step-serial: THESEUS_WKV7_FAMILY=seq is set       */
     THESEUS_WKV7_FAMILY_FP32 = 2,       /* step-serial: fp32 token tensors                   */
     THESEUS_WKV7_FAMILY_HEAD_SIZE = 3,  /* step-serial: N != 64                              */
-    THESEUS_WKV7_FAMILY_SIZE = 4        /* step-serial: a token tensor >= 2 GiB or one head's
+    THESEUS_WKV7_FAMILY_SIZE = 4,       /* step-serial: a token tensor >= 2 GiB or one head's
                                            saved states >= 4 GiB (32-bit buffer offsets)     */
+    THESEUS_WKV7_FAMILY_FLAGS = 5       /* step-serial: a call of the *_ex entry points with
+                                           flags (exp decay or key-value states)             */
 };
 
 /* ABI version of this header; bumped on any incompatible change. */
@@ -115,6 +129,30 @@ int theseus_wkv7_backward(int B, int T, int H, int N, int dtype,
                           void* dr, void* dw, void* dk, void* dv, void* da, void* db,
                           float* ds0, void* workspace, size_t workspace_bytes,
                           hipStream_t stream);
+
+/* theseus_wkv7_forward / _backward with options (theseus_wkv7_flags; 0 gives exactly
+ * the functions above).  With THESEUS_WKV7_DECAY_EXP and the GDN operand mapping
+ * r = q/sqrt(N), w = g, k = k, v = beta v, a = k, b = -exp(g) beta k
+ * ("wkv_inputs", convert_qwen2rwkv_lightning.py:385) they run the gated delta rule of
+ * the reference's teacher layers (theseus/hf_model.py:28-52 dispatches those to
+ * transformers' torch_chunk/recurrent_gated_delta_rule).  Calls with flags run on the
+ * step-serial kernels (any N 2..128, bf16 or fp32); a T=1 forward without saved states
+ * and without THESEUS_WKV7_STATE_KEY_VALUE runs the single-step kernel.  Workspace
+ * sizes: theseus_wkv7_workspace_size_ex.  Unknown flags: THESEUS_WKV7_ERR_FLAGS. */
+int theseus_wkv7_forward_ex(int B, int T, int H, int N, int dtype, int flags,
+                            const void* r, const void* w, const void* k, const void* v,
+                            const void* a, const void* b, const float* s0,
+                            void* y, float* sT, float* ckpt, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+int theseus_wkv7_backward_ex(int B, int T, int H, int N, int dtype, int flags,
+                             const void* r, const void* w, const void* k, const void* v,
+                             const void* a, const void* b, const float* ckpt,
+                             const void* dy, const float* dsT,
+                             void* dr, void* dw, void* dk, void* dv, void* da, void* db,
+                             float* ds0, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+/* Workspace bytes of theseus_wkv7_forward_ex (backward = 0) or _backward_ex (1). */
+size_t theseus_wkv7_workspace_size_ex(int B, int T, int H, int N, int dtype, int flags, int backward);
 
 /* One recurrent step (T = 1) that updates `state` [B,H,N,N] float32 IN PLACE
  * and writes y [B,H,N].  r..b are [B,H,N] (a [B,1,H,N] tensor).  The

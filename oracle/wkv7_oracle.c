@@ -9,6 +9,9 @@
  * Layouts  : token vectors [B,T,H,N] at ((b*T+t)*H+h)*N+n (cu:25);
  *            state [B,H,N,N] at ((b*H+h)*N+i)*N+j, i = value row, j = key
  *            column (cu:21).
+ * mode     : 0 = the reference's decay exp(-e^{-1/2} sigmoid(w)) (cu:27);
+ *            1 = exp(w), unclamped (the GDN teacher's decay,
+ *            convert_qwen2rwkv_lightning.py:384).
  * Parallel over (b,h) with OpenMP; every (b,h) is independent, so results
  * do not depend on the thread count.
  */
@@ -20,11 +23,19 @@
 
 static inline double sigm(double x) { return 1.0 / (1.0 + exp(-x)); }
 
+static inline double dec(int mode, double w) { return mode ? exp(w) : exp(-DECAY_SCALE * sigm(w)); }
+/* d(log d)/dw */
+static inline double dlogd(int mode, double w) {
+    if (mode) return 1.0;
+    double s = sigm(w);
+    return -DECAY_SCALE * s * (1.0 - s);
+}
+
 static inline long tok(int b, int t, int h, int T, int H, int N) {
     return (((long)b * T + t) * H + h) * N;
 }
 
-void wkv7_oracle_forward(int B, int T, int H, int N, const double* r, const double* w,
+void wkv7_oracle_forward(int B, int T, int H, int N, int mode, const double* r, const double* w,
                          const double* k, const double* v, const double* a, const double* b,
                          const double* s0, double* y, double* sT) {
 #pragma omp parallel for schedule(dynamic)
@@ -36,7 +47,7 @@ void wkv7_oracle_forward(int B, int T, int H, int N, const double* r, const doub
         memcpy(S, s0 + (long)bh * N * N, sizeof(double) * N * N);
         for (int t = 0; t < T; t++) {
             long o = tok(bb, t, h, T, H, N);
-            for (int j = 0; j < N; j++) d[j] = exp(-DECAY_SCALE * sigm(w[o + j]));
+            for (int j = 0; j < N; j++) d[j] = dec(mode, w[o + j]);
             for (int i = 0; i < N; i++) {           /* sa_i = sum_j S_ij a_j */
                 double acc = 0.0;
                 for (int j = 0; j < N; j++) acc += S[i * N + j] * a[o + j];
@@ -57,7 +68,7 @@ void wkv7_oracle_forward(int B, int T, int H, int N, const double* r, const doub
     }
 }
 
-void wkv7_oracle_backward(int B, int T, int H, int N, const double* r, const double* w,
+void wkv7_oracle_backward(int B, int T, int H, int N, int mode, const double* r, const double* w,
                           const double* k, const double* v, const double* a, const double* b,
                           const double* s0, const double* dy, const double* dsT,
                           double* dr, double* dw, double* dk, double* dv, double* da,
@@ -77,7 +88,7 @@ void wkv7_oracle_backward(int B, int T, int H, int N, const double* r, const dou
             long o = tok(bb, t, h, T, H, N);
             const double* Sp = hist + NN * t;
             double* Sn = hist + NN * (t + 1);
-            for (int j = 0; j < N; j++) d[j] = exp(-DECAY_SCALE * sigm(w[o + j]));
+            for (int j = 0; j < N; j++) d[j] = dec(mode, w[o + j]);
             for (int i = 0; i < N; i++) {
                 double acc = 0.0;
                 for (int j = 0; j < N; j++) acc += Sp[i * N + j] * a[o + j];
@@ -103,8 +114,7 @@ void wkv7_oracle_backward(int B, int T, int H, int N, const double* r, const dou
                 q[i] = accq;
             }
             for (int j = 0; j < N; j++) {                     /* cu:68-72 */
-                double s = sigm(w[o + j]);
-                double dj = exp(-DECAY_SCALE * s);
+                double dj = dec(mode, w[o + j]);
                 double gr = 0, gw = 0, gk = 0, gb = 0, ga = 0;
                 for (int i = 0; i < N; i++) {
                     double g = G[i * N + j];
@@ -115,7 +125,7 @@ void wkv7_oracle_backward(int B, int T, int H, int N, const double* r, const dou
                     ga += q[i] * Sp[i * N + j];
                 }
                 dr[o + j] = gr;
-                dw[o + j] = gw * dj * (-DECAY_SCALE) * s * (1.0 - s);
+                dw[o + j] = gw * dj * dlogd(mode, w[o + j]);
                 dk[o + j] = gk;
                 db[o + j] = gb;
                 da[o + j] = ga;
@@ -125,7 +135,7 @@ void wkv7_oracle_backward(int B, int T, int H, int N, const double* r, const dou
                 for (int j = 0; j < N; j++) acc += G[i * N + j] * k[o + j];
                 dv[o + i] = acc;
             }
-            for (int j = 0; j < N; j++) d[j] = exp(-DECAY_SCALE * sigm(w[o + j]));
+            for (int j = 0; j < N; j++) d[j] = dec(mode, w[o + j]);
             for (int i = 0; i < N; i++)                       /* cu:74 */
                 for (int j = 0; j < N; j++)
                     G[i * N + j] = G[i * N + j] * d[j] + q[i] * a[o + j];

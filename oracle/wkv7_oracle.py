@@ -59,25 +59,46 @@ def _sigmoid(x):
     return 1.0 / (1.0 + np.exp(-x))
 
 
-def decay(w):
-    """d = exp(-e^{-1/2} * sigmoid(w)); w is the pre-sigmoid logit (wkv7.py:19)."""
-    return np.exp(-DECAY_SCALE * _sigmoid(np.asarray(w, dtype=np.float64)))
+def decay(w, mode="rwkv"):
+    """Per-key decay of a step.
+
+    mode "rwkv": d = exp(-e^{-1/2} * sigmoid(w)), w the pre-sigmoid logit (wkv7.py:19).
+    mode "exp":  d = exp(w), no clamp or sigmoid -- the GDN teacher's decay as the
+    converter's contract states it ("wkv_decay_operation": "exp(g), NO
+    clamp/sigmoid/exp(-exp(w))", convert_qwen2rwkv_lightning.py:384).
+    """
+    w = np.asarray(w, dtype=np.float64)
+    if mode == "exp":
+        return np.exp(w)
+    if mode != "rwkv":
+        raise ValueError(mode)
+    return np.exp(-DECAY_SCALE * _sigmoid(w))
+
+
+def dlogd_dw(w, mode="rwkv"):
+    """d(log d)/dw: -e^{-1/2} sigmoid(w)(1 - sigmoid(w)) for "rwkv" (cu:69), 1 for "exp"."""
+    w = np.asarray(w, dtype=np.float64)
+    if mode == "exp":
+        return np.ones_like(w)
+    sg = _sigmoid(w)
+    return -DECAY_SCALE * sg * (1.0 - sg)
 
 
 def _f64(*xs):
     return [np.ascontiguousarray(np.asarray(x, dtype=np.float64)) for x in xs]
 
 
-def forward(r, w, k, v, a, b, s0, return_states=False):
+def forward(r, w, k, v, a, b, s0, return_states=False, mode="rwkv"):
     """Forward recurrence (theseus/wkv7.py:16-28, kernels/wkv7_state.cu:24-38).
 
     r..b: [B,T,H,N]; s0: [B,H,N,N] (row = value i, column = key j).
     Returns y [B,T,H,N] float64 and sT [B,H,N,N] float64; with
     ``return_states`` also the stacked states [B,H,T+1,N,N] (S_0..S_T).
+    ``mode`` picks the decay (``decay``).
     """
     r, w, k, v, a, b, s0 = _f64(r, w, k, v, a, b, s0)
     B, T, H, N = r.shape
-    d = decay(w)
+    d = decay(w, mode)
     S = s0.copy()
     y = np.empty_like(r)
     states = [S.copy()] if return_states else None
@@ -97,17 +118,18 @@ def forward(r, w, k, v, a, b, s0, return_states=False):
     return y, S
 
 
-def backward(r, w, k, v, a, b, s0, dy, dsT):
+def backward(r, w, k, v, a, b, s0, dy, dsT, mode="rwkv"):
     """Reverse-mode adjoint of ``forward`` (kernels/wkv7_state.cu:49-78).
 
     Returns (dr, dw, dk, dv, da, db, ds0), all float64; the first six are
-    [B,T,H,N], ds0 is [B,H,N,N].
+    [B,T,H,N], ds0 is [B,H,N,N].  ``mode`` picks the decay; only dw's factor
+    d(log d)/dw depends on it.
     """
     r, w, k, v, a, b, s0, dy, dsT = _f64(r, w, k, v, a, b, s0, dy, dsT)
     B, T, H, N = r.shape
-    _, _, states = forward(r, w, k, v, a, b, s0, return_states=True)
-    sig = _sigmoid(w)
-    d = np.exp(-DECAY_SCALE * sig)
+    _, _, states = forward(r, w, k, v, a, b, s0, return_states=True, mode=mode)
+    d = decay(w, mode)
+    fw = dlogd_dw(w, mode)
     grads = [np.zeros_like(r) for _ in range(6)]
     dr, dw, dk, dv, da, db = grads
     G = dsT.copy()                                          # cu:50
@@ -120,8 +142,7 @@ def backward(r, w, k, v, a, b, s0, dy, dsT):
         G = G + dyt[..., None] * rt[:, :, None, :]          # cu:63 (ds += dy r)
         q = np.einsum("bhij,bhj->bhi", G, bt)               # cu:64 (dotgrad)
         dr[:, t] = np.einsum("bhi,bhij->bhj", dyt, Sn)      # cu:68
-        dw[:, t] = (np.einsum("bhij,bhij->bhj", G, Sp) * dt
-                    * (-DECAY_SCALE) * sig[:, t] * (1.0 - sig[:, t]))  # cu:69
+        dw[:, t] = np.einsum("bhij,bhij->bhj", G, Sp) * dt * fw[:, t]  # cu:69
         dk[:, t] = np.einsum("bhij,bhi->bhj", G, vt)        # cu:70
         db[:, t] = np.einsum("bhij,bhi->bhj", G, sa)        # cu:71
         da[:, t] = np.einsum("bhi,bhij->bhj", q, Sp)        # cu:72
@@ -145,9 +166,9 @@ def _lib():
                 f"{path} is missing; build it with `make -C oracle`")
         lib = ctypes.CDLL(str(path))
         dp = ctypes.POINTER(ctypes.c_double)
-        lib.wkv7_oracle_forward.argtypes = [ctypes.c_int] * 4 + [dp] * 9
+        lib.wkv7_oracle_forward.argtypes = [ctypes.c_int] * 5 + [dp] * 9
         lib.wkv7_oracle_forward.restype = None
-        lib.wkv7_oracle_backward.argtypes = [ctypes.c_int] * 4 + [dp] * 16
+        lib.wkv7_oracle_backward.argtypes = [ctypes.c_int] * 5 + [dp] * 16
         lib.wkv7_oracle_backward.restype = None
         _LIB = lib
     return _LIB
@@ -161,22 +182,50 @@ def _ptr(x):
     return x.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
 
 
-def forward_c(r, w, k, v, a, b, s0):
+_MODES = {"rwkv": 0, "exp": 1}
+
+
+def forward_c(r, w, k, v, a, b, s0, mode="rwkv"):
     r, w, k, v, a, b, s0 = _f64(r, w, k, v, a, b, s0)
     B, T, H, N = r.shape
     y = np.empty_like(r)
     sT = np.empty_like(s0)
-    _lib().wkv7_oracle_forward(B, T, H, N, *map(_ptr, (r, w, k, v, a, b, s0, y, sT)))
+    _lib().wkv7_oracle_forward(B, T, H, N, _MODES[mode], *map(_ptr, (r, w, k, v, a, b, s0, y, sT)))
     return y, sT
 
 
-def backward_c(r, w, k, v, a, b, s0, dy, dsT):
+def backward_c(r, w, k, v, a, b, s0, dy, dsT, mode="rwkv"):
     r, w, k, v, a, b, s0, dy, dsT = _f64(r, w, k, v, a, b, s0, dy, dsT)
     B, T, H, N = r.shape
     outs = [np.empty_like(r) for _ in range(6)] + [np.empty_like(s0)]
     _lib().wkv7_oracle_backward(
-        B, T, H, N, *map(_ptr, (r, w, k, v, a, b, s0, dy, dsT, *outs)))
+        B, T, H, N, _MODES[mode], *map(_ptr, (r, w, k, v, a, b, s0, dy, dsT, *outs)))
     return tuple(outs)
+
+
+# ----------------------------------------------------------------------------
+# GDN (gated delta rule) as the recurrence in "exp" decay mode
+# ----------------------------------------------------------------------------
+def gdn_operands(q, k, v, g, beta):
+    """The WKV operands of a GDN step, as the converter's contract maps them
+    (convert_qwen2rwkv_lightning.py:385, "wkv_inputs": "r=q/sqrt(Dk), w=g, k=k,
+    v=beta*v, a=k, b=-exp(g)*beta*k"): q, k, v [B,T,H,N] (q and k already
+    L2-normalised if the layer does so), g, beta [B,T,H].  w is g broadcast
+    over the keys, to be used with mode "exp"."""
+    q, k, v, g, beta = _f64(q, k, v, g, beta)
+    N = q.shape[-1]
+    gb = np.broadcast_to(g[..., None], q.shape)
+    return (q / np.sqrt(N), np.ascontiguousarray(gb), k, beta[..., None] * v, k.copy(),
+            -np.exp(g)[..., None] * beta[..., None] * k)
+
+
+def gdn_forward(q, k, v, g, beta, s0_kv):
+    """GDN output and final state through ``forward`` in "exp" mode.  The GDN state
+    is [B,H,key,value] ("gdn_state_layout": "B,Hv,K,V", :382), the transpose of
+    the recurrence's [B,H,value,key]."""
+    ops = gdn_operands(q, k, v, g, beta)
+    y, sT = forward(*ops, np.swapaxes(np.asarray(s0_kv, dtype=np.float64), -1, -2), mode="exp")
+    return y, np.ascontiguousarray(np.swapaxes(sT, -1, -2))
 
 
 # ----------------------------------------------------------------------------

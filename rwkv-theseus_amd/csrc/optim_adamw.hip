@@ -31,6 +31,18 @@ constexpr int CHUNK = THESEUS_ADAMW_CHUNK;
 constexpr int THREADS = 256;
 constexpr int BATCH = 32;  // tensors per launch
 
+// Streaming loads and stores marked non-temporal: every byte is touched once per pass
+// (measured on MI355X at 112 M parameters: update 0.619 -> 0.593 ms, norm pass 98 -> 67 us).
+typedef float vf4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_nt(const float4* p) {
+    const vf4 t = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(p));
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ void st_nt(float4* p, float4 v) {
+    const vf4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<vf4*>(p));
+}
+
 struct TensorArg {
     float* p;
     const float* g;
@@ -89,7 +101,7 @@ __global__ __launch_bounds__(THREADS) void grad_sumsq(Batch bt, double* __restri
         const float4* g4 = reinterpret_cast<const float4*>(g);
 #pragma unroll 4
         for (int q = threadIdx.x; q < nv; q += THREADS) {
-            const float4 x = g4[q];
+            const float4 x = ld_nt(g4 + q);
             acc += (double)x.x * x.x + (double)x.y * x.y + (double)x.z * x.z + (double)x.w * x.w;
         }
         e0 = nv * 4;
@@ -154,13 +166,13 @@ __global__ __launch_bounds__(THREADS) void adamw(Batch bt, Hyper h, const float*
         float4* v4 = reinterpret_cast<float4*>(v);
 #pragma unroll 4
         for (int q = threadIdx.x; q < nv; q += THREADS) {
-            float4 pp = p4[q], mm = m4[q], vv = v4[q];
-            const float4 gg = g4[q];
+            float4 pp = ld_nt(p4 + q), mm = ld_nt(m4 + q), vv = ld_nt(v4 + q);
+            const float4 gg = ld_nt(g4 + q);
             adamw_one(pp.x, gg.x * mult, mm.x, vv.x, t, h);
             adamw_one(pp.y, gg.y * mult, mm.y, vv.y, t, h);
             adamw_one(pp.z, gg.z * mult, mm.z, vv.z, t, h);
             adamw_one(pp.w, gg.w * mult, mm.w, vv.w, t, h);
-            p4[q] = pp, m4[q] = mm, v4[q] = vv;
+            st_nt(p4 + q, pp), st_nt(m4 + q, mm), st_nt(v4 + q, vv);
         }
         e0 = nv * 4;
     }

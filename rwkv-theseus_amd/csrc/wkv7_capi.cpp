@@ -42,8 +42,9 @@ static bool force_seq() {
 // N = 64, token tensors under 2 GiB and one head's saved states under 4 GiB:
 // both are addressed with 32-bit buffer offsets (the token tensors' range
 // check also drops rows past a partial chunk, so the limit is 2^31).
-int chunk_refusal(int B, int T, int H, int N, int dtype) {
+int chunk_refusal(int B, int T, int H, int N, int dtype, int flags) {
     if (force_seq()) return THESEUS_WKV7_FAMILY_FORCED;
+    if (flags) return THESEUS_WKV7_FAMILY_FLAGS;
     if (dtype != THESEUS_WKV7_BF16) return THESEUS_WKV7_FAMILY_FP32;
     if (N != 64) return THESEUS_WKV7_FAMILY_HEAD_SIZE;
     if ((long long)B * T * H * N * 2 >= (1ll << 31) ||
@@ -51,7 +52,9 @@ int chunk_refusal(int B, int T, int H, int N, int dtype) {
         return THESEUS_WKV7_FAMILY_SIZE;
     return 0;
 }
-static bool chunk_ok(int B, int T, int H, int N, int dtype) { return chunk_refusal(B, T, H, N, dtype) == 0; }
+static bool chunk_ok(int B, int T, int H, int N, int dtype, int flags) {
+    return chunk_refusal(B, T, H, N, dtype, flags) == 0;
+}
 
 // CUs of the current device, which the chunked kernels' schedule spreads the
 // heads over (one workgroup each).  THESEUS_WKV7_CUS=<n> plans for n instead
@@ -69,24 +72,27 @@ static int cu_count() {
 }
 
 void launch_forward(const Fwd& p) {
-    if (p.T == 1 && !p.ckpt && !force_seq()) {
+    if (p.T == 1 && !p.ckpt && !force_seq() && !(p.flags & FLAG_STATE_KV)) {
         // one step without saved states (the serving step through the operator):
         // the single-step kernel, s0 -> sT
-        launch_decode(Dec{p.B, p.H, p.N, p.dtype, p.r, p.w, p.k, p.v, p.a, p.b, p.s0, p.sT, p.y, p.stream});
-    } else if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_forward(p, cu_count());
+        Dec d{p.B, p.H, p.N, p.dtype, p.r, p.w, p.k, p.v, p.a, p.b, p.s0, p.sT, p.y, p.stream};
+        d.flags = p.flags;
+        launch_decode(d);
+    } else if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype, p.flags)) launch_chunk_forward(p, cu_count());
     else launch_seq_forward(p);
 }
 void launch_backward(const Bwd& p) {
-    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype)) launch_chunk_backward(p, cu_count());
+    if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype, p.flags)) launch_chunk_backward(p, cu_count());
     else launch_seq_backward(p);
 }
 // The chunked kernels' handoffs; the step-serial backward replays each
 // 16-step segment into its workspace (its forward needs none).
-size_t forward_workspace(int B, int T, int H, int N, int dtype) {
-    return chunk_ok(B, T, H, N, dtype) ? chunk_forward_workspace(B, T, H, cu_count()) : 0;
+size_t forward_workspace(int B, int T, int H, int N, int dtype, int flags) {
+    return chunk_ok(B, T, H, N, dtype, flags) ? chunk_forward_workspace(B, T, H, cu_count()) : 0;
 }
-size_t backward_workspace(int B, int T, int H, int N, int dtype) {
-    return chunk_ok(B, T, H, N, dtype) ? chunk_backward_workspace(B, T, H, cu_count()) : seq_backward_workspace(B, H, N);
+size_t backward_workspace(int B, int T, int H, int N, int dtype, int flags) {
+    return chunk_ok(B, T, H, N, dtype, flags) ? chunk_backward_workspace(B, T, H, cu_count())
+                                              : seq_backward_workspace(B, H, N);
 }
 
 }  // namespace wkv7
@@ -103,6 +109,7 @@ const char* theseus_wkv7_error_string(int status) {
         case THESEUS_WKV7_ERR_NULL: return "null pointer argument";
         case THESEUS_WKV7_ERR_WORKSPACE: return "workspace too small";
         case THESEUS_WKV7_ERR_LAUNCH: return "HIP kernel launch failed";
+        case THESEUS_WKV7_ERR_FLAGS: return "unknown flags (THESEUS_WKV7_DECAY_EXP | THESEUS_WKV7_STATE_KEY_VALUE)";
         case THESEUS_WKV7_ERR_SCRATCH:
             return "sizes need more handoff scratch than the library's static array holds "
                    "(THESEUS_WKV7_NOALLOC_SCRATCH_BYTES); use theseus_wkv7_forward with a workspace";
@@ -112,7 +119,7 @@ const char* theseus_wkv7_error_string(int status) {
 
 int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype) {
     if (int e = check_dims(B, T, H, N, dtype)) return -e;
-    return wkv7::chunk_refusal(B, T, H, N, dtype);
+    return wkv7::chunk_refusal(B, T, H, N, dtype, 0);
 }
 
 int theseus_wkv7_checkpoint_interval(void) { return wkv7::kCkptInterval; }
@@ -131,16 +138,45 @@ size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtyp
     return wkv7::backward_workspace(B, T, H, N, dtype);
 }
 
+int theseus_wkv7_forward_ex(int B, int T, int H, int N, int dtype, int flags, const void* r,
+                            const void* w, const void* k, const void* v, const void* a, const void* b,
+                            const float* s0, void* y, float* sT, float* ckpt, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+    if (int e = check_dims(B, T, H, N, dtype)) return e;
+    if (flags & ~wkv7::FLAGS_ALL) return THESEUS_WKV7_ERR_FLAGS;
+    if (!r || !w || !k || !v || !a || !b || !s0 || !y || !sT) return THESEUS_WKV7_ERR_NULL;
+    const size_t need = wkv7::forward_workspace(B, T, H, N, dtype, flags);
+    if (workspace_bytes < need || (need && !workspace)) return THESEUS_WKV7_ERR_WORKSPACE;
+    wkv7::Fwd p{B, T, H, N, dtype, r, w, k, v, a, b, s0, y, sT, ckpt, workspace, stream};
+    p.flags = flags;
+    wkv7::launch_forward(p);
+    return launch_status();
+}
+
 int theseus_wkv7_forward(int B, int T, int H, int N, int dtype, const void* r, const void* w,
                          const void* k, const void* v, const void* a, const void* b,
                          const float* s0, void* y, float* sT, float* ckpt, void* workspace,
                          size_t workspace_bytes, hipStream_t stream) {
+    return theseus_wkv7_forward_ex(B, T, H, N, dtype, 0, r, w, k, v, a, b, s0, y, sT, ckpt, workspace,
+                                   workspace_bytes, stream);
+}
+
+int theseus_wkv7_backward_ex(int B, int T, int H, int N, int dtype, int flags, const void* r,
+                             const void* w, const void* k, const void* v, const void* a, const void* b,
+                             const float* ckpt, const void* dy, const float* dsT, void* dr, void* dw,
+                             void* dk, void* dv, void* da, void* db, float* ds0, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
     if (int e = check_dims(B, T, H, N, dtype)) return e;
-    if (!r || !w || !k || !v || !a || !b || !s0 || !y || !sT) return THESEUS_WKV7_ERR_NULL;
-    const size_t need = wkv7::forward_workspace(B, T, H, N, dtype);
+    if (flags & ~wkv7::FLAGS_ALL) return THESEUS_WKV7_ERR_FLAGS;
+    if (!r || !w || !k || !v || !a || !b || !ckpt || !dy || !dr || !dw || !dk || !dv || !da ||
+        !db || !ds0)
+        return THESEUS_WKV7_ERR_NULL;
+    const size_t need = wkv7::backward_workspace(B, T, H, N, dtype, flags);
     if (workspace_bytes < need || (need && !workspace)) return THESEUS_WKV7_ERR_WORKSPACE;
-    wkv7::Fwd p{B, T, H, N, dtype, r, w, k, v, a, b, s0, y, sT, ckpt, workspace, stream};
-    wkv7::launch_forward(p);
+    wkv7::Bwd p{B, T, H, N, dtype, r, w, k, v, a, b, ckpt, dy, dsT,
+                dr, dw, dk, dv, da, db, ds0, workspace, stream};
+    p.flags = flags;
+    wkv7::launch_backward(p);
     return launch_status();
 }
 
@@ -149,16 +185,14 @@ int theseus_wkv7_backward(int B, int T, int H, int N, int dtype, const void* r, 
                           const float* ckpt, const void* dy, const float* dsT, void* dr,
                           void* dw, void* dk, void* dv, void* da, void* db, float* ds0,
                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (int e = check_dims(B, T, H, N, dtype)) return e;
-    if (!r || !w || !k || !v || !a || !b || !ckpt || !dy || !dr || !dw || !dk || !dv || !da ||
-        !db || !ds0)
-        return THESEUS_WKV7_ERR_NULL;
-    const size_t need = wkv7::backward_workspace(B, T, H, N, dtype);
-    if (workspace_bytes < need || (need && !workspace)) return THESEUS_WKV7_ERR_WORKSPACE;
-    wkv7::Bwd p{B, T, H, N, dtype, r, w, k, v, a, b, ckpt, dy, dsT,
-                dr, dw, dk, dv, da, db, ds0, workspace, stream};
-    wkv7::launch_backward(p);
-    return launch_status();
+    return theseus_wkv7_backward_ex(B, T, H, N, dtype, 0, r, w, k, v, a, b, ckpt, dy, dsT, dr, dw, dk, dv,
+                                    da, db, ds0, workspace, workspace_bytes, stream);
+}
+
+size_t theseus_wkv7_workspace_size_ex(int B, int T, int H, int N, int dtype, int flags, int backward) {
+    if (check_dims(B, T, H, N, dtype) != THESEUS_WKV7_OK || (flags & ~wkv7::FLAGS_ALL)) return 0;
+    return backward ? wkv7::backward_workspace(B, T, H, N, dtype, flags)
+                    : wkv7::forward_workspace(B, T, H, N, dtype, flags);
 }
 
 int theseus_wkv7_decode_step(int B, int H, int N, int dtype, const void* r, const void* w,

@@ -45,6 +45,23 @@ __device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rc
 // log of the per-key decay: log d = -e^{-1/2} * sigmoid(w).
 __device__ __forceinline__ float log_decay(float w) { return -DECAY_SCALE * sigmoidf_(w); }
 
+// Decay modes (THESEUS_WKV7_DECAY_EXP of theseus_wkv7.h).  MODE_RWKV: the reference's
+// d = exp(-e^{-1/2} sigmoid(w)) (kernels/wkv7_state.cu:27).  MODE_EXP: d = exp(w) with no
+// clamp -- the GDN teacher's decay, w = g (convert_qwen2rwkv_lightning.py:383-384).
+constexpr int MODE_RWKV = 0, MODE_EXP = 1;
+template <int MODE> __device__ __forceinline__ float decay_of(float w) {
+    if constexpr (MODE == MODE_EXP) return __expf(w);
+    else return __expf(log_decay(w));
+}
+// d * d(log d)/dw: the factor that turns sum_i G_ij S_{t-1,ij} into dw_j (cu:69)
+template <int MODE> __device__ __forceinline__ float dw_factor(float w, float d) {
+    if constexpr (MODE == MODE_EXP) return d;
+    else {
+        const float s = sigmoidf_(w);
+        return d * (-DECAY_SCALE) * s * (1.f - s);
+    }
+}
+
 __host__ __device__ constexpr inline long ckpt_count(int T) { return (T + CKPT - 1) / CKPT + 1; }
 
 // Sum over each 16-lane row of the wave, left in every lane of the row: DPP

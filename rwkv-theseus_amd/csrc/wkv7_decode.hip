@@ -15,7 +15,7 @@
 
 namespace wkv7 {
 
-template <typename T, int VEC, int NP, int G>
+template <typename T, int VEC, int NP, int G, int MODE>
 __global__ __launch_bounds__(16 * G) void decode_step(
     int H, int N, const T* __restrict__ r, const T* __restrict__ w, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ a, const T* __restrict__ b,
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(16 * G) void decode_step(
             const int j = VEC * (l16 + 16 * m) + e;
             const bool ok = j < N;
             kr[m][e] = ok ? io<T>::ld(r, o + j) : 0.f;
-            kd[m][e] = ok ? __expf(log_decay(io<T>::ld(w, o + j))) : 1.f;
+            kd[m][e] = ok ? decay_of<MODE>(io<T>::ld(w, o + j)) : 1.f;
             kk[m][e] = ok ? io<T>::ld(k, o + j) : 0.f;
             ka[m][e] = ok ? io<T>::ld(a, o + j) : 0.f;
             kb[m][e] = ok ? io<T>::ld(b, o + j) : 0.f;
@@ -129,7 +129,7 @@ template <> __device__ __forceinline__ void ld4<bf16_t>(const bf16_t* p, float (
     x[2] = __uint_as_float(u.y << 16), x[3] = __uint_as_float(u.y & 0xffff0000u);
 }
 
-template <typename T>
+template <typename T, int MODE>
 __global__ __launch_bounds__(64) void decode_step64(
     const T* __restrict__ r, const T* __restrict__ w, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ a, const T* __restrict__ b, const float* s_in, float* s_out, T* __restrict__ y) {
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64) void decode_step64(
     for (int rr = 0; rr < 16; rr++) vi[rr] = io<T>::ld(v, o + 4 * rr + grp);
     float kd[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) kd[e] = __expf(log_decay(kw[e]));
+    for (int e = 0; e < 4; e++) kd[e] = decay_of<MODE>(kw[e]);
     float yv = 0.f;
 #pragma unroll
     for (int rr = 0; rr < 16; rr++) {
@@ -174,27 +174,34 @@ __global__ __launch_bounds__(64) void decode_step64(
 
 namespace wkv7 {
 
-template <typename T, int VEC, int NP, int G>
+template <typename T, int VEC, int NP, int G, int MODE>
 static void decode_launch(const Dec& p) {
-    hipLaunchKernelGGL((decode_step<T, VEC, NP, G>), dim3(p.B * p.H), dim3(16 * G), 0, p.stream, p.H, p.N,
+    hipLaunchKernelGGL((decode_step<T, VEC, NP, G, MODE>), dim3(p.B * p.H), dim3(16 * G), 0, p.stream, p.H, p.N,
                        (const T*)p.r, (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b,
                        p.state_in, p.state, (T*)p.y);
 }
-template <typename T>
+template <typename T, int MODE>
 static void decode_t(const Dec& p) {
     if (p.N == 64) {
-        hipLaunchKernelGGL((decode_step64<T>), dim3(p.B * p.H), dim3(64), 0, p.stream, (const T*)p.r, (const T*)p.w,
-                           (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state_in, p.state, (T*)p.y);
+        hipLaunchKernelGGL((decode_step64<T, MODE>), dim3(p.B * p.H), dim3(64), 0, p.stream, (const T*)p.r,
+                           (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a, (const T*)p.b, p.state_in,
+                           p.state, (T*)p.y);
     } else if (p.N % 4 == 0) {
-        if (p.N <= 64) decode_launch<T, 4, 64, 4>(p);
-        else decode_launch<T, 4, 128, 16>(p);
+        if (p.N <= 64) decode_launch<T, 4, 64, 4, MODE>(p);
+        else decode_launch<T, 4, 128, 16, MODE>(p);
     } else {
-        decode_launch<T, 1, 128, 16>(p);
+        decode_launch<T, 1, 128, 16, MODE>(p);
     }
 }
 
+// (states [value][key] only: a call with FLAG_STATE_KV runs the step-serial forward)
 void launch_decode(const Dec& p) {
-    if (p.dtype == 0) decode_t<bf16_t>(p); else decode_t<float>(p);
+    const bool ex = p.flags & FLAG_DECAY_EXP;
+    if (p.dtype == 0) {
+        if (ex) decode_t<bf16_t, MODE_EXP>(p); else decode_t<bf16_t, MODE_RWKV>(p);
+    } else {
+        if (ex) decode_t<float, MODE_EXP>(p); else decode_t<float, MODE_RWKV>(p);
+    }
 }
 
 }  // namespace wkv7

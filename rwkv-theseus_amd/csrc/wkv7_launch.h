@@ -8,6 +8,10 @@
 namespace wkv7 {
 
 constexpr int kCkptInterval = 16;  // must equal CKPT in wkv7_common.h
+// theseus_wkv7_flags (include/theseus_wkv7.h)
+constexpr int FLAG_DECAY_EXP = 1;  // d = exp(w), unclamped
+constexpr int FLAG_STATE_KV = 2;   // caller states stored [key][value]
+constexpr int FLAGS_ALL = FLAG_DECAY_EXP | FLAG_STATE_KV;
 
 struct Fwd {
     int B, T, H, N, dtype;
@@ -18,6 +22,7 @@ struct Fwd {
     float* ckpt;  // may be null
     void* ws;     // workspace (the chunked kernels' handoffs)
     hipStream_t stream;
+    int flags = 0;
 };
 
 struct Bwd {
@@ -30,6 +35,7 @@ struct Bwd {
     float* ds0;
     void* ws;
     hipStream_t stream;
+    int flags = 0;
 };
 
 struct Dec {
@@ -39,6 +45,7 @@ struct Dec {
     float* state;           // written
     void* y;
     hipStream_t stream;
+    int flags = 0;          // FLAG_DECAY_EXP only
 };
 
 void launch_seq_forward(const Fwd& p);
@@ -55,7 +62,7 @@ size_t chunk_backward_workspace(int B, int T, int H, int cus);
 // the call, else the step-serial ones.
 void launch_forward(const Fwd& p);
 void launch_backward(const Bwd& p);
-size_t forward_workspace(int B, int T, int H, int N, int dtype);
-size_t backward_workspace(int B, int T, int H, int N, int dtype);
+size_t forward_workspace(int B, int T, int H, int N, int dtype, int flags = 0);
+size_t backward_workspace(int B, int T, int H, int N, int dtype, int flags = 0);
 
 }  // namespace wkv7

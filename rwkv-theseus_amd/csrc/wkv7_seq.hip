@@ -13,25 +13,32 @@
 // da) by the lane that owns column j, reading the transposed gradient state
 // from LDS -- a fixed-order reduction, so results are deterministic (the
 // reference uses fp32 atomicAdd, cu:68-72).
+//
+// MODE picks the decay (MODE_RWKV / MODE_EXP, wkv7_common.h); `kv` != 0 means the
+// caller's states (s0, sT, dsT, ds0) are stored [key][value] (GDN's layout) instead of
+// [value][key]: lane i then reads and writes element (j, i) at j*N + i, which is
+// coalesced across lanes.  Saved states always use [value][key].
 #include "wkv7_common.h"
 
 namespace wkv7 {
 
-template <typename T, int NP>
+template <typename T, int NP, int MODE>
 __global__ __launch_bounds__(NP) void seq_forward(
-    int Tn, int H, int N, const T* __restrict__ r, const T* __restrict__ w,
+    int Tn, int H, int N, int kv, const T* __restrict__ r, const T* __restrict__ w,
     const T* __restrict__ k, const T* __restrict__ v, const T* __restrict__ a,
-    const T* __restrict__ b, const float* __restrict__ s0, T* __restrict__ y,
-    float* __restrict__ sT, float* __restrict__ ckpt) {
+    const T* __restrict__ b, const float* s0, T* __restrict__ y,
+    float* sT, float* __restrict__ ckpt) {
     const int bh = blockIdx.x, bb = bh / H, h = bh % H, i = threadIdx.x;
     const bool row = i < N;
     const long NN = (long)N * N;
     const long ncp = ckpt_count(Tn);
     __shared__ float vec[2][5][NP];  // r, d, k, a, b for the current / next step
 
+    // element (i, j) of a caller state: [value][key], or [key][value] when kv
+    const long ei = kv ? 1 : N, ej = kv ? N : 1;
     float st[NP];
 #pragma unroll
-    for (int j = 0; j < NP; j++) st[j] = (row && j < N) ? s0[bh * NN + (long)i * N + j] : 0.f;
+    for (int j = 0; j < NP; j++) st[j] = (row && j < N) ? s0[bh * NN + i * ei + j * ej] : 0.f;
     if (ckpt && row) {
 #pragma unroll
         for (int j = 0; j < NP; j++)
@@ -42,7 +49,7 @@ __global__ __launch_bounds__(NP) void seq_forward(
         const long o = ((long)(bb * Tn + t) * H + h) * N;
         if (row) {
             vec[buf][0][i] = io<T>::ld(r, o + i);
-            vec[buf][1][i] = __expf(log_decay(io<T>::ld(w, o + i)));
+            vec[buf][1][i] = decay_of<MODE>(io<T>::ld(w, o + i));
             vec[buf][2][i] = io<T>::ld(k, o + i);
             vec[buf][3][i] = io<T>::ld(a, o + i);
             vec[buf][4][i] = io<T>::ld(b, o + i);
@@ -79,16 +86,16 @@ __global__ __launch_bounds__(NP) void seq_forward(
     if (row) {
 #pragma unroll
         for (int j = 0; j < NP; j++)
-            if (j < N) sT[bh * NN + (long)i * N + j] = st[j];
+            if (j < N) sT[bh * NN + i * ei + j * ej] = st[j];
     }
 }
 
 // Workspace floats per (b,h) for seq_backward: CKPT+1 states and CKPT sa rows.
 __host__ __device__ inline long seq_ws_floats(int N) { return (long)(CKPT + 1) * N * N + (long)CKPT * N; }
 
-template <typename T, int NP>
+template <typename T, int NP, int MODE>
 __global__ __launch_bounds__(NP) void seq_backward(
-    int Tn, int H, int N, const T* __restrict__ r, const T* __restrict__ w,
+    int Tn, int H, int N, int kv, const T* __restrict__ r, const T* __restrict__ w,
     const T* __restrict__ k, const T* __restrict__ v, const T* __restrict__ a,
     const T* __restrict__ b, const float* __restrict__ ckpt, const T* __restrict__ dy,
     const float* __restrict__ dsT, T* __restrict__ dr, T* __restrict__ dw,
@@ -117,10 +124,12 @@ __global__ __launch_bounds__(NP) void seq_backward(
     float* vsa = vv + NP;
     float* vq = vsa + NP;
 
-    // G row `tid` (gradient w.r.t. the state), kept in registers.
+    // G row `tid` (gradient w.r.t. the state), kept in registers; element (i, j) of a
+    // caller state at i*ei + j*ej ([value][key], or [key][value] when kv)
+    const long ei = kv ? 1 : N, ej = kv ? N : 1;
     float g[NP];
 #pragma unroll
-    for (int j = 0; j < NP; j++) g[j] = (lane_ok && j < N && dsT) ? dsT[bh * NN + (long)tid * N + j] : 0.f;
+    for (int j = 0; j < NP; j++) g[j] = (lane_ok && j < N && dsT) ? dsT[bh * NN + tid * ei + j * ej] : 0.f;
 
     const int nseg = (Tn + CKPT - 1) / CKPT;
     for (int c = nseg - 1; c >= 0; c--) {
@@ -140,7 +149,7 @@ __global__ __launch_bounds__(NP) void seq_backward(
             const long o = ((long)(bb * Tn + t0 + u) * H + h) * N;
             __syncthreads();
             if (lane_ok) {
-                vd[tid] = __expf(log_decay(io<T>::ld(w, o + tid)));
+                vd[tid] = decay_of<MODE>(io<T>::ld(w, o + tid));
                 vk[tid] = io<T>::ld(k, o + tid);
                 va[tid] = io<T>::ld(a, o + tid);
                 vb[tid] = io<T>::ld(b, o + tid);
@@ -167,11 +176,10 @@ __global__ __launch_bounds__(NP) void seq_backward(
             __syncthreads();  // previous column phase done with the vectors / G^T
             if (lane_ok) {
                 const float wv = io<T>::ld(w, o + tid);
-                const float s = sigmoidf_(wv);
-                const float dd = __expf(-DECAY_SCALE * s);
+                const float dd = decay_of<MODE>(wv);
                 vr[tid] = io<T>::ld(r, o + tid);
                 vd[tid] = dd;
-                vf[tid] = dd * (-DECAY_SCALE) * s * (1.f - s);
+                vf[tid] = dw_factor<MODE>(wv, dd);
                 vk[tid] = io<T>::ld(k, o + tid);
                 va[tid] = io<T>::ld(a, o + tid);
                 vb[tid] = io<T>::ld(b, o + tid);
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(NP) void seq_backward(
     if (lane_ok) {
 #pragma unroll
         for (int j = 0; j < NP; j++)
-            if (j < N) ds0[bh * NN + (long)tid * N + j] = g[j];
+            if (j < N) ds0[bh * NN + tid * ei + j * ej] = g[j];
     }
 }
 
@@ -239,19 +247,24 @@ __global__ __launch_bounds__(NP) void seq_backward(
 
 namespace wkv7 {
 
-template <typename T, int NP>
+template <typename T, int NP, int MODE>
 static void seq_forward_t(const Fwd& p) {
-    hipLaunchKernelGGL((seq_forward<T, NP>), dim3(p.B * p.H), dim3(NP), 0, p.stream, p.T, p.H, p.N,
-                       (const T*)p.r, (const T*)p.w, (const T*)p.k, (const T*)p.v, (const T*)p.a,
-                       (const T*)p.b, p.s0, (T*)p.y, p.sT, p.ckpt);
+    hipLaunchKernelGGL((seq_forward<T, NP, MODE>), dim3(p.B * p.H), dim3(NP), 0, p.stream, p.T, p.H, p.N,
+                       (p.flags & FLAG_STATE_KV) ? 1 : 0, (const T*)p.r, (const T*)p.w, (const T*)p.k,
+                       (const T*)p.v, (const T*)p.a, (const T*)p.b, p.s0, (T*)p.y, p.sT, p.ckpt);
+}
+template <typename T, int NP>
+static void seq_forward_m(const Fwd& p) {
+    if (p.flags & FLAG_DECAY_EXP) seq_forward_t<T, NP, MODE_EXP>(p);
+    else seq_forward_t<T, NP, MODE_RWKV>(p);
 }
 
 void launch_seq_forward(const Fwd& p) {
     const bool bf = p.dtype == 0;
     if (p.N <= 64) {
-        if (bf) seq_forward_t<bf16_t, 64>(p); else seq_forward_t<float, 64>(p);
+        if (bf) seq_forward_m<bf16_t, 64>(p); else seq_forward_m<float, 64>(p);
     } else {
-        if (bf) seq_forward_t<bf16_t, 128>(p); else seq_forward_t<float, 128>(p);
+        if (bf) seq_forward_m<bf16_t, 128>(p); else seq_forward_m<float, 128>(p);
     }
 }
 
@@ -259,24 +272,29 @@ size_t seq_backward_workspace(int B, int H, int N) {
     return (size_t)B * H * seq_ws_floats(N) * sizeof(float);
 }
 
-template <typename T, int NP>
+template <typename T, int NP, int MODE>
 static void seq_backward_t(const Bwd& p) {
     const size_t lds = (size_t)(NP * NP + 10 * NP) * sizeof(float);
     if (lds > 65536)  // above the default dynamic-LDS cap; gfx950 has 160 KB per CU
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&seq_backward<T, NP>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&seq_backward<T, NP, MODE>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((seq_backward<T, NP>), dim3(p.B * p.H), dim3(NP), lds, p.stream, p.T, p.H,
-                       p.N, (const T*)p.r, (const T*)p.w, (const T*)p.k, (const T*)p.v,
-                       (const T*)p.a, (const T*)p.b, p.ckpt, (const T*)p.dy, p.dsT, (T*)p.dr,
+    hipLaunchKernelGGL((seq_backward<T, NP, MODE>), dim3(p.B * p.H), dim3(NP), lds, p.stream, p.T, p.H,
+                       p.N, (p.flags & FLAG_STATE_KV) ? 1 : 0, (const T*)p.r, (const T*)p.w, (const T*)p.k,
+                       (const T*)p.v, (const T*)p.a, (const T*)p.b, p.ckpt, (const T*)p.dy, p.dsT, (T*)p.dr,
                        (T*)p.dw, (T*)p.dk, (T*)p.dv, (T*)p.da, (T*)p.db, p.ds0, (float*)p.ws);
+}
+template <typename T, int NP>
+static void seq_backward_m(const Bwd& p) {
+    if (p.flags & FLAG_DECAY_EXP) seq_backward_t<T, NP, MODE_EXP>(p);
+    else seq_backward_t<T, NP, MODE_RWKV>(p);
 }
 
 void launch_seq_backward(const Bwd& p) {
     const bool bf = p.dtype == 0;
     if (p.N <= 64) {
-        if (bf) seq_backward_t<bf16_t, 64>(p); else seq_backward_t<float, 64>(p);
+        if (bf) seq_backward_m<bf16_t, 64>(p); else seq_backward_m<float, 64>(p);
     } else {
-        if (bf) seq_backward_t<bf16_t, 128>(p); else seq_backward_t<float, 128>(p);
+        if (bf) seq_backward_m<bf16_t, 128>(p); else seq_backward_m<float, 128>(p);
     }
 }
 

@@ -1,0 +1,106 @@
+"""Gated delta rule (the GDN layers of the reference's Qwen3.5 teacher) on the WKV7
+kernels in exp-decay mode.
+
+The reference runs its teacher's GDN layers through transformers' torch functions
+(``torch_chunk_gated_delta_rule`` / ``torch_recurrent_gated_delta_rule``, wrapped at
+theseus/hf_model.py:28-52).  Its converter states the same recurrence as a WKV7 call
+(convert_qwen2rwkv_lightning.py:381-385):
+
+    decay d = exp(g), no clamp or sigmoid          ("wkv_decay_operation")
+    r = q/sqrt(Dk), w = g, k = k, v = beta*v, a = k, b = -exp(g)*beta*k   ("wkv_inputs")
+    state [B, Hv, K, V]                            ("gdn_state_layout")
+
+``gated_delta_rule`` maps GDN's inputs that way and calls the HIP kernels through
+``theseus_wkv7_forward_ex`` / ``_backward_ex`` with THESEUS_WKV7_DECAY_EXP and
+THESEUS_WKV7_STATE_KEY_VALUE (no state transpose); the mapping is torch ops, so autograd
+carries the kernels' gradients back to q, k, v, g and beta.  Like transformers'
+functions it computes in float32 (the operands are passed to the kernels as float32)
+and returns the output in the query's dtype.  The state must be square (K == V, the
+kernels' N, 2..128).
+
+``chunk_gated_delta_rule`` and ``recurrent_gated_delta_rule`` have transformers'
+signatures; ``patch_transformers(module)`` installs them into a transformers model
+module (e.g. ``transformers.models.qwen3_5.modeling_qwen3_5``) for CUDA tensors,
+leaving CPU calls to transformers' own functions, as the reference's wrapper does.
+"""
+from __future__ import annotations
+
+import functools
+
+import torch
+
+from .wkv7 import DECAY_EXP, STATE_KEY_VALUE, wkv7_ex
+
+
+def l2norm(x, dim=-1, eps=1e-6):
+    """x * rsqrt(sum(x*x) + eps): the q/k normalisation of GDN layers
+    ("gdn_qk_normalization", convert_qwen2rwkv_lightning.py:381)."""
+    return x * torch.rsqrt((x * x).sum(dim=dim, keepdim=True) + eps)
+
+
+def gated_delta_rule(query, key, value, g, beta, initial_state=None, output_final_state=False,
+                     use_qk_l2norm_in_kernel=False):
+    """query, key [B,T,H,K]; value [B,T,H,V]; g, beta [B,T,H]; initial_state [B,H,K,V]
+    (zeros if None).  Returns (output [B,T,H,V] in query's dtype, final state [B,H,K,V]
+    float32 or None)."""
+    B, T, H, K = query.shape
+    V = value.shape[-1]
+    if K != V or not 2 <= K <= 128:
+        raise ValueError(f"gated_delta_rule on the WKV7 kernels needs K == V in 2..128 (got K={K}, V={V})")
+    if key.shape != query.shape or value.shape[:3] != (B, T, H) or g.shape != (B, T, H) or beta.shape != (B, T, H):
+        raise ValueError("gated_delta_rule: expected query/key [B,T,H,K], value [B,T,H,V], g/beta [B,T,H]")
+    out_dtype = query.dtype
+    if use_qk_l2norm_in_kernel:
+        query, key = l2norm(query), l2norm(key)
+    q, k, v, gf, bf = (x.float() for x in (query, key, value, g, beta))
+    eg = torch.exp(gf)
+    r = q * (K ** -0.5)
+    w = gf.unsqueeze(-1).expand(B, T, H, K).contiguous()
+    vb = v * bf.unsqueeze(-1)
+    b = -(eg * bf).unsqueeze(-1) * k
+    s0 = (torch.zeros(B, H, K, V, device=query.device, dtype=torch.float32) if initial_state is None
+          else initial_state.float().contiguous())
+    y, sT = wkv7_ex(r, w, k, vb, k, b, s0, flags=DECAY_EXP | STATE_KEY_VALUE)
+    return y.to(out_dtype), (sT if output_final_state else None)
+
+
+def _no_varlen(kwargs):
+    if kwargs.get("cu_seqlens") is not None:
+        raise NotImplementedError("packed variable-length sequences (cu_seqlens) are not supported")
+
+
+def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
+                           output_final_state=False, use_qk_l2norm_in_kernel=False, **kwargs):
+    """transformers' ``torch_chunk_gated_delta_rule`` signature (chunk_size is not used)."""
+    _no_varlen(kwargs)
+    return gated_delta_rule(query, key, value, g, beta, initial_state, output_final_state,
+                            use_qk_l2norm_in_kernel)
+
+
+def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state, output_final_state,
+                               use_qk_l2norm_in_kernel=False, **kwargs):
+    """transformers' ``torch_recurrent_gated_delta_rule`` signature."""
+    _no_varlen(kwargs)
+    return gated_delta_rule(query, key, value, g, beta, initial_state, output_final_state,
+                            use_qk_l2norm_in_kernel)
+
+
+def patch_transformers(module):
+    """Route ``module.torch_chunk_gated_delta_rule`` / ``torch_recurrent_gated_delta_rule``
+    to the HIP kernels for CUDA tensors with a square state (K == V <= 128) and no packed
+    sequences (cu_seqlens); any other call goes to the function that was there.  Returns
+    the previous pair."""
+    old = (module.torch_chunk_gated_delta_rule, module.torch_recurrent_gated_delta_rule)
+
+    def route(ours, theirs):
+        @functools.wraps(theirs)
+        def call(query, key, value, *args, **kwargs):
+            if (query.is_cuda and 2 <= query.shape[-1] == value.shape[-1] <= 128
+                    and kwargs.get("cu_seqlens") is None):
+                return ours(query, key, value, *args, **kwargs)
+            return theirs(query, key, value, *args, **kwargs)
+        return call
+
+    module.torch_chunk_gated_delta_rule = route(chunk_gated_delta_rule, old[0])
+    module.torch_recurrent_gated_delta_rule = route(recurrent_gated_delta_rule, old[1])
+    return old

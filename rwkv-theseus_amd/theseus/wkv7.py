@@ -35,6 +35,10 @@ LIB_PATH = Path(__file__).resolve().parent / "libtheseus_wkv7.so"
 
 _BF16, _FP32 = 0, 1
 
+# theseus_wkv7_flags (include/theseus_wkv7.h)
+DECAY_EXP = 1           # d = exp(w), unclamped (the GDN teacher's decay)
+STATE_KEY_VALUE = 2     # states [B,H,key,value] (GDN's layout) instead of [B,H,value,key]
+
 # theseus_wkv7_family codes (include/theseus_wkv7.h) -> why the step-serial kernels run
 _FAMILY_FORCED = 1
 _FALLBACK_REASON = {
@@ -113,6 +117,12 @@ class Extension:
         # forward without a workspace argument (static device scratch; allocates nothing)
         lib.theseus_wkv7_forward_noalloc.argtypes = [i32] * 5 + [vp] * 10 + [vp]
         lib.theseus_wkv7_forward_noalloc.restype = i32
+        lib.theseus_wkv7_forward_ex.argtypes = [i32] * 6 + [vp] * 10 + [vp, sz, vp]
+        lib.theseus_wkv7_forward_ex.restype = i32
+        lib.theseus_wkv7_backward_ex.argtypes = [i32] * 6 + [vp] * 16 + [vp, sz, vp]
+        lib.theseus_wkv7_backward_ex.restype = i32
+        lib.theseus_wkv7_workspace_size_ex.argtypes = [i32] * 7
+        lib.theseus_wkv7_workspace_size_ex.restype = sz
         lib.theseus_wkv7_kernel_family.argtypes = [i32] * 5
         lib.theseus_wkv7_kernel_family.restype = i32
         self.abi_version = lib.theseus_wkv7_abi_version()
@@ -160,8 +170,9 @@ class Extension:
                 raise RuntimeError("input mismatch")
 
     # -- reference-compatible entry points --------------------------------
-    def forward(self, r, w, k, v, a, b, s0, save_history):
-        """-> [y, end, saved]; saved is empty when save_history is False (cpp:16-25)."""
+    def forward(self, r, w, k, v, a, b, s0, save_history, flags=0):
+        """-> [y, end, saved]; saved is empty when save_history is False (cpp:16-25).
+        ``flags`` (DECAY_EXP, STATE_KEY_VALUE) selects theseus_wkv7_forward_ex."""
         self._check(r, (w, k, v, a, b))
         B, T, H, N = r.shape
         if not (s0.device == r.device and s0.dtype == torch.float32 and s0.is_contiguous()):
@@ -177,18 +188,27 @@ class Extension:
             else:
                 saved = torch.empty((0,), dtype=torch.float32, device=r.device)
             dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
-            if T > 1 or save_history:  # (a T=1 step without saved states runs the single-step kernel)
-                self._warn_fallback(B, T, H, N, dt)
-            ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_forward_workspace_size(B, T, H, N, dt)), r.device)
-            status = self.lib.theseus_wkv7_forward(
-                B, T, H, N, dt, *map(_ptr, (r, w, k, v, a, b, s0, y, end)),
-                _ptr(saved) if save_history else ctypes.c_void_p(0), _ptr(ws),
-                ctypes.c_size_t(ws_bytes), _stream(r.device))
+            ck = _ptr(saved) if save_history else ctypes.c_void_p(0)
+            if flags:
+                ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_workspace_size_ex(B, T, H, N, dt, flags, 0)),
+                                          r.device)
+                status = self.lib.theseus_wkv7_forward_ex(
+                    B, T, H, N, dt, flags, *map(_ptr, (r, w, k, v, a, b, s0, y, end)), ck, _ptr(ws),
+                    ctypes.c_size_t(ws_bytes), _stream(r.device))
+            else:
+                if T > 1 or save_history:  # (a T=1 step without saved states runs the single-step kernel)
+                    self._warn_fallback(B, T, H, N, dt)
+                ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_forward_workspace_size(B, T, H, N, dt)),
+                                          r.device)
+                status = self.lib.theseus_wkv7_forward(
+                    B, T, H, N, dt, *map(_ptr, (r, w, k, v, a, b, s0, y, end)), ck, _ptr(ws),
+                    ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)
         return [y, end, saved]
 
-    def backward(self, r, w, k, v, a, b, saved, dy, dend):
-        """-> [dr, dw, dk, dv, da, db, ds0] (cpp:26-37).  dend may be None (zero)."""
+    def backward(self, r, w, k, v, a, b, saved, dy, dend, flags=0):
+        """-> [dr, dw, dk, dv, da, db, ds0] (cpp:26-37).  dend may be None (zero).
+        ``flags`` must be those of the forward that made ``saved``."""
         self._check(r, (w, k, v, a, b, dy))
         B, T, H, N = r.shape
         if not (saved.device == r.device and saved.dtype == torch.float32
@@ -203,12 +223,18 @@ class Extension:
             grads = [torch.empty_like(r) for _ in range(6)]
             ds0 = torch.empty((B, H, N, N), dtype=torch.float32, device=r.device)
             dt = _BF16 if r.dtype == torch.bfloat16 else _FP32
-            self._warn_fallback(B, T, H, N, dt)
-            ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N, dt)), r.device)
-            status = self.lib.theseus_wkv7_backward(
-                B, T, H, N, dt,
-                *map(_ptr, (r, w, k, v, a, b, saved, dy, dend, *grads, ds0, ws)),
-                ctypes.c_size_t(ws_bytes), _stream(r.device))
+            ptrs = map(_ptr, (r, w, k, v, a, b, saved, dy, dend, *grads, ds0))
+            if flags:
+                ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_workspace_size_ex(B, T, H, N, dt, flags, 1)),
+                                          r.device)
+                status = self.lib.theseus_wkv7_backward_ex(B, T, H, N, dt, flags, *ptrs, _ptr(ws),
+                                                           ctypes.c_size_t(ws_bytes), _stream(r.device))
+            else:
+                self._warn_fallback(B, T, H, N, dt)
+                ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N, dt)),
+                                          r.device)
+                status = self.lib.theseus_wkv7_backward(B, T, H, N, dt, *ptrs, _ptr(ws),
+                                                        ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)
         return grads + [ds0]
 
@@ -280,6 +306,40 @@ def wkv7(r, w, k, v, a, b, state, backend="cuda"):
         y, end, _ = extension().forward(*xs, state.float().contiguous(), False)
         return y, end
     return _WKV.apply(r, w, k, v, a, b, state)
+
+
+class _WKVFlags(torch.autograd.Function):
+    """_WKV with theseus_wkv7_flags (the *_ex entry points)."""
+
+    @staticmethod
+    def forward(ctx, flags, r, w, k, v, a, b, state):
+        xs = [x.contiguous() for x in (r, w, k, v, a, b)]
+        y, end, saved = extension().forward(*xs, state.float().contiguous(), True, flags=flags)
+        ctx.save_for_backward(*xs, saved)
+        ctx.flags = flags
+        return y, end
+
+    @staticmethod
+    def backward(ctx, dy, dend):
+        *xs, saved = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(xs[0])
+        dend = None if dend is None else dend.float().contiguous()
+        grads = extension().backward(*xs, saved, dy.to(xs[0].dtype).contiguous(), dend, flags=ctx.flags)
+        return (None,) + tuple(g.to(x.dtype) for g, x in zip(grads[:6], xs)) + (grads[6],)
+
+
+def wkv7_ex(r, w, k, v, a, b, state, flags=0):
+    """``wkv7(..., backend="cuda")`` with theseus_wkv7_flags: DECAY_EXP (d = exp(w),
+    unclamped) and/or STATE_KEY_VALUE (``state`` and the returned state are
+    [B,H,key,value]).  flags=0 is ``wkv7`` itself."""
+    if not r.is_cuda:
+        raise ValueError("CUDA backend requested on CPU; use backend='reference' for tests")
+    if not torch.is_grad_enabled() or not any(x.requires_grad for x in (r, w, k, v, a, b, state)):
+        xs = [x.contiguous() for x in (r, w, k, v, a, b)]
+        y, end, _ = extension().forward(*xs, state.float().contiguous(), False, flags=flags)
+        return y, end
+    return _WKVFlags.apply(flags, r, w, k, v, a, b, state)
 
 
 def decode_step_(r, w, k, v, a, b, state):
