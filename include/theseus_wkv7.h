@@ -91,13 +91,9 @@ int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype);
 
 /* Steps between saved states (16); the saved-state tensor of a T-step
  * forward holds theseus_wkv7_checkpoint_count(T) states
- * [B,H,count,N,N] (4 bytes per element): state after steps 0,16,32,... and,
- * last, the final state after step T (plain float32).  The earlier slots are
- * the library's own encoding (the chunked kernels store each element as a
- * bf16 hi:lo word pair, the operands their backward multiplies with), so the
- * tensor is only meant to be passed back to theseus_wkv7_backward.  Replaces
- * the full [B,H,T+1,N,N] float32 history that kernels/wkv7_state.cpp:21-22
- * allocates. */
+ * [B,H,count,N,N] float32: state after steps 0,16,32,... and, last, the final
+ * state after step T.  Replaces the full [B,H,T+1,N,N] history that
+ * kernels/wkv7_state.cpp:21-22 allocates. */
 int theseus_wkv7_checkpoint_interval(void);
 long long theseus_wkv7_checkpoint_count(int T);
 

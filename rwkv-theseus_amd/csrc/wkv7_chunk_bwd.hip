@@ -33,10 +33,6 @@
 //    chunk's three phases in sequence; phase 0 may not write the slot (the
 //    consumers still read it in that tick), so the operands of the first 32
 //    keys it computes wait in registers until phase 1.
-//  * Saved states arrive split (the forward stores each element as a word with
-//    the bf16 hi part in the upper and the lo part in the lower half; the last
-//    slot, the final state, is plain fp32): the S side forms its operand pairs
-//    from them with byte permutes.
 //  * Consumers, 8 waves in two sides.  The H side (waves 0-3: wave c owns value
 //    rows 16c..16c+15 of H = dL/dS in registers) forms H', Q and the first part
 //    of dV in stage B and publishes H' and Q^T rows; the S side (waves 4-7, the
@@ -145,14 +141,6 @@ __device__ __forceinline__ bool consumer_sync(uint32_t* cnt, uint32_t target) {
 __device__ __forceinline__ f32x4_t nan4() {
     const float x = __builtin_nanf("");
     return f32x4_t{x, x, x, x};
-}
-// Saved words (element = bf16 hi << 16 | bf16 lo) of elements 0..3 (a) and 4..7 (b) ->
-// the packed hi and lo operand fragments of the 8 elements (as pack8 makes them)
-__device__ __forceinline__ void unpack_words(uint4 a, uint4 b, uint4& hi, uint4& lo) {
-    hi = make_uint4(__builtin_amdgcn_perm(a.y, a.x, 0x07060302u), __builtin_amdgcn_perm(a.w, a.z, 0x07060302u),
-                    __builtin_amdgcn_perm(b.y, b.x, 0x07060302u), __builtin_amdgcn_perm(b.w, b.z, 0x07060302u));
-    lo = make_uint4(__builtin_amdgcn_perm(a.y, a.x, 0x05040100u), __builtin_amdgcn_perm(a.w, a.z, 0x05040100u),
-                    __builtin_amdgcn_perm(b.y, b.x, 0x05040100u), __builtin_amdgcn_perm(b.w, b.z, 0x05040100u));
 }
 // split-precision K=32 product (both operands split)
 __device__ __forceinline__ f32x4_t mm32s(uint4 ah, uint4 al, uint4 bh, uint4 bl) {
@@ -673,10 +661,10 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         }
     } else {
         // ======================= S side: rows i_own of S0; key strip j_own: dR, dA, dw =======================
-        // the next chunk's saved state (hi:lo words) as rows (same layout as Ht) and as the
-        // key strip, S0s[m] = S0[32(m/8) + 16((m/4)%2) + 4q + m%4][j_own], loaded a tick ahead
-        uint4 S0n[4];
-        uint32_t S0s[16];
+        // the next chunk's saved state as rows (same layout as Ht) and as the key strip,
+        // S0s[m] = S0[32(m/8) + 16((m/4)%2) + 4q + m%4][j_own], loaded a tick ahead
+        f32x4_t S0n[4];
+        float S0s[16];
         float carry = 0.f;  // the dlogd carry for key j_own
         bool bad = false;   // a rendezvous timed out: every later output is NaN
         // buffer loads from a head's saved states: one lane offset, the rest in
@@ -686,14 +674,14 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             const uint32_t vo = (uint32_t)((i_own * NK + 4 * q) * 4), so = (uint32_t)(cc * NN * 4);
 #pragma unroll
             for (int tj = 0; tj < 4; tj++)
-                S0n[tj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ckr, vo + 64 * tj, so, 0));
+                S0n[tj] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ckr, vo + 64 * tj, so, 0));
         };
         auto load_strip = [&](__amdgpu_buffer_rsrc_t ckr, int cc) {
             const uint32_t vo = (uint32_t)((4 * q * NK + j_own) * 4);
 #pragma unroll
             for (int m = 0; m < 16; m++)
-                S0s[m] = __builtin_amdgcn_raw_buffer_load_b32(
-                    ckr, vo + (m & 3) * NK * 4, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0);
+                S0s[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    ckr, vo + (m & 3) * NK * 4, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0));
         };
         // The previous tick's chunk (stream index np) is completed a tick late, once the H
         // side's dlogd terms of it are published: this side's terms zp, tp, its fw and its
@@ -767,8 +755,14 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 f32x4_t x1 = zero4();
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
+                    float sv[8];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        sv[e] = S0n[2 * s][e];
+                        sv[4 + e] = S0n[2 * s + 1][e];
+                    }
                     uint4 sbh, sbl;
-                    unpack_words(S0n[2 * s], S0n[2 * s + 1], sbh, sbl);
+                    pack8(sv, sbh, sbl);
                     const uint4 ah = fragp_sw<SwLane>(S.At[0], r16, 32 * s, lane), al = fragp_sw<SwLane>(S.At[1], r16, 32 * s, lane);
                     x1 = mma32(x1, ah, sbh);
                     x1 = mma32(x1, ah, sbl);
@@ -788,9 +782,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
             strip_fw(S, st);
             uint4 oh[2], ol[2];  // this chunk's saved-state strip (loaded a tick ago)
 #pragma unroll
-            for (int s = 0; s < 2; s++)
-                unpack_words(make_uint4(S0s[8 * s], S0s[8 * s + 1], S0s[8 * s + 2], S0s[8 * s + 3]),
-                             make_uint4(S0s[8 * s + 4], S0s[8 * s + 5], S0s[8 * s + 6], S0s[8 * s + 7]), oh[s], ol[s]);
+            for (int s = 0; s < 2; s++) pack8(&S0s[8 * s], oh[s], ol[s]);
             // the next chunk's state, a tick ahead: strip, then rows.  The memory counter is
             // in order, so this strip must be consumed before they are issued (or using it
             // would wait for them too): the asm pins that order.

@@ -40,14 +40,6 @@
 //    chunk x-5).  Their outputs leave in whole 128-byte rows: y through LDS,
 //    stored a tick late by all four waves, and each wave's saved-state rows
 //    regrouped eight at a time.
-//
-// Saved states (for the backward) are stored already split: the state at the
-// start of chunk c goes to slot c as one 32-bit word per element, the bf16 hi
-// part (the fp32 value truncated) in the upper half and the bf16 lo part
-// (the remainder, rounded) in the lower half -- the very operand pair the
-// consumer forms from it for its own products, so storing it costs byte
-// permutes only, and the backward reads its operands without splitting them
-// again.  The last slot (the state after the last step) is plain fp32.
 #include "wkv7_launch.h"
 #include "wkv7_io.h"
 #include "wkv7_sched.h"
@@ -352,6 +344,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 const long off = (long)i_own * NK + 16 * tj + 4 * q;
                 const float4 x = *reinterpret_cast<const float4*>(s0 + bh * NN + off);
                 St[tj] = f32x4_t{x.x, x.y, x.z, x.w};
+                if (ckpt) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + off) = x;
             }
           } else {  // ... else the handoff of boundary m + 1
             const float bad = handoff_wait(flags + m + 1, 4) ? 1.f : __builtin_nanf("");
@@ -368,7 +361,6 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             const int t0 = c * CH, L = min(CH, Tn - t0);
             if (n > 0) y_rows(n - 1);  // the previous tick's y
             f32x4_t sa = zero4(), yy = zero4();
-            uint32_t wd[4][4];  // this chunk's starting state as saved words (hi:lo), [tj][e]
 #pragma unroll
             for (int s = 0; s < 2; s++) {  // K = 64 over keys in two permuted K=32 steps
                 float sv[8];
@@ -379,13 +371,6 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 }
                 uint4 sh, sl;
                 pack8(sv, sh, sl);
-                // dword u of sh / sl holds elements 2u, 2u+1 (low half first): word = hi << 16 | lo
-                const uint32_t hs[4] = {sh.x, sh.y, sh.z, sh.w}, ls[4] = {sl.x, sl.y, sl.z, sl.w};
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    wd[2 * s + (u >> 1)][2 * (u & 1)] = __builtin_amdgcn_perm(hs[u], ls[u], 0x05040100u);
-                    wd[2 * s + (u >> 1)][2 * (u & 1) + 1] = __builtin_amdgcn_perm(hs[u], ls[u], 0x07060302u);
-                }
                 const uint4 pah = fragp_sw<SwLane>(S.P[0], r16, 32 * s, lane), pal = fragp_sw<SwLane>(S.P[1], r16, 32 * s, lane);
                 const uint4 p2h = fragp_sw<SwLane>(S.P2[0], r16, 32 * s, lane), p2l = fragp_sw<SwLane>(S.P2[1], r16, 32 * s, lane);
                 sa = mma32(sa, pah, sh);
@@ -421,16 +406,16 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 quad_rows_bf16(yy, lane);
             yrow0 = (uint32_t)(((long)(bb * Tn + t0) * H + h) * NK * 2);
             yL = L;
-            if (ckpt) {  // slot c (saved words): this wave's rows, 8 at a time through sq, 4 whole rows per store
+            if (ckpt) {  // S_{c+1}: this wave's rows, 8 at a time through sq, 4 whole rows per store
                 float* const sq = sm.sq[cw];
-                float* const dst = ckpt + (bh * ncp + c) * NN + (long)(16 * cw) * NK;
+                float* const dst = ckpt + (bh * ncp + c + 1) * NN + (long)(16 * cw) * NK;
 #pragma unroll
                 for (int p = 0; p < 2; p++) {
                     if ((r16 >> 3) == p) {
 #pragma unroll
                         for (int tj = 0; tj < 4; tj++)
-                            *reinterpret_cast<uint4*>(sq + (r16 & 7) * LDR + 16 * tj + 4 * q) =
-                                make_uint4(wd[tj][0], wd[tj][1], wd[tj][2], wd[tj][3]);
+                            *reinterpret_cast<float4*>(sq + (r16 & 7) * LDR + 16 * tj + 4 * q) =
+                                make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
                     }
 #pragma unroll
                     for (int u = 0; u < 2; u++) {
@@ -441,17 +426,12 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             }
             lds_barrier();
           }
-          // the final state (also the last saved slot, plain fp32), or the handoff at boundary m
+          // the final state, or the handoff at boundary m
 #pragma unroll
           for (int tj = 0; tj < 4; tj++) {
               const long off = (long)i_own * NK + 16 * tj + 4 * q;
-              const float4 x = make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
-              if (sg.handoff) {
-                  handoff_put4(hand + m * NN + off, x.x, x.y, x.z, x.w);
-              } else {
-                  *reinterpret_cast<float4*>(sT + bh * NN + off) = x;
-                  if (ckpt) *reinterpret_cast<float4*>(ckpt + (bh * ncp + ncp - 1) * NN + off) = x;
-              }
+              if (sg.handoff) handoff_put4(hand + m * NN + off, St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+              else *reinterpret_cast<float4*>(sT + bh * NN + off) = make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
           }
           if (sg.handoff) handoff_signal(flags + m);
         }
