@@ -267,9 +267,11 @@ def bench_optim(args, cfg):
 
 def bench_gdn(args, cfg):
     """GDN forward (no grad) and forward+backward at B=1, T=2048, H=32, K=V=128, bf16 q/k/v
-    with the layers' in-kernel q/k L2 norm, through theseus.gdn (the WKV7 step-serial
-    kernels in exp-decay mode, N=128), beside transformers' torch_chunk_gated_delta_rule
-    (its torch fallback, the function the reference's teacher runs without FLA)."""
+    with the layers' in-kernel q/k L2 norm, through theseus.gdn: the forward on the chunked
+    MFMA kernels (theseus_gdn_forward: gdn_prep, gdn_scan), forward+backward on the WKV7
+    step-serial kernels in exp-decay mode; beside transformers' torch_chunk_gated_delta_rule
+    (its torch fallback, the function the reference's teacher runs without FLA) and the
+    step-serial forward of the same call."""
     import inspect
 
     import torch
@@ -310,23 +312,51 @@ def bench_gdn(args, cfg):
         with torch.no_grad():
             hf_chunk(q, k, v, gg, beta, initial_state=s0, output_final_state=True, use_qk_l2norm_in_kernel=True)
 
+    # the kernels alone (fp32 operands prepared as the drop-in prepares them), and the same
+    # forward on the step-serial WKV7 kernels (the path used before the chunked one)
+    from theseus import wkv7 as W
+    qn, kn = (gdn.l2norm(x).float().contiguous() for x in (q, k))
+    vf, gf, bf = v.float().contiguous(), gg.float().contiguous(), beta.float().contiguous()
+    ext = W.extension()
+    st = torch.cuda.current_stream()
+
+    def kernels_ms(n_rep):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ext.gdn_forward(qn, kn, vf, gf, bf, s0)
+        torch.cuda.synchronize()
+        ev[0].record(st)
+        for _ in range(n_rep):
+            ext.gdn_forward(qn, kn, vf, gf, bf, s0)
+        ev[1].record(st)
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / n_rep
+
+    def serial_fwd():
+        with torch.no_grad():
+            W.wkv7_ex(qn * N ** -0.5, gf.unsqueeze(-1).expand(B, T, H, N).contiguous(), kn,
+                      vf * bf.unsqueeze(-1), kn, -(torch.exp(gf) * bf).unsqueeze(-1) * kn, s0,
+                      flags=W.DECAY_EXP | W.STATE_KEY_VALUE)
+
     n = max(2, args.steps // 10)
-    ms = {"ours_fwd": timed(ours_fwd, n), "ours_fwd_bwd": timed(ours_fwd_bwd, n),
+    ms = {"ours_fwd": timed(ours_fwd, n), "ours_fwd_kernels": kernels_ms(n), "ours_fwd_bwd": timed(ours_fwd_bwd, n),
+          "step_serial_fwd": timed(serial_fwd, max(1, n // 2)),
           "transformers_torch_chunk_fwd": timed(hf_fwd, max(1, n // 2))}
-    # compulsory bytes of the forward: q, k, v in (bf16), g, beta in (fp32), out (bf16),
-    # state in and out (fp32)
-    fwd_bytes = B * T * H * N * 2 * 4 + B * T * H * 4 * 2 + 2 * B * H * N * N * 4
-    gbps = fwd_bytes / (ms["ours_fwd"] * 1e-3) / 1e9
+    # compulsory bytes of the two kernels: q, k, v in and o out (fp32), g, beta in (fp32),
+    # state in and out (fp32); the per-chunk operands they pass through the workspace are
+    # not counted
+    fwd_bytes = B * T * H * N * 4 * 4 + B * T * H * 4 * 2 + 2 * B * H * N * N * 4
+    gbps = fwd_bytes / (ms["ours_fwd_kernels"] * 1e-3) / 1e9
     print(json.dumps({
         "metric": "GDN (gated delta rule) forward tokens/s, Qwen3.5 GDN geometry (H=32, K=V=128)",
         "value": round(B * T / (ms["ours_fwd"] * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": n,
         "warmup": 2, "ms_per_step": round(ms["ours_fwd"], 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16 I/O, fp32 compute", "data": "synthetic",
         "config": {"workload": "gdn_forward", "B": B, "T": T, "H": H, "K": N, "V": N,
-                   "kernels": "step-serial WKV7, exp decay, key-value states"},
+                   "kernels": "forward: chunked MFMA GDN (gdn_prep + gdn_scan); fwd+bwd: step-serial WKV7, "
+                              "exp decay, key-value states"},
         "ms_by_impl": {k2: round(v2, 4) for k2, v2 in ms.items()},
         "speedup_vs_transformers_torch_chunk": round(ms["transformers_torch_chunk_fwd"] / ms["ours_fwd"], 2),
-        "roofline": {"kernel": "forward", "bound": "latency (step-serial)", "achieved": round(gbps, 1),
+        "roofline": {"kernel": "forward", "bound": "latency (chunk-to-chunk chain)", "achieved": round(gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                      "traffic": None, "alg_bytes_per_launch": fwd_bytes}}), flush=True)
 

@@ -6,6 +6,7 @@
 // tensors), picks the kernel family, launches on the caller's stream and
 // reports launch failures like C10_CUDA_KERNEL_LAUNCH_CHECK (cpp:24,36).
 #include "../../include/theseus_wkv7.h"
+#include "../../include/theseus_gdn.h"
 
 #include <hip/hip_runtime.h>
 
@@ -202,6 +203,28 @@ int theseus_wkv7_decode_step(int B, int H, int N, int dtype, const void* r, cons
     if (!r || !w || !k || !v || !a || !b || !state || !y) return THESEUS_WKV7_ERR_NULL;
     wkv7::Dec p{B, H, N, dtype, r, w, k, v, a, b, state, state, y, stream};
     wkv7::launch_decode(p);
+    return launch_status();
+}
+
+// The chunked GDN kernels: N = 64 or 128, B*H workgroups (at most 65535 along the
+// operand kernel's grid y), and one head's chunk records under 4 GiB (32-bit DMA offsets).
+static int gdn_dims(int B, int T, int H, int N) {
+    if (B < 1 || H < 1 || T < 1 || (N != 64 && N != 128) || (long long)B * H > 65535) return THESEUS_WKV7_ERR_SHAPE;
+    return wkv7::gdn_forward_workspace(1, T, 1, N) >= (1ull << 32) ? THESEUS_WKV7_ERR_SHAPE : THESEUS_WKV7_OK;
+}
+
+size_t theseus_gdn_forward_workspace_size(int B, int T, int H, int N) {
+    return gdn_dims(B, T, H, N) ? 0 : wkv7::gdn_forward_workspace(B, T, H, N);
+}
+
+int theseus_gdn_forward(int B, int T, int H, int N, const float* q, const float* k, const float* v,
+                        const float* g, const float* beta, const float* s0, float* o, float* sT,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (int e = gdn_dims(B, T, H, N)) return e;
+    if (!q || !k || !v || !g || !beta || !s0 || !o || !sT) return THESEUS_WKV7_ERR_NULL;
+    if (!workspace || workspace_bytes < wkv7::gdn_forward_workspace(B, T, H, N)) return THESEUS_WKV7_ERR_WORKSPACE;
+    wkv7::Gdn p{B, T, H, N, q, k, v, g, beta, s0, o, sT, workspace, 1, stream};
+    wkv7::launch_gdn_forward(p);
     return launch_status();
 }
 

@@ -58,6 +58,22 @@ void launch_chunk_backward(const Bwd& p, int cus);
 size_t chunk_forward_workspace(int B, int T, int H, int cus);
 size_t chunk_backward_workspace(int B, int T, int H, int cus);
 
+// Gated delta rule forward on the chunked MFMA kernels (gdn_chunk.hip): fp32 q, k, v
+// [B,T,H,N], g, beta [B,T,H], states [B,H,key,value] when kv, else [value][key];
+// N = 64 or 128.  The workspace holds every chunk's operands.
+struct Gdn {
+    int B, T, H, N;
+    const float *q, *k, *v, *g, *beta;
+    const float* s0;
+    float* o;
+    float* sT;
+    void* ws;
+    int kv;
+    hipStream_t stream;
+};
+size_t gdn_forward_workspace(int B, int T, int H, int N);
+void launch_gdn_forward(const Gdn& p);
+
 // Family dispatch (wkv7_capi.cpp): the chunked MFMA kernels when they cover
 // the call, else the step-serial ones.
 void launch_forward(const Fwd& p);

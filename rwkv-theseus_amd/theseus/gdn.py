@@ -13,7 +13,9 @@ theseus/hf_model.py:28-52).  Its converter states the same recurrence as a WKV7 
 ``gated_delta_rule`` maps GDN's inputs that way and calls the HIP kernels through
 ``theseus_wkv7_forward_ex`` / ``_backward_ex`` with THESEUS_WKV7_DECAY_EXP and
 THESEUS_WKV7_STATE_KEY_VALUE (no state transpose); the mapping is torch ops, so autograd
-carries the kernels' gradients back to q, k, v, g and beta.  Like transformers'
+carries the kernels' gradients back to q, k, v, g and beta.  When no gradient is wanted
+(the teacher's forward) and the head size is 64 or 128, it runs the chunked MFMA forward
+of the gated delta rule instead (``theseus_gdn_forward``, include/theseus_gdn.h).  Like transformers'
 functions it computes in float32 (the operands are passed to the kernels as float32)
 and returns the output in the query's dtype.  The state must be square (K == V, the
 kernels' N, 2..128).
@@ -29,7 +31,10 @@ import functools
 
 import torch
 
-from .wkv7 import DECAY_EXP, STATE_KEY_VALUE, wkv7_ex
+from .wkv7 import DECAY_EXP, STATE_KEY_VALUE, extension, wkv7_ex
+
+# head sizes of the chunked forward (theseus_gdn_forward); others use the step-serial kernels
+CHUNKED_HEAD_SIZES = (64, 128)
 
 
 def l2norm(x, dim=-1, eps=1e-6):
@@ -53,13 +58,18 @@ def gated_delta_rule(query, key, value, g, beta, initial_state=None, output_fina
     if use_qk_l2norm_in_kernel:
         query, key = l2norm(query), l2norm(key)
     q, k, v, gf, bf = (x.float() for x in (query, key, value, g, beta))
+    s0 = (torch.zeros(B, H, K, V, device=query.device, dtype=torch.float32) if initial_state is None
+          else initial_state.float().contiguous())
+    leaves = (query, key, value, g, beta) + (() if initial_state is None else (initial_state,))
+    if K in CHUNKED_HEAD_SIZES and not (torch.is_grad_enabled() and any(x.requires_grad for x in leaves)):
+        # no gradients wanted (the teacher's case): the chunked MFMA forward
+        o, sT = extension().gdn_forward(*(x.contiguous() for x in (q, k, v, gf, bf)), s0)
+        return o.to(out_dtype), (sT if output_final_state else None)
     eg = torch.exp(gf)
     r = q * (K ** -0.5)
     w = gf.unsqueeze(-1).expand(B, T, H, K).contiguous()
     vb = v * bf.unsqueeze(-1)
     b = -(eg * bf).unsqueeze(-1) * k
-    s0 = (torch.zeros(B, H, K, V, device=query.device, dtype=torch.float32) if initial_state is None
-          else initial_state.float().contiguous())
     y, sT = wkv7_ex(r, w, k, vb, k, b, s0, flags=DECAY_EXP | STATE_KEY_VALUE)
     return y.to(out_dtype), (sT if output_final_state else None)
 

@@ -125,6 +125,11 @@ class Extension:
         lib.theseus_wkv7_workspace_size_ex.restype = sz
         lib.theseus_wkv7_kernel_family.argtypes = [i32] * 5
         lib.theseus_wkv7_kernel_family.restype = i32
+        # chunked gated-delta-rule forward (include/theseus_gdn.h)
+        lib.theseus_gdn_forward.argtypes = [i32] * 4 + [vp] * 8 + [vp, sz, vp]
+        lib.theseus_gdn_forward.restype = i32
+        lib.theseus_gdn_forward_workspace_size.argtypes = [i32] * 4
+        lib.theseus_gdn_forward_workspace_size.restype = sz
         self.abi_version = lib.theseus_wkv7_abi_version()
         self.checkpoint_interval = lib.theseus_wkv7_checkpoint_interval()
 
@@ -205,6 +210,32 @@ class Extension:
                     ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)
         return [y, end, saved]
+
+    def gdn_forward(self, q, k, v, g, beta, s0):
+        """Gated delta rule forward on the chunked kernels (theseus_gdn_forward):
+        q, k, v [B,T,H,N] and g, beta [B,T,H] float32 CUDA tensors (q, k normalised by
+        the caller when the layer does so; q is scaled by 1/sqrt(N) inside), s0
+        [B,H,key,value] float32.  N = 64 or 128.  Returns (o [B,T,H,N], sT) float32."""
+        B, T, H, N = q.shape
+        for x in (q, k, v):
+            if not (x.is_cuda and x.dtype == torch.float32 and x.is_contiguous() and x.shape == q.shape):
+                raise RuntimeError("theseus_gdn: expected contiguous CUDA float32 q, k, v [B,T,H,N]")
+        for x in (g, beta):
+            if not (x.device == q.device and x.dtype == torch.float32 and x.is_contiguous()
+                    and tuple(x.shape) == (B, T, H)):
+                raise RuntimeError("theseus_gdn: expected contiguous float32 g, beta [B,T,H]")
+        if not (s0.device == q.device and s0.dtype == torch.float32 and s0.is_contiguous()
+                and tuple(s0.shape) == (B, H, N, N)):
+            raise RuntimeError("theseus_gdn: expected contiguous float32 initial state [B,H,N,N]")
+        with _on(q.device):
+            o = torch.empty_like(q)
+            sT = torch.empty_like(s0)
+            ws, nbytes = _workspace(self.lib.theseus_gdn_forward_workspace_size(B, T, H, N), q.device)
+            p = lambda t: t.data_ptr()  # noqa: E731
+            self._raise(self.lib.theseus_gdn_forward(
+                B, T, H, N, p(q), p(k), p(v), p(g), p(beta), p(s0), p(o), p(sT),
+                None if ws is None else p(ws), nbytes, _stream(q.device)))
+        return o, sT
 
     def backward(self, r, w, k, v, a, b, saved, dy, dend, flags=0):
         """-> [dr, dw, dk, dv, da, db, ds0] (cpp:26-37).  dend may be None (zero).

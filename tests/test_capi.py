@@ -252,3 +252,25 @@ def test_fused_timemix_covers_only_what_its_grid_addresses():
     assert fused.available(ok, 64)
     assert not fused.available(big, 64) and not fused.available(two, 64)
     assert not fused.available(ok.float(), 64) and not fused.available(ok, 32)
+
+
+def test_gdn_abi_exported_bound_and_validated():
+    """include/theseus_gdn.h: every declared function exported and bound with the header's
+    arity; sizes are checked before anything is enqueued (N must be 64 or 128)."""
+    ext = W.extension()
+    arity = declared_arity(ROOT / "include" / "theseus_gdn.h")
+    assert arity == {"theseus_gdn_forward": 15, "theseus_gdn_forward_workspace_size": 4}
+    for name, n in arity.items():
+        fn = getattr(ext.lib, name)
+        assert fn.argtypes is not None and len(fn.argtypes) == n, (name, n)
+    lib = ext.lib
+    # one record per 16-step chunk: 43264 bytes at N = 128, 22784 at N = 64
+    assert lib.theseus_gdn_forward_workspace_size(1, 2048, 32, 128) == 32 * 128 * 43264
+    assert lib.theseus_gdn_forward_workspace_size(2, 17, 3, 64) == 2 * 3 * 2 * 22784
+    # a head's records must stay under 4 GiB: 99273 chunks of 43264 bytes do, 99274 do not
+    assert lib.theseus_gdn_forward_workspace_size(1, 16 * 99273, 1, 128) == 99273 * 43264
+    assert lib.theseus_gdn_forward_workspace_size(1, 16 * 99274, 1, 128) == 0
+    for B, T, H, N in [(1, 4, 1, 32), (1, 4, 1, 100), (0, 4, 1, 64), (1, 0, 1, 64), (1, 4, 70000, 64)]:
+        assert lib.theseus_gdn_forward_workspace_size(B, T, H, N) == 0
+        assert lib.theseus_gdn_forward(B, T, H, N, *[None] * 8, None, 0, None) == 1
+    assert lib.theseus_gdn_forward(1, 4, 1, 64, *[None] * 8, None, 0, None) == 3  # null pointers

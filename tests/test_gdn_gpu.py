@@ -182,3 +182,49 @@ def test_patched_transformers_gated_deltanet_layer():
         finally:
             M.torch_chunk_gated_delta_rule, M.torch_recurrent_gated_delta_rule = old
     assert rel_l2(got.cpu(), ref.cpu()) <= 1e-4
+
+
+def _chunked_inputs(B, T, H, N, seed, g_scale=1.0):
+    gen = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64)  # noqa: E731
+    q, k = (torch.nn.functional.normalize(rn(B, T, H, N), dim=-1) for _ in range(2))
+    v = rn(B, T, H, N)
+    g = -torch.exp(rn(B, T, H)) * g_scale
+    beta = torch.sigmoid(rn(B, T, H))
+    s0 = .1 * rn(B, H, N, N)
+    return q, k, v, g, beta, s0
+
+
+@pytest.mark.parametrize("B,T,H,N,g_scale", [
+    (1, 1, 2, 64, 1.0), (2, 15, 3, 64, 1.0), (1, 16, 2, 128, 1.0), (2, 45, 2, 128, 1.0),
+    (1, 200, 3, 64, 1.0), (1, 130, 2, 128, 20.0), (1, 77, 2, 128, 0.0),
+])
+def test_chunked_gdn_forward_against_oracle(B, T, H, N, g_scale):
+    """theseus_gdn_forward (the chunked MFMA forward) against the float64 oracle's gated delta
+    rule: tails, one step, both head sizes, ordinary decays, decays of e^{-20 e^x} per step
+    (the state forgets within a step or two) and no decay.  Bar: the fp32-I/O bar, rel-L2
+    <= 1e-4 on o and on the final state, max-abs <= 2e-2 on the state."""
+    q, k, v, g, beta, s0 = _chunked_inputs(B, T, H, N, seed=T * 7 + N + int(g_scale), g_scale=g_scale)
+    print(f"  chunked gdn B={B} T={T} H={H} N={N} g_scale={g_scale}", flush=True)
+    ext = W.extension()
+    o, sT = ext.gdn_forward(*(x.float().cuda().contiguous() for x in (q, k, v, g, beta, s0)))
+    torch.cuda.synchronize()
+    ry, rs = O.gdn_forward(*(x.float().double().numpy() for x in (q, k, v, g, beta, s0)))
+    go, gs = o.double().cpu().numpy(), sT.double().cpu().numpy()
+    print(f"    o rel_l2={rel_l2(go, ry):.2e}  sT rel_l2={rel_l2(gs, rs):.2e} max_abs={max_abs(gs, rs):.2e}",
+          flush=True)
+    assert np.isfinite(go).all() and np.isfinite(gs).all()
+    assert rel_l2(go, ry) <= 1e-4 and rel_l2(gs, rs) <= 1e-4 and max_abs(gs, rs) <= 2e-2
+
+
+def test_chunked_gdn_matches_the_step_serial_path():
+    """No-grad calls of theseus.gdn take the chunked forward, calls that need gradients the
+    WKV7 kernels in exp mode: the two agree (both fp32 I/O, different summation orders)."""
+    B, T, H, N = 1, 100, 4, 128
+    q, k, v, g, beta, s0 = (x.float().cuda() for x in _chunked_inputs(B, T, H, N, seed=11))
+    with torch.no_grad():
+        o1, s1 = gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0, output_final_state=True)
+    leaves = [x.clone().requires_grad_() for x in (q, k, v, g, beta, s0)]
+    o2, s2 = gdn.chunk_gated_delta_rule(*leaves[:5], initial_state=leaves[5], output_final_state=True)
+    assert rel_l2(o1.cpu(), o2.detach().cpu()) <= 1e-4
+    assert rel_l2(s1.cpu(), s2.detach().cpu()) <= 1e-4
