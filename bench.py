@@ -312,8 +312,8 @@ def bench_gdn(args, cfg):
         with torch.no_grad():
             hf_chunk(q, k, v, gg, beta, initial_state=s0, output_final_state=True, use_qk_l2norm_in_kernel=True)
 
-    # the kernels alone (fp32 operands prepared as the drop-in prepares them), and the same
-    # forward on the step-serial WKV7 kernels (the path used before the chunked one)
+    # the kernels alone (the drop-in's own call: bf16 q/k/v, in-kernel q/k norm), and the
+    # same forward on the step-serial WKV7 kernels (the path used before the chunked one)
     from theseus import wkv7 as W
     qn, kn = (gdn.l2norm(x).float().contiguous() for x in (q, k))
     vf, gf, bf = v.float().contiguous(), gg.float().contiguous(), beta.float().contiguous()
@@ -322,11 +322,11 @@ def bench_gdn(args, cfg):
 
     def kernels_ms(n_rep):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        ext.gdn_forward(qn, kn, vf, gf, bf, s0)
+        ext.gdn_forward(q, k, v, gf, bf, s0, qk_l2norm=True)
         torch.cuda.synchronize()
         ev[0].record(st)
         for _ in range(n_rep):
-            ext.gdn_forward(qn, kn, vf, gf, bf, s0)
+            ext.gdn_forward(q, k, v, gf, bf, s0, qk_l2norm=True)
         ev[1].record(st)
         torch.cuda.synchronize()
         return ev[0].elapsed_time(ev[1]) / n_rep
@@ -341,10 +341,10 @@ def bench_gdn(args, cfg):
     ms = {"ours_fwd": timed(ours_fwd, n), "ours_fwd_kernels": kernels_ms(n), "ours_fwd_bwd": timed(ours_fwd_bwd, n),
           "step_serial_fwd": timed(serial_fwd, max(1, n // 2)),
           "transformers_torch_chunk_fwd": timed(hf_fwd, max(1, n // 2))}
-    # compulsory bytes of the two kernels: q, k, v in and o out (fp32), g, beta in (fp32),
+    # compulsory bytes of the two kernels: q, k, v in and o out (bf16), g, beta in (fp32),
     # state in and out (fp32); the per-chunk operands they pass through the workspace are
     # not counted
-    fwd_bytes = B * T * H * N * 4 * 4 + B * T * H * 4 * 2 + 2 * B * H * N * N * 4
+    fwd_bytes = B * T * H * N * 2 * 4 + B * T * H * 4 * 2 + 2 * B * H * N * N * 4
     gbps = fwd_bytes / (ms["ours_fwd_kernels"] * 1e-3) / 1e9
     print(json.dumps({
         "metric": "GDN (gated delta rule) forward tokens/s, Qwen3.5 GDN geometry (H=32, K=V=128)",

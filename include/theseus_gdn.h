@@ -9,9 +9,8 @@
  *   S_t = e^{g_t} S_{t-1} + beta_t k_t (v_t - e^{g_t} S_{t-1}^T k_t)^T,
  *   o_t = S_t^T q_t / sqrt(N)                  (S: [key][value], N = K = V)
  *
- * q and k are used as given (L2-normalise them first when the layer does,
- * use_qk_l2norm_in_kernel); q is scaled by 1/sqrt(N) inside.  Forward only, no
- * saved states: the reference's teacher runs these layers without gradients.
+ * q is scaled by 1/sqrt(N) inside.  Forward only, no saved states: the reference's
+ * teacher runs these layers without gradients.
  * Status codes are those of theseus_wkv7.h.
  */
 #ifndef THESEUS_GDN_H
@@ -26,17 +25,20 @@ extern "C" {
 typedef struct ihipStream_t* hipStream_t;
 
 /* Chunked gated delta rule forward on the caller's stream.
- *   q, k, v  [B,T,H,N] float32 contiguous     g, beta  [B,T,H] float32
- *   s0, sT   [B,H,N(key),N(value)] float32     o        [B,T,H,N] float32
+ *   q, k, v, o  [B,T,H,N] contiguous, all of dtype (theseus_wkv7_dtype: BF16 or FP32;
+ *               arithmetic is float32 either way, as in transformers' functions)
+ *   g, beta     [B,T,H] float32          s0, sT  [B,H,N(key),N(value)] float32
+ *   qk_l2norm   nonzero: q and k are L2-normalised first, x / sqrt(sum x^2 + 1e-6)
+ *               (use_qk_l2norm_in_kernel); zero: used as given
  *   N = 64 or 128 (else THESEUS_WKV7_ERR_SHAPE); workspace of
  *   theseus_gdn_forward_workspace_size bytes (every 16-step chunk's operands,
- *   35 KB per chunk at N = 128), not shared with a call that can run at the
+ *   42 KB per chunk at N = 128), not shared with a call that can run at the
  *   same time.  Replaces the forward of transformers' torch_chunk_gated_delta_rule
  *   (chunk_size is not used) and torch_recurrent_gated_delta_rule. */
-int theseus_gdn_forward(int B, int T, int H, int N, const float* q, const float* k,
-                        const float* v, const float* g, const float* beta, const float* s0,
-                        float* o, float* sT, void* workspace, size_t workspace_bytes,
-                        hipStream_t stream);
+int theseus_gdn_forward(int B, int T, int H, int N, int dtype, int qk_l2norm, const void* q,
+                        const void* k, const void* v, const float* g, const float* beta,
+                        const float* s0, void* o, float* sT, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
 /* Workspace bytes of theseus_gdn_forward (0 for invalid sizes). */
 size_t theseus_gdn_forward_workspace_size(int B, int T, int H, int N);
 

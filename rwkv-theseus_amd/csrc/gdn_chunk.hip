@@ -54,7 +54,13 @@ struct GdnRec {
 };
 static_assert(GdnRec<128>::BYTES % 256 == 0 && GdnRec<64>::BYTES % 256 == 0, "record alignment");
 
+// four consecutive elements as float
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 ld4(const bf16_t* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
 
 // LDS DMA of 1 KB: lane l moves 16 bytes from the buffer at soff + voff to lds_off + 16 l
 // (lds_off: byte address in LDS, made scalar for M0).  Issued from inline asm like
@@ -72,11 +78,13 @@ __device__ __forceinline__ void dma_kb(uint32_t lds_off, i32x4_t rs, uint32_t vo
 // Operands of chunk blockIdx.x of head blockIdx.y (one wave).
 // Lane (q4, r16) holds token t = r16's keys of K-step ks in the permuted K=32
 // order (32ks + 4q4 + e, then 32ks + 16 + 4q4 + e), and D-layout tiles with
-// rows 4q4 + e, column r16.
+// rows 4q4 + e, column r16.  q, k, v are float32 or bfloat16 (TI); with qk_norm, q
+// and k are L2-normalised here, x / sqrt(sum x^2 + 1e-6) as the layers do it
+// (use_qk_l2norm_in_kernel).
 // ---------------------------------------------------------------------------
-template <int NK>
-__global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, const float* __restrict__ q,
-                                               const float* __restrict__ k, const float* __restrict__ v,
+template <int NK, typename TI>
+__global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const TI* __restrict__ q,
+                                               const TI* __restrict__ k, const TI* __restrict__ v,
                                                const float* __restrict__ g, const float* __restrict__ beta,
                                                uint8_t* __restrict__ ws) {
     using R = GdnRec<NK>;
@@ -88,7 +96,7 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, const float* __res
     const long tok0 = (long)bb * Tn + t0;
     auto row = [&](int t) { return ((tok0 + t) * H + h) * (long)NK; };
     const float rs = 1.f / __builtin_sqrtf((float)NK);
-    __shared__ float gsh[3][GC];  // gamma_t, gamma_{t-1}, beta_t (steps past the end: 0)
+    __shared__ float gsh[4][GC];  // gamma_t, gamma_{t-1}, beta_t, k_t's norm factor (past the end: 0)
 
     const bool tv = r16 < L;
     const float gt = tv ? g[(tok0 + r16) * H + h] : 0.f;
@@ -96,29 +104,44 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, const float* __res
     const float gam = row_prefix_sum(gt);
     const float gm1 = row_prev(gam, 0.f);
     const float gL = row_last(gam);
-    if (q4 == 0) {
-        gsh[0][r16] = gam;
-        gsh[1][r16] = gm1;
-        gsh[2][r16] = bt;
-    }
-    // rows of k and q (zero past the end), split; q kept for R~
-    uint4 kh[KS], kl[KS], qh[KS], ql[KS];
-    float qr[KS][8];
+    // rows of k and q (zero past the end); q kept for R~
+    float kr[KS][8], qr[KS][8];
+    float ssk = 0.f, ssq = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-        float kr[8];
         const int c0 = 32 * ks + 4 * q4;
         if (tv) {
             const float4 a = ld4(k + row(r16) + c0), b = ld4(k + row(r16) + c0 + 16);
             const float4 x = ld4(q + row(r16) + c0), y = ld4(q + row(r16) + c0 + 16);
-            kr[0] = a.x, kr[1] = a.y, kr[2] = a.z, kr[3] = a.w, kr[4] = b.x, kr[5] = b.y, kr[6] = b.z, kr[7] = b.w;
+            kr[ks][0] = a.x, kr[ks][1] = a.y, kr[ks][2] = a.z, kr[ks][3] = a.w;
+            kr[ks][4] = b.x, kr[ks][5] = b.y, kr[ks][6] = b.z, kr[ks][7] = b.w;
             qr[ks][0] = x.x, qr[ks][1] = x.y, qr[ks][2] = x.z, qr[ks][3] = x.w;
             qr[ks][4] = y.x, qr[ks][5] = y.y, qr[ks][6] = y.z, qr[ks][7] = y.w;
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) kr[e] = qr[ks][e] = 0.f;
+            for (int e = 0; e < 8; e++) kr[ks][e] = qr[ks][e] = 0.f;
         }
-        pack8(kr, kh[ks], kl[ks]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) ssk += kr[ks][e] * kr[ks][e], ssq += qr[ks][e] * qr[ks][e];
+    }
+    float nk = 1.f, nq = 1.f;  // the rows' L2-norm factors (the four lane groups of a token hold its keys)
+    if (qk_norm) {
+        ssk += __shfl_xor(ssk, 16), ssq += __shfl_xor(ssq, 16);
+        ssk += __shfl_xor(ssk, 32), ssq += __shfl_xor(ssq, 32);
+        nk = __frsqrt_rn(ssk + 1e-6f), nq = __frsqrt_rn(ssq + 1e-6f);
+    }
+    if (q4 == 0) {
+        gsh[0][r16] = gam;
+        gsh[1][r16] = gm1;
+        gsh[2][r16] = bt;
+        gsh[3][r16] = nk;
+    }
+    uint4 kh[KS], kl[KS], qh[KS], ql[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) kr[ks][e] *= nk, qr[ks][e] *= nq;
+        pack8(kr[ks], kh[ks], kl[ks]);
         pack8(qr[ks], qh[ks], ql[ks]);
     }
     // KK[t][s] = k_t.k_s, KR[t][s] = k_t.q_s (contractions over the keys)
@@ -164,7 +187,7 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, const float* __res
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int t = 4 * q4 + e;
-            vv[e] = t < L ? gsh[2][t] * v[row(t) + 16 * rb + r16] : 0.f;
+            vv[e] = t < L ? gsh[2][t] * io<TI>::ld(v, row(t) + 16 * rb + r16) : 0.f;
         }
         const Pk pv = pk(vv);
         uint2* vf = reinterpret_cast<uint2*>(rec + R::VF) + (size_t)(2 * rb) * 64 + lane;
@@ -184,7 +207,7 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, const float* __res
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int t = 4 * q4 + e;
-                const float kv = t < L ? k[row(t) + 16 * tj + r16] : 0.f;
+                const float kv = t < L ? io<TI>::ld(k, row(t) + 16 * tj + r16) * gsh[3][t] : 0.f;
                 at[e] = kv * __expf(gsh[1][t]);
                 bhat[e] = -gsh[2][t] * kv * __expf(gL - gsh[1][t]);
                 khat[e] = kv * __expf(gL - gsh[0][t]);
@@ -211,23 +234,27 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, const float* __res
 }
 
 // ---------------------------------------------------------------------------
-// Each head's chunks in order: wave w keeps value rows 16w .. 16w+15 of the fp32
-// state, St[tj][e] = X[i_own][16tj + 4q4 + e] (as the WKV7 forward's consumers).
-// States s0 / sT are [key][value] when kv (GDN's layout), else [value][key].
-// Records are double-buffered in LDS: chunk c + 1's comes in by DMA (each wave
-// moves every NW-th kilobyte) while chunk c's is read; one barrier per chunk.
+// Each head's chunks in order.  A head's value rows are split over `row groups`
+// (workgroups rg * BH + bh, so that with BH a multiple of 8 a head's groups share an
+// XCD and its L2); wave w of group rg keeps the 16 rows of block rb = rg * NW + w,
+// St[tj][e] = X[i_own][16tj + 4q4 + e] (as the WKV7 forward's consumers).  States
+// s0 / sT are [key][value] when kv (GDN's layout), else [value][key].  Records are
+// double-buffered in LDS: chunk c + 1's comes in by DMA (each wave moves every NW-th
+// kilobyte) while chunk c's is read; one barrier per chunk.
 // ---------------------------------------------------------------------------
-template <int NK>
-__global__ __launch_bounds__(4 * NK) void gdn_scan(int Tn, int H, int kv, const float* __restrict__ s0,
-                                                   float* __restrict__ o, float* __restrict__ sT,
+template <int NK, typename TO>
+__global__ __launch_bounds__(4 * NK) void gdn_scan(int Tn, int H, int BH, int kv, const float* __restrict__ s0,
+                                                   TO* __restrict__ o, float* __restrict__ sT,
                                                    const uint8_t* __restrict__ ws) {
     using R = GdnRec<NK>;
-    constexpr int KS = R::KS, TJ = R::TJ, NW = NK / 16;
+    constexpr int KS = R::KS, TJ = R::TJ;
     __shared__ __attribute__((aligned(1024))) uint8_t recs[2][R::DMA_BLOCKS * 1024];
-    const int bh = blockIdx.x, bb = bh / H, h = bh - bb * H;
+    const int bh = blockIdx.x % BH, rg = blockIdx.x / BH, bb = bh / H, h = bh - bb * H;
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // waves per group (the host launches whole waves, at least one: the DMA loop steps by NW)
+    const int NW = max(1, __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6)));
     const int lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
-    const int i_own = 16 * wv + r16;
+    const int rb = rg * NW + wv, i_own = 16 * rb + r16;
     const long NN = (long)NK * NK, ei = kv ? 1 : NK, ej = kv ? NK : 1;
     const int nchunk = (Tn + GC - 1) / GC;
     // this head's records (the host keeps them under 4 GB, so 32-bit offsets reach them)
@@ -266,7 +293,7 @@ __global__ __launch_bounds__(4 * NK) void gdn_scan(int Tn, int H, int kv, const 
             yy = mma32(mma32(mma32(yy, p2h, sh), p2h, sl), p2l, sh);
         }
         // + Q' V and Q2 V on the K=16 instruction, in their own accumulators
-        const uint2* vf = reinterpret_cast<const uint2*>(rec + R::VF) + (2 * wv) * 64 + lane;
+        const uint2* vf = reinterpret_cast<const uint2*>(rec + R::VF) + (2 * rb) * 64 + lane;
         const uint2 vh = vf[0], vl = vf[64];
         {
             const uint2* qf = reinterpret_cast<const uint2*>(rec + R::QF) + lane;
@@ -277,7 +304,7 @@ __global__ __launch_bounds__(4 * NK) void gdn_scan(int Tn, int H, int kv, const 
 #pragma unroll
         for (int e = 0; e < 4; e++) {  // y[t][i_own], t = 4q4 + e
             const int t = 4 * q4 + e;
-            if (t < L) o[((tok0 + t) * H + h) * NK + i_own] = yy[e];
+            if (t < L) io<TO>::st(o, ((tok0 + t) * H + h) * NK + i_own, yy[e]);
         }
         // X^T <- e^{gamma_L} X^T + [B^^T K^^T] [SA; V]   (K = 32: SA rows, then V rows)
         uint2 sah, sal;
@@ -305,19 +332,28 @@ size_t gdn_forward_workspace(int B, int T, int H, int N) {
     const size_t rec = N == 128 ? GdnRec<128>::BYTES : GdnRec<64>::BYTES;
     return (size_t)B * H * ((T + GC - 1) / GC) * rec;
 }
+// Row groups per head for the scan: groups of four waves (64 value rows).  Measured at
+// B=1, T=2048 (MI355X): N=128 in 2 groups 0.248 ms against 0.279 (1), 0.292 (4) and
+// 0.380 (8); N=64 in 1 group 0.168 ms against 0.192 (2) -- every group moves the whole
+// record into its LDS, and groups of fewer waves wait on that more than they gain.
+static int gdn_row_groups(int N) { return N / 64; }
+template <int NK, typename TI>
+static void launch_gdn(const Gdn& p) {
+    const int nchunk = (p.T + GC - 1) / GC, BH = p.B * p.H;
+    const int rgs = gdn_row_groups(NK), lanes = 64 * (NK / 16) / rgs;
+    hipLaunchKernelGGL((gdn_prep<NK, TI>), dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, p.qk_norm,
+                       static_cast<const TI*>(p.q), static_cast<const TI*>(p.k), static_cast<const TI*>(p.v), p.g,
+                       p.beta, static_cast<uint8_t*>(p.ws));
+    hipLaunchKernelGGL((gdn_scan<NK, TI>), dim3(BH * rgs), dim3(lanes), 0, p.stream, p.T, p.H, BH, p.kv, p.s0,
+                       static_cast<TI*>(p.o), p.sT, static_cast<const uint8_t*>(p.ws));
+}
 void launch_gdn_forward(const Gdn& p) {
-    const int nchunk = (p.T + GC - 1) / GC;
-    const dim3 pg(nchunk, p.B * p.H);
     if (p.N == 128) {
-        hipLaunchKernelGGL(gdn_prep<128>, pg, dim3(64), 0, p.stream, p.T, p.H, p.q, p.k, p.v, p.g, p.beta,
-                           static_cast<uint8_t*>(p.ws));
-        hipLaunchKernelGGL(gdn_scan<128>, dim3(p.B * p.H), dim3(512), 0, p.stream, p.T, p.H, p.kv, p.s0, p.o,
-                           p.sT, static_cast<const uint8_t*>(p.ws));
+        if (p.dtype == 0) launch_gdn<128, bf16_t>(p);
+        else launch_gdn<128, float>(p);
     } else {
-        hipLaunchKernelGGL(gdn_prep<64>, pg, dim3(64), 0, p.stream, p.T, p.H, p.q, p.k, p.v, p.g, p.beta,
-                           static_cast<uint8_t*>(p.ws));
-        hipLaunchKernelGGL(gdn_scan<64>, dim3(p.B * p.H), dim3(256), 0, p.stream, p.T, p.H, p.kv, p.s0, p.o,
-                           p.sT, static_cast<const uint8_t*>(p.ws));
+        if (p.dtype == 0) launch_gdn<64, bf16_t>(p);
+        else launch_gdn<64, float>(p);
     }
 }
 

@@ -217,13 +217,14 @@ size_t theseus_gdn_forward_workspace_size(int B, int T, int H, int N) {
     return gdn_dims(B, T, H, N) ? 0 : wkv7::gdn_forward_workspace(B, T, H, N);
 }
 
-int theseus_gdn_forward(int B, int T, int H, int N, const float* q, const float* k, const float* v,
-                        const float* g, const float* beta, const float* s0, float* o, float* sT,
+int theseus_gdn_forward(int B, int T, int H, int N, int dtype, int qk_l2norm, const void* q, const void* k,
+                        const void* v, const float* g, const float* beta, const float* s0, void* o, float* sT,
                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (int e = gdn_dims(B, T, H, N)) return e;
+    if (dtype != THESEUS_WKV7_BF16 && dtype != THESEUS_WKV7_FP32) return THESEUS_WKV7_ERR_DTYPE;
     if (!q || !k || !v || !g || !beta || !s0 || !o || !sT) return THESEUS_WKV7_ERR_NULL;
     if (!workspace || workspace_bytes < wkv7::gdn_forward_workspace(B, T, H, N)) return THESEUS_WKV7_ERR_WORKSPACE;
-    wkv7::Gdn p{B, T, H, N, q, k, v, g, beta, s0, o, sT, workspace, 1, stream};
+    wkv7::Gdn p{B, T, H, N, dtype, qk_l2norm ? 1 : 0, q, k, v, g, beta, s0, o, sT, workspace, 1, stream};
     wkv7::launch_gdn_forward(p);
     return launch_status();
 }

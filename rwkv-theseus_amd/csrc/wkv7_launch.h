@@ -58,14 +58,16 @@ void launch_chunk_backward(const Bwd& p, int cus);
 size_t chunk_forward_workspace(int B, int T, int H, int cus);
 size_t chunk_backward_workspace(int B, int T, int H, int cus);
 
-// Gated delta rule forward on the chunked MFMA kernels (gdn_chunk.hip): fp32 q, k, v
-// [B,T,H,N], g, beta [B,T,H], states [B,H,key,value] when kv, else [value][key];
-// N = 64 or 128.  The workspace holds every chunk's operands.
+// Gated delta rule forward on the chunked MFMA kernels (gdn_chunk.hip): q, k, v and o
+// [B,T,H,N] in dtype (0 = bf16, 1 = fp32), g, beta [B,T,H] fp32, states [B,H,key,value]
+// when kv, else [value][key]; N = 64 or 128; qk_norm: L2-normalise q and k first.  The
+// workspace holds every chunk's operands.
 struct Gdn {
-    int B, T, H, N;
-    const float *q, *k, *v, *g, *beta;
+    int B, T, H, N, dtype, qk_norm;
+    const void *q, *k, *v;
+    const float *g, *beta;
     const float* s0;
-    float* o;
+    void* o;
     float* sT;
     void* ws;
     int kv;

@@ -55,16 +55,20 @@ def gated_delta_rule(query, key, value, g, beta, initial_state=None, output_fina
     if key.shape != query.shape or value.shape[:3] != (B, T, H) or g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError("gated_delta_rule: expected query/key [B,T,H,K], value [B,T,H,V], g/beta [B,T,H]")
     out_dtype = query.dtype
-    if use_qk_l2norm_in_kernel:
-        query, key = l2norm(query), l2norm(key)
-    q, k, v, gf, bf = (x.float() for x in (query, key, value, g, beta))
     s0 = (torch.zeros(B, H, K, V, device=query.device, dtype=torch.float32) if initial_state is None
           else initial_state.float().contiguous())
     leaves = (query, key, value, g, beta) + (() if initial_state is None else (initial_state,))
     if K in CHUNKED_HEAD_SIZES and not (torch.is_grad_enabled() and any(x.requires_grad for x in leaves)):
-        # no gradients wanted (the teacher's case): the chunked MFMA forward
-        o, sT = extension().gdn_forward(*(x.contiguous() for x in (q, k, v, gf, bf)), s0)
+        # no gradients wanted (the teacher's case): the chunked MFMA forward, which takes
+        # bf16 or fp32 q/k/v as they are and normalises q and k itself
+        io = query.dtype if query.dtype in (torch.bfloat16, torch.float32) else torch.float32
+        q, k, v = (x.to(io).contiguous() for x in (query, key, value))
+        o, sT = extension().gdn_forward(q, k, v, g.float().contiguous(), beta.float().contiguous(), s0,
+                                        qk_l2norm=use_qk_l2norm_in_kernel)
         return o.to(out_dtype), (sT if output_final_state else None)
+    if use_qk_l2norm_in_kernel:
+        query, key = l2norm(query), l2norm(key)
+    q, k, v, gf, bf = (x.float() for x in (query, key, value, g, beta))
     eg = torch.exp(gf)
     r = q * (K ** -0.5)
     w = gf.unsqueeze(-1).expand(B, T, H, K).contiguous()

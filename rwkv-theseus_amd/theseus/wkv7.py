@@ -126,7 +126,7 @@ class Extension:
         lib.theseus_wkv7_kernel_family.argtypes = [i32] * 5
         lib.theseus_wkv7_kernel_family.restype = i32
         # chunked gated-delta-rule forward (include/theseus_gdn.h)
-        lib.theseus_gdn_forward.argtypes = [i32] * 4 + [vp] * 8 + [vp, sz, vp]
+        lib.theseus_gdn_forward.argtypes = [i32] * 6 + [vp] * 8 + [vp, sz, vp]
         lib.theseus_gdn_forward.restype = i32
         lib.theseus_gdn_forward_workspace_size.argtypes = [i32] * 4
         lib.theseus_gdn_forward_workspace_size.restype = sz
@@ -211,15 +211,18 @@ class Extension:
         self._raise(status)
         return [y, end, saved]
 
-    def gdn_forward(self, q, k, v, g, beta, s0):
-        """Gated delta rule forward on the chunked kernels (theseus_gdn_forward):
-        q, k, v [B,T,H,N] and g, beta [B,T,H] float32 CUDA tensors (q, k normalised by
-        the caller when the layer does so; q is scaled by 1/sqrt(N) inside), s0
-        [B,H,key,value] float32.  N = 64 or 128.  Returns (o [B,T,H,N], sT) float32."""
+    def gdn_forward(self, q, k, v, g, beta, s0, qk_l2norm=False):
+        """Gated delta rule forward on the chunked kernels (theseus_gdn_forward): q, k, v
+        [B,T,H,N] CUDA tensors of one dtype (bfloat16 or float32), g, beta [B,T,H] and s0
+        [B,H,key,value] float32; N = 64 or 128.  qk_l2norm: L2-normalise q and k in the
+        kernel (use_qk_l2norm_in_kernel).  q is scaled by 1/sqrt(N) inside.  Returns
+        (o [B,T,H,N] in q's dtype, sT float32)."""
         B, T, H, N = q.shape
+        if q.dtype not in (torch.bfloat16, torch.float32):
+            raise RuntimeError("theseus_gdn: expected bfloat16 or float32 q, k, v")
         for x in (q, k, v):
-            if not (x.is_cuda and x.dtype == torch.float32 and x.is_contiguous() and x.shape == q.shape):
-                raise RuntimeError("theseus_gdn: expected contiguous CUDA float32 q, k, v [B,T,H,N]")
+            if not (x.is_cuda and x.dtype == q.dtype and x.is_contiguous() and x.shape == q.shape):
+                raise RuntimeError("theseus_gdn: expected contiguous CUDA q, k, v [B,T,H,N] of one dtype")
         for x in (g, beta):
             if not (x.device == q.device and x.dtype == torch.float32 and x.is_contiguous()
                     and tuple(x.shape) == (B, T, H)):
@@ -233,8 +236,8 @@ class Extension:
             ws, nbytes = _workspace(self.lib.theseus_gdn_forward_workspace_size(B, T, H, N), q.device)
             p = lambda t: t.data_ptr()  # noqa: E731
             self._raise(self.lib.theseus_gdn_forward(
-                B, T, H, N, p(q), p(k), p(v), p(g), p(beta), p(s0), p(o), p(sT),
-                None if ws is None else p(ws), nbytes, _stream(q.device)))
+                B, T, H, N, _BF16 if q.dtype == torch.bfloat16 else _FP32, 1 if qk_l2norm else 0, p(q), p(k), p(v), p(g), p(beta), p(s0),
+                p(o), p(sT), None if ws is None else p(ws), nbytes, _stream(q.device)))
         return o, sT
 
     def backward(self, r, w, k, v, a, b, saved, dy, dend, flags=0):

@@ -259,7 +259,7 @@ def test_gdn_abi_exported_bound_and_validated():
     arity; sizes are checked before anything is enqueued (N must be 64 or 128)."""
     ext = W.extension()
     arity = declared_arity(ROOT / "include" / "theseus_gdn.h")
-    assert arity == {"theseus_gdn_forward": 15, "theseus_gdn_forward_workspace_size": 4}
+    assert arity == {"theseus_gdn_forward": 17, "theseus_gdn_forward_workspace_size": 4}
     for name, n in arity.items():
         fn = getattr(ext.lib, name)
         assert fn.argtypes is not None and len(fn.argtypes) == n, (name, n)
@@ -272,5 +272,6 @@ def test_gdn_abi_exported_bound_and_validated():
     assert lib.theseus_gdn_forward_workspace_size(1, 16 * 99274, 1, 128) == 0
     for B, T, H, N in [(1, 4, 1, 32), (1, 4, 1, 100), (0, 4, 1, 64), (1, 0, 1, 64), (1, 4, 70000, 64)]:
         assert lib.theseus_gdn_forward_workspace_size(B, T, H, N) == 0
-        assert lib.theseus_gdn_forward(B, T, H, N, *[None] * 8, None, 0, None) == 1
-    assert lib.theseus_gdn_forward(1, 4, 1, 64, *[None] * 8, None, 0, None) == 3  # null pointers
+        assert lib.theseus_gdn_forward(B, T, H, N, 1, 0, *[None] * 8, None, 0, None) == 1
+    assert lib.theseus_gdn_forward(1, 4, 1, 64, 5, 0, *[None] * 8, None, 0, None) == 2  # dtype
+    assert lib.theseus_gdn_forward(1, 4, 1, 64, 0, 1, *[None] * 8, None, 0, None) == 3  # null pointers

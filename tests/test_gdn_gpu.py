@@ -210,6 +210,10 @@ def test_chunked_gdn_forward_against_oracle(B, T, H, N, g_scale):
     o, sT = ext.gdn_forward(*(x.float().cuda().contiguous() for x in (q, k, v, g, beta, s0)))
     torch.cuda.synchronize()
     ry, rs = O.gdn_forward(*(x.float().double().numpy() for x in (q, k, v, g, beta, s0)))
+    if g_scale == 1.0:  # the same through the in-kernel L2 norm of unnormalised q, k
+        o2, s2 = ext.gdn_forward(*(x.float().cuda().contiguous() for x in (3 * q, .5 * k, v, g, beta, s0)),
+                                 qk_l2norm=True)
+        assert rel_l2(o2.cpu(), torch.from_numpy(ry)) <= 1e-4 and rel_l2(s2.cpu(), torch.from_numpy(rs)) <= 1e-4
     go, gs = o.double().cpu().numpy(), sT.double().cpu().numpy()
     print(f"    o rel_l2={rel_l2(go, ry):.2e}  sT rel_l2={rel_l2(gs, rs):.2e} max_abs={max_abs(gs, rs):.2e}",
           flush=True)
@@ -228,3 +232,23 @@ def test_chunked_gdn_matches_the_step_serial_path():
     o2, s2 = gdn.chunk_gated_delta_rule(*leaves[:5], initial_state=leaves[5], output_final_state=True)
     assert rel_l2(o1.cpu(), o2.detach().cpu()) <= 1e-4
     assert rel_l2(s1.cpu(), s2.detach().cpu()) <= 1e-4
+
+
+def test_chunked_gdn_bf16_io_and_in_kernel_norm():
+    """bf16 q/k/v in and o out (the teacher's dtype) with the in-kernel q/k L2 norm, against
+    the float64 oracle on the same bf16 inputs normalised in float64: o within the bf16
+    output bar, the float32 state within the float32 bar."""
+    B, T, H, N = 2, 70, 3, 128
+    gen = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(B, T, H, N, generator=gen).to(torch.bfloat16) for _ in range(3))
+    g = -torch.exp(torch.randn(B, T, H, generator=gen))
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    s0 = .1 * torch.randn(B, H, N, N, generator=gen)
+    o, sT = W.extension().gdn_forward(q.cuda(), k.cuda(), v.cuda(), g.cuda(), beta.cuda(), s0.cuda(),
+                                      qk_l2norm=True)
+    assert o.dtype == torch.bfloat16
+    qn, kn = (gdn.l2norm(x.double()) for x in (q, k))
+    ry, rs = O.gdn_forward(qn.numpy(), kn.numpy(), v.double().numpy(), g.double().numpy(),
+                           beta.double().numpy(), s0.double().numpy())
+    assert rel_l2(o.float().cpu(), torch.from_numpy(ry)) <= 5e-3
+    assert rel_l2(sT.cpu(), torch.from_numpy(rs)) <= 1e-4 and max_abs(sT.cpu(), torch.from_numpy(rs)) <= 2e-2
