@@ -315,89 +315,4 @@ __device__ __forceinline__ void tri_inverse(const f32x4_t& L, const f32x4_t& LT,
     TiT = MT + mm16s(pM, pL8T);
 }
 
-// ---------------------------------------------------------------------------
-// Single-precision-half operands.  A float16 operand (11-bit significand) is 8x
-// finer than bfloat16, so products whose operands stay inside the float16 range
-// need one MFMA, where a bfloat16 pair needs three.  Same lane layouts as the
-// bfloat16 instructions (checked on gfx950 with an in-bounds probe);
-// v_cvt_pk_f16_f32 rounds to nearest even.
-// ---------------------------------------------------------------------------
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ f32x4_t mmh32(f32x4_t acc, uint4 a, uint4 b) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), acc,
-                                                  0, 0, 0);
-}
-__device__ __forceinline__ f32x4_t mmh16(f32x4_t acc, uint2 a, uint2 b) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), acc,
-                                                 0, 0, 0);
-}
-// two floats -> packed float16 pair (element 0 in the low half)
-__device__ __forceinline__ uint32_t h2(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
-}
-__device__ __forceinline__ uint4 h8(const float* x) {
-    return make_uint4(h2(x[0], x[1]), h2(x[2], x[3]), h2(x[4], x[5]), h2(x[6], x[7]));
-}
-__device__ __forceinline__ uint2 h4(const f32x4_t& x) { return make_uint2(h2(x[0], x[1]), h2(x[2], x[3])); }
-// element e of packed float16
-__device__ __forceinline__ float h_el(uint2 u, int e) {
-    const uint32_t w = e < 2 ? u.x : u.y;
-    return (float)__builtin_bit_cast(f16x2_t, w)[e & 1];
-}
-// packed bfloat16 -> packed float16 (exact inside the float16 range)
-__device__ __forceinline__ uint32_t bf2_h2(uint32_t u) {
-    return h2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
-}
-__device__ __forceinline__ uint2 bf4_h4(uint2 u) { return make_uint2(bf2_h2(u.x), bf2_h2(u.y)); }
-// the same, times s
-__device__ __forceinline__ uint2 bf4_h4s(uint2 u, float s) {
-    return make_uint2(h2(__uint_as_float(u.x << 16) * s, __uint_as_float(u.x & 0xffff0000u) * s),
-                      h2(__uint_as_float(u.y << 16) * s, __uint_as_float(u.y & 0xffff0000u) * s));
-}
-// (I - L)^{-1} as in tri_inverse, float16 operands (one MFMA per product; the
-// running products and sums stay float32)
-__device__ __forceinline__ void tri_inverse_h(const f32x4_t& L, const f32x4_t& LT, int lane, f32x4_t& Ti,
-                                              f32x4_t& TiT) {
-    const uint2 pL = h4(L), pLT = h4(LT);
-    const f32x4_t L2 = mmh16(zero4(), pLT, pL), L2T = mmh16(zero4(), pL, pLT);
-    const uint2 pL2 = h4(L2), pL2T = h4(L2T);
-    const f32x4_t L4 = mmh16(zero4(), pL2T, pL2), L4T = mmh16(zero4(), pL2, pL2T);
-    const uint2 pL4 = h4(L4), pL4T = h4(L4T);
-    const uint2 pL8T = h4(mmh16(zero4(), pL4, pL4T));
-    f32x4_t M, MT;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float d = (4 * (lane >> 4) + e) == (lane & 15) ? 1.f : 0.f;
-        M[e] = L[e] + d;
-        MT[e] = LT[e] + d;
-    }
-    uint2 pM = h4(M);
-    M = mmh16(M, pL2T, pM);
-    MT = mmh16(MT, pM, pL2T);
-    pM = h4(M);
-    M = mmh16(M, pL4T, pM);
-    MT = mmh16(MT, pM, pL4T);
-    pM = h4(M);
-    Ti = mmh16(M, pL8T, pM);
-    TiT = mmh16(MT, pM, pL8T);
-}
-// Largest |x| over the wave (every lane gets it): row reductions by DPP, then the
-// four rows by permlane swaps.
-__device__ __forceinline__ float wave_absmax(float x) {
-    x = fabsf(x);
-    x = fmaxf(x, dpp_f<0xb1>(0.f, x));   // quad_perm 1,0,3,2
-    x = fmaxf(x, dpp_f<0x4e>(0.f, x));   // quad_perm 2,3,0,1
-    x = fmaxf(x, dpp_f<0x141>(0.f, x));  // row_half_mirror
-    x = fmaxf(x, dpp_f<0x140>(0.f, x));  // row_mirror
-    const uint32_t u = __float_as_uint(x);
-    const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    x = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
-    const uint32_t v = __float_as_uint(x);
-    const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
-}
-
 }  // namespace wkv7
