@@ -243,7 +243,7 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
 // kilobyte) while chunk c's is read; one barrier per chunk.
 // ---------------------------------------------------------------------------
 template <int NK, typename TO>
-__global__ __launch_bounds__(4 * NK) void gdn_scan(int Tn, int H, int BH, int kv, const float* __restrict__ s0,
+__global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, const float* __restrict__ s0,
                                                    TO* __restrict__ o, float* __restrict__ sT,
                                                    const uint8_t* __restrict__ ws) {
     using R = GdnRec<NK>;
@@ -336,7 +336,7 @@ size_t gdn_forward_workspace(int B, int T, int H, int N) {
 // B=1, T=2048 (MI355X): N=128 in 2 groups 0.248 ms against 0.279 (1), 0.292 (4) and
 // 0.380 (8); N=64 in 1 group 0.168 ms against 0.192 (2) -- every group moves the whole
 // record into its LDS, and groups of fewer waves wait on that more than they gain.
-static int gdn_row_groups(int N) { return N / 64; }
+static int gdn_row_groups(int N) { return N / 64; }  // (256 lanes each: the kernel's bound)
 template <int NK, typename TI>
 static void launch_gdn(const Gdn& p) {
     const int nchunk = (p.T + GC - 1) / GC, BH = p.B * p.H;

@@ -58,7 +58,8 @@ def gated_delta_rule(query, key, value, g, beta, initial_state=None, output_fina
     s0 = (torch.zeros(B, H, K, V, device=query.device, dtype=torch.float32) if initial_state is None
           else initial_state.float().contiguous())
     leaves = (query, key, value, g, beta) + (() if initial_state is None else (initial_state,))
-    if K in CHUNKED_HEAD_SIZES and not (torch.is_grad_enabled() and any(x.requires_grad for x in leaves)):
+    if (K in CHUNKED_HEAD_SIZES and not (torch.is_grad_enabled() and any(x.requires_grad for x in leaves))
+            and extension().lib.theseus_gdn_forward_workspace_size(B, T, H, K) > 0):
         # no gradients wanted (the teacher's case): the chunked MFMA forward, which takes
         # bf16 or fp32 q/k/v as they are and normalises q and k itself
         io = query.dtype if query.dtype in (torch.bfloat16, torch.float32) else torch.float32
