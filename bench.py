@@ -312,6 +312,12 @@ def bench_gdn(args, cfg):
         with torch.no_grad():
             hf_chunk(q, k, v, gg, beta, initial_state=s0, output_final_state=True, use_qk_l2norm_in_kernel=True)
 
+    xh = [t.detach().clone().requires_grad_() for t in (q, k, v, gg, beta, s0)]
+
+    def hf_fwd_bwd():
+        o, st = hf_chunk(*xh[:5], initial_state=xh[5], output_final_state=True, use_qk_l2norm_in_kernel=True)
+        (o.float().sum() + st.sum()).backward()
+
     # the kernels alone (the drop-in's own call: bf16 q/k/v, in-kernel q/k norm), and the
     # same forward on the step-serial WKV7 kernels (the path used before the chunked one)
     from theseus import wkv7 as W
@@ -340,7 +346,8 @@ def bench_gdn(args, cfg):
     n = max(2, args.steps // 10)
     ms = {"ours_fwd": timed(ours_fwd, n), "ours_fwd_kernels": kernels_ms(n), "ours_fwd_bwd": timed(ours_fwd_bwd, n),
           "step_serial_fwd": timed(serial_fwd, max(1, n // 2)),
-          "transformers_torch_chunk_fwd": timed(hf_fwd, max(1, n // 2))}
+          "transformers_torch_chunk_fwd": timed(hf_fwd, max(1, n // 2)),
+          "transformers_torch_chunk_fwd_bwd": timed(hf_fwd_bwd, max(1, n // 2))}
     # compulsory bytes of the two kernels: q, k, v in and o out (bf16), g, beta in (fp32),
     # state in and out (fp32); the per-chunk operands they pass through the workspace are
     # not counted

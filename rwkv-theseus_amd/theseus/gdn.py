@@ -100,18 +100,27 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state, output
                             use_qk_l2norm_in_kernel)
 
 
+def _wants_grad(args, kwargs):
+    return torch.is_grad_enabled() and any(
+        isinstance(x, torch.Tensor) and x.requires_grad for x in list(args) + list(kwargs.values()))
+
+
 def patch_transformers(module):
     """Route ``module.torch_chunk_gated_delta_rule`` / ``torch_recurrent_gated_delta_rule``
-    to the HIP kernels for CUDA tensors with a square state (K == V <= 128) and no packed
-    sequences (cu_seqlens); any other call goes to the function that was there.  Returns
-    the previous pair."""
+    to the HIP kernels for CUDA tensors with a square state (K == V <= 128), no packed
+    sequences (cu_seqlens) and no gradient wanted (the teacher's forward, on the chunked
+    kernels); any other call goes to the function that was there -- with gradients,
+    transformers' own chunked torch function (37 ms forward+backward at B=1, T=2048,
+    H=32, K=V=128 on MI355X) beats the step-serial backward (190 ms).  Returns the
+    previous pair."""
     old = (module.torch_chunk_gated_delta_rule, module.torch_recurrent_gated_delta_rule)
 
     def route(ours, theirs):
         @functools.wraps(theirs)
         def call(query, key, value, *args, **kwargs):
             if (query.is_cuda and 2 <= query.shape[-1] == value.shape[-1] <= 128
-                    and kwargs.get("cu_seqlens") is None):
+                    and kwargs.get("cu_seqlens") is None
+                    and not _wants_grad((query, key, value) + args, kwargs)):
                 return ours(query, key, value, *args, **kwargs)
             return theirs(query, key, value, *args, **kwargs)
         return call

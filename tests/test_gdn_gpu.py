@@ -252,3 +252,24 @@ def test_chunked_gdn_bf16_io_and_in_kernel_norm():
                            beta.double().numpy(), s0.double().numpy())
     assert rel_l2(o.float().cpu(), torch.from_numpy(ry)) <= 5e-3
     assert rel_l2(sT.cpu(), torch.from_numpy(rs)) <= 1e-4 and max_abs(sT.cpu(), torch.from_numpy(rs)) <= 2e-2
+
+
+def test_patch_routes_gradient_calls_to_transformers():
+    """patch_transformers sends no-grad CUDA calls to the chunked kernels and calls that need
+    gradients back to the function it replaced (transformers' own is faster there)."""
+    import types
+    calls = []
+
+    def theirs(query, key, value, g, beta, **kw):
+        calls.append("theirs")
+        return query, None
+
+    mod = types.SimpleNamespace(torch_chunk_gated_delta_rule=theirs, torch_recurrent_gated_delta_rule=theirs)
+    gdn.patch_transformers(mod)
+    q, k, v, g, beta, s0 = _gdn_inputs(1, 20, 2, 64, seed=4)
+    with torch.no_grad():
+        o, _ = mod.torch_chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0)
+    assert calls == [] and o.shape == q.shape
+    qg = q.clone().requires_grad_()
+    mod.torch_chunk_gated_delta_rule(qg, k, v, g, beta, initial_state=s0)
+    assert calls == ["theirs"]
