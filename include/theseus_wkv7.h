@@ -101,9 +101,16 @@ long long theseus_wkv7_checkpoint_count(int T);
  * need for these sizes and dtype on the current device (0 when none).  The
  * chunked kernels use it when B*H heads outnumber the device's CUs: heads are
  * then cut between workgroups, which hand the carried state over through it;
- * the step-serial backward replays each 16-step segment into it.  Contents
- * need not be initialised (each call clears what it uses, on its stream), and
- * a workspace must not be shared by calls that may run at the same time. */
+ * the step-serial backward replays each 16-step segment into it.  For few
+ * heads (chunked kernels, 3*B*H <= CUs, T > 112) the forward size also covers
+ * the time-split forward: a forward without saved states given that much runs
+ * the two halves of every head's steps at once (three workgroups per head)
+ * and joins them with a fix-up kernel, which agrees with the one-pass kernels
+ * to float32 rounding; given less (none is needed at such sizes) it runs the
+ * one-pass kernels.  The split's buffers are 4 * B*H * (3*N*N + N*16*2m)
+ * bytes, m = ceil(ceil(T/16) / 2).  Contents need not be initialised (each
+ * call clears what it uses, on its stream), and a workspace must not be
+ * shared by calls that may run at the same time. */
 size_t theseus_wkv7_forward_workspace_size(int B, int T, int H, int N, int dtype);
 size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtype);
 
@@ -165,8 +172,9 @@ int theseus_wkv7_decode_step(int B, int H, int N, int dtype,
 
 /* Bytes of the library's static device scratch array, which
  * theseus_wkv7_forward_noalloc uses in place of a caller workspace.  8 MiB
- * holds the forward's handoffs for up to ~500 workgroups (a call needs
- * theseus_wkv7_forward_workspace_size bytes: 4.2 MB at most on 256 CUs). */
+ * holds the forward's handoffs for up to ~500 workgroups (4.2 MB at most on
+ * 256 CUs; theseus_wkv7_forward_workspace_size, except at sizes where that
+ * also covers the time-split forward, which the handoffs never need). */
 #define THESEUS_WKV7_NOALLOC_SCRATCH_BYTES (8u << 20)
 
 /* theseus_wkv7_forward without a workspace argument, for callers that cannot
@@ -174,7 +182,9 @@ int theseus_wkv7_decode_step(int B, int H, int N, int dtype,
  * harnesses that forbid hipMalloc).  No counterpart in the reference, whose
  * forward allocates its outputs and history itself (kernels/wkv7_state.cpp:16-25).
  * Same arguments, kernels and results as theseus_wkv7_forward (bitwise), minus
- * workspace/workspace_bytes: the chunked kernels' handoffs go through a static
+ * workspace/workspace_bytes, except that it never takes the time-split path
+ * (it runs the one-pass kernels theseus_wkv7_forward runs when given less
+ * workspace than the split needs): the chunked kernels' handoffs go through a static
  * device array of THESEUS_WKV7_NOALLOC_SCRATCH_BYTES that the library owns (one
  * per device, held until the process ends).  Calls whose sizes need more
  * return THESEUS_WKV7_ERR_SCRATCH without enqueuing anything.  The call

@@ -72,6 +72,17 @@ static int cu_count() {
     return n;
 }
 
+// The time-split forward: few heads (three jobs per head, one CU each) and at least
+// 8 chunks; it needs no saved states and its own workspace (split_ok below).
+static bool split_shape(int B, int T, int H, int N, int dtype, int flags) {
+    return chunk_ok(B, T, H, N, dtype, flags) && (T + kCkptInterval - 1) / kCkptInterval >= 8 &&
+           3ll * B * H <= cu_count();
+}
+static bool split_ok(const Fwd& p) {
+    return !p.ckpt && split_shape(p.B, p.T, p.H, p.N, p.dtype, p.flags) &&
+           p.ws && p.ws_bytes >= chunk_forward_split_workspace(p.B, p.T, p.H);
+}
+
 void launch_forward(const Fwd& p) {
     if (p.T == 1 && !p.ckpt && !force_seq() && !(p.flags & FLAG_STATE_KV)) {
         // one step without saved states (the serving step through the operator):
@@ -79,7 +90,8 @@ void launch_forward(const Fwd& p) {
         Dec d{p.B, p.H, p.N, p.dtype, p.r, p.w, p.k, p.v, p.a, p.b, p.s0, p.sT, p.y, p.stream};
         d.flags = p.flags;
         launch_decode(d);
-    } else if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype, p.flags)) launch_chunk_forward(p, cu_count());
+    } else if (split_ok(p)) launch_chunk_forward_split(p, cu_count());
+    else if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype, p.flags)) launch_chunk_forward(p, cu_count());
     else launch_seq_forward(p);
 }
 void launch_backward(const Bwd& p) {
@@ -90,6 +102,12 @@ void launch_backward(const Bwd& p) {
 // 16-step segment into its workspace (its forward needs none).
 size_t forward_workspace(int B, int T, int H, int N, int dtype, int flags) {
     return chunk_ok(B, T, H, N, dtype, flags) ? chunk_forward_workspace(B, T, H, cu_count()) : 0;
+}
+size_t forward_workspace_fast(int B, int T, int H, int N, int dtype, int flags) {
+    const size_t need = forward_workspace(B, T, H, N, dtype, flags);
+    if (!split_shape(B, T, H, N, dtype, flags)) return need;
+    const size_t split = chunk_forward_split_workspace(B, T, H);
+    return split > need ? split : need;
 }
 size_t backward_workspace(int B, int T, int H, int N, int dtype, int flags) {
     return chunk_ok(B, T, H, N, dtype, flags) ? chunk_backward_workspace(B, T, H, cu_count())
@@ -131,7 +149,7 @@ long long theseus_wkv7_checkpoint_count(int T) {
 
 size_t theseus_wkv7_forward_workspace_size(int B, int T, int H, int N, int dtype) {
     if (check_dims(B, T, H, N, dtype) != THESEUS_WKV7_OK) return 0;
-    return wkv7::forward_workspace(B, T, H, N, dtype);
+    return wkv7::forward_workspace_fast(B, T, H, N, dtype);
 }
 
 size_t theseus_wkv7_backward_workspace_size(int B, int T, int H, int N, int dtype) {
@@ -150,6 +168,7 @@ int theseus_wkv7_forward_ex(int B, int T, int H, int N, int dtype, int flags, co
     if (workspace_bytes < need || (need && !workspace)) return THESEUS_WKV7_ERR_WORKSPACE;
     wkv7::Fwd p{B, T, H, N, dtype, r, w, k, v, a, b, s0, y, sT, ckpt, workspace, stream};
     p.flags = flags;
+    p.ws_bytes = workspace_bytes;
     wkv7::launch_forward(p);
     return launch_status();
 }
@@ -193,7 +212,7 @@ int theseus_wkv7_backward(int B, int T, int H, int N, int dtype, const void* r, 
 size_t theseus_wkv7_workspace_size_ex(int B, int T, int H, int N, int dtype, int flags, int backward) {
     if (check_dims(B, T, H, N, dtype) != THESEUS_WKV7_OK || (flags & ~wkv7::FLAGS_ALL)) return 0;
     return backward ? wkv7::backward_workspace(B, T, H, N, dtype, flags)
-                    : wkv7::forward_workspace(B, T, H, N, dtype, flags);
+                    : wkv7::forward_workspace_fast(B, T, H, N, dtype, flags);
 }
 
 int theseus_wkv7_decode_step(int B, int H, int N, int dtype, const void* r, const void* w,

@@ -109,11 +109,28 @@ __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&
 }
 }  // namespace
 
+// The time-split forward (SPLIT): the state after a chunk is affine in the state before
+// it, so with few heads each head's chunks are halved and the halves run at once, as
+// three jobs per head: run 0 = chunks [0, m) from s0; run 1 = chunks [m, 2m) from a zero
+// state; run 2 = chunks [m, 2m) from the identity with v = 0, whose "y" is z_t = Phi_t r_t
+// and whose final state is the transition Phi of the second half.  split_fixup then
+// forms y_t = y0_t + S_m z_t and sT = S_m Phi + S0_end (wkv7_capi.cpp decides when).
+struct SplitArgs {
+    int BH = 0, m = 0;
+    float* sm = nullptr;     // run 0's final states [BH][64][64]
+    float* s0end = nullptr;  // run 1's final states
+    float* phi = nullptr;    // run 2's final states
+    float* y0 = nullptr;     // run 1's y tiles [BH][m][4 waves][64 lanes][4] float32
+    float* z = nullptr;      // run 2's y tiles, the same layout
+};
+
+template <bool SPLIT>
 __global__ __launch_bounds__(512) void chunk_forward_bf16(
     Sched sc, int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ k, const bf16_t* __restrict__ v, const bf16_t* __restrict__ a,
     const bf16_t* __restrict__ b, const float* __restrict__ s0, bf16_t* __restrict__ y,
-    float* __restrict__ sT, float* __restrict__ ckpt, uint32_t* __restrict__ flags, float* __restrict__ hand) {
+    float* __restrict__ sT, float* __restrict__ ckpt, uint32_t* __restrict__ flags, float* __restrict__ hand,
+    SplitArgs sp) {
     __shared__ FwdLds sm;
     const int m = machine_of_block(sc), nstream = stream_len(sc, m);
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -123,12 +140,19 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     const bool producer = wv < NPROD;
     const int pw = wv, cw = wv - NPROD;
     const long rstride = (long)H * NK;                              // between consecutive tokens of one head
-    const uint32_t tbytes = (uint32_t)((long)sc.J * Tn * NK * 2);  // bytes of one [B,T,H,64] tensor
+    // bytes of one [B,T,H,64] tensor (SPLIT: the schedule's jobs are three per head)
+    const uint32_t tbytes = (uint32_t)((long)(SPLIT ? sp.BH : sc.J) * Tn * NK * 2);
     // stream position (cursor) -> byte offset of the chunk's first row, its valid length
+    // (SPLIT: job j is run j / BH of head j % BH; runs 1 and 2 start at chunk m)
+    auto run_of = [&](int j) { return SPLIT ? j / sp.BH : 0; };
     auto chunk_off = [&](const Cursor& cu) {
-        return (uint32_t)(((long)(cu.bb * Tn + cu.step * CH) * H + cu.h) * NK * 2);
+        if (!SPLIT) return (uint32_t)(((long)(cu.bb * Tn + cu.step * CH) * H + cu.h) * NK * 2);
+        const int run = run_of(cu.j), head = cu.j - run * sp.BH, b2 = head / H, h2 = head - b2 * H;
+        return (uint32_t)(((long)(b2 * Tn + (cu.step + (run ? sp.m : 0)) * CH) * H + h2) * NK * 2);
     };
-    auto chunk_len = [&](const Cursor& cu) { return min(CH, Tn - cu.step * CH); };
+    auto chunk_len = [&](const Cursor& cu) {
+        return min(CH, Tn - (cu.step + (SPLIT && run_of(cu.j) ? sp.m : 0)) * CH);
+    };
 
     // ---------------- producer state ----------------
     uint32_t voff[2];  // this lane's LDS DMA offsets
@@ -233,7 +257,9 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             };
             {   // ---- phase 0: V by LDS DMA; keys 0-31: decays and operands ----
                 vm_wait0();  // this chunk's inputs (LDS DMA issued in the previous chunk's phase 2)
-                stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride, L, lane);
+                // (run 2 of the time split: v = 0)
+                stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride,
+                            SPLIT && run_of(cx.j) == 2 ? 0 : L, lane);
                 float g0[8];
                 decay_scan(0, g0);
                 operands(S, raw, g0, 0);
@@ -336,13 +362,24 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
         };
         for (int j = m * sc.L / sc.n; j <= jlast; j++) {
           const Seg sg = seg_of(sc, m, j);
-          const int bb = j / H, h = j - bb * H;
-          const long bh = j;
+          const int run = SPLIT ? j / sp.BH : 0;           // (SPLIT: the job's run and head)
+          const int head = SPLIT ? j - run * sp.BH : j;
+          const int bb = head / H, h = head - bb * H;
+          const long bh = head;
+          const int c_run = SPLIT && run ? sp.m : 0;      // the run's first chunk
           if (sg.fresh) {  // the initial state: s0 at the head's start ...
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
                 const long off = (long)i_own * NK + 16 * tj + 4 * q;
-                const float4 x = *reinterpret_cast<const float4*>(s0 + bh * NN + off);
+                float4 x;
+                if (!SPLIT || run == 0) {
+                    x = *reinterpret_cast<const float4*>(s0 + bh * NN + off);
+                } else {  // run 1: zero; run 2: the identity
+                    const int c0 = 16 * tj + 4 * q;
+                    const float one = run == 2 ? 1.f : 0.f;
+                    x = make_float4(i_own == c0 ? one : 0.f, i_own == c0 + 1 ? one : 0.f,
+                                    i_own == c0 + 2 ? one : 0.f, i_own == c0 + 3 ? one : 0.f);
+                }
                 St[tj] = f32x4_t{x.x, x.y, x.z, x.w};
                 if (ckpt) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + off) = x;
             }
@@ -357,7 +394,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
           for (int kk = 0; kk < sg.count; kk++, n++) {
             // ---------------- consumer: rows i_own through chunk c of head j ----------------
             const Slot& S = sm.slot[n % NSLOT];
-            const int c = sg.step0 + kk;
+            const int c = sg.step0 + kk + c_run;
             const int t0 = c * CH, L = min(CH, Tn - t0);
             if (n > 0) y_rows(n - 1);  // the previous tick's y
             f32x4_t sa = zero4(), yy = zero4();
@@ -401,11 +438,18 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
                 St[tj] = mma32(mma32(mma32(St[tj] * f32x4_t{el.x, el.y, el.z, el.w}, ah, bhi), ah, blo), al, bhi);
             }
-            // this tick's y into yq (lane (q, 4m + jj): row 4q + jj, values 16cw + 4m .. +3)
-            *reinterpret_cast<uint2*>(&sm.yq[n & 1][(4 * q + (lane & 3)) * NK + 16 * cw + 4 * (r16 >> 2)]) =
-                quad_rows_bf16(yy, lane);
-            yrow0 = (uint32_t)(((long)(bb * Tn + t0) * H + h) * NK * 2);
-            yL = L;
+            if (!SPLIT || run == 0) {
+                // this tick's y into yq (lane (q, 4m + jj): row 4q + jj, values 16cw + 4m .. +3)
+                *reinterpret_cast<uint2*>(&sm.yq[n & 1][(4 * q + (lane & 3)) * NK + 16 * cw + 4 * (r16 >> 2)]) =
+                    quad_rows_bf16(yy, lane);
+                yrow0 = (uint32_t)(((long)(bb * Tn + t0) * H + h) * NK * 2);
+                yL = L;
+            } else {  // runs 1 and 2: float32 tiles for split_fixup in the register layout,
+                      // [head][chunk - m][wave][lane][e] = Y[4q + e][i_own] (1 KB per wave)
+                float* const yd = (run == 1 ? sp.y0 : sp.z) + ((((long)head * sp.m + (c - sp.m)) * 4 + cw) * 64 + lane) * 4;
+                *reinterpret_cast<float4*>(yd) = make_float4(yy[0], yy[1], yy[2], yy[3]);
+                yL = 0;  // (nothing for y_rows)
+            }
             if (ckpt) {  // S_{c+1}: this wave's rows, 8 at a time through sq, 4 whole rows per store
                 float* const sq = sm.sq[cw];
                 float* const dst = ckpt + (bh * ncp + c + 1) * NN + (long)(16 * cw) * NK;
@@ -430,8 +474,9 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
 #pragma unroll
           for (int tj = 0; tj < 4; tj++) {
               const long off = (long)i_own * NK + 16 * tj + 4 * q;
+              float* const dst = !SPLIT || run == 0 ? (SPLIT ? sp.sm : sT) : run == 1 ? sp.s0end : sp.phi;
               if (sg.handoff) handoff_put4(hand + m * NN + off, St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
-              else *reinterpret_cast<float4*>(sT + bh * NN + off) = make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+              else *reinterpret_cast<float4*>(dst + bh * NN + off) = make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
           }
           if (sg.handoff) handoff_signal(flags + m);
         }
@@ -451,9 +496,138 @@ void launch_chunk_forward(const Fwd& p, int cus) {
         hand = reinterpret_cast<float*>(static_cast<char*>(p.ws) + sched_flag_bytes(sc));
         hipLaunchKernelGGL(clear_words, dim3(1), dim3(256), 0, p.stream, flags, sc.G);
     }
-    hipLaunchKernelGGL(chunk_forward_bf16, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
+    hipLaunchKernelGGL(chunk_forward_bf16<false>, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
-                       (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, p.ckpt, flags, hand);
+                       (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, p.ckpt, flags, hand,
+                       SplitArgs{});
+}
+
+// ---------------------------------------------------------------------------
+// Time-split forward without saved states (few heads): one launch of the three runs
+// (3 B*H jobs, one workgroup each: the caller checks 3 B*H <= CUs), then the fix-up.
+// Workspace: S_m, S0_end, Phi ([B*H][64][64] each), y0 and z ([B*H][m][16 * 64]).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int FXG = 4;       // chunks per split_fixup workgroup (one per wave)
+constexpr int FXR = NK + 4;  // padded LDS row (floats)
+// y_t = bf16(y0_t + S_m z_t) over the second half's steps, and sT = S_m Phi + S0_end, on
+// the matrix cores with split-bf16 operands (hi*hi + hi*lo + lo*hi, as in the chunk
+// kernels).  Workgroup (group, head), 4 waves.  Groups below the last: wave w takes
+// chunk 4 group + w: Y[t][i] = y0 + sum_k Z[t][k] S_m[i][k], its z tile turned into rows
+// through the wave's LDS, y0 read straight in the accumulator layout, y out in whole
+// 128-byte rows through LDS.  The last group: wave w takes final-state rows 16w .. 16w+15.
+__global__ __launch_bounds__(256) void split_fixup(int Tn, int H, int m, const float* __restrict__ sm,
+                                                   const float* __restrict__ s0end, const float* __restrict__ phi,
+                                                   const float* __restrict__ y0, const float* __restrict__ z,
+                                                   bf16_t* __restrict__ y, float* __restrict__ sT) {
+    __shared__ float zt[FXG][CH * FXR];      // per wave: its z tile as rows [t][k]
+    __shared__ uint16_t yt[FXG][CH * NK];    // per wave: its y tile [t][i]
+    const int grp = blockIdx.x, ngrp = gridDim.x - 1, head = blockIdx.y, bb = head / H, h = head - bb * H;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int q = lane >> 4, r16 = lane & 15;
+    const long NN = NK * NK;
+    const float* const S = sm + head * NN;
+    // 8 consecutive floats as split-bf16 operand halves
+    auto op8 = [](const float* p, uint4& hi, uint4& lo) {
+        const float4 x0 = *reinterpret_cast<const float4*>(p), x1 = *reinterpret_cast<const float4*>(p + 4);
+        const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        pack8(v, hi, lo);
+    };
+    if (grp < ngrp) {
+        const int c = grp * FXG + w;  // chunk of the second half (wave-uniform)
+        if (c >= m) return;
+        // B operand S_m^T: lane (q, r16) of tile n, K step s holds S_m[16n + r16][32s + 8q .. +7]
+        uint4 bh[4][2], bl[4][2];
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int s = 0; s < 2; s++) op8(S + (16 * n + r16) * NK + 32 * s + 8 * q, bh[n][s], bl[n][s]);
+        // the z tile (float4 u*64 + lane holds Z[4q + e][16u + r16]) into rows
+        const long tile = ((long)head * m + c) * 256;  // float4 index of the chunk's tile
+        float* const zw = zt[w];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float4 x = reinterpret_cast<const float4*>(z)[tile + u * 64 + lane];
+            float* const d = zw + 4 * q * FXR + 16 * u + r16;
+            d[0] = x.x, d[FXR] = x.y, d[2 * FXR] = x.z, d[3 * FXR] = x.w;
+        }
+        wave_lds_fence();
+        uint4 ah[2], al[2];  // A operand Z: lane (q, r16) holds Z[r16][32s + 8q .. +7]
+#pragma unroll
+        for (int s = 0; s < 2; s++) op8(zw + r16 * FXR + 32 * s + 8 * q, ah[s], al[s]);
+        uint16_t* const yw = yt[w];
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const float4 x = reinterpret_cast<const float4*>(y0)[tile + n * 64 + lane];  // y0[4q + e][16n + r16]
+            f32x4_t acc = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                acc = mma32(acc, ah[s], bh[n][s]);
+                acc = mma32(acc, ah[s], bl[n][s]);
+                acc = mma32(acc, al[s], bh[n][s]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) yw[(4 * q + e) * NK + 16 * n + r16] = f32_to_bf16(acc[e]);
+        }
+        wave_lds_fence();
+        // 16 rows of 128 bytes: 8 lanes per row, two rows per lane
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const int rr = 8 * hf + (lane >> 3), pc = lane & 7, tabs = CH * (m + c) + rr;
+            if (tabs < Tn)
+                *reinterpret_cast<uint4*>(y + ((long)(bb * Tn + tabs) * H + h) * NK + 8 * pc) =
+                    *reinterpret_cast<const uint4*>(&yw[rr * NK + 8 * pc]);
+        }
+    } else {
+        // rows i = 16w + 4q + e, columns j = 16n + r16:  sT = S0_end + S_m Phi
+        uint4 ah[2], al[2];  // A operand S_m: lane (q, r16) holds S_m[16w + r16][32s + 8q .. +7]
+#pragma unroll
+        for (int s = 0; s < 2; s++) op8(S + (16 * w + r16) * NK + 32 * s + 8 * q, ah[s], al[s]);
+        const float* const P = phi + head * NN;
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            f32x4_t acc;
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = s0end[head * NN + (16 * w + 4 * q + e) * NK + 16 * n + r16];
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                float v[8];  // B operand Phi: lane (q, r16) holds Phi[32s + 8q .. +7][16n + r16]
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = P[(32 * s + 8 * q + e) * NK + 16 * n + r16];
+                uint4 bh, bl;
+                pack8(v, bh, bl);
+                acc = mma32(acc, ah[s], bh);
+                acc = mma32(acc, ah[s], bl);
+                acc = mma32(acc, al[s], bh);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) sT[head * NN + (16 * w + 4 * q + e) * NK + 16 * n + r16] = acc[e];
+        }
+    }
+}
+}  // namespace
+
+// m = ceil(chunks / 2): runs 1 and 2 end with an empty chunk when the count is odd
+// (its steps are padding, which keeps the state)
+size_t chunk_forward_split_workspace(int B, int T, int H) {
+    const size_t BH = (size_t)B * H, m = ((size_t)(T + CH - 1) / CH + 1) / 2;
+    return BH * (3 * NK * NK + 2 * 16 * m * NK) * sizeof(float);
+}
+void launch_chunk_forward_split(const Fwd& p, int cus) {
+    const int BH = p.B * p.H, m = ((p.T + CH - 1) / CH + 1) / 2;
+    float* const base = static_cast<float*>(p.ws);
+    SplitArgs sp;
+    sp.BH = BH, sp.m = m;
+    sp.sm = base, sp.s0end = base + (size_t)BH * NK * NK, sp.phi = base + 2 * (size_t)BH * NK * NK;
+    sp.y0 = base + 3 * (size_t)BH * NK * NK, sp.z = sp.y0 + (size_t)BH * 16 * m * NK;
+    const Sched sc = plan_schedule(3 * BH, m, cus);  // 3 B*H <= cus: one job per workgroup, no cuts
+    hipLaunchKernelGGL(chunk_forward_bf16<true>, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
+                       (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
+                       (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, nullptr, nullptr,
+                       nullptr, sp);
+    // groups of FXG chunks, then one for the final state; heads along y (at most cus / 3)
+    hipLaunchKernelGGL(split_fixup, dim3((m + FXG - 1) / FXG + 1, BH), dim3(256), 0, p.stream, p.T, p.H, m, sp.sm,
+                       sp.s0end, sp.phi, sp.y0, sp.z, (bf16_t*)p.y, p.sT);
 }
 
 }  // namespace wkv7

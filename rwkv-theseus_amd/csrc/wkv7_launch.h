@@ -20,9 +20,10 @@ struct Fwd {
     void* y;
     float* sT;
     float* ckpt;  // may be null
-    void* ws;     // workspace (the chunked kernels' handoffs)
+    void* ws;     // workspace (the chunked kernels' handoffs; the time split's buffers)
     hipStream_t stream;
     int flags = 0;
+    size_t ws_bytes = 0;  // bytes at ws (0: take no path that needs more than forward_workspace)
 };
 
 struct Bwd {
@@ -57,6 +58,10 @@ void launch_chunk_forward(const Fwd& p, int cus);
 void launch_chunk_backward(const Bwd& p, int cus);
 size_t chunk_forward_workspace(int B, int T, int H, int cus);
 size_t chunk_backward_workspace(int B, int T, int H, int cus);
+// The time-split forward (no saved states, 3 B*H <= cus): the two halves of every head
+// at once, then a fix-up kernel; its workspace holds the halves' states and outputs.
+void launch_chunk_forward_split(const Fwd& p, int cus);
+size_t chunk_forward_split_workspace(int B, int T, int H);
 
 // Gated delta rule forward on the chunked MFMA kernels (gdn_chunk.hip): q, k, v and o
 // [B,T,H,N] in dtype (0 = bf16, 1 = fp32), g, beta [B,T,H] fp32, states [B,H,key,value]
@@ -81,6 +86,8 @@ void launch_gdn_forward(const Gdn& p);
 void launch_forward(const Fwd& p);
 void launch_backward(const Bwd& p);
 size_t forward_workspace(int B, int T, int H, int N, int dtype, int flags = 0);
+// forward_workspace, or more where the time-split forward could take the call
+size_t forward_workspace_fast(int B, int T, int H, int N, int dtype, int flags = 0);
 size_t backward_workspace(int B, int T, int H, int N, int dtype, int flags = 0);
 
 }  // namespace wkv7

@@ -25,6 +25,9 @@ pytestmark = pytest.mark.gpu
 REL_L2 = 5e-3
 MAX_ABS = 2e-2
 REL_L2_FP32 = 1e-4
+# the time-split forward against the one-pass kernels on the same inputs: the two round
+# differently (fp32 fix-up sums against split-bf16 matrix-core products), nothing more
+SPLIT_VS_ONE_PASS = 1e-4
 NAMES = ["y", "sT", "dr", "dw", "dk", "dv", "da", "db", "ds0"]
 
 
@@ -150,10 +153,7 @@ def test_decays_at_the_ends_of_their_range(mode, N):
 
 
 # -- config 1: chunked calls with carried state == one unchunked call ------------------
-def test_config1_chunked_equals_unchunked():
-    inp = wkv7_inputs(1, 4096, 80, 64, seed=20261, dtype=torch.bfloat16)
-    xs = [inp[n].cuda() for n in "rwkvab"]
-    s0 = inp["s0"].cuda()
+def _config1_runs(xs, s0):
     with torch.no_grad():
         y_full, s_full = W.wkv7(*xs, s0)
         s = s0
@@ -161,14 +161,35 @@ def test_config1_chunked_equals_unchunked():
         for c in range(8):
             y, s = W.wkv7(*(x[:, c * 512:(c + 1) * 512].contiguous() for x in xs), s)
             ys.append(y)
-        y_chunk = torch.cat(ys, 1)
     torch.cuda.synchronize()
-    # the 512-step boundaries fall on the 16-step grid: same arithmetic, same bits
-    assert torch.equal(y_chunk, y_full)
-    assert torch.equal(s, s_full)
+    return y_full, s_full, torch.cat(ys, 1), s
+
+
+def test_config1_chunked_equals_unchunked(monkeypatch):
+    """The reference's config-1 check: 8 calls of 512 steps with the state carried give
+    the single 4096-step call's y and final state.  On the one-pass kernels (planned for
+    239 CUs: 80 heads uncut, too many for the time split) the 512-step boundaries fall on
+    the 16-step grid, so the arithmetic and the bits are the same.  The default plan (256
+    CUs) takes the time-split forward for both, split at different steps: each matches
+    the oracle and the one-pass result to rounding."""
+    inp = wkv7_inputs(1, 4096, 80, 64, seed=20261, dtype=torch.bfloat16)
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
     y_ref, s_ref = O.forward_c(*(inp[n].double().numpy() for n in "rwkvab"), inp["s0"].double().numpy())
-    _check("y", y_full, y_ref, torch.bfloat16)
-    _check("sT", s_full, s_ref, torch.bfloat16)
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "239")
+    one = _config1_runs(xs, s0)
+    assert torch.equal(one[2], one[0])
+    assert torch.equal(one[3], one[1])
+    _check("y", one[0], y_ref, torch.bfloat16)
+    _check("sT", one[1], s_ref, torch.bfloat16)
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    split = _config1_runs(xs, s0)
+    for name, got, ref, o in [("y", split[0], y_ref, one[0]), ("sT", split[1], s_ref, one[1]),
+                              ("y", split[2], y_ref, one[0]), ("sT", split[3], s_ref, one[1])]:
+        _check(name, got, ref, torch.bfloat16)
+        rl = rel_l2(got.float().cpu().numpy(), o.float().cpu().numpy())
+        print(f"    {name:4s} split-vs-one-pass rel_l2={rl:.2e}", flush=True)
+        assert rl <= SPLIT_VS_ONE_PASS, (name, rl)
 
 
 # -- config 4: in-place decode ---------------------------------------------------------
@@ -280,7 +301,8 @@ def test_cut_schedule_is_bitwise_the_uncut_one(B, T, H, monkeypatch):
     run bit for bit -- partial chunks (T % 16 != 0) then fall mid-stream."""
     print(f"  cut schedule B={B} T={T} H={H}", flush=True)
     inp = wkv7_inputs(B, T, H, 64, seed=700 + T + H, dtype=torch.bfloat16, s0_std=0.1, with_dsT=True)
-    monkeypatch.setenv("THESEUS_WKV7_CUS", "100000")  # one head per workgroup: nothing cut
+    # one head per workgroup: nothing cut (and too few CUs for the time-split forward)
+    monkeypatch.setenv("THESEUS_WKV7_CUS", str(B * H))
     base = _ext_fwd_bwd(inp)
     names = ["y", "sT", "saved"] + NAMES[2:] + ["y_nograd", "sT_nograd"]
     for cus in (1, 2, 3, 4, 5, 7):
@@ -389,3 +411,72 @@ def test_argument_errors_on_gpu():
     with pytest.raises(RuntimeError, match="invalid dend"):
         ext.backward(x, x, x, x, x, x, torch.zeros(1, 1, 2, 8, 8, device="cuda"), x,
                      torch.zeros(1, 1, 8, 7, device="cuda"))
+
+
+# -- the time-split forward (few heads, no saved states) --------------------------------
+def _capi_forward(lib, xs, s0, ws, ws_bytes):
+    import ctypes
+    B, T, H, N = xs[0].shape
+    y = torch.full((B, T, H, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    sT = torch.full((B, H, N, N), float("nan"), dtype=torch.float32, device="cuda")
+    p = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
+    st = lib.theseus_wkv7_forward(B, T, H, N, 0, *map(p, (*xs, s0, y, sT)), p(None), p(ws),
+                                  ctypes.c_size_t(ws_bytes),
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, lib.theseus_wkv7_error_string(st)
+    torch.cuda.synchronize()
+    return y, sT
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 128, 2), (2, 300, 3), (1, 1000, 5), (3, 512, 4), (1, 113, 1)])
+def test_time_split_forward_against_oracle_and_one_pass(B, T, H, monkeypatch):
+    """With 3*B*H <= CUs and at least 8 chunks, a forward without saved states given
+    theseus_wkv7_forward_workspace_size bytes runs each head's two halves at once
+    (runs from s0, from zero and from the identity) and joins them with the fix-up
+    kernel; given no workspace it runs the one-pass kernels.  Odd chunk counts leave
+    the second half an empty last chunk; partial chunks fall at the end (T % 16)."""
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    N = 64
+    print(f"  time split B={B} T={T} H={H}", flush=True)
+    inp = wkv7_inputs(B, T, H, N, seed=1100 + T + H, dtype=torch.bfloat16, s0_std=0.1)
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
+    lib = W.extension().lib
+    need = int(lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0))
+    m = (-(-T // 16) + 1) // 2
+    assert need == 4 * B * H * (3 * N * N + N * 16 * 2 * m)
+    ws = torch.full((need // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    y_s, s_s = _capi_forward(lib, xs, s0, ws, need)
+    # the split path ran: the first half's final states are in the workspace
+    assert bool(torch.isfinite(ws[:B * H * N * N]).all())
+    y_1, s_1 = _capi_forward(lib, xs, s0, None, 0)
+    y_ref, s_ref = O.forward_c(*(inp[n].double().numpy() for n in "rwkvab"), inp["s0"].double().numpy())
+    for name, got, ref, o in [("y", y_s, y_ref, y_1), ("sT", s_s, s_ref, s_1)]:
+        _check(name, got, ref, torch.bfloat16)
+        rl = rel_l2(got.float().cpu().numpy(), o.float().cpu().numpy())
+        print(f"    {name:4s} split-vs-one-pass rel_l2={rl:.2e}", flush=True)
+        assert rl <= SPLIT_VS_ONE_PASS, (name, rl)
+    # and through the operator: a no-grad call takes the split, a grad call does not
+    with torch.no_grad():
+        y_op, s_op = W.wkv7(*xs, s0)
+    torch.cuda.synchronize()
+    assert torch.equal(y_op, y_s) and torch.equal(s_op, s_s)
+
+
+def test_time_split_is_not_taken_beyond_its_limits(monkeypatch):
+    """Too many heads for three CUs each, fewer than 8 chunks, or saved states
+    requested: the forward workspace is the one-pass kernels' (none here), and the
+    saved-state forward's y and state equal the no-grad one-pass call's bit for bit."""
+    lib = W.extension().lib
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    assert lib.theseus_wkv7_forward_workspace_size(1, 512, 86, 64, 0) == 0   # 258 > 256
+    assert lib.theseus_wkv7_forward_workspace_size(1, 112, 2, 64, 0) == 0    # 7 chunks
+    assert lib.theseus_wkv7_forward_workspace_size(1, 512, 85, 64, 0) > 0
+    assert lib.theseus_wkv7_forward_workspace_size(1, 512, 2, 64, 1) == 0    # fp32: step-serial
+    inp = wkv7_inputs(1, 200, 2, 64, seed=77, dtype=torch.bfloat16, s0_std=0.1)
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
+    ext = W.extension()
+    y_h, s_h, saved = ext.forward(*xs, s0, True)
+    y_1, s_1 = _capi_forward(lib, xs, s0, None, 0)
+    assert torch.equal(y_h, y_1) and torch.equal(s_h, s_1)
