@@ -102,13 +102,14 @@ long long theseus_wkv7_checkpoint_count(int T);
  * chunked kernels use it when B*H heads outnumber the device's CUs: heads are
  * then cut between workgroups, which hand the carried state over through it;
  * the step-serial backward replays each 16-step segment into it.  For few
- * heads (chunked kernels, 3*B*H <= CUs, T > 112) the forward size also covers
- * the time-split forward: a forward without saved states given that much runs
- * the two halves of every head's steps at once (three workgroups per head)
- * and joins them with a fix-up kernel, which agrees with the one-pass kernels
- * to float32 rounding; given less (none is needed at such sizes) it runs the
- * one-pass kernels.  The split's buffers are 4 * B*H * (3*N*N + N*16*2m)
- * bytes, m = ceil(ceil(T/16) / 2).  Contents need not be initialised (each
+ * heads (chunked kernels, 2*B*H <= CUs, T > 112) the forward size also covers
+ * the time-split forward: a forward without saved states given that much cuts
+ * every head's steps into k = min(4, CUs / (B*H)) segments (fewer if the last
+ * would be empty) that run at once, one workgroup each, and chains them with
+ * a fix-up kernel; it agrees with the one-pass kernels to float32 rounding.
+ * Given less (none is needed at such sizes) it runs the one-pass kernels.
+ * The split's buffers are 4 * B*H * ((2k-1)*N*N + 2(k-1)*m*16*N) bytes,
+ * m = ceil(ceil(T/16) / k).  Contents need not be initialised (each
  * call clears what it uses, on its stream), and a workspace must not be
  * shared by calls that may run at the same time. */
 size_t theseus_wkv7_forward_workspace_size(int B, int T, int H, int N, int dtype);

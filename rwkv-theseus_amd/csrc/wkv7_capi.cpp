@@ -72,15 +72,15 @@ static int cu_count() {
     return n;
 }
 
-// The time-split forward: few heads (three jobs per head, one CU each) and at least
-// 8 chunks; it needs no saved states and its own workspace (split_ok below).
+// The time-split forward: few heads (at least two jobs per head, one CU each) and at
+// least 8 chunks; it needs no saved states and its own workspace (split_ok below).
 static bool split_shape(int B, int T, int H, int N, int dtype, int flags) {
     return chunk_ok(B, T, H, N, dtype, flags) && (T + kCkptInterval - 1) / kCkptInterval >= 8 &&
-           3ll * B * H <= cu_count();
+           2ll * B * H <= cu_count() && chunk_forward_split_segments(B * H, T, cu_count()) >= 2;
 }
 static bool split_ok(const Fwd& p) {
-    return !p.ckpt && split_shape(p.B, p.T, p.H, p.N, p.dtype, p.flags) &&
-           p.ws && p.ws_bytes >= chunk_forward_split_workspace(p.B, p.T, p.H);
+    return !p.ckpt && split_shape(p.B, p.T, p.H, p.N, p.dtype, p.flags) && p.ws &&
+           p.ws_bytes >= chunk_forward_split_workspace(p.B, p.T, p.H, cu_count());
 }
 
 void launch_forward(const Fwd& p) {
@@ -106,7 +106,7 @@ size_t forward_workspace(int B, int T, int H, int N, int dtype, int flags) {
 size_t forward_workspace_fast(int B, int T, int H, int N, int dtype, int flags) {
     const size_t need = forward_workspace(B, T, H, N, dtype, flags);
     if (!split_shape(B, T, H, N, dtype, flags)) return need;
-    const size_t split = chunk_forward_split_workspace(B, T, H);
+    const size_t split = chunk_forward_split_workspace(B, T, H, cu_count());
     return split > need ? split : need;
 }
 size_t backward_workspace(int B, int T, int H, int N, int dtype, int flags) {

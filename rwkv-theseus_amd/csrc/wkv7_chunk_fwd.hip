@@ -110,18 +110,22 @@ __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&
 }  // namespace
 
 // The time-split forward (SPLIT): the state after a chunk is affine in the state before
-// it, so with few heads each head's chunks are halved and the halves run at once, as
-// three jobs per head: run 0 = chunks [0, m) from s0; run 1 = chunks [m, 2m) from a zero
-// state; run 2 = chunks [m, 2m) from the identity with v = 0, whose "y" is z_t = Phi_t r_t
-// and whose final state is the transition Phi of the second half.  split_fixup then
-// forms y_t = y0_t + S_m z_t and sT = S_m Phi + S0_end (wkv7_capi.cpp decides when).
+// it, S_{c+1} = S_c M_c + U_c, so with few heads each head's chunks are cut into k
+// segments of m that all run at once, one job (workgroup) per (segment, head):
+//  * segment 0 runs from s0 and writes y as usual, its final state S_1 to the workspace;
+//  * segment s >= 1 runs two states side by side on the same chunk operands, each
+//    consumer wave holding its rows of both: one from zero (y0 and the final state U_s),
+//    one from the identity with v = 0 ("y" z_t = Phi_t r_t and the final state, the
+//    segment's transition Phi_s).
+// split_fixup then chains S_{s+1} = S_s Phi_s + U_s, forms y_t = y0_t + S_s z_t over
+// segment s and writes sT = S_k (wkv7_capi.cpp decides when).
 struct SplitArgs {
-    int BH = 0, m = 0;
-    float* sm = nullptr;     // run 0's final states [BH][64][64]
-    float* s0end = nullptr;  // run 1's final states
-    float* phi = nullptr;    // run 2's final states
-    float* y0 = nullptr;     // run 1's y tiles [BH][m][4 waves][64 lanes][4] float32
-    float* z = nullptr;      // run 2's y tiles, the same layout
+    int BH = 0, m = 0, k = 0;  // heads, chunks per segment, segments
+    float* send0 = nullptr;    // S_1 [BH][64][64]
+    float* uend = nullptr;     // U_s [k - 1][BH][64][64]
+    float* phi = nullptr;      // Phi_s, the same layout
+    float* y0 = nullptr;       // segments 1.. from zero: y tiles [k - 1][BH][m][4 waves][64 lanes][4] float32
+    float* z = nullptr;        // the identity runs' tiles, the same layout
 };
 
 template <bool SPLIT>
@@ -140,18 +144,18 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     const bool producer = wv < NPROD;
     const int pw = wv, cw = wv - NPROD;
     const long rstride = (long)H * NK;                              // between consecutive tokens of one head
-    // bytes of one [B,T,H,64] tensor (SPLIT: the schedule's jobs are three per head)
+    // bytes of one [B,T,H,64] tensor (SPLIT: the schedule's jobs are k per head)
     const uint32_t tbytes = (uint32_t)((long)(SPLIT ? sp.BH : sc.J) * Tn * NK * 2);
     // stream position (cursor) -> byte offset of the chunk's first row, its valid length
-    // (SPLIT: job j is run j / BH of head j % BH; runs 1 and 2 start at chunk m)
-    auto run_of = [&](int j) { return SPLIT ? j / sp.BH : 0; };
+    // (SPLIT: job j is segment j / BH of head j % BH, whose steps start at chunk m * segment;
+    //  chunks past the end of the last segment have no valid steps)
     auto chunk_off = [&](const Cursor& cu) {
         if (!SPLIT) return (uint32_t)(((long)(cu.bb * Tn + cu.step * CH) * H + cu.h) * NK * 2);
-        const int run = run_of(cu.j), head = cu.j - run * sp.BH, b2 = head / H, h2 = head - b2 * H;
-        return (uint32_t)(((long)(b2 * Tn + (cu.step + (run ? sp.m : 0)) * CH) * H + h2) * NK * 2);
+        const int sg = cu.j / sp.BH, head = cu.j - sg * sp.BH, b2 = head / H, h2 = head - b2 * H;
+        return (uint32_t)(((long)(b2 * Tn + (cu.step + sg * sp.m) * CH) * H + h2) * NK * 2);
     };
     auto chunk_len = [&](const Cursor& cu) {
-        return min(CH, Tn - (cu.step + (SPLIT && run_of(cu.j) ? sp.m : 0)) * CH);
+        return min(CH, Tn - (cu.step + (SPLIT ? cu.j / sp.BH * sp.m : 0)) * CH);
     };
 
     // ---------------- producer state ----------------
@@ -219,7 +223,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
 
     // ---------------- consumer state: S^T tiles St[tj][e] = S[i_own][16tj + 4q + e] ----------------
     const int i_own = 16 * cw + r16;
-    f32x4_t St[4];
+    f32x4_t St[4], Sp[4];  // (Sp: SPLIT's identity run)
     if (producer) {
         // this producer's first chunk
         if (pw < nstream) {
@@ -257,9 +261,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
             };
             {   // ---- phase 0: V by LDS DMA; keys 0-31: decays and operands ----
                 vm_wait0();  // this chunk's inputs (LDS DMA issued in the previous chunk's phase 2)
-                // (run 2 of the time split: v = 0)
-                stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride,
-                            SPLIT && run_of(cx.j) == 2 ? 0 : L, lane);
+                stage_plane(S.V, dma_rsrc(v, tbytes), v, chunk_off(cx), voff, rstride, L, lane);
                 float g0[8];
                 decay_scan(0, g0);
                 operands(S, raw, g0, 0);
@@ -362,23 +364,24 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
         };
         for (int j = m * sc.L / sc.n; j <= jlast; j++) {
           const Seg sg = seg_of(sc, m, j);
-          const int run = SPLIT ? j / sp.BH : 0;           // (SPLIT: the job's run and head)
-          const int head = SPLIT ? j - run * sp.BH : j;
+          const int sgm = SPLIT ? j / sp.BH : 0;          // (SPLIT: the job's segment and head)
+          const int head = SPLIT ? j - sgm * sp.BH : j;
           const int bb = head / H, h = head - bb * H;
           const long bh = head;
-          const int c_run = SPLIT && run ? sp.m : 0;      // the run's first chunk
+          const int c_seg = SPLIT ? sgm * sp.m : 0;       // the segment's first chunk
+          const bool dual = SPLIT && sgm > 0;              // the zero and identity runs
           if (sg.fresh) {  // the initial state: s0 at the head's start ...
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
                 const long off = (long)i_own * NK + 16 * tj + 4 * q;
                 float4 x;
-                if (!SPLIT || run == 0) {
+                if (!dual) {
                     x = *reinterpret_cast<const float4*>(s0 + bh * NN + off);
-                } else {  // run 1: zero; run 2: the identity
+                } else {  // zero, and the identity in Sp
                     const int c0 = 16 * tj + 4 * q;
-                    const float one = run == 2 ? 1.f : 0.f;
-                    x = make_float4(i_own == c0 ? one : 0.f, i_own == c0 + 1 ? one : 0.f,
-                                    i_own == c0 + 2 ? one : 0.f, i_own == c0 + 3 ? one : 0.f);
+                    x = make_float4(0.f, 0.f, 0.f, 0.f);
+                    Sp[tj] = f32x4_t{i_own == c0 ? 1.f : 0.f, i_own == c0 + 1 ? 1.f : 0.f,
+                                     i_own == c0 + 2 ? 1.f : 0.f, i_own == c0 + 3 ? 1.f : 0.f};
                 }
                 St[tj] = f32x4_t{x.x, x.y, x.z, x.w};
                 if (ckpt) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + off) = x;
@@ -394,10 +397,10 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
           for (int kk = 0; kk < sg.count; kk++, n++) {
             // ---------------- consumer: rows i_own through chunk c of head j ----------------
             const Slot& S = sm.slot[n % NSLOT];
-            const int c = sg.step0 + kk + c_run;
+            const int c = sg.step0 + kk + c_seg;
             const int t0 = c * CH, L = min(CH, Tn - t0);
-            if (n > 0) y_rows(n - 1);  // the previous tick's y
-            f32x4_t sa = zero4(), yy = zero4();
+            if (n > 0 && !dual) y_rows(n - 1);  // the previous tick's y
+            f32x4_t sa = zero4(), yy = zero4(), sa2 = zero4(), yy2 = zero4();
 #pragma unroll
             for (int s = 0; s < 2; s++) {  // K = 64 over keys in two permuted K=32 steps
                 float sv[8];
@@ -416,6 +419,20 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 yy = mma32(yy, p2h, sh);
                 yy = mma32(yy, p2h, sl);
                 yy = mma32(yy, p2l, sh);
+                if (dual) {  // the identity run on the same operand fragments
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        sv[e] = Sp[2 * s][e];
+                        sv[4 + e] = Sp[2 * s + 1][e];
+                    }
+                    pack8(sv, sh, sl);
+                    sa2 = mma32(sa2, pah, sh);
+                    sa2 = mma32(sa2, pah, sl);
+                    sa2 = mma32(sa2, pal, sh);
+                    yy2 = mma32(yy2, p2h, sh);
+                    yy2 = mma32(yy2, p2h, sl);
+                    yy2 = mma32(yy2, p2l, sh);
+                }
             }
             // V parts on the K=16 instruction, in their own accumulators
             const uint2 vfr = ldtr_sw<SwDma>(S.V, 0, 16 * cw, lane);  // V[s = 4q+e][i_own]
@@ -427,27 +444,33 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 sa += sv;
                 yy += yv;
             }
-            // S_new^T = S^T diag(e^{gL}) + [B^^T K^^T] [SA; V]   (K = 32: SA rows, then V rows)
-            uint2 sah, sal;
+            // S_new^T = S^T diag(e^{gL}) + [B^^T K^^T] [SA; V]   (K = 32: SA rows, then V rows;
+            // the identity run has no V rows)
+            uint2 sah, sal, sah2, sal2;
             pack4(sa, sah, sal);
+            if (dual) pack4(sa2, sah2, sal2);
             const uint4 bhi = cat(sah, vfr), blo = cat(sal, make_uint2(0, 0));
+            const uint4 bhi2 = cat(sah2, make_uint2(0, 0)), blo2 = cat(sal2, make_uint2(0, 0));
 #pragma unroll
             for (int tj = 0; tj < 4; tj++) {
                 const uint4 ah = cat(ldtr_sw<SwLane>(S.Bh[0], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Kh[0], 0, 16 * tj, lane));
                 const uint4 al = cat(ldtr_sw<SwLane>(S.Bh[1], 0, 16 * tj, lane), ldtr_sw<SwLane>(S.Kh[1], 0, 16 * tj, lane));
                 const float4 el = *reinterpret_cast<const float4*>(&S.egL[16 * tj + 4 * q]);
-                St[tj] = mma32(mma32(mma32(St[tj] * f32x4_t{el.x, el.y, el.z, el.w}, ah, bhi), ah, blo), al, bhi);
+                const f32x4_t e4 = {el.x, el.y, el.z, el.w};
+                St[tj] = mma32(mma32(mma32(St[tj] * e4, ah, bhi), ah, blo), al, bhi);
+                if (dual) Sp[tj] = mma32(mma32(mma32(Sp[tj] * e4, ah, bhi2), ah, blo2), al, bhi2);
             }
-            if (!SPLIT || run == 0) {
+            if (!dual) {
                 // this tick's y into yq (lane (q, 4m + jj): row 4q + jj, values 16cw + 4m .. +3)
                 *reinterpret_cast<uint2*>(&sm.yq[n & 1][(4 * q + (lane & 3)) * NK + 16 * cw + 4 * (r16 >> 2)]) =
                     quad_rows_bf16(yy, lane);
                 yrow0 = (uint32_t)(((long)(bb * Tn + t0) * H + h) * NK * 2);
                 yL = L;
-            } else {  // runs 1 and 2: float32 tiles for split_fixup in the register layout,
-                      // [head][chunk - m][wave][lane][e] = Y[4q + e][i_own] (1 KB per wave)
-                float* const yd = (run == 1 ? sp.y0 : sp.z) + ((((long)head * sp.m + (c - sp.m)) * 4 + cw) * 64 + lane) * 4;
-                *reinterpret_cast<float4*>(yd) = make_float4(yy[0], yy[1], yy[2], yy[3]);
+            } else {  // float32 tiles for split_fixup in the register layout,
+                      // [segment - 1][head][chunk in segment][wave][lane][e] = Y[4q + e][i_own]
+                const long o = (((((long)(sgm - 1) * sp.BH + head) * sp.m + (c - c_seg)) * 4 + cw) * 64 + lane) * 4;
+                *reinterpret_cast<float4*>(sp.y0 + o) = make_float4(yy[0], yy[1], yy[2], yy[3]);
+                *reinterpret_cast<float4*>(sp.z + o) = make_float4(yy2[0], yy2[1], yy2[2], yy2[3]);
                 yL = 0;  // (nothing for y_rows)
             }
             if (ckpt) {  // S_{c+1}: this wave's rows, 8 at a time through sq, 4 whole rows per store
@@ -474,9 +497,12 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
 #pragma unroll
           for (int tj = 0; tj < 4; tj++) {
               const long off = (long)i_own * NK + 16 * tj + 4 * q;
-              float* const dst = !SPLIT || run == 0 ? (SPLIT ? sp.sm : sT) : run == 1 ? sp.s0end : sp.phi;
+              float* const dst = !SPLIT ? sT : dual ? sp.uend + (long)(sgm - 1) * sp.BH * NN : sp.send0;
               if (sg.handoff) handoff_put4(hand + m * NN + off, St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
               else *reinterpret_cast<float4*>(dst + bh * NN + off) = make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+              if (dual)
+                  *reinterpret_cast<float4*>(sp.phi + ((long)(sgm - 1) * sp.BH + bh) * NN + off) =
+                      make_float4(Sp[tj][0], Sp[tj][1], Sp[tj][2], Sp[tj][3]);
           }
           if (sg.handoff) handoff_signal(flags + m);
         }
@@ -503,131 +529,162 @@ void launch_chunk_forward(const Fwd& p, int cus) {
 }
 
 // ---------------------------------------------------------------------------
-// Time-split forward without saved states (few heads): one launch of the three runs
-// (3 B*H jobs, one workgroup each: the caller checks 3 B*H <= CUs), then the fix-up.
-// Workspace: S_m, S0_end, Phi ([B*H][64][64] each), y0 and z ([B*H][m][16 * 64]).
+// Time-split forward without saved states (few heads): one launch of the k*B*H jobs (one
+// workgroup each: the caller checks k*B*H <= CUs), then the fix-up.
 // ---------------------------------------------------------------------------
 namespace {
 constexpr int FXG = 4;       // chunks per split_fixup workgroup (one per wave)
 constexpr int FXR = NK + 4;  // padded LDS row (floats)
-// y_t = bf16(y0_t + S_m z_t) over the second half's steps, and sT = S_m Phi + S0_end, on
-// the matrix cores with split-bf16 operands (hi*hi + hi*lo + lo*hi, as in the chunk
-// kernels).  Workgroup (group, head), 4 waves.  Groups below the last: wave w takes
-// chunk 4 group + w: Y[t][i] = y0 + sum_k Z[t][k] S_m[i][k], its z tile turned into rows
-// through the wave's LDS, y0 read straight in the accumulator layout, y out in whole
-// 128-byte rows through LDS.  The last group: wave w takes final-state rows 16w .. 16w+15.
-__global__ __launch_bounds__(256) void split_fixup(int Tn, int H, int m, const float* __restrict__ sm,
-                                                   const float* __restrict__ s0end, const float* __restrict__ phi,
-                                                   const float* __restrict__ y0, const float* __restrict__ z,
-                                                   bf16_t* __restrict__ y, float* __restrict__ sT) {
-    __shared__ float zt[FXG][CH * FXR];      // per wave: its z tile as rows [t][k]
+// Workgroup (group, head), 4 waves, on the matrix cores with split-bf16 operands (hi*hi +
+// hi*lo + lo*hi, as in the chunk kernels).  First the state at the start of the group's
+// segment s, S_s, is chained in LDS from S_1 = send0: S_{u+1} = S_u Phi_u + U_u, wave w
+// forming rows 16w .. 16w+15.  The last group stores S_k as sT.  The others: wave w takes
+// chunk 4 (group mod groups per segment) + w of segment s and forms
+// Y[t][i] = y0[t][i] + sum_j z[t][j] S_s[i][j]: its z tile turned into rows through the
+// wave's LDS, y0 read straight in the accumulator layout, y out in whole 128-byte rows.
+__global__ __launch_bounds__(256) void split_fixup(int Tn, int H, SplitArgs sp, bf16_t* __restrict__ y,
+                                                   float* __restrict__ sT) {
+    __shared__ float st[NK * FXR];           // S_s [i][j]
+    __shared__ float zt[FXG][CH * FXR];      // per wave: its z tile as rows [t][j]
     __shared__ uint16_t yt[FXG][CH * NK];    // per wave: its y tile [t][i]
-    const int grp = blockIdx.x, ngrp = gridDim.x - 1, head = blockIdx.y, bb = head / H, h = head - bb * H;
+    const int ngm = (sp.m + FXG - 1) / FXG;  // chunk groups per segment
+    const int grp = blockIdx.x, head = blockIdx.y, bb = head / H, h = head - bb * H;
+    const bool last = grp == (sp.k - 1) * ngm;
+    const int sgm = last ? sp.k : 1 + grp / ngm;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int q = lane >> 4, r16 = lane & 15;
     const long NN = NK * NK;
-    const float* const S = sm + head * NN;
     // 8 consecutive floats as split-bf16 operand halves
     auto op8 = [](const float* p, uint4& hi, uint4& lo) {
         const float4 x0 = *reinterpret_cast<const float4*>(p), x1 = *reinterpret_cast<const float4*>(p + 4);
         const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         pack8(v, hi, lo);
     };
-    if (grp < ngrp) {
-        const int c = grp * FXG + w;  // chunk of the second half (wave-uniform)
-        if (c >= m) return;
-        // B operand S_m^T: lane (q, r16) of tile n, K step s holds S_m[16n + r16][32s + 8q .. +7]
-        uint4 bh[4][2], bl[4][2];
+    // rows 16w .. 16w+15 of S_1 (float4 number u*64 + lane of the strip)
 #pragma unroll
-        for (int n = 0; n < 4; n++)
+    for (int u = 0; u < 4; u++) {
+        const int f = 4 * (u * 64 + lane), r = 16 * w + f / NK, c = f % NK;
+        *reinterpret_cast<float4*>(&st[r * FXR + c]) =
+            *reinterpret_cast<const float4*>(sp.send0 + head * NN + r * NK + c);
+    }
+    wave_lds_fence();
+    for (int u = 1; u < sgm; u++) {  // S_{u+1} = S_u Phi_u + U_u, this wave's rows
+        const long o = ((long)(u - 1) * sp.BH + head) * NN;
+        uint4 ah[2], al[2];  // A operand S_u: lane (q, r16) holds S_u[16w + r16][32t + 8q .. +7]
 #pragma unroll
-            for (int s = 0; s < 2; s++) op8(S + (16 * n + r16) * NK + 32 * s + 8 * q, bh[n][s], bl[n][s]);
-        // the z tile (float4 u*64 + lane holds Z[4q + e][16u + r16]) into rows
-        const long tile = ((long)head * m + c) * 256;  // float4 index of the chunk's tile
-        float* const zw = zt[w];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float4 x = reinterpret_cast<const float4*>(z)[tile + u * 64 + lane];
-            float* const d = zw + 4 * q * FXR + 16 * u + r16;
-            d[0] = x.x, d[FXR] = x.y, d[2 * FXR] = x.z, d[3 * FXR] = x.w;
-        }
-        wave_lds_fence();
-        uint4 ah[2], al[2];  // A operand Z: lane (q, r16) holds Z[r16][32s + 8q .. +7]
-#pragma unroll
-        for (int s = 0; s < 2; s++) op8(zw + r16 * FXR + 32 * s + 8 * q, ah[s], al[s]);
-        uint16_t* const yw = yt[w];
-#pragma unroll
-        for (int n = 0; n < 4; n++) {
-            const float4 x = reinterpret_cast<const float4*>(y0)[tile + n * 64 + lane];  // y0[4q + e][16n + r16]
-            f32x4_t acc = {x.x, x.y, x.z, x.w};
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                acc = mma32(acc, ah[s], bh[n][s]);
-                acc = mma32(acc, ah[s], bl[n][s]);
-                acc = mma32(acc, al[s], bh[n][s]);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++) yw[(4 * q + e) * NK + 16 * n + r16] = f32_to_bf16(acc[e]);
-        }
-        wave_lds_fence();
-        // 16 rows of 128 bytes: 8 lanes per row, two rows per lane
-#pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            const int rr = 8 * hf + (lane >> 3), pc = lane & 7, tabs = CH * (m + c) + rr;
-            if (tabs < Tn)
-                *reinterpret_cast<uint4*>(y + ((long)(bb * Tn + tabs) * H + h) * NK + 8 * pc) =
-                    *reinterpret_cast<const uint4*>(&yw[rr * NK + 8 * pc]);
-        }
-    } else {
-        // rows i = 16w + 4q + e, columns j = 16n + r16:  sT = S0_end + S_m Phi
-        uint4 ah[2], al[2];  // A operand S_m: lane (q, r16) holds S_m[16w + r16][32s + 8q .. +7]
-#pragma unroll
-        for (int s = 0; s < 2; s++) op8(S + (16 * w + r16) * NK + 32 * s + 8 * q, ah[s], al[s]);
-        const float* const P = phi + head * NN;
+        for (int t = 0; t < 2; t++) op8(&st[(16 * w + r16) * FXR + 32 * t + 8 * q], ah[t], al[t]);
+        wave_lds_fence();  // (the strip is overwritten below)
 #pragma unroll
         for (int n = 0; n < 4; n++) {
             f32x4_t acc;
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[e] = s0end[head * NN + (16 * w + 4 * q + e) * NK + 16 * n + r16];
+            for (int e = 0; e < 4; e++) acc[e] = sp.uend[o + (16 * w + 4 * q + e) * NK + 16 * n + r16];
 #pragma unroll
-            for (int s = 0; s < 2; s++) {
-                float v[8];  // B operand Phi: lane (q, r16) holds Phi[32s + 8q .. +7][16n + r16]
+            for (int t = 0; t < 2; t++) {
+                float v[8];  // B operand Phi_u: lane (q, r16) holds Phi_u[32t + 8q .. +7][16n + r16]
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = P[(32 * s + 8 * q + e) * NK + 16 * n + r16];
+                for (int e = 0; e < 8; e++) v[e] = sp.phi[o + (32 * t + 8 * q + e) * NK + 16 * n + r16];
                 uint4 bh, bl;
                 pack8(v, bh, bl);
-                acc = mma32(acc, ah[s], bh);
-                acc = mma32(acc, ah[s], bl);
-                acc = mma32(acc, al[s], bh);
+                acc = mma32(acc, ah[t], bh);
+                acc = mma32(acc, ah[t], bl);
+                acc = mma32(acc, al[t], bh);
             }
 #pragma unroll
-            for (int e = 0; e < 4; e++) sT[head * NN + (16 * w + 4 * q + e) * NK + 16 * n + r16] = acc[e];
+            for (int e = 0; e < 4; e++) st[(16 * w + 4 * q + e) * FXR + 16 * n + r16] = acc[e];
         }
+        wave_lds_fence();
+    }
+    if (last) {  // sT = S_k, this wave's rows
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int f = 4 * (u * 64 + lane), r = 16 * w + f / NK, c = f % NK;
+            *reinterpret_cast<float4*>(sT + head * NN + r * NK + c) = *reinterpret_cast<const float4*>(&st[r * FXR + c]);
+        }
+        return;
+    }
+    __syncthreads();  // all of S_s
+    const int c = (grp % ngm) * FXG + w;  // chunk within segment sgm (wave-uniform)
+    if (c >= sp.m || CH * (sgm * sp.m + c) >= Tn) return;
+    // B operand S_s^T: lane (q, r16) of tile n, K step t holds S_s[16n + r16][32t + 8q .. +7]
+    uint4 bh[4][2], bl[4][2];
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) op8(&st[(16 * n + r16) * FXR + 32 * t + 8 * q], bh[n][t], bl[n][t]);
+    // the z tile (float4 u*64 + lane holds Z[4q + e][16u + r16]) into rows
+    const long tile = (((long)(sgm - 1) * sp.BH + head) * sp.m + c) * 256;  // float4 index of the chunk's tile
+    float* const zw = zt[w];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const float4 x = reinterpret_cast<const float4*>(sp.z)[tile + u * 64 + lane];
+        float* const d = zw + 4 * q * FXR + 16 * u + r16;
+        d[0] = x.x, d[FXR] = x.y, d[2 * FXR] = x.z, d[3 * FXR] = x.w;
+    }
+    wave_lds_fence();
+    uint4 ah[2], al[2];  // A operand Z: lane (q, r16) holds Z[r16][32t + 8q .. +7]
+#pragma unroll
+    for (int t = 0; t < 2; t++) op8(zw + r16 * FXR + 32 * t + 8 * q, ah[t], al[t]);
+    uint16_t* const yw = yt[w];
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+        const float4 x = reinterpret_cast<const float4*>(sp.y0)[tile + n * 64 + lane];  // y0[4q + e][16n + r16]
+        f32x4_t acc = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            acc = mma32(acc, ah[t], bh[n][t]);
+            acc = mma32(acc, ah[t], bl[n][t]);
+            acc = mma32(acc, al[t], bh[n][t]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) yw[(4 * q + e) * NK + 16 * n + r16] = f32_to_bf16(acc[e]);
+    }
+    wave_lds_fence();
+    // 16 rows of 128 bytes: 8 lanes per row, two rows per lane
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        const int rr = 8 * hf + (lane >> 3), pc = lane & 7, tabs = CH * (sgm * sp.m + c) + rr;
+        if (tabs < Tn)
+            *reinterpret_cast<uint4*>(y + ((long)(bb * Tn + tabs) * H + h) * NK + 8 * pc) =
+                *reinterpret_cast<const uint4*>(&yw[rr * NK + 8 * pc]);
     }
 }
+
+// chunks per segment for k segments of n chunks
+int seg_chunks(int n, int k) { return (n + k - 1) / k; }
 }  // namespace
 
-// m = ceil(chunks / 2): runs 1 and 2 end with an empty chunk when the count is odd
-// (its steps are padding, which keeps the state)
-size_t chunk_forward_split_workspace(int B, int T, int H) {
-    const size_t BH = (size_t)B * H, m = ((size_t)(T + CH - 1) / CH + 1) / 2;
-    return BH * (3 * NK * NK + 2 * 16 * m * NK) * sizeof(float);
+// Segments of the time-split forward for B*H heads of n chunks on `cus` CUs: as many as fit
+// one job per CU, at most 4 (the fix-up chains the segments' transitions one after another),
+// each with at least one valid chunk; 1 = no split.
+int chunk_forward_split_segments(int BH, int T, int cus) {
+    const int n = (T + CH - 1) / CH;
+    int k = BH > 0 ? min(4, cus / BH) : 1;
+    while (k > 1 && (long)(k - 1) * seg_chunks(n, k) >= n) k--;
+    return max(k, 1);
+}
+size_t chunk_forward_split_workspace(int B, int T, int H, int cus) {
+    const int BH = B * H, k = chunk_forward_split_segments(BH, T, cus);
+    if (k < 2) return 0;
+    const size_t m = seg_chunks((T + CH - 1) / CH, k);
+    return (size_t)BH * ((2 * k - 1) * (size_t)NK * NK + 2 * (k - 1) * m * CH * NK) * sizeof(float);
 }
 void launch_chunk_forward_split(const Fwd& p, int cus) {
-    const int BH = p.B * p.H, m = ((p.T + CH - 1) / CH + 1) / 2;
-    float* const base = static_cast<float*>(p.ws);
     SplitArgs sp;
-    sp.BH = BH, sp.m = m;
-    sp.sm = base, sp.s0end = base + (size_t)BH * NK * NK, sp.phi = base + 2 * (size_t)BH * NK * NK;
-    sp.y0 = base + 3 * (size_t)BH * NK * NK, sp.z = sp.y0 + (size_t)BH * 16 * m * NK;
-    const Sched sc = plan_schedule(3 * BH, m, cus);  // 3 B*H <= cus: one job per workgroup, no cuts
+    sp.BH = p.B * p.H, sp.k = chunk_forward_split_segments(sp.BH, p.T, cus);
+    sp.m = seg_chunks((p.T + CH - 1) / CH, sp.k);
+    const size_t NN = (size_t)NK * NK, per = (size_t)(sp.k - 1) * sp.BH;
+    float* const base = static_cast<float*>(p.ws);
+    sp.send0 = base, sp.uend = base + sp.BH * NN, sp.phi = sp.uend + per * NN;
+    sp.y0 = sp.phi + per * NN, sp.z = sp.y0 + per * sp.m * CH * NK;
+    const Sched sc = plan_schedule(sp.k * sp.BH, sp.m, cus);  // one job per workgroup, no cuts
     hipLaunchKernelGGL(chunk_forward_bf16<true>, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
                        (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, nullptr, nullptr,
                        nullptr, sp);
-    // groups of FXG chunks, then one for the final state; heads along y (at most cus / 3)
-    hipLaunchKernelGGL(split_fixup, dim3((m + FXG - 1) / FXG + 1, BH), dim3(256), 0, p.stream, p.T, p.H, m, sp.sm,
-                       sp.s0end, sp.phi, sp.y0, sp.z, (bf16_t*)p.y, p.sT);
+    // chunk groups of segments 1 .. k-1, then one for the final state; heads along y
+    hipLaunchKernelGGL(split_fixup, dim3((sp.k - 1) * ((sp.m + FXG - 1) / FXG) + 1, sp.BH), dim3(256), 0,
+                       p.stream, p.T, p.H, sp, (bf16_t*)p.y, p.sT);
 }
 
 }  // namespace wkv7

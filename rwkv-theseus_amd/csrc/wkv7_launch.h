@@ -58,10 +58,12 @@ void launch_chunk_forward(const Fwd& p, int cus);
 void launch_chunk_backward(const Bwd& p, int cus);
 size_t chunk_forward_workspace(int B, int T, int H, int cus);
 size_t chunk_backward_workspace(int B, int T, int H, int cus);
-// The time-split forward (no saved states, 3 B*H <= cus): the two halves of every head
-// at once, then a fix-up kernel; its workspace holds the halves' states and outputs.
+// The time-split forward (no saved states, few heads): each head's chunks cut into
+// k = chunk_forward_split_segments(...) >= 2 segments that run at once, then a fix-up
+// kernel; its workspace holds the segments' states, transitions and outputs.
+int chunk_forward_split_segments(int BH, int T, int cus);
 void launch_chunk_forward_split(const Fwd& p, int cus);
-size_t chunk_forward_split_workspace(int B, int T, int H);
+size_t chunk_forward_split_workspace(int B, int T, int H, int cus);
 
 // Gated delta rule forward on the chunked MFMA kernels (gdn_chunk.hip): q, k, v and o
 // [B,T,H,N] in dtype (0 = bf16, 1 = fp32), g, beta [B,T,H] fp32, states [B,H,key,value]

@@ -168,15 +168,15 @@ def _config1_runs(xs, s0):
 def test_config1_chunked_equals_unchunked(monkeypatch):
     """The reference's config-1 check: 8 calls of 512 steps with the state carried give
     the single 4096-step call's y and final state.  On the one-pass kernels (planned for
-    239 CUs: 80 heads uncut, too many for the time split) the 512-step boundaries fall on
+    159 CUs: 80 heads uncut, too many for the time split) the 512-step boundaries fall on
     the 16-step grid, so the arithmetic and the bits are the same.  The default plan (256
-    CUs) takes the time-split forward for both, split at different steps: each matches
-    the oracle and the one-pass result to rounding."""
+    CUs) takes the time-split forward (3 segments per head) for both, split at different
+    steps: each matches the oracle and the one-pass result to rounding."""
     inp = wkv7_inputs(1, 4096, 80, 64, seed=20261, dtype=torch.bfloat16)
     xs = [inp[n].cuda() for n in "rwkvab"]
     s0 = inp["s0"].cuda()
     y_ref, s_ref = O.forward_c(*(inp[n].double().numpy() for n in "rwkvab"), inp["s0"].double().numpy())
-    monkeypatch.setenv("THESEUS_WKV7_CUS", "239")
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "159")
     one = _config1_runs(xs, s0)
     assert torch.equal(one[2], one[0])
     assert torch.equal(one[3], one[1])
@@ -428,26 +428,40 @@ def _capi_forward(lib, xs, s0, ws, ws_bytes):
     return y, sT
 
 
-@pytest.mark.parametrize("B,T,H", [(1, 128, 2), (2, 300, 3), (1, 1000, 5), (3, 512, 4), (1, 113, 1)])
+def _segments(BH, T, cus=256):
+    """Segments and chunks per segment of the time-split forward (as the library plans)."""
+    n = -(-T // 16)
+    k = min(4, cus // BH)
+    while k > 1 and (k - 1) * -(-n // k) >= n:
+        k -= 1
+    return k, -(-n // k)
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 128, 2), (2, 300, 3), (1, 1000, 5), (3, 512, 4), (1, 113, 1),
+                                   (1, 144, 2), (2, 300, 40), (1, 256, 100)])
 def test_time_split_forward_against_oracle_and_one_pass(B, T, H, monkeypatch):
-    """With 3*B*H <= CUs and at least 8 chunks, a forward without saved states given
-    theseus_wkv7_forward_workspace_size bytes runs each head's two halves at once
-    (runs from s0, from zero and from the identity) and joins them with the fix-up
-    kernel; given no workspace it runs the one-pass kernels.  Odd chunk counts leave
-    the second half an empty last chunk; partial chunks fall at the end (T % 16)."""
+    """With at least two CUs per head and at least 8 chunks, a forward without saved
+    states given theseus_wkv7_forward_workspace_size bytes cuts each head's chunks into
+    k = min(4, CUs / (B*H)) segments (fewer if the last would be empty) that run at once
+    -- segment 0 from s0, each later one from zero and from the identity side by side --
+    and chains them in the fix-up kernel; given no workspace it runs the one-pass
+    kernels.  Here k = 4, 4, 4, 4, 4, 3 (9 chunks), 3 (80 heads), 2 (100 heads); the last
+    segment ends with empty chunks when k does not divide the chunk count, and partial
+    chunks fall at the end (T % 16)."""
     monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
     N = 64
-    print(f"  time split B={B} T={T} H={H}", flush=True)
+    k, m = _segments(B * H, T)
+    print(f"  time split B={B} T={T} H={H}: {k} segments of {m} chunks", flush=True)
+    assert k >= 2
     inp = wkv7_inputs(B, T, H, N, seed=1100 + T + H, dtype=torch.bfloat16, s0_std=0.1)
     xs = [inp[n].cuda() for n in "rwkvab"]
     s0 = inp["s0"].cuda()
     lib = W.extension().lib
     need = int(lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0))
-    m = (-(-T // 16) + 1) // 2
-    assert need == 4 * B * H * (3 * N * N + N * 16 * 2 * m)
+    assert need == 4 * B * H * ((2 * k - 1) * N * N + 2 * (k - 1) * m * 16 * N)
     ws = torch.full((need // 4,), float("nan"), dtype=torch.float32, device="cuda")
     y_s, s_s = _capi_forward(lib, xs, s0, ws, need)
-    # the split path ran: the first half's final states are in the workspace
+    # the split path ran: the first segment's final states are in the workspace
     assert bool(torch.isfinite(ws[:B * H * N * N]).all())
     y_1, s_1 = _capi_forward(lib, xs, s0, None, 0)
     y_ref, s_ref = O.forward_c(*(inp[n].double().numpy() for n in "rwkvab"), inp["s0"].double().numpy())
@@ -464,14 +478,14 @@ def test_time_split_forward_against_oracle_and_one_pass(B, T, H, monkeypatch):
 
 
 def test_time_split_is_not_taken_beyond_its_limits(monkeypatch):
-    """Too many heads for three CUs each, fewer than 8 chunks, or saved states
+    """Too many heads for two CUs each, fewer than 8 chunks, or saved states
     requested: the forward workspace is the one-pass kernels' (none here), and the
     saved-state forward's y and state equal the no-grad one-pass call's bit for bit."""
     lib = W.extension().lib
     monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
-    assert lib.theseus_wkv7_forward_workspace_size(1, 512, 86, 64, 0) == 0   # 258 > 256
+    assert lib.theseus_wkv7_forward_workspace_size(1, 512, 129, 64, 0) == 0  # 258 > 256
     assert lib.theseus_wkv7_forward_workspace_size(1, 112, 2, 64, 0) == 0    # 7 chunks
-    assert lib.theseus_wkv7_forward_workspace_size(1, 512, 85, 64, 0) > 0
+    assert lib.theseus_wkv7_forward_workspace_size(1, 512, 128, 64, 0) > 0
     assert lib.theseus_wkv7_forward_workspace_size(1, 512, 2, 64, 1) == 0    # fp32: step-serial
     inp = wkv7_inputs(1, 200, 2, 64, seed=77, dtype=torch.bfloat16, s0_std=0.1)
     xs = [inp[n].cuda() for n in "rwkvab"]
