@@ -20,7 +20,8 @@ config 2 it is the algorithmic bytes plus the saved states the config mandates
 0.384 ms, which caps the algorithmic fraction near 55 %.
 
 Other configurations (``--config``): c1 = 8 chained T=512 forward calls without
-saved states (state carried), B=1, H=80; c4 = 256 in-place decode steps at
+saved states (state carried), B=1, H=80, with one T=4096 call timed beside them (both
+on the time-split forward: 80 heads leave CUs for 3 segments per head); c4 = 256 in-place decode steps at
 B=64, with one fused T=256 forward timed beside them; c3 = the TimeMix layer;
 c4tm = config 4 through a whole TimeMix layer (C=5120, bf16 serving weights): 256
 tokens per step, served out of place (the reference's T=1 forward), in place
@@ -535,6 +536,15 @@ def main():
                 torch.cuda.synchronize()
                 call_ms.append(a0.elapsed_time(a1))
         kern["fwd"] = (sum(call_ms) / len(call_ms), alg_bytes(B, Tc, H, N, "fwd"))
+        # the same T tokens as one call (no saved states), calls back to back
+        reps = max(3, min(args.steps, 10))
+        a0, a1 = ev(), ev()
+        a0.record(stream)
+        for _ in range(reps):
+            ext.forward(*xs, s0, False)
+        a1.record(stream)
+        torch.cuda.synchronize()
+        single_ms = a0.elapsed_time(a1) / reps
     else:
         fwd_ms, bwd_ms = [], []
         for _ in range(max(3, min(args.steps, 10))):
@@ -612,6 +622,7 @@ def main():
     if args.config == "c1":
         line["config"].update(calls=NSPLIT, T_per_call=Tc, saved_states=False)
         line["call_ms"] = round(kern["fwd"][0], 4)
+        line["single_call_T4096_ms"] = round(single_ms, 4)
     if args.config == "c4":
         line["config"].update(steps_per_call=1, saved_states=False)
         line["decode_step_ms"] = round(kern["decode"][0], 4)
