@@ -31,6 +31,14 @@
 // chunk's record comes into LDS by DMA while the current one is used (all waves
 // read the same record), so the scan reads nothing else from memory.
 // Products use split-bf16 operands (hi + lo, three MFMAs), as the WKV7 kernels.
+//
+// With few heads (the teacher's 32 heads of 128 keys fill 64 of 256 CUs) the scan is
+// cut in time like the WKV7 forward's time split: X after a chunk is affine in X before
+// it, X_{c+1} = X_c M_c + U_c, so each head's chunks form k segments scanned at once.
+// Segment 0 starts from s0; segment s >= 1 carries two states in every wave, one from
+// zero (its output y0 and final U_s) and one from the identity with v = 0 (its output
+// z_t = Phi_t r_t and final Phi_s), both on the same record.  gdn_split_fixup then
+// chains X_{s+1} = X_s Phi_s + U_s and forms y_t = y0_t + X_s z_t.
 #include "wkv7_io.h"
 #include "wkv7_launch.h"
 
@@ -242,14 +250,26 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
 // double-buffered in LDS: chunk c + 1's comes in by DMA (each wave moves every NW-th
 // kilobyte) while chunk c's is read; one barrier per chunk.
 // ---------------------------------------------------------------------------
-template <int NK, typename TO>
+// The time split's buffers (float32): X_1 [BH][N][N] (internal [value][key] layout), U_s
+// and Phi_s [k - 1][BH][N][N], and the y0 and z tiles [k - 1][BH][m][N/16 row blocks][64
+// lanes][4] (lane (q4, r16) of row block rb: y[4q4 + e][16rb + r16]).
+struct GdnSplit {
+    int m = 0, k = 0;  // chunks per segment, segments
+    float *send0 = nullptr, *uend = nullptr, *phi = nullptr, *y0 = nullptr, *z = nullptr;
+};
+
+template <int NK, typename TO, bool SPLIT>
 __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, const float* __restrict__ s0,
                                                    TO* __restrict__ o, float* __restrict__ sT,
-                                                   const uint8_t* __restrict__ ws) {
+                                                   const uint8_t* __restrict__ ws, GdnSplit sp) {
     using R = GdnRec<NK>;
     constexpr int KS = R::KS, TJ = R::TJ;
     __shared__ __attribute__((aligned(1024))) uint8_t recs[2][R::DMA_BLOCKS * 1024];
-    const int bh = blockIdx.x % BH, rg = blockIdx.x / BH, bb = bh / H, h = bh - bb * H;
+    // workgroup (segment * row groups + rg) * BH + bh (SPLIT; else rg * BH + bh)
+    constexpr int RGS = NK / 64;
+    const int bh = blockIdx.x % BH, rest = blockIdx.x / BH, rg = SPLIT ? rest % RGS : rest;
+    const int sgm = SPLIT ? rest / RGS : 0, bb = bh / H, h = bh - bb * H;
+    const bool dual = SPLIT && sgm > 0;  // the zero and identity runs
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     // waves per group (the host launches whole waves, at least one: the DMA loop steps by NW)
     const int NW = max(1, __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6)));
@@ -257,6 +277,7 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
     const int rb = rg * NW + wv, i_own = 16 * rb + r16;
     const long NN = (long)NK * NK, ei = kv ? 1 : NK, ej = kv ? NK : 1;
     const int nchunk = (Tn + GC - 1) / GC;
+    const int c0 = SPLIT ? sgm * sp.m : 0, c1 = SPLIT ? min(nchunk, c0 + sp.m) : nchunk;  // this segment's chunks
     // this head's records (the host keeps them under 4 GB, so 32-bit offsets reach them)
     const i32x4_t rs = dma_rsrc(ws + (size_t)bh * nchunk * R::BYTES, (uint32_t)((size_t)nchunk * R::BYTES));
     auto fetch = [&](int c, int buf) {
@@ -265,21 +286,24 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
         const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)recs[buf];
         for (int j = wv; j < R::DMA_BLOCKS; j += NW) dma_kb(base + 1024 * j, rs, (uint32_t)(1024 * j + 16 * lane), so);
     };
-    fetch(0, 0);
-    f32x4_t St[TJ];
+    fetch(c0, 0);
+    f32x4_t St[TJ], Sp[TJ];  // (Sp: the identity run)
 #pragma unroll
     for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) St[tj][e] = s0[bh * NN + i_own * ei + (16 * tj + 4 * q4 + e) * ej];
+        for (int e = 0; e < 4; e++) {
+            St[tj][e] = dual ? 0.f : s0[bh * NN + i_own * ei + (16 * tj + 4 * q4 + e) * ej];
+            Sp[tj][e] = i_own == 16 * tj + 4 * q4 + e ? 1.f : 0.f;
+        }
     vm_wait0();
     __syncthreads();
-    for (int c = 0; c < nchunk; c++) {
-        if (c + 1 < nchunk) fetch(c + 1, (c + 1) & 1);
-        const uint8_t* const rec = recs[c & 1];
+    for (int c = c0; c < c1; c++) {
+        if (c + 1 < c1) fetch(c + 1, (c - c0 + 1) & 1);
+        const uint8_t* const rec = recs[(c - c0) & 1];
         const int t0 = c * GC, L = min(GC, Tn - t0);
         const long tok0 = (long)bb * Tn + t0;
         // SA = P X0^T and Y = P2 X0^T over the keys (permuted K=32 steps)
-        f32x4_t sa = zero4(), yy = zero4();
+        f32x4_t sa = zero4(), yy = zero4(), sa2 = zero4(), yy2 = zero4();
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             const float sv[8] = {St[2 * ks][0], St[2 * ks][1], St[2 * ks][2], St[2 * ks][3],
@@ -291,6 +315,13 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
             const uint4 ph = pf[0], pl = pf[64], p2h = p2[0], p2l = p2[64];
             sa = mma32(mma32(mma32(sa, ph, sh), ph, sl), pl, sh);
             yy = mma32(mma32(mma32(yy, p2h, sh), p2h, sl), p2l, sh);
+            if (dual) {  // the identity run on the same record
+                const float sw[8] = {Sp[2 * ks][0], Sp[2 * ks][1], Sp[2 * ks][2], Sp[2 * ks][3],
+                                     Sp[2 * ks + 1][0], Sp[2 * ks + 1][1], Sp[2 * ks + 1][2], Sp[2 * ks + 1][3]};
+                pack8(sw, sh, sl);
+                sa2 = mma32(mma32(mma32(sa2, ph, sh), ph, sl), pl, sh);
+                yy2 = mma32(mma32(mma32(yy2, p2h, sh), p2h, sl), p2l, sh);
+            }
         }
         // + Q' V and Q2 V on the K=16 instruction, in their own accumulators
         const uint2* vf = reinterpret_cast<const uint2*>(rec + R::VF) + (2 * rb) * 64 + lane;
@@ -301,36 +332,239 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
             sa += mma16(mma16(mma16(zero4(), q1h, vh), q1h, vl), q1l, vh);
             yy += mma16(mma16(mma16(zero4(), q2h, vh), q2h, vl), q2l, vh);
         }
+        if (!dual) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {  // y[t][i_own], t = 4q4 + e
-            const int t = 4 * q4 + e;
-            if (t < L) io<TO>::st(o, ((tok0 + t) * H + h) * NK + i_own, yy[e]);
+            for (int e = 0; e < 4; e++) {  // y[t][i_own], t = 4q4 + e
+                const int t = 4 * q4 + e;
+                if (t < L) io<TO>::st(o, ((tok0 + t) * H + h) * NK + i_own, yy[e]);
+            }
+        } else {  // the tiles for gdn_split_fixup
+            const long f4 = ((((long)(sgm - 1) * BH + bh) * sp.m + (c - c0)) * TJ + rb) * 64 + lane;
+            reinterpret_cast<float4*>(sp.y0)[f4] = make_float4(yy[0], yy[1], yy[2], yy[3]);
+            reinterpret_cast<float4*>(sp.z)[f4] = make_float4(yy2[0], yy2[1], yy2[2], yy2[3]);
         }
-        // X^T <- e^{gamma_L} X^T + [B^^T K^^T] [SA; V]   (K = 32: SA rows, then V rows)
-        uint2 sah, sal;
+        // X^T <- e^{gamma_L} X^T + [B^^T K^^T] [SA; V]   (K = 32: SA rows, then V rows;
+        // the identity run has no V rows)
+        uint2 sah, sal, sah2, sal2;
         pack4(sa, sah, sal);
+        if (dual) pack4(sa2, sah2, sal2);
         const uint4 bhi = cat(sah, vh), blo = cat(sal, vl);
+        const uint4 bhi2 = cat(sah2, make_uint2(0, 0)), blo2 = cat(sal2, make_uint2(0, 0));
         const float egL = *reinterpret_cast<const float*>(rec + R::EL);
 #pragma unroll
         for (int tj = 0; tj < TJ; tj++) {
             const uint4* uf = reinterpret_cast<const uint4*>(rec + R::UF) + (2 * tj) * 64 + lane;
             const uint4 ah = uf[0], al = uf[64];
             St[tj] = mma32(mma32(mma32(St[tj] * egL, ah, bhi), ah, blo), al, bhi);
+            if (dual) Sp[tj] = mma32(mma32(mma32(Sp[tj] * egL, ah, bhi2), ah, blo2), al, bhi2);
         }
         vm_wait0();      // this wave's part of the next record is in LDS
         __syncthreads();  // every wave's part is, and nobody still reads this one
     }
+    if (!SPLIT) {
 #pragma unroll
-    for (int tj = 0; tj < TJ; tj++)
+        for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) sT[bh * NN + i_own * ei + (16 * tj + 4 * q4 + e) * ej] = St[tj][e];
+            for (int e = 0; e < 4; e++) sT[bh * NN + i_own * ei + (16 * tj + 4 * q4 + e) * ej] = St[tj][e];
+    } else {  // X_1, or U_s and Phi_s, in the internal layout (float4 per tile)
+        const long o4 = ((dual ? (long)(sgm - 1) * BH : 0) + bh) * NN + (long)i_own * NK;
+        float* const dst = dual ? sp.uend : sp.send0;
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) {
+            *reinterpret_cast<float4*>(dst + o4 + 16 * tj + 4 * q4) = make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+            if (dual)
+                *reinterpret_cast<float4*>(sp.phi + o4 + 16 * tj + 4 * q4) =
+                    make_float4(Sp[tj][0], Sp[tj][1], Sp[tj][2], Sp[tj][3]);
+        }
+    }
 }
 
+// ---------------------------------------------------------------------------
+// The time split's fix-up, two kernels.  gdn_split_chain (one workgroup per head, N/16
+// waves, wave w on rows 16w .. 16w+15) chains X_{s+1} = X_s Phi_s + U_s in LDS on the
+// matrix cores (split-bf16 operands), storing X_{s+1} over U_s (which only it reads; the
+// same lane reads each U element before writing it) and X_k as sT in the caller's
+// layout.  Phi_s (as split B operands in LDS) and U_s (registers) come one step ahead.  gdn_split_y then forms y_t = y0_t + X_s z_t for every chunk of segments
+// 1 .. k-1: workgroup (chunk group, head), wave w keeps output columns 16w .. 16w+15
+// (rows of X_s as its B operand in registers); per chunk the z tile is turned into rows in
+// LDS, y0 comes in the accumulator layout, o leaves in whole rows through LDS.
+// ---------------------------------------------------------------------------
+constexpr int GFY = 8;  // chunks per gdn_split_y workgroup
+__device__ __forceinline__ void op8f(const float* p, uint4& hi, uint4& lo) {  // 8 floats, split
+    const float4 x0 = *reinterpret_cast<const float4*>(p), x1 = *reinterpret_cast<const float4*>(p + 4);
+    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    pack8(v, hi, lo);
+}
+// X_s of segment s >= 1: X_1 in send0, X_s (s >= 2) in the U_{s-1} slot
+__device__ __forceinline__ const float* seg_state(const GdnSplit& sp, int BH, int bh, int s, long NN) {
+    return s == 1 ? sp.send0 + bh * NN : sp.uend + ((long)(s - 2) * BH + bh) * NN;
+}
+
+template <int NK>
+__global__ __launch_bounds__(64 * (NK / 16)) void gdn_split_chain(int BH, int kv, GdnSplit sp, float* __restrict__ sT) {
+    constexpr int KS = NK / 32, TJ = NK / 16, XR = NK + 4, NT = 64 * TJ;
+    __shared__ float st[NK * XR];              // X_s [i][j]
+    __shared__ uint4 fr[TJ * KS * 2 * 64];     // Phi_s as split B operands [n][t][hi, lo][lane]
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int q = lane >> 4, r16 = lane & 15;
+    const long NN = (long)NK * NK;
+    // Fragment entries (n, t, lane') = KS per thread, number v*NT + tid: Phi[32t + 8q' + e][16n + r']
+    // for e = 0..7, loaded a step ahead and split once here, not by every wave.  (Plain
+    // float arrays in macros: arrays behind lambdas end up in scratch memory.)
+    float pv[KS][8];
+    float uf[TJ][4];  // U_u[16w + 4q + e][16n + r16]
+#define GDN_CHAIN_LOAD(u_)                                                                                    \
+    do {                                                                                                      \
+        const long ol_ = ((long)((u_) - 1) * BH + bh) * NN;                                                   \
+        _Pragma("unroll") for (int v = 0; v < KS; v++) {                                                      \
+            const int x_ = v * NT + tid, l_ = x_ & 63, t_ = (x_ >> 6) % KS, n_ = (x_ >> 6) / KS;              \
+            _Pragma("unroll") for (int e = 0; e < 8; e++)                                                     \
+                pv[v][e] = sp.phi[ol_ + (32 * t_ + 8 * (l_ >> 4) + e) * NK + 16 * n_ + (l_ & 15)];            \
+        }                                                                                                     \
+        _Pragma("unroll") for (int n = 0; n < TJ; n++)                                                        \
+            _Pragma("unroll") for (int e = 0; e < 4; e++) uf[n][e] = sp.uend[ol_ + (16 * w + 4 * q + e) * NK + 16 * n + r16]; \
+    } while (0)
+#define GDN_CHAIN_STAGE()                                                                                     \
+    do {                                                                                                      \
+        _Pragma("unroll") for (int v = 0; v < KS; v++) {                                                      \
+            const int x_ = v * NT + tid, l_ = x_ & 63, f_ = x_ >> 6;                                          \
+            uint4 h_, lo_;                                                                                    \
+            pack8(pv[v], h_, lo_);                                                                            \
+            fr[(2 * f_) * 64 + l_] = h_;                                                                      \
+            fr[(2 * f_ + 1) * 64 + l_] = lo_;                                                                 \
+        }                                                                                                     \
+    } while (0)
+#pragma unroll
+    for (int u = 0; u < NK / 16; u++) {  // rows 16w .. 16w+15 of X_1 (float4 u*64 + lane of the strip)
+        const int f = 4 * (u * 64 + lane), r = 16 * w + f / NK, c = f % NK;
+        *reinterpret_cast<float4*>(&st[r * XR + c]) = *reinterpret_cast<const float4*>(sp.send0 + bh * NN + r * NK + c);
+    }
+    GDN_CHAIN_LOAD(1);
+    GDN_CHAIN_STAGE();
+    __syncthreads();
+    for (int u = 1; u < sp.k; u++) {  // X_{u+1} = X_u Phi_u + U_u, this wave's rows
+        const long ob = ((long)(u - 1) * BH + bh) * NN;
+        float acc0[TJ][4];
+#pragma unroll
+        for (int n = 0; n < TJ; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc0[n][e] = uf[n][e];
+        if (u + 1 < sp.k) GDN_CHAIN_LOAD(u + 1);  // the next step's operands, in flight during this one
+        uint4 ah[KS], al[KS];  // A operand X_u: lane (q, r16) holds X_u[16w + r16][32t + 8q .. +7]
+#pragma unroll
+        for (int t = 0; t < KS; t++) op8f(&st[(16 * w + r16) * XR + 32 * t + 8 * q], ah[t], al[t]);
+        wave_lds_fence();  // (the strip is overwritten below)
+#pragma unroll
+        for (int n = 0; n < TJ; n++) {
+            f32x4_t acc = {acc0[n][0], acc0[n][1], acc0[n][2], acc0[n][3]};
+#pragma unroll
+            for (int t = 0; t < KS; t++) {
+                const uint4 bhv = fr[(2 * (n * KS + t)) * 64 + lane], blv = fr[(2 * (n * KS + t) + 1) * 64 + lane];
+                acc = mma32(acc, ah[t], bhv);
+                acc = mma32(acc, ah[t], blv);
+                acc = mma32(acc, al[t], bhv);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                st[(16 * w + 4 * q + e) * XR + 16 * n + r16] = acc[e];
+                if (u + 1 < sp.k) sp.uend[ob + (16 * w + 4 * q + e) * NK + 16 * n + r16] = acc[e];  // X_{u+1}
+            }
+        }
+        __syncthreads();  // everyone is done with Phi_u
+        if (u + 1 < sp.k) GDN_CHAIN_STAGE();
+        __syncthreads();
+    }
+#undef GDN_CHAIN_LOAD
+#undef GDN_CHAIN_STAGE
+    const long ei = kv ? 1 : NK, ej = kv ? NK : 1;  // sT = X_k, this wave's rows, in the caller's layout
+#pragma unroll
+    for (int u = 0; u < NK / 16; u++) {
+        const int f = 4 * (u * 64 + lane), i = 16 * w + f / NK, j0 = f % NK;
+#pragma unroll
+        for (int e = 0; e < 4; e++) sT[bh * NN + i * ei + (j0 + e) * ej] = st[i * XR + j0 + e];
+    }
+}
+
+template <int NK, typename TO>
+__global__ __launch_bounds__(64 * (NK / 16)) void gdn_split_y(int Tn, int H, int BH, GdnSplit sp, TO* __restrict__ o) {
+    constexpr int KS = NK / 32, TJ = NK / 16, XR = NK + 4, NT = 64 * TJ;
+    __shared__ float zt[GC * XR];    // the chunk's z tile as rows [t][j]
+    __shared__ TO yt[GC * NK];       // its o tile [t][i]
+    const int ngy = (sp.m + GFY - 1) / GFY;  // chunk groups per segment
+    const int sgm = 1 + blockIdx.x / ngy, cg = blockIdx.x % ngy, bh = blockIdx.y, bb = bh / H, h = bh - bb * H;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int q = lane >> 4, r16 = lane & 15;
+    const long NN = (long)NK * NK;
+    // B operand X_s^T for output columns 16w .. 16w+15: lane (q, r16) holds X_s[16w + r16][32t + 8q .. +7]
+    const float* const X = seg_state(sp, BH, bh, sgm, NN);
+    uint4 bhv[KS], blv[KS];
+#pragma unroll
+    for (int t = 0; t < KS; t++) op8f(X + (16 * w + r16) * NK + 32 * t + 8 * q, bhv[t], blv[t]);
+    // this group's chunks that hold steps; each chunk's tiles are loaded one chunk ahead
+    const int cend = min(min(sp.m, (cg + 1) * GFY), (Tn + GC - 1) / GC - sgm * sp.m);
+    const long tile0 = (((long)(sgm - 1) * BH + bh) * sp.m) * TJ * 64;  // float4 index of the segment's tiles
+    float4 zn = {}, yn = {};  // float4 tid of the z tile; y0[4q + e][16w + r16]
+    auto load = [&](int c) {
+        zn = reinterpret_cast<const float4*>(sp.z)[tile0 + (long)c * TJ * 64 + tid];
+        yn = reinterpret_cast<const float4*>(sp.y0)[tile0 + (long)c * TJ * 64 + w * 64 + lane];
+    };
+    if (cg * GFY < cend) load(cg * GFY);
+    for (int c = cg * GFY; c < cend; c++) {  // (block-uniform)
+        const float4 zc = zn, x = yn;
+        if (c + 1 < cend) load(c + 1);
+        {   // z tile: float4 tid (row block tid / 64, lane tid % 64) holds z[4q' + e][16 (tid / 64) + r']
+            float* const d = zt + 4 * ((tid >> 4) & 3) * XR + 16 * (tid >> 6) + (tid & 15);
+            d[0] = zc.x, d[XR] = zc.y, d[2 * XR] = zc.z, d[3 * XR] = zc.w;
+        }
+        __syncthreads();
+        f32x4_t acc = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int t = 0; t < KS; t++) {
+            uint4 ah, al;  // A operand Z: lane (q, r16) holds z[r16][32t + 8q .. +7]
+            op8f(zt + r16 * XR + 32 * t + 8 * q, ah, al);
+            acc = mma32(acc, ah, bhv[t]);
+            acc = mma32(acc, ah, blv[t]);
+            acc = mma32(acc, al, bhv[t]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) io<TO>::st(yt, (4 * q + e) * NK + 16 * w + r16, acc[e]);
+        __syncthreads();
+        // 16 rows of NK outputs in 16-byte pieces
+        constexpr int PR = NK * (int)sizeof(TO) / 16;
+        for (int idx = tid; idx < GC * PR; idx += NT) {
+            const int rr = idx / PR, pc = idx - rr * PR, tabs = GC * (sgm * sp.m + c) + rr;
+            if (tabs < Tn)
+                reinterpret_cast<uint4*>(o + ((long)(bb * Tn + tabs) * H + h) * NK)[pc] =
+                    reinterpret_cast<const uint4*>(yt + rr * NK)[pc];
+        }
+        __syncthreads();  // (zt and yt are rewritten by the next chunk)
+    }
+}
+
+// chunks per segment for k segments of n chunks
+int gdn_seg_chunks(int n, int k) { return (n + k - 1) / k; }
 }  // namespace
 
 size_t gdn_forward_workspace(int B, int T, int H, int N) {
     const size_t rec = N == 128 ? GdnRec<128>::BYTES : GdnRec<64>::BYTES;
     return (size_t)B * H * ((T + GC - 1) / GC) * rec;
+}
+// Segments of the time-split scan: with at least 8 chunks, as many as fit one workgroup
+// per CU (B*H*N/64 per segment), at most 4, each with at least one chunk; 1 = no split.
+int gdn_split_segments(int B, int T, int H, int N, int cus) {
+    const int n = (T + GC - 1) / GC, per = B * H * (N / 64);
+    if (n < 8 || per < 1) return 1;
+    int k = min(4, cus / per);
+    while (k > 1 && (long)(k - 1) * gdn_seg_chunks(n, k) >= n) k--;
+    return max(k, 1);
+}
+size_t gdn_forward_workspace_split(int B, int T, int H, int N, int cus) {
+    const int k = gdn_split_segments(B, T, H, N, cus);
+    if (k < 2) return gdn_forward_workspace(B, T, H, N);
+    const size_t m = gdn_seg_chunks((T + GC - 1) / GC, k), BH = (size_t)B * H, NN = (size_t)N * N;
+    const size_t recs = (gdn_forward_workspace(B, T, H, N) + 255) / 256 * 256;
+    return recs + BH * ((2 * k - 1) * NN + 2 * (k - 1) * m * GC * N) * sizeof(float);
 }
 // Row groups per head for the scan: groups of four waves (64 value rows).  Measured at
 // B=1, T=2048 (MI355X): N=128 in 2 groups 0.248 ms against 0.279 (1), 0.292 (4) and
@@ -344,8 +578,26 @@ static void launch_gdn(const Gdn& p) {
     hipLaunchKernelGGL((gdn_prep<NK, TI>), dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, p.qk_norm,
                        static_cast<const TI*>(p.q), static_cast<const TI*>(p.k), static_cast<const TI*>(p.v), p.g,
                        p.beta, static_cast<uint8_t*>(p.ws));
-    hipLaunchKernelGGL((gdn_scan<NK, TI>), dim3(BH * rgs), dim3(lanes), 0, p.stream, p.T, p.H, BH, p.kv, p.s0,
-                       static_cast<TI*>(p.o), p.sT, static_cast<const uint8_t*>(p.ws));
+    const int k = gdn_split_segments(p.B, p.T, p.H, NK, p.cus);
+    if (k < 2 || p.ws_bytes < gdn_forward_workspace_split(p.B, p.T, p.H, NK, p.cus)) {
+        hipLaunchKernelGGL((gdn_scan<NK, TI, false>), dim3(BH * rgs), dim3(lanes), 0, p.stream, p.T, p.H, BH, p.kv,
+                           p.s0, static_cast<TI*>(p.o), p.sT, static_cast<const uint8_t*>(p.ws), GdnSplit{});
+        return;
+    }
+    // the time split: buffers after the records
+    GdnSplit sp;
+    sp.k = k, sp.m = gdn_seg_chunks(nchunk, k);
+    const size_t NN = (size_t)NK * NK, per = (size_t)(k - 1) * BH;
+    float* const base = reinterpret_cast<float*>(static_cast<uint8_t*>(p.ws) +
+                                                 (gdn_forward_workspace(p.B, p.T, p.H, NK) + 255) / 256 * 256);
+    sp.send0 = base, sp.uend = base + BH * NN, sp.phi = sp.uend + per * NN;
+    sp.y0 = sp.phi + per * NN, sp.z = sp.y0 + per * sp.m * GC * NK;
+    hipLaunchKernelGGL((gdn_scan<NK, TI, true>), dim3(k * BH * rgs), dim3(lanes), 0, p.stream, p.T, p.H, BH, p.kv,
+                       p.s0, static_cast<TI*>(p.o), p.sT, static_cast<const uint8_t*>(p.ws), sp);
+    hipLaunchKernelGGL((gdn_split_chain<NK>), dim3(BH), dim3(64 * (NK / 16)), 0, p.stream, BH, p.kv, sp, p.sT);
+    // chunk groups of segments 1 .. k-1; heads along y
+    hipLaunchKernelGGL((gdn_split_y<NK, TI>), dim3((k - 1) * ((sp.m + GFY - 1) / GFY), BH), dim3(64 * (NK / 16)), 0,
+                       p.stream, p.T, p.H, BH, sp, static_cast<TI*>(p.o));
 }
 void launch_gdn_forward(const Gdn& p) {
     if (p.N == 128) {

@@ -233,7 +233,7 @@ static int gdn_dims(int B, int T, int H, int N) {
 }
 
 size_t theseus_gdn_forward_workspace_size(int B, int T, int H, int N) {
-    return gdn_dims(B, T, H, N) ? 0 : wkv7::gdn_forward_workspace(B, T, H, N);
+    return gdn_dims(B, T, H, N) ? 0 : wkv7::gdn_forward_workspace_split(B, T, H, N, wkv7::cu_count());
 }
 
 int theseus_gdn_forward(int B, int T, int H, int N, int dtype, int qk_l2norm, const void* q, const void* k,
@@ -244,6 +244,8 @@ int theseus_gdn_forward(int B, int T, int H, int N, int dtype, int qk_l2norm, co
     if (!q || !k || !v || !g || !beta || !s0 || !o || !sT) return THESEUS_WKV7_ERR_NULL;
     if (!workspace || workspace_bytes < wkv7::gdn_forward_workspace(B, T, H, N)) return THESEUS_WKV7_ERR_WORKSPACE;
     wkv7::Gdn p{B, T, H, N, dtype, qk_l2norm ? 1 : 0, q, k, v, g, beta, s0, o, sT, workspace, 1, stream};
+    p.ws_bytes = workspace_bytes;
+    p.cus = wkv7::cu_count();
     wkv7::launch_gdn_forward(p);
     return launch_status();
 }

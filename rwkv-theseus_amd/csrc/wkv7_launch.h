@@ -79,8 +79,14 @@ struct Gdn {
     void* ws;
     int kv;
     hipStream_t stream;
+    size_t ws_bytes = 0;  // bytes at ws: the time-split scan runs when they cover its buffers
+    int cus = 0;          // CUs the time split may spread the segments over (0: no split)
 };
+// the operand records (the least a call needs); with the time split's buffers when it
+// applies (gdn_split_segments >= 2)
 size_t gdn_forward_workspace(int B, int T, int H, int N);
+size_t gdn_forward_workspace_split(int B, int T, int H, int N, int cus);
+int gdn_split_segments(int B, int T, int H, int N, int cus);
 void launch_gdn_forward(const Gdn& p);
 
 // Family dispatch (wkv7_capi.cpp): the chunked MFMA kernels when they cover

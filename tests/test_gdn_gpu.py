@@ -273,3 +273,63 @@ def test_patch_routes_gradient_calls_to_transformers():
     qg = q.clone().requires_grad_()
     mod.torch_chunk_gated_delta_rule(qg, k, v, g, beta, initial_state=s0)
     assert calls == ["theirs"]
+
+
+def _gdn_capi(lib, q, k, v, g, beta, s0, qk_norm, ws_bytes):
+    """theseus_gdn_forward with a workspace of ws_bytes (the time split runs when it covers
+    theseus_gdn_forward_workspace_size, the one-pass scan with just the records)."""
+    B, T, H, N = q.shape
+    o = torch.full_like(q, float("nan"))
+    sT = torch.full_like(s0, float("nan"))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device="cuda")
+    p = lambda t: t.data_ptr()  # noqa: E731
+    st = lib.theseus_gdn_forward(B, T, H, N, 0 if q.dtype == torch.bfloat16 else 1, int(qk_norm), p(q), p(k),
+                                 p(v), p(g), p(beta), p(s0), p(o), p(sT), p(ws), ws_bytes,
+                                 torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.theseus_wkv7_error_string(st)
+    torch.cuda.synchronize()
+    return o, sT, ws
+
+
+@pytest.mark.parametrize("B,T,H,N,dtype", [
+    (1, 300, 4, 128, torch.float32), (2, 200, 3, 64, torch.float32), (1, 130, 2, 128, torch.bfloat16),
+    (1, 1024, 32, 128, torch.bfloat16), (1, 512, 48, 64, torch.float32)])
+def test_chunked_gdn_time_split(B, T, H, N, dtype, monkeypatch):
+    """With at least 8 chunks and CUs for 2+ workgroups per row group, a workspace of
+    theseus_gdn_forward_workspace_size runs the scan in k = min(4, CUs / (B*H*N/64))
+    segments at once (segment 0 from s0; later ones from zero and from the identity, side
+    by side) and chains them in the fix-up kernel; with just the operand records it runs
+    the one-pass scan.  Both against the float64 oracle at the I/O dtype's bar, and
+    against each other (float32 I/O: rel-L2 <= 1e-5; bf16 o: the output bar).  The
+    teacher's geometry (32 heads, K = V = 128) at T=1024 included; 48 heads of 64 keys
+    would fit 5 segments, the cap is 4."""
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    lib = W.extension().lib
+    qd, kd, vd, g, beta, s0 = _chunked_inputs(B, T, H, N, seed=T + H + N)
+    q, k, v = (x.to(dtype).cuda().contiguous() for x in (qd, kd, vd))
+    g, beta, s0 = (x.float().cuda().contiguous() for x in (g, beta, s0))
+    full = int(lib.theseus_gdn_forward_workspace_size(B, T, H, N))
+    rec = B * H * -(-T // 16) * (43264 if N == 128 else 22784)
+    n = -(-T // 16)
+    kseg = min(4, 256 // (B * H * (N // 64)))
+    while kseg > 1 and (kseg - 1) * -(-n // kseg) >= n:
+        kseg -= 1
+    m = -(-n // kseg)
+    print(f"  gdn time split B={B} T={T} H={H} N={N} {dtype}: {kseg} segments of {m} chunks", flush=True)
+    assert kseg >= 2
+    assert full == -(-rec // 256) * 256 + 4 * B * H * ((2 * kseg - 1) * N * N + 2 * (kseg - 1) * m * 16 * N)
+    o_s, s_s, ws = _gdn_capi(lib, q, k, v, g, beta, s0, False, full)
+    # the split ran: its first buffer (segment 0's final states) is written
+    x1 = ws[-(-rec // 256) * 256:].view(torch.float32)[:B * H * N * N]
+    assert bool(torch.isfinite(x1).all())
+    o_1, s_1, _ = _gdn_capi(lib, q, k, v, g, beta, s0, False, rec)
+    ry, rs = O.gdn_forward(*(x.to(dtype).double().numpy() if i < 3 else x.float().double().numpy()
+                             for i, x in enumerate((qd, kd, vd, g.cpu(), beta.cpu(), s0.cpu()))))
+    bar = 1e-4 if dtype == torch.float32 else 5e-3
+    for name, a, b, r in [("o", o_s, o_1, ry), ("sT", s_s, s_1, rs)]:
+        a64, b64 = a.double().cpu().numpy(), b.double().cpu().numpy()
+        e_ref, e_one = rel_l2(a64, r), rel_l2(a64, b64)
+        print(f"    {name}: split vs oracle {e_ref:.2e}, vs one-pass {e_one:.2e}", flush=True)
+        assert np.isfinite(a64).all()
+        assert e_ref <= (1e-4 if name == "sT" else bar) and e_one <= (1e-5 if dtype == torch.float32 or name == "sT" else bar)
+    assert max_abs(s_s.cpu(), rs) <= 2e-2

@@ -25,9 +25,25 @@ pytestmark = pytest.mark.gpu
 REL_L2 = 5e-3
 MAX_ABS = 2e-2
 REL_L2_FP32 = 1e-4
-# the time-split forward against the one-pass kernels on the same inputs: the two round
-# differently (fp32 fix-up sums against split-bf16 matrix-core products), nothing more
+# the time-split forward against the one-pass kernels on the same inputs (each is also
+# checked against the oracle): the two round differently (fp32 fix-up sums against
+# split-bf16 matrix-core products), nothing more -- float32 states within rel-L2 1e-4;
+# bf16 y within rel-L2 1e-3 and, elementwise, twice the oracle bar (each output is within
+# that bar of the exact value; with no decay at all the states grow to hundreds and the
+# two differ by up to two bf16 ULPs where |y| ~ 100)
 SPLIT_VS_ONE_PASS = 1e-4
+
+
+def _split_vs_one_pass(name, got, one):
+    a = got.float().cpu().numpy().astype(np.float64)
+    b = one.float().cpu().numpy().astype(np.float64)
+    rl = rel_l2(a, b)
+    print(f"    {name:4s} split-vs-one-pass rel_l2={rl:.2e} max_abs={max_abs(a, b):.2e}", flush=True)
+    if got.dtype == torch.float32:
+        assert rl <= SPLIT_VS_ONE_PASS, (name, rl)
+    else:
+        assert rl <= 1e-3, (name, rl)
+        assert np.all(np.abs(a - b) <= 2 * (MAX_ABS + 2.0 ** -7 * np.maximum(np.abs(a), np.abs(b)))), name
 NAMES = ["y", "sT", "dr", "dw", "dk", "dv", "da", "db", "ds0"]
 
 
@@ -187,9 +203,7 @@ def test_config1_chunked_equals_unchunked(monkeypatch):
     for name, got, ref, o in [("y", split[0], y_ref, one[0]), ("sT", split[1], s_ref, one[1]),
                               ("y", split[2], y_ref, one[0]), ("sT", split[3], s_ref, one[1])]:
         _check(name, got, ref, torch.bfloat16)
-        rl = rel_l2(got.float().cpu().numpy(), o.float().cpu().numpy())
-        print(f"    {name:4s} split-vs-one-pass rel_l2={rl:.2e}", flush=True)
-        assert rl <= SPLIT_VS_ONE_PASS, (name, rl)
+        _split_vs_one_pass(name, got, o)
 
 
 # -- config 4: in-place decode ---------------------------------------------------------
@@ -467,9 +481,7 @@ def test_time_split_forward_against_oracle_and_one_pass(B, T, H, monkeypatch):
     y_ref, s_ref = O.forward_c(*(inp[n].double().numpy() for n in "rwkvab"), inp["s0"].double().numpy())
     for name, got, ref, o in [("y", y_s, y_ref, y_1), ("sT", s_s, s_ref, s_1)]:
         _check(name, got, ref, torch.bfloat16)
-        rl = rel_l2(got.float().cpu().numpy(), o.float().cpu().numpy())
-        print(f"    {name:4s} split-vs-one-pass rel_l2={rl:.2e}", flush=True)
-        assert rl <= SPLIT_VS_ONE_PASS, (name, rl)
+        _split_vs_one_pass(name, got, o)
     # and through the operator: a no-grad call takes the split, a grad call does not
     with torch.no_grad():
         y_op, s_op = W.wkv7(*xs, s0)
@@ -494,3 +506,30 @@ def test_time_split_is_not_taken_beyond_its_limits(monkeypatch):
     y_h, s_h, saved = ext.forward(*xs, s0, True)
     y_1, s_1 = _capi_forward(lib, xs, s0, None, 0)
     assert torch.equal(y_h, y_1) and torch.equal(s_h, s_1)
+
+
+@pytest.mark.parametrize("mode", ["wide", "max_decay", "no_decay"])
+def test_time_split_forward_at_the_ends_of_the_decay_range(mode, monkeypatch):
+    """The time split's identity runs at the decay limits: w ~ N(0, 8^2), w = +30 (every
+    step at the strongest decay: the transitions Phi_s shrink towards the a b^T part) and
+    w = -30 (no decay: Phi_s stays near the identity).  y and the final state against the
+    oracle and the one-pass kernels, 4 segments per head."""
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    B, T, H, N = 1, 400, 6, 64
+    inp = wkv7_inputs(B, T, H, N, seed=4343, dtype=torch.bfloat16, s0_std=0.1)
+    w = inp["w"].float()
+    w = {"wide": 8.0 * w, "max_decay": torch.full_like(w, 30.0), "no_decay": torch.full_like(w, -30.0)}[mode]
+    inp["w"] = w.to(torch.bfloat16).contiguous()
+    print(f"  time split decays={mode} B={B} T={T} H={H}", flush=True)
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
+    lib = W.extension().lib
+    need = int(lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0))
+    assert need > 0
+    ws = torch.empty((need,), dtype=torch.uint8, device="cuda")
+    y_s, s_s = _capi_forward(lib, xs, s0, ws, need)
+    y_1, s_1 = _capi_forward(lib, xs, s0, None, 0)
+    y_ref, s_ref = O.forward_c(*(inp[n].double().numpy() for n in "rwkvab"), inp["s0"].double().numpy())
+    for name, got, ref, o in [("y", y_s, y_ref, y_1), ("sT", s_s, s_ref, s_1)]:
+        _check(name, got, ref, torch.bfloat16)
+        _split_vs_one_pass(name, got, o)
