@@ -389,7 +389,7 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
 // (rows of X_s as its B operand in registers); per chunk the z tile is turned into rows in
 // LDS, y0 comes in the accumulator layout, o leaves in whole rows through LDS.
 // ---------------------------------------------------------------------------
-constexpr int GFY = 8;  // chunks per gdn_split_y workgroup
+constexpr int GFY = 8;  // chunks per gdn_split_y workgroup (2 measured slower: 21.6 against 19.3 us)
 __device__ __forceinline__ void op8f(const float* p, uint4& hi, uint4& lo) {  // 8 floats, split
     const float4 x0 = *reinterpret_cast<const float4*>(p), x1 = *reinterpret_cast<const float4*>(p + 4);
     const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -455,34 +455,40 @@ __global__ __launch_bounds__(64 * (NK / 16)) void gdn_split_chain(int BH, int kv
 #pragma unroll
         for (int t = 0; t < KS; t++) op8f(&st[(16 * w + r16) * XR + 32 * t + 8 * q], ah[t], al[t]);
         wave_lds_fence();  // (the strip is overwritten below)
+        // the TJ output tiles' products interleaved (independent accumulator chains)
+        f32x4_t acc[TJ];
 #pragma unroll
-        for (int n = 0; n < TJ; n++) {
-            f32x4_t acc = {acc0[n][0], acc0[n][1], acc0[n][2], acc0[n][3]};
+        for (int n = 0; n < TJ; n++) acc[n] = f32x4_t{acc0[n][0], acc0[n][1], acc0[n][2], acc0[n][3]};
 #pragma unroll
-            for (int t = 0; t < KS; t++) {
+        for (int t = 0; t < KS; t++)
+#pragma unroll
+            for (int n = 0; n < TJ; n++) {
                 const uint4 bhv = fr[(2 * (n * KS + t)) * 64 + lane], blv = fr[(2 * (n * KS + t) + 1) * 64 + lane];
-                acc = mma32(acc, ah[t], bhv);
-                acc = mma32(acc, ah[t], blv);
-                acc = mma32(acc, al[t], bhv);
+                acc[n] = mma32(acc[n], ah[t], bhv);
+                acc[n] = mma32(acc[n], ah[t], blv);
+                acc[n] = mma32(acc[n], al[t], bhv);
             }
+#pragma unroll
+        for (int n = 0; n < TJ; n++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                st[(16 * w + 4 * q + e) * XR + 16 * n + r16] = acc[e];
-                if (u + 1 < sp.k) sp.uend[ob + (16 * w + 4 * q + e) * NK + 16 * n + r16] = acc[e];  // X_{u+1}
+                st[(16 * w + 4 * q + e) * XR + 16 * n + r16] = acc[n][e];
+                if (u + 1 < sp.k) sp.uend[ob + (16 * w + 4 * q + e) * NK + 16 * n + r16] = acc[n][e];  // X_{u+1}
             }
-        }
         __syncthreads();  // everyone is done with Phi_u
         if (u + 1 < sp.k) GDN_CHAIN_STAGE();
-        __syncthreads();
+        __syncthreads();  // (and, after the last step, every row of X_k is in st)
     }
 #undef GDN_CHAIN_LOAD
 #undef GDN_CHAIN_STAGE
-    const long ei = kv ? 1 : NK, ej = kv ? NK : 1;  // sT = X_k, this wave's rows, in the caller's layout
+    // sT = X_k in the caller's layout, whole rows: float4 number v*NT + tid of row a,
+    // columns c .. c+3 (kv: sT[a = j][c = i] = X[i][j], read down a column of st)
 #pragma unroll
-    for (int u = 0; u < NK / 16; u++) {
-        const int f = 4 * (u * 64 + lane), i = 16 * w + f / NK, j0 = f % NK;
-#pragma unroll
-        for (int e = 0; e < 4; e++) sT[bh * NN + i * ei + (j0 + e) * ej] = st[i * XR + j0 + e];
+    for (int v = 0; v < NK * NK / 4 / NT; v++) {
+        const int f = 4 * (v * NT + tid), a = f / NK, c = f % NK;
+        const float4 x = kv ? make_float4(st[c * XR + a], st[(c + 1) * XR + a], st[(c + 2) * XR + a], st[(c + 3) * XR + a])
+                            : *reinterpret_cast<const float4*>(&st[a * XR + c]);
+        *reinterpret_cast<float4*>(sT + bh * NN + f) = x;
     }
 }
 
