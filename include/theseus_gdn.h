@@ -32,7 +32,11 @@ typedef struct ihipStream_t* hipStream_t;
  *               (use_qk_l2norm_in_kernel); zero: used as given
  *   N = 64 or 128 (else THESEUS_WKV7_ERR_SHAPE); workspace of
  *   theseus_gdn_forward_workspace_size bytes (every 16-step chunk's operands,
- *   42 KB per chunk at N = 128), not shared with a call that can run at the
+ *   42 KB per chunk at N = 128, and, with few heads -- B*H*N/64 workgroups at
+ *   most half the CUs, T > 112 -- the buffers of the time-split scan, which
+ *   cuts each head's chunks into k = min(4, CUs / (B*H*N/64)) segments run at
+ *   once; a workspace of just the operand records runs the one-pass scan, to
+ *   float32 rounding the same), not shared with a call that can run at the
  *   same time.  Replaces the forward of transformers' torch_chunk_gated_delta_rule
  *   (chunk_size is not used) and torch_recurrent_gated_delta_rule. */
 int theseus_gdn_forward(int B, int T, int H, int N, int dtype, int qk_l2norm, const void* q,
