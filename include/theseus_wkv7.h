@@ -104,12 +104,13 @@ long long theseus_wkv7_checkpoint_count(int T);
  * the step-serial backward replays each 16-step segment into it.  For few
  * heads (chunked kernels, 2*B*H <= CUs, T > 112) the forward size also covers
  * the time-split forward: a forward without saved states given that much cuts
- * every head's steps into k = min(4, CUs / (B*H)) segments (fewer if the last
- * would be empty) that run at once, one workgroup each, and chains them with
- * a fix-up kernel; it agrees with the one-pass kernels to float32 rounding.
- * Given less (none is needed at such sizes) it runs the one-pass kernels.
- * The split's buffers are 4 * B*H * ((2k-1)*N*N + 2(k-1)*m*16*N) bytes,
- * m = ceil(ceil(T/16) / k).  Contents need not be initialised (each
+ * every head's steps into k = min(4, CUs / (B*H)) segments that run at once,
+ * one workgroup each, and chains them with a fix-up kernel; it agrees with
+ * the one-pass kernels to float32 rounding.  Given less (none is needed at
+ * such sizes) it runs the one-pass kernels.  The split's buffers are
+ * 4 * B*H * ((2k-1)*N*N + 2(k-1)*m*16*N) bytes, m the chunk count of each
+ * segment after the first (segment 0, which carries one state instead of
+ * two, takes ceil(T/16) - (k-1)m, about 1.2 m).  Contents need not be initialised (each
  * call clears what it uses, on its stream), and a workspace must not be
  * shared by calls that may run at the same time. */
 size_t theseus_wkv7_forward_workspace_size(int B, int T, int H, int N, int dtype);

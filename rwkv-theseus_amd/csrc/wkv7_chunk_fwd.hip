@@ -111,7 +111,9 @@ __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&
 
 // The time-split forward (SPLIT): the state after a chunk is affine in the state before
 // it, S_{c+1} = S_c M_c + U_c, so with few heads each head's chunks are cut into k
-// segments of m that all run at once, one job (workgroup) per (segment, head):
+// segments that all run at once, one job (workgroup) per (segment, head), segment 0 of m0
+// chunks and the others of m (segment 0 carries one state and ticks faster, so it takes
+// more chunks):
 //  * segment 0 runs from s0 and writes y as usual, its final state S_1 to the workspace;
 //  * segment s >= 1 runs two states side by side on the same chunk operands, each
 //    consumer wave holding its rows of both: one from zero (y0 and the final state U_s),
@@ -120,7 +122,8 @@ __device__ __forceinline__ f32x4_t mm_keys8(const uint4 (&xh)[2], const uint4 (&
 // split_fixup then chains S_{s+1} = S_s Phi_s + U_s, forms y_t = y0_t + S_s z_t over
 // segment s and writes sT = S_k (wkv7_capi.cpp decides when).
 struct SplitArgs {
-    int BH = 0, m = 0, k = 0;  // heads, chunks per segment, segments
+    int BH = 0, m = 0, k = 0;  // heads, chunks of segments 1 .., segments
+    int m0 = 0;                // chunks of segment 0
     float* send0 = nullptr;    // S_1 [BH][64][64]
     float* uend = nullptr;     // U_s [k - 1][BH][64][64]
     float* phi = nullptr;      // Phi_s, the same layout
@@ -136,7 +139,10 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     float* __restrict__ sT, float* __restrict__ ckpt, uint32_t* __restrict__ flags, float* __restrict__ hand,
     SplitArgs sp) {
     __shared__ FwdLds sm;
-    const int m = machine_of_block(sc), nstream = stream_len(sc, m);
+    const int m = machine_of_block(sc);
+    // (SPLIT: one job per machine, job m; its segment's length)
+    const int nstream = SPLIT ? (m < sp.BH ? sp.m0 : sp.m) : stream_len(sc, m);
+    auto seg_first = [&](int sg) { return sg == 0 ? 0 : sp.m0 + (sg - 1) * sp.m; };  // (SPLIT) first chunk
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int lane = tid & 63, q = lane >> 4, r16 = lane & 15;
     const long NN = (long)NK * NK;
@@ -147,15 +153,14 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     // bytes of one [B,T,H,64] tensor (SPLIT: the schedule's jobs are k per head)
     const uint32_t tbytes = (uint32_t)((long)(SPLIT ? sp.BH : sc.J) * Tn * NK * 2);
     // stream position (cursor) -> byte offset of the chunk's first row, its valid length
-    // (SPLIT: job j is segment j / BH of head j % BH, whose steps start at chunk m * segment;
-    //  chunks past the end of the last segment have no valid steps)
+    // (SPLIT: job j is segment j / BH of head j % BH, whose steps start at seg_first)
     auto chunk_off = [&](const Cursor& cu) {
         if (!SPLIT) return (uint32_t)(((long)(cu.bb * Tn + cu.step * CH) * H + cu.h) * NK * 2);
         const int sg = cu.j / sp.BH, head = cu.j - sg * sp.BH, b2 = head / H, h2 = head - b2 * H;
-        return (uint32_t)(((long)(b2 * Tn + (cu.step + sg * sp.m) * CH) * H + h2) * NK * 2);
+        return (uint32_t)(((long)(b2 * Tn + (cu.step + seg_first(sg)) * CH) * H + h2) * NK * 2);
     };
     auto chunk_len = [&](const Cursor& cu) {
-        return min(CH, Tn - (cu.step + (SPLIT ? cu.j / sp.BH * sp.m : 0)) * CH);
+        return min(CH, Tn - (cu.step + (SPLIT ? seg_first(cu.j / sp.BH) : 0)) * CH);
     };
 
     // ---------------- producer state ----------------
@@ -368,7 +373,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
           const int head = SPLIT ? j - sgm * sp.BH : j;
           const int bb = head / H, h = head - bb * H;
           const long bh = head;
-          const int c_seg = SPLIT ? sgm * sp.m : 0;       // the segment's first chunk
+          const int c_seg = SPLIT ? seg_first(sgm) : 0;    // the segment's first chunk
           const bool dual = SPLIT && sgm > 0;              // the zero and identity runs
           if (sg.fresh) {  // the initial state: s0 at the head's start ...
 #pragma unroll
@@ -394,7 +399,7 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 St[tj] = f32x4_t{x.x, x.y, x.z, x.w} * bad;
             }
           }
-          for (int kk = 0; kk < sg.count; kk++, n++) {
+          for (int kk = 0; kk < (SPLIT ? nstream : sg.count); kk++, n++) {
             // ---------------- consumer: rows i_own through chunk c of head j ----------------
             const Slot& S = sm.slot[n % NSLOT];
             const int c = sg.step0 + kk + c_seg;
@@ -605,7 +610,8 @@ __global__ __launch_bounds__(256) void split_fixup(int Tn, int H, SplitArgs sp, 
     }
     __syncthreads();  // all of S_s
     const int c = (grp % ngm) * FXG + w;  // chunk within segment sgm (wave-uniform)
-    if (c >= sp.m || CH * (sgm * sp.m + c) >= Tn) return;
+    const int cfirst = sp.m0 + (sgm - 1) * sp.m;  // the segment's first chunk
+    if (c >= sp.m || CH * (cfirst + c) >= Tn) return;
     // B operand S_s^T: lane (q, r16) of tile n, K step t holds S_s[16n + r16][32t + 8q .. +7]
     uint4 bh[4][2], bl[4][2];
 #pragma unroll
@@ -643,15 +649,26 @@ __global__ __launch_bounds__(256) void split_fixup(int Tn, int H, SplitArgs sp, 
     // 16 rows of 128 bytes: 8 lanes per row, two rows per lane
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
-        const int rr = 8 * hf + (lane >> 3), pc = lane & 7, tabs = CH * (sgm * sp.m + c) + rr;
+        const int rr = 8 * hf + (lane >> 3), pc = lane & 7, tabs = CH * (cfirst + c) + rr;
         if (tabs < Tn)
             *reinterpret_cast<uint4*>(y + ((long)(bb * Tn + tabs) * H + h) * NK + 8 * pc) =
                 *reinterpret_cast<const uint4*>(&yw[rr * NK + 8 * pc]);
     }
 }
 
-// chunks per segment for k segments of n chunks
-int seg_chunks(int n, int k) { return (n + k - 1) / k; }
+// Lengths of k segments over n chunks: segment 0 (one state per consumer wave) ticks about
+// 1.2x faster than the others (two states; measured per workgroup at T=4096: 1.59 against
+// 1.90 us with 80 heads, 1.45 against 1.71 with 16), so m0 = n - (k-1) m chunks go to it
+// with m minimising max(5 m0, 6 m); every segment holds at least one chunk and none runs
+// past the end.
+void split_lengths(int n, int k, int& m0, int& m) {
+    int best = 1 << 30;
+    m0 = n, m = 0;
+    for (int mm = 1; n - (k - 1) * mm >= 1; mm++) {
+        const int r = n - (k - 1) * mm, cost = max(5 * r, 6 * mm);
+        if (cost < best) best = cost, m0 = r, m = mm;
+    }
+}
 }  // namespace
 
 // Segments of the time-split forward for B*H heads of n chunks on `cus` CUs: as many as fit
@@ -659,25 +676,26 @@ int seg_chunks(int n, int k) { return (n + k - 1) / k; }
 // each with at least one valid chunk; 1 = no split.
 int chunk_forward_split_segments(int BH, int T, int cus) {
     const int n = (T + CH - 1) / CH;
-    int k = BH > 0 ? min(4, cus / BH) : 1;
-    while (k > 1 && (long)(k - 1) * seg_chunks(n, k) >= n) k--;
-    return max(k, 1);
+    const int k = BH > 0 ? min(4, cus / BH) : 1;
+    return max(1, min(k, n));
 }
 size_t chunk_forward_split_workspace(int B, int T, int H, int cus) {
     const int BH = B * H, k = chunk_forward_split_segments(BH, T, cus);
     if (k < 2) return 0;
-    const size_t m = seg_chunks((T + CH - 1) / CH, k);
-    return (size_t)BH * ((2 * k - 1) * (size_t)NK * NK + 2 * (k - 1) * m * CH * NK) * sizeof(float);
+    int m0, m;
+    split_lengths((T + CH - 1) / CH, k, m0, m);
+    return (size_t)BH * ((2 * k - 1) * (size_t)NK * NK + 2 * (k - 1) * (size_t)m * CH * NK) * sizeof(float);
 }
 void launch_chunk_forward_split(const Fwd& p, int cus) {
     SplitArgs sp;
     sp.BH = p.B * p.H, sp.k = chunk_forward_split_segments(sp.BH, p.T, cus);
-    sp.m = seg_chunks((p.T + CH - 1) / CH, sp.k);
+    split_lengths((p.T + CH - 1) / CH, sp.k, sp.m0, sp.m);
     const size_t NN = (size_t)NK * NK, per = (size_t)(sp.k - 1) * sp.BH;
     float* const base = static_cast<float*>(p.ws);
     sp.send0 = base, sp.uend = base + sp.BH * NN, sp.phi = sp.uend + per * NN;
     sp.y0 = sp.phi + per * NN, sp.z = sp.y0 + per * sp.m * CH * NK;
-    const Sched sc = plan_schedule(sp.k * sp.BH, sp.m, cus);  // one job per workgroup, no cuts
+    // one job per workgroup, no cuts (jobs planned at the longest segment; each runs its own)
+    const Sched sc = plan_schedule(sp.k * sp.BH, max(sp.m0, sp.m), cus);
     hipLaunchKernelGGL(chunk_forward_bf16<true>, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
                        (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, nullptr, nullptr,

@@ -443,12 +443,20 @@ def _capi_forward(lib, xs, s0, ws, ws_bytes):
 
 
 def _segments(BH, T, cus=256):
-    """Segments and chunks per segment of the time-split forward (as the library plans)."""
+    """Segments, and chunks of segment 0 and of each later one, of the time-split forward
+    as the library plans them: k = min(4, CUs / (B*H), chunks); segment 0 (one state per
+    wave, about 1.2x faster per chunk) takes m0 = n - (k-1) m chunks, m minimising
+    max(5 m0, 6 m)."""
     n = -(-T // 16)
-    k = min(4, cus // BH)
-    while k > 1 and (k - 1) * -(-n // k) >= n:
-        k -= 1
-    return k, -(-n // k)
+    k = min(4, cus // BH, n)
+    best = None
+    for m in range(1, n):
+        m0 = n - (k - 1) * m
+        if m0 < 1:
+            break
+        if best is None or max(5 * m0, 6 * m) < best[0]:
+            best = (max(5 * m0, 6 * m), m0, m)
+    return k, best[1], best[2]
 
 
 @pytest.mark.parametrize("B,T,H", [(1, 128, 2), (2, 300, 3), (1, 1000, 5), (3, 512, 4), (1, 113, 1),
@@ -456,16 +464,16 @@ def _segments(BH, T, cus=256):
 def test_time_split_forward_against_oracle_and_one_pass(B, T, H, monkeypatch):
     """With at least two CUs per head and at least 8 chunks, a forward without saved
     states given theseus_wkv7_forward_workspace_size bytes cuts each head's chunks into
-    k = min(4, CUs / (B*H)) segments (fewer if the last would be empty) that run at once
-    -- segment 0 from s0, each later one from zero and from the identity side by side --
-    and chains them in the fix-up kernel; given no workspace it runs the one-pass
-    kernels.  Here k = 4, 4, 4, 4, 4, 3 (9 chunks), 3 (80 heads), 2 (100 heads); the last
-    segment ends with empty chunks when k does not divide the chunk count, and partial
-    chunks fall at the end (T % 16)."""
+    k = min(4, CUs / (B*H)) segments that run at once -- segment 0 from s0, each later
+    one from zero and from the identity side by side -- and chains them in the fix-up
+    kernel; given no workspace it runs the one-pass kernels.  Here k = 4 (1-12 heads),
+    3 (80 heads), 2 (100 heads), segment 0 about 1.2x as long as the others (m0 = 2, 4,
+    18, 8, 2, 3, 7, 9 chunks against m = 2, 5, 15, 8, 2, 2, 6, 7); partial chunks fall at
+    the end (T % 16)."""
     monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
     N = 64
-    k, m = _segments(B * H, T)
-    print(f"  time split B={B} T={T} H={H}: {k} segments of {m} chunks", flush=True)
+    k, m0, m = _segments(B * H, T)
+    print(f"  time split B={B} T={T} H={H}: {k} segments, {m0} + {m} chunks", flush=True)
     assert k >= 2
     inp = wkv7_inputs(B, T, H, N, seed=1100 + T + H, dtype=torch.bfloat16, s0_std=0.1)
     xs = [inp[n].cuda() for n in "rwkvab"]
