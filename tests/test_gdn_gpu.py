@@ -311,10 +311,8 @@ def test_chunked_gdn_time_split(B, T, H, N, dtype, monkeypatch):
     full = int(lib.theseus_gdn_forward_workspace_size(B, T, H, N))
     rec = B * H * -(-T // 16) * (43264 if N == 128 else 22784)
     n = -(-T // 16)
-    kseg = min(4, 256 // (B * H * (N // 64)))
-    while kseg > 1 and (kseg - 1) * -(-n // kseg) >= n:
-        kseg -= 1
-    m = -(-n // kseg)
+    kseg = min(4, 256 // (B * H * (N // 64)), n)
+    m = min(range(1, n), key=lambda mm: (max(n - (kseg - 1) * mm, mm) if n - (kseg - 1) * mm >= 1 else n * 9, mm))
     print(f"  gdn time split B={B} T={T} H={H} N={N} {dtype}: {kseg} segments of {m} chunks", flush=True)
     assert kseg >= 2
     assert full == -(-rec // 256) * 256 + 4 * B * H * ((2 * kseg - 1) * N * N + 2 * (kseg - 1) * m * 16 * N)
