@@ -541,3 +541,40 @@ def test_time_split_forward_at_the_ends_of_the_decay_range(mode, monkeypatch):
     for name, got, ref, o in [("y", y_s, y_ref, y_1), ("sT", s_s, s_ref, s_1)]:
         _check(name, got, ref, torch.bfloat16)
         _split_vs_one_pass(name, got, o)
+
+
+def test_time_split_forward_captured_in_a_graph(monkeypatch):
+    """A serving prefill may capture the no-grad forward in a HIP graph: the time split's
+    two kernels (no memset, workspace from the graph's pool) replay to the eager result,
+    bit for bit, on every replay, with eager work and synchronisations between replays
+    and new inputs copied in before each."""
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    B, T, H, N = 1, 512, 8, 64
+    ins = [wkv7_inputs(B, T, H, N, seed=5000 + i, dtype=torch.bfloat16, s0_std=0.1) for i in range(3)]
+    lib = W.extension().lib
+    assert lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0) > 0  # the split applies
+    xs = [ins[0][n].cuda() for n in "rwkvab"]
+    s0 = ins[0]["s0"].cuda()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side), torch.no_grad():
+        for _ in range(2):
+            W.wkv7(*xs, s0)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph), torch.no_grad():
+        y_g, s_g = W.wkv7(*xs, s0)
+    for i in (1, 2, 0, 1):
+        with torch.no_grad():
+            for x, n in zip(xs, "rwkvab"):
+                x.copy_(ins[i][n].cuda())
+            s0.copy_(ins[i]["s0"].cuda())
+            graph.replay()
+            torch.cuda.synchronize()
+            y_e, s_e = W.wkv7(*xs, s0)
+            junk = torch.randn(1 << 20, device="cuda").sum()  # unrelated eager work
+        torch.cuda.synchronize()
+        print(f"  replay with inputs {i}: y equal {torch.equal(y_g, y_e)}, sT equal {torch.equal(s_g, s_e)}",
+              flush=True)
+        assert torch.equal(y_g, y_e) and torch.equal(s_g, s_e), i
+        assert bool(torch.isfinite(junk))
