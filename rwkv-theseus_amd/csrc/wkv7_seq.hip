@@ -211,14 +211,28 @@ __global__ __launch_bounds__(NP) void seq_backward(
             const float* Sn = Sp + NN;
             float gr = 0.f, gw = 0.f, gk = 0.f, gb = 0.f, ga = 0.f;
             if (lane_ok) {
-                for (int i = 0; i < N; i++) {
-                    const float gij = Gs[i * NP + ((i + j) & (NP - 1))];
-                    const float sp = Sp[(long)i * N + j];
-                    gr += vdy[i] * Sn[(long)i * N + j];
-                    gw += gij * sp;
-                    gk += gij * vv[i];
-                    gb += gij * vsa[i];
-                    ga += vq[i] * sp;
+                // 16 rows' state loads in flight at a time (each a coalesced row of the
+                // replayed state), not one dependent load after another
+                for (int i0 = 0; i0 < N; i0 += 16) {
+                    float spv[16], snv[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        const int i = i0 + u;
+                        spv[u] = i < N ? Sp[(long)i * N + j] : 0.f;
+                        snv[u] = i < N ? Sn[(long)i * N + j] : 0.f;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        const int i = i0 + u;
+                        if (i < N) {
+                            const float gij = Gs[i * NP + ((i + j) & (NP - 1))];
+                            gr += vdy[i] * snv[u];
+                            gw += gij * spv[u];
+                            gk += gij * vv[i];
+                            gb += gij * vsa[i];
+                            ga += vq[i] * spv[u];
+                        }
+                    }
                 }
                 io<T>::st(dr, o + j, gr);
                 io<T>::st(dw, o + j, gw * vf[j]);
