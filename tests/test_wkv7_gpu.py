@@ -460,7 +460,7 @@ def _segments(BH, T, cus=256):
 
 
 @pytest.mark.parametrize("B,T,H", [(1, 128, 2), (2, 300, 3), (1, 1000, 5), (3, 512, 4), (1, 113, 1),
-                                   (1, 144, 2), (2, 300, 40), (1, 256, 100)])
+                                   (1, 144, 2), (2, 300, 40), (1, 256, 100), (1, 16381, 2)])
 def test_time_split_forward_against_oracle_and_one_pass(B, T, H, monkeypatch):
     """With at least two CUs per head and at least 8 chunks, a forward without saved
     states given theseus_wkv7_forward_workspace_size bytes cuts each head's chunks into
@@ -468,8 +468,8 @@ def test_time_split_forward_against_oracle_and_one_pass(B, T, H, monkeypatch):
     one from zero and from the identity side by side -- and chains them in the fix-up
     kernel; given no workspace it runs the one-pass kernels.  Here k = 4 (1-12 heads),
     3 (80 heads), 2 (100 heads), segment 0 about 1.2x as long as the others (m0 = 2, 4,
-    18, 8, 2, 3, 7, 9 chunks against m = 2, 5, 15, 8, 2, 2, 6, 7); partial chunks fall at
-    the end (T % 16)."""
+    18, 8, 2, 3, 7, 9, 292 chunks against m = 2, 5, 15, 8, 2, 2, 6, 7, 244); partial chunks
+    fall at the end (T % 16)."""
     monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
     N = 64
     k, m0, m = _segments(B * H, T)
