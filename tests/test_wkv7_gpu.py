@@ -578,3 +578,36 @@ def test_time_split_forward_captured_in_a_graph(monkeypatch):
               flush=True)
         assert torch.equal(y_g, y_e) and torch.equal(s_g, s_e), i
         assert bool(torch.isfinite(junk))
+
+
+def test_time_split_calls_on_concurrent_streams(monkeypatch):
+    """Two time-split forwards on two streams, each with its own workspace, may run at the
+    same time: the split shares nothing between calls (no counters, no handoffs), so each
+    equals the same call made alone, bit for bit."""
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "256")
+    lib = W.extension().lib
+    shapes = [(1, 400, 6), (2, 300, 3)]
+    ins = [wkv7_inputs(B, T, H, 64, seed=6100 + T, dtype=torch.bfloat16, s0_std=0.1) for B, T, H in shapes]
+    calls = []
+    for (B, T, H), inp in zip(shapes, ins):
+        need = int(lib.theseus_wkv7_forward_workspace_size(B, T, H, 64, 0))
+        assert need > 0
+        calls.append(([inp[n].cuda() for n in "rwkvab"], inp["s0"].cuda(),
+                      torch.empty((need,), dtype=torch.uint8, device="cuda"), need))
+    alone = [_capi_forward(lib, xs, s0, ws, need) for xs, s0, ws, need in calls]
+    streams = [torch.cuda.Stream() for _ in calls]
+    outs = []
+    import ctypes
+    p = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
+    for (xs, s0, ws, need), st in zip(calls, streams):
+        st.wait_stream(torch.cuda.current_stream())
+        B, T, H, N = xs[0].shape
+        y = torch.full((B, T, H, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        sT = torch.full((B, H, N, N), float("nan"), dtype=torch.float32, device="cuda")
+        with torch.cuda.stream(st):
+            assert lib.theseus_wkv7_forward(B, T, H, N, 0, *map(p, (*xs, s0, y, sT)), p(None), p(ws),
+                                            ctypes.c_size_t(need), ctypes.c_void_p(st.cuda_stream)) == 0
+        outs.append((y, sT))
+    torch.cuda.synchronize()
+    for (y, sT), (ya, sa) in zip(outs, alone):
+        assert torch.equal(y, ya) and torch.equal(sT, sa)
