@@ -24,7 +24,18 @@ constexpr int HG = 8;    // heads per block of the kk / GroupNorm backward kerne
 struct V8 {
     float x[8];
 };
+// Inputs read exactly once are loaded non-temporally (ld_str8, ld_str4, ld_f8s): measured at
+// config 3, kk_bwd 156 -> 138 µs and kk_fwd 91 -> 82 µs with them; the shift-lerp forward,
+// whose threads re-read the row before their first token, keeps ordinary loads (it ran 4 %
+// slower with them).  Stores stay ordinary: their results are read by the next kernel.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_raw8(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint4 ld_str8(const uint16_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ V8 cvt_bf8(uint4 u) {
     V8 r;
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
@@ -35,7 +46,11 @@ __device__ __forceinline__ V8 cvt_bf8(uint4 u) {
     }
     return r;
 }
-__device__ __forceinline__ V8 ld_bf8(const uint16_t* p) { return cvt_bf8(ld_raw8(p)); }
+__device__ __forceinline__ V8 ld_f8s(const float* p) {
+    const f32x4v_t a = __builtin_nontemporal_load(reinterpret_cast<const f32x4v_t*>(p));
+    const f32x4v_t b = __builtin_nontemporal_load(reinterpret_cast<const f32x4v_t*>(p + 4));
+    return V8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+}
 __device__ __forceinline__ V8 ld_f8(const float* p) {
     const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
     return V8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
@@ -114,7 +129,10 @@ constexpr int UG = 4;
 struct V4 {
     float x[4];
 };
-__device__ __forceinline__ uint2 ld_raw4(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+__device__ __forceinline__ uint2 ld_str4(const uint16_t* p) {
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    return make_uint2(v.x, v.y);
+}
 __device__ __forceinline__ V4 cvt_bf4(uint2 u) {
     return V4{{bf16_to_f32((uint16_t)(u.x & 0xffffu)), bf16_to_f32((uint16_t)(u.x >> 16)),
                bf16_to_f32((uint16_t)(u.y & 0xffffu)), bf16_to_f32((uint16_t)(u.y >> 16))}};
@@ -147,16 +165,16 @@ __global__ __launch_bounds__(64) void shift_lerp_bwd(long M, int T, int C, const
     const uint2 zero = make_uint2(0, 0);
     uint2 dcur[6];  // gradient rows of the group's first token
 #pragma unroll
-    for (int n = 0; n < 6; n++) dcur[n] = ld_raw4(dn[n] + m0 * C + c);
-    uint2 xprev = (m0 % T) > 0 ? ld_raw4(x + (m0 - 1) * C + c) : ld_raw4(st + (m0 / T) * C + c);
+    for (int n = 0; n < 6; n++) dcur[n] = ld_str4(dn[n] + m0 * C + c);
+    uint2 xprev = (m0 % T) > 0 ? ld_str4(x + (m0 - 1) * C + c) : ld_str4(st + (m0 / T) * C + c);
     for (long m = m0; m < m1; m += UG) {
         uint2 dr[UG][6], xr[UG];
 #pragma unroll
         for (int u = 0; u < UG; u++) {
             const long row = m + 1 + u;  // (the last token's successor may lie past m1)
 #pragma unroll
-            for (int n = 0; n < 6; n++) dr[u][n] = row < M ? ld_raw4(dn[n] + row * C + c) : zero;
-            xr[u] = m + u < m1 ? ld_raw4(x + (m + u) * C + c) : zero;
+            for (int n = 0; n < 6; n++) dr[u][n] = row < M ? ld_str4(dn[n] + row * C + c) : zero;
+            xr[u] = m + u < m1 ? ld_str4(x + (m + u) * C + c) : zero;
         }
 #pragma unroll
         for (int u = 0; u < UG; u++) {
@@ -164,7 +182,7 @@ __global__ __launch_bounds__(64) void shift_lerp_bwd(long M, int T, int C, const
             if (mm < m1) {
                 const int t = (int)(mm % T), b = (int)(mm / T);
                 const V4 xv = cvt_bf4(xr[u]);
-                const V4 pv = cvt_bf4(t > 0 ? (u == 0 ? xprev : xr[u - 1]) : ld_raw4(st + (long)b * C + c));
+                const V4 pv = cvt_bf4(t > 0 ? (u == 0 ? xprev : xr[u - 1]) : ld_str4(st + (long)b * C + c));
                 V4 gx, gs;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -218,43 +236,57 @@ __global__ __launch_bounds__(256) void reduce_blocks(const float* __restrict__ p
 }
 
 // ---------------------------------------------------------------- kk / k-mod
-__global__ __launch_bounds__(256) void kk_fwd(long rows, int H, int C, const uint16_t* __restrict__ k,
+// The forward kernels: ceil(H / 8) x ceil(M / (4 U)) workgroups of 256 lanes, head groups
+// first (workgroups next in line read neighbouring 1 KB runs of the same tokens; token-first
+// order made both kernels 8-10 % slower); wave w takes 8 consecutive heads (a whole 1 KB run
+// of a token per load) of the tokens 4 U tb + U w + u, u < U, all U tokens' loads issued
+// before any is used and the parameter vectors loaded once (gn_fwd: 127 -> 121 µs at
+// config 3 against one (token, head) row per 8 lanes).
+constexpr int KU = 4;  // tokens per wave of kk_fwd
+__global__ __launch_bounds__(256) void kk_fwd(long M, int H, int C, const uint16_t* __restrict__ k,
                                               const float* __restrict__ a, const float* __restrict__ kkp,
                                               const float* __restrict__ kap, uint16_t* kw, uint16_t* aw,
                                               uint16_t* bw) {
-    const long row = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
-    const int sub = threadIdx.x & 7;
-    const bool ok = row < rows;
-    const long m = ok ? row / H : 0;
-    const int h = ok ? (int)(row % H) : 0;
-    const int c = h * HN + 8 * sub;
-    const long o = m * C + c;
-    V8 kv{}, av{};
-    if (ok) {
-        kv = ld_bf8(k + o);
-        av = ld_f8(a + o);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, sub = l & 7;
+    const int ng = (H + 7) / 8, h = (int)(blockIdx.x % ng) * 8 + (l >> 3);
+    const bool hok = h < H;
+    const int c = (hok ? h : 0) * HN + 8 * sub;
+    const long mb = ((long)(blockIdx.x / ng) * 4 + w) * KU;
+    uint4 kr[KU];
+    V8 av[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const bool ok = hok && mb + u < M;
+        const long o = ok ? (mb + u) * C + c : c;
+        kr[u] = ld_str8(k + o);
+        av[u] = ld_f8s(a + o);
     }
     const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c);
-    float u[8], ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        u[e] = kv.x[e] * kk_.x[e];
-        ss += u[e] * u[e];
-    }
-    ss = sum8(ss);
-    const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
-    V8 ow, oa, ob;
+    for (int u = 0; u < KU; u++) {
+        const V8 kv = cvt_bf8(kr[u]);
+        float uu[8], ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float kkv = u[e] * inv;
-        ow.x[e] = kv.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e]);
-        oa.x[e] = -kkv;
-        ob.x[e] = kkv * av.x[e];
-    }
-    if (ok) {
-        st_bf8(kw + o, ow);
-        st_bf8(aw + o, oa);
-        st_bf8(bw + o, ob);
+        for (int e = 0; e < 8; e++) {
+            uu[e] = kv.x[e] * kk_.x[e];
+            ss += uu[e] * uu[e];
+        }
+        ss = sum8(ss);
+        const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+        V8 ow, oa, ob;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float kkv = uu[e] * inv;
+            ow.x[e] = kv.x[e] * (1.f + (av[u].x[e] - 1.f) * ka.x[e]);
+            oa.x[e] = -kkv;
+            ob.x[e] = kkv * av[u].x[e];
+        }
+        if (hok && mb + u < M) {
+            const long o = (mb + u) * C + c;
+            st_bf8(kw + o, ow);
+            st_bf8(aw + o, oa);
+            st_bf8(bw + o, ob);
+        }
     }
 }
 
@@ -266,25 +298,33 @@ __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16
                                               const float* __restrict__ kap, uint16_t* dk, float* da,
                                               float* __restrict__ part) {
     __shared__ float red[2][32][HN + 1];
-    // 32 rows = 4 tokens x HG consecutive heads, so a wave reads whole 1 KB runs of a token
+    // 32 rows = 4 tokens x HG consecutive heads, so a wave reads whole 1 KB runs of a token;
+    // the next step's rows are loaded before this step's arithmetic
     const int rs = threadIdx.x >> 3, sub = threadIdx.x & 7, hh = rs % HG, tt = rs / HG;
     const int h = blockIdx.x * HG + hh;
     const bool hok = h < H;
     const int c = (hok ? h : 0) * HN + 8 * sub;
     const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c);
     float acc_kk[8] = {}, acc_ka[8] = {};
+    uint4 nk, nw, na, nb;
+    V8 nav;
+    auto fetch = [&](int it) {
+        const long m = (long)blockIdx.y * TB + it * 4 + tt;
+        const long o = hok && m < M ? m * C + c : c;
+        nk = ld_str8(k + o);
+        nav = ld_f8s(a + o);
+        nw = ld_str8(dkw + o);
+        na = ld_str8(daw + o);
+        nb = ld_str8(dbw + o);
+    };
+    fetch(0);
     for (int it = 0; it < TB / 4; it++) {
         const long m = (long)blockIdx.y * TB + it * 4 + tt;
         const bool ok = hok && m < M;
         const long o = m * C + c;
-        V8 kv{}, av{}, gw{}, ga{}, gb{};
-        if (ok) {
-            kv = ld_bf8(k + o);
-            av = ld_f8(a + o);
-            gw = ld_bf8(dkw + o);
-            ga = ld_bf8(daw + o);
-            gb = ld_bf8(dbw + o);
-        }
+        V8 kv = cvt_bf8(nk), av = nav, gw = cvt_bf8(nw), ga = cvt_bf8(na), gb = cvt_bf8(nb);
+        if (!ok) kv = av = gw = ga = gb = V8{};
+        if (it + 1 < TB / 4) fetch(it + 1);
         float u[8], ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -334,46 +374,53 @@ __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16
 }
 
 // ---------------------------------------------------------------- GroupNorm + bonus + gate
-__global__ __launch_bounds__(256) void gn_fwd(long rows, int H, int C, const uint16_t* __restrict__ y,
+constexpr int FU = 4;  // tokens per wave of gn_fwd (mapped as kk_fwd)
+__global__ __launch_bounds__(256) void gn_fwd(long M, int H, int C, const uint16_t* __restrict__ y,
                                               const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                                               const float* __restrict__ a, const float* __restrict__ kap,
                                               const uint16_t* __restrict__ v, const uint16_t* __restrict__ g,
                                               const float* __restrict__ rkp, const float* __restrict__ lwp,
                                               const float* __restrict__ lbp, float eps, uint16_t* out) {
-    const long row = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
-    const int sub = threadIdx.x & 7;
-    const bool ok = row < rows;
-    const long m = ok ? row / H : 0;
-    const int h = ok ? (int)(row % H) : 0;
-    const int c = h * HN + 8 * sub;
-    const long o = m * C + c;
-    V8 yv{}, rv{}, kv{}, av{}, vv{}, gv{};
-    if (ok) {
-        yv = ld_bf8(y + o);
-        rv = ld_bf8(r + o);
-        kv = ld_bf8(k + o);
-        av = ld_f8(a + o);
-        vv = ld_bf8(v + o);
-        gv = ld_bf8(g + o);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, sub = l & 7;
+    const int ng = (H + 7) / 8, h = (int)(blockIdx.x % ng) * 8 + (l >> 3);
+    const bool hok = h < H;
+    const int c = (hok ? h : 0) * HN + 8 * sub;
+    const long mb = ((long)(blockIdx.x / ng) * 4 + w) * FU;
+    uint4 yr[FU], rr[FU], kr[FU], vr[FU], gr[FU];
+    V8 av[FU];
+#pragma unroll
+    for (int u = 0; u < FU; u++) {
+        const bool ok = hok && mb + u < M;
+        const long o = ok ? (mb + u) * C + c : c;
+        yr[u] = ld_str8(y + o);
+        rr[u] = ld_str8(r + o);
+        kr[u] = ld_str8(k + o);
+        vr[u] = ld_str8(v + o);
+        gr[u] = ld_str8(g + o);
+        av[u] = ld_f8s(a + o);
     }
     const V8 ka = ld_f8(kap + c), rk = ld_f8(rkp + c), lw = ld_f8(lwp + c), lb = ld_f8(lbp + c);
-    float s = 0.f, cd = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        s += yv.x[e];
-        cd += rv.x[e] * (kv.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e])) * rk.x[e];
+    for (int u = 0; u < FU; u++) {
+        const V8 yv = cvt_bf8(yr[u]), rv = cvt_bf8(rr[u]), kv = cvt_bf8(kr[u]), vv = cvt_bf8(vr[u]), gv = cvt_bf8(gr[u]);
+        float s = 0.f, cd = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            s += yv.x[e];
+            cd += rv.x[e] * (kv.x[e] * (1.f + (av[u].x[e] - 1.f) * ka.x[e])) * rk.x[e];
+        }
+        const float mean = sum8(s) * (1.f / HN);
+        cd = sum8(cd);
+        float var = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) var += (yv.x[e] - mean) * (yv.x[e] - mean);
+        const float rstd = rsqrtf(sum8(var) * (1.f / HN) + eps);
+        V8 ov;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            ov.x[e] = ((yv.x[e] - mean) * rstd * lw.x[e] + lb.x[e] + cd * vv.x[e]) * gv.x[e];
+        if (hok && mb + u < M) st_bf8(out + (mb + u) * C + c, ov);
     }
-    const float mean = sum8(s) * (1.f / HN);
-    cd = sum8(cd);
-    float var = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; e++) var += (yv.x[e] - mean) * (yv.x[e] - mean);
-    const float rstd = rsqrtf(sum8(var) * (1.f / HN) + eps);
-    V8 ov;
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-        ov.x[e] = ((yv.x[e] - mean) * rstd * lw.x[e] + lb.x[e] + cd * vv.x[e]) * gv.x[e];
-    if (ok) st_bf8(out + o, ov);
 }
 
 // grid (ceil(H/HG), ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
@@ -393,20 +440,27 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
     const int c = (hok ? h : 0) * HN + 8 * sub;
     const V8 ka = ld_f8(kap + c), rk = ld_f8(rkp + c), lw = ld_f8(lwp + c), lb = ld_f8(lbp + c);
     float acc[4][8] = {};  // dr_k, dln_w, dln_b, dk_a
+    uint4 ny, nr, nk, nv, ng, no;
+    V8 nav;
+    auto fetch = [&](int it) {
+        const long m = (long)blockIdx.y * TB + it * 4 + tt;
+        const long o = hok && m < M ? m * C + c : c;
+        ny = ld_str8(y + o);
+        nr = ld_str8(r + o);
+        nk = ld_str8(k + o);
+        nav = ld_f8s(a + o);
+        nv = ld_str8(v + o);
+        ng = ld_str8(g + o);
+        no = ld_str8(dout + o);
+    };
+    fetch(0);
     for (int it = 0; it < TB / 4; it++) {
         const long m = (long)blockIdx.y * TB + it * 4 + tt;
         const bool ok = hok && m < M;
         const long o = m * C + c;
-        V8 yv{}, rv{}, kv{}, av{}, vv{}, gv{}, go{};
-        if (ok) {
-            yv = ld_bf8(y + o);
-            rv = ld_bf8(r + o);
-            kv = ld_bf8(k + o);
-            av = ld_f8(a + o);
-            vv = ld_bf8(v + o);
-            gv = ld_bf8(g + o);
-            go = ld_bf8(dout + o);
-        }
+        V8 yv = cvt_bf8(ny), rv = cvt_bf8(nr), kv = cvt_bf8(nk), av = nav, vv = cvt_bf8(nv), gv = cvt_bf8(ng), go = cvt_bf8(no);
+        if (!ok) yv = rv = kv = av = vv = gv = go = V8{};
+        if (it + 1 < TB / 4) fetch(it + 1);
         float km[8], s = 0.f, cd = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -531,8 +585,8 @@ int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const float* a, const 
     if (int e = tm_check(B, T, C)) return e;
     if (!k || !a || !k_k || !k_a || !kw || !aw || !bw) return THESEUS_WKV7_ERR_NULL;
     const int H = C / tmix::HN;
-    const long rows = (long)B * T * H;
-    hipLaunchKernelGGL(tmix::kk_fwd, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, stream, rows, H, C,
+    const long M = (long)B * T;
+    hipLaunchKernelGGL(tmix::kk_fwd, dim3((unsigned)((M + 4 * tmix::KU - 1) / (4 * tmix::KU) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
                        (const uint16_t*)k, a, k_k, k_a, (uint16_t*)kw, (uint16_t*)aw, (uint16_t*)bw);
     return tm_status();
 }
@@ -563,8 +617,8 @@ int theseus_tm_gn_fwd(int B, int T, int C, const void* y, const void* r, const v
     if (int e = tm_check(B, T, C)) return e;
     if (!y || !r || !k || !a || !k_a || !v || !g || !r_k || !ln_w || !ln_b || !out) return THESEUS_WKV7_ERR_NULL;
     const int H = C / tmix::HN;
-    const long rows = (long)B * T * H;
-    hipLaunchKernelGGL(tmix::gn_fwd, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, stream, rows, H, C,
+    const long M = (long)B * T;
+    hipLaunchKernelGGL(tmix::gn_fwd, dim3((unsigned)((M + 4 * tmix::FU - 1) / (4 * tmix::FU) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
                        (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, a, k_a, (const uint16_t*)v,
                        (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)out);
     return tm_status();
