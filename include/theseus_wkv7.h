@@ -93,7 +93,13 @@ int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype);
  * forward holds theseus_wkv7_checkpoint_count(T) states
  * [B,H,count,N,N] float32: state after steps 0,16,32,... and, last, the final
  * state after step T.  Replaces the full [B,H,T+1,N,N] history that
- * kernels/wkv7_state.cpp:21-22 allocates. */
+ * kernels/wkv7_state.cpp:21-22 allocates.  The states are for the backward
+ * of the same kernel family (theseus_wkv7_kernel_family of the same sizes):
+ * the step-serial kernels keep every state in [value][key] order; the
+ * chunked kernels keep the last (the final state, equal to sT) in that
+ * order and states 0 .. count-2 in their tiled order, S[i][j] (value i,
+ * key j) at float ((i/16*4 + j/16)*64 + 16*(j%16/4) + i%16)*4 + j%4 of
+ * the N x N block. */
 int theseus_wkv7_checkpoint_interval(void);
 long long theseus_wkv7_checkpoint_count(int T);
 

@@ -670,18 +670,20 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         // buffer loads from a head's saved states: one lane offset, the rest in
         // scalar and immediate offsets (no per-load address arithmetic)
         auto ck_rsrc = [&](int j) { return make_rsrc(ckpt + (long)j * ncp * NN, (uint32_t)(ncp * NN * 4)); };
-        auto load_rows = [&](__amdgpu_buffer_rsrc_t ckr, int cc) {
-            const uint32_t vo = (uint32_t)((i_own * NK + 4 * q) * 4), so = (uint32_t)(cc * NN * 4);
+        // (saved states before the last are in the forward's tiled order: S[i][j] at float
+        // ((i/16 * 4 + j/16) * 64 + 16 * (j%16/4) + i%16) * 4 + j%4, wkv7_chunk_fwd.hip)
+        auto load_rows = [&](__amdgpu_buffer_rsrc_t ckr, int cc) {  // rows i_own: one whole KB per load
+            const uint32_t vo = (uint32_t)((cw * 1024 + 4 * lane) * 4), so = (uint32_t)(cc * NN * 4);
 #pragma unroll
             for (int tj = 0; tj < 4; tj++)
-                S0n[tj] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ckr, vo + 64 * tj, so, 0));
+                S0n[tj] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ckr, vo + 1024 * tj, so, 0));
         };
-        auto load_strip = [&](__amdgpu_buffer_rsrc_t ckr, int cc) {
-            const uint32_t vo = (uint32_t)((4 * q * NK + j_own) * 4);
+        auto load_strip = [&](__amdgpu_buffer_rsrc_t ckr, int cc) {  // key j_own = 16 cw + r16
+            const uint32_t vo = (uint32_t)((cw * 256 + 64 * (r16 >> 2) + 16 * q + (r16 & 3)) * 4);
 #pragma unroll
             for (int m = 0; m < 16; m++)
                 S0s[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    ckr, vo + (m & 3) * NK * 4, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0));
+                    ckr, vo + (m & 3) * 16, (uint32_t)((cc * NN + (32 * (m >> 3) + 16 * ((m >> 2) & 1)) * NK) * 4), 0));
         };
         // The previous tick's chunk (stream index np) is completed a tick late, once the H
         // side's dlogd terms of it are published: this side's terms zp, tp, its fw and its

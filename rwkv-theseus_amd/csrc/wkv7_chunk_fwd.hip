@@ -39,7 +39,9 @@
 //    (chunk x in slot x % 5, free from tick x-4 since its last reader was
 //    chunk x-5).  Their outputs leave in whole 128-byte rows: y through LDS,
 //    stored a tick late by all four waves, and each wave's saved-state rows
-//    regrouped eight at a time.
+//    regrouped eight at a time; the saved states S_c straight from the
+//    registers in the tiled order, in chunk c's tick while its first products
+//    run.
 #include "wkv7_launch.h"
 #include "wkv7_io.h"
 #include "wkv7_sched.h"
@@ -131,7 +133,34 @@ struct SplitArgs {
     float* z = nullptr;        // the identity runs' tiles, the same layout
 };
 
-template <bool SPLIT>
+// Saved states.  State c < ceil(T/16) (the state chunk c starts from) is stored in the
+// tiled order: S[i][j] (value i, key j) at float
+//   ((i/16 * 4 + j/16) * 64 + 16 * (j%16/4) + i%16) * 4 + j%4,
+// which is each consumer wave's register layout (wave i/16, tile j/16, lane, element), so
+// every store is a whole KB.  The last one, the final state, is stored in the plain
+// [value][key] order (it equals sT) by FWD_SAVE_STATE: this wave's 16 rows of St, 8 at a
+// time through its sq plane, four whole 256-byte rows per store.
+#define FWD_SAVE_STATE(e)                                                                                     \
+    do {                                                                                                      \
+        float* const sq_ = sm.sq[cw];                                                                         \
+        float* const dst_ = ckpt + (bh * ncp + (e)) * NN + (long)(16 * cw) * NK;                             \
+        _Pragma("unroll") for (int p_ = 0; p_ < 2; p_++) {                                                    \
+            if ((r16 >> 3) == p_) {                                                                           \
+                _Pragma("unroll") for (int tj_ = 0; tj_ < 4; tj_++)                                           \
+                    *reinterpret_cast<float4*>(sq_ + (r16 & 7) * LDR + 16 * tj_ + 4 * q) =                   \
+                        make_float4(St[tj_][0], St[tj_][1], St[tj_][2], St[tj_][3]);                          \
+            }                                                                                                 \
+            _Pragma("unroll") for (int u_ = 0; u_ < 2; u_++) {                                                \
+                const int rr_ = 4 * u_ + (lane >> 4), cc_ = 4 * (lane & 15);                                  \
+                *reinterpret_cast<float4*>(dst_ + (8 * p_ + rr_) * NK + cc_) =                                \
+                    *reinterpret_cast<const float4*>(sq_ + rr_ * LDR + cc_);                                  \
+            }                                                                                                 \
+        }                                                                                                     \
+    } while (0)
+
+// CKPT: saved states are written (ckpt is not null); a template argument so that the
+// forward without them keeps its tick in one basic block.
+template <bool SPLIT, bool CKPT>
 __global__ __launch_bounds__(512) void chunk_forward_bf16(
     Sched sc, int Tn, int H, const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
     const bf16_t* __restrict__ k, const bf16_t* __restrict__ v, const bf16_t* __restrict__ a,
@@ -389,7 +418,6 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                                      i_own == c0 + 2 ? 1.f : 0.f, i_own == c0 + 3 ? 1.f : 0.f};
                 }
                 St[tj] = f32x4_t{x.x, x.y, x.z, x.w};
-                if (ckpt) *reinterpret_cast<float4*>(ckpt + bh * ncp * NN + off) = x;
             }
           } else {  // ... else the handoff of boundary m + 1
             const float bad = handoff_wait(flags + m + 1, 4) ? 1.f : __builtin_nanf("");
@@ -424,6 +452,19 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 yy = mma32(yy, p2h, sh);
                 yy = mma32(yy, p2h, sl);
                 yy = mma32(yy, p2l, sh);
+                if (CKPT && s == 0) {
+                    // S_c, the state this tick starts from, saved while these products run,
+                    // straight from the registers in the tiled order (one whole KB per
+                    // store): 0.327 -> 0.300 ms at config 2 against saving S_{c+1} after
+                    // the update through the row regrouping
+                    __builtin_amdgcn_sched_barrier(0);
+                    float* const dst = ckpt + (bh * ncp + c) * NN + (long)(16 * cw) * NK;
+#pragma unroll
+                    for (int tj = 0; tj < 4; tj++)
+                        *reinterpret_cast<float4*>(dst + (tj * 64 + lane) * 4) =
+                            make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 if (dual) {  // the identity run on the same operand fragments
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
@@ -478,27 +519,11 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
                 *reinterpret_cast<float4*>(sp.z + o) = make_float4(yy2[0], yy2[1], yy2[2], yy2[3]);
                 yL = 0;  // (nothing for y_rows)
             }
-            if (ckpt) {  // S_{c+1}: this wave's rows, 8 at a time through sq, 4 whole rows per store
-                float* const sq = sm.sq[cw];
-                float* const dst = ckpt + (bh * ncp + c + 1) * NN + (long)(16 * cw) * NK;
-#pragma unroll
-                for (int p = 0; p < 2; p++) {
-                    if ((r16 >> 3) == p) {
-#pragma unroll
-                        for (int tj = 0; tj < 4; tj++)
-                            *reinterpret_cast<float4*>(sq + (r16 & 7) * LDR + 16 * tj + 4 * q) =
-                                make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
-                    }
-#pragma unroll
-                    for (int u = 0; u < 2; u++) {
-                        const int rr = 4 * u + (lane >> 4), cc = 4 * (lane & 15);
-                        *reinterpret_cast<float4*>(dst + (8 * p + rr) * NK + cc) = *reinterpret_cast<const float4*>(sq + rr * LDR + cc);
-                    }
-                }
-            }
             lds_barrier();
           }
-          // the final state, or the handoff at boundary m
+          // the final state, or the handoff at boundary m (its saved state is then made by
+          // the workgroup that continues the head, in its first tick)
+          if (CKPT && !sg.handoff) FWD_SAVE_STATE(sg.step0 + sg.count);
 #pragma unroll
           for (int tj = 0; tj < 4; tj++) {
               const long off = (long)i_own * NK + 16 * tj + 4 * q;
@@ -527,7 +552,8 @@ void launch_chunk_forward(const Fwd& p, int cus) {
         hand = reinterpret_cast<float*>(static_cast<char*>(p.ws) + sched_flag_bytes(sc));
         hipLaunchKernelGGL(clear_words, dim3(1), dim3(256), 0, p.stream, flags, sc.G);
     }
-    hipLaunchKernelGGL(chunk_forward_bf16<false>, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
+    const auto kern = p.ckpt ? chunk_forward_bf16<false, true> : chunk_forward_bf16<false, false>;
+    hipLaunchKernelGGL(kern, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
                        (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, p.ckpt, flags, hand,
                        SplitArgs{});
@@ -696,7 +722,7 @@ void launch_chunk_forward_split(const Fwd& p, int cus) {
     sp.y0 = sp.phi + per * NN, sp.z = sp.y0 + per * sp.m * CH * NK;
     // one job per workgroup, no cuts (jobs planned at the longest segment; each runs its own)
     const Sched sc = plan_schedule(sp.k * sp.BH, max(sp.m0, sp.m), cus);
-    hipLaunchKernelGGL(chunk_forward_bf16<true>, dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
+    hipLaunchKernelGGL((chunk_forward_bf16<true, false>), dim3(sc.G), dim3(512), 0, p.stream, sc, p.T, p.H,
                        (const bf16_t*)p.r, (const bf16_t*)p.w, (const bf16_t*)p.k, (const bf16_t*)p.v,
                        (const bf16_t*)p.a, (const bf16_t*)p.b, p.s0, (bf16_t*)p.y, p.sT, nullptr, nullptr,
                        nullptr, sp);

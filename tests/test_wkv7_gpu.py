@@ -388,6 +388,47 @@ def test_backward_is_deterministic_and_dend_none_is_zero():
     assert empty.numel() == 0
 
 
+def _untile(saved):
+    """Saved states of the chunked kernels, [..., 64, 64] in their tiled order (S[i][j],
+    value i, key j, at float ((i//16*4 + j//16)*64 + 16*(j%16//4) + i%16)*4 + j%4), back
+    to [value][key]."""
+    lead = saved.shape[:-2]
+    k = len(lead)
+    t = saved.reshape(*lead, 4, 4, 4, 16, 4)  # [i//16][j//16][j%16//4][i%16][j%4]
+    return t.permute(*range(k), k, k + 3, k + 1, k + 2, k + 4).reshape(*lead, 64, 64)
+
+
+def test_untile_inverts_the_documented_order():
+    s = torch.arange(64 * 64, dtype=torch.float32).reshape(64, 64)  # s[i][j] = 64 i + j
+    tiled = torch.empty(64 * 64)
+    for i in range(64):
+        for j in range(64):
+            tiled[((i // 16 * 4 + j // 16) * 64 + 16 * (j % 16 // 4) + i % 16) * 4 + j % 4] = s[i, j]
+    assert torch.equal(_untile(tiled.reshape(64, 64)), s)
+
+
+def test_saved_states_are_the_step_serial_kernels_states(monkeypatch):
+    """The chunked forward stores saved states 0 .. count-2 in its tiled order and the last
+    (the final state) in plain [value][key] order; untiled, they are the states the
+    step-serial forward saves (plain order throughout) to fp32 rounding, and state 0 is s0."""
+    inp = wkv7_inputs(2, 70, 3, 64, seed=15, dtype=torch.bfloat16, s0_std=0.1)
+    ext = W.extension()
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0 = inp["s0"].cuda()
+    assert ext.kernel_family(2, 70, 3, 64, 0) == 0  # bf16: the chunked kernels
+    _, end, saved = ext.forward(*xs, s0, True)
+    monkeypatch.setenv("THESEUS_WKV7_FAMILY", "seq")
+    _, end_q, saved_q = ext.forward(*xs, s0, True)
+    torch.cuda.synchronize()
+    assert saved.shape == saved_q.shape == (2, 3, 6, 64, 64)
+    got = torch.cat([_untile(saved[:, :, :-1]), saved[:, :, -1:]], dim=2)
+    assert torch.equal(got[:, :, 0], s0)
+    assert torch.equal(saved[:, :, -1], end)
+    rel = ((got - saved_q).norm() / saved_q.norm()).item()
+    err = (got - saved_q).abs().max().item()
+    assert rel <= 1e-5 and err <= 1e-4 * saved_q.abs().max().item(), (rel, err)
+
+
 def test_current_stream_is_honoured():
     inp = wkv7_inputs(2, 40, 2, 64, seed=6, dtype=torch.bfloat16, s0_std=0.1)
     xs = [inp[n].cuda() for n in "rwkvab"]
