@@ -105,6 +105,10 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
     auto row = [&](int t) { return ((tok0 + t) * H + h) * (long)NK; };
     const float rs = 1.f / __builtin_sqrtf((float)NK);
     __shared__ float gsh[4][GC];  // gamma_t, gamma_{t-1}, beta_t, k_t's norm factor (past the end: 0)
+    // v as rows [t][value] (past the end: 0), loaded with k and q and read back per block of
+    // 16 values: the V operand's elementwise loads at the end of the kernel had cost 18 µs
+    // of a 189 µs teacher-geometry call
+    __shared__ float vsh[GC][NK + 4];
 
     const bool tv = r16 < L;
     const float gt = tv ? g[(tok0 + r16) * H + h] : 0.f;
@@ -113,6 +117,13 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
     const float gm1 = row_prev(gam, 0.f);
     const float gL = row_last(gam);
     // rows of k and q (zero past the end); q kept for R~
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        const int c0 = 32 * ks + 4 * q4;
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(&vsh[r16][c0]) = tv ? ld4(v + row(r16) + c0) : z;
+        *reinterpret_cast<float4*>(&vsh[r16][c0 + 16]) = tv ? ld4(v + row(r16) + c0 + 16) : z;
+    }
     float kr[KS][8], qr[KS][8];
     float ssk = 0.f, ssq = 0.f;
 #pragma unroll
@@ -159,7 +170,7 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
         KK = mma32(mma32(mma32(KK, kh[ks], kh[ks]), kh[ks], kl[ks]), kl[ks], kh[ks]);
         KR = mma32(mma32(mma32(KR, kh[ks], qh[ks]), kh[ks], ql[ks]), kl[ks], qh[ks]);
     }
-    __syncthreads();  // gsh
+    __syncthreads();  // gsh, vsh
     // the chunk matrices in D layout (element [rr][cc], rr = 4q4 + e, cc = r16); the
     // decay ratios are exponentials of differences that are <= 0 where the mask keeps them
     const int cc = r16;
@@ -195,7 +206,7 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int t = 4 * q4 + e;
-            vv[e] = t < L ? gsh[2][t] * io<TI>::ld(v, row(t) + 16 * rb + r16) : 0.f;
+            vv[e] = gsh[2][t] * vsh[t][16 * rb + r16];  // (zero past the end)
         }
         const Pk pv = pk(vv);
         uint2* vf = reinterpret_cast<uint2*>(rec + R::VF) + (size_t)(2 * rb) * 64 + lane;
