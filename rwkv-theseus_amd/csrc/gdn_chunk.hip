@@ -215,6 +215,16 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
     }
     // per pair of 16-key tiles (one K-step): P, P2 and the update operands
     const float egam = __expf(gam) * rs;  // R~ row scale of token r16
+    float ea[4], eb[4], ek[4];  // the tiles' token scalings (t = 4q4 + e), formed once
+    const TI* krow[4];          // and k's row of token t, key r16
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = 4 * q4 + e;
+        krow[e] = k + row(t < L ? t : 0) + r16;
+        ea[e] = __expf(gsh[1][t]);
+        eb[e] = -gsh[2][t] * __expf(gL - gsh[1][t]);
+        ek[e] = __expf(gL - gsh[0][t]);
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
         Pk pPT[2], pP2T[2];
@@ -226,10 +236,10 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int t = 4 * q4 + e;
-                const float kv = t < L ? io<TI>::ld(k, row(t) + 16 * tj + r16) * gsh[3][t] : 0.f;
-                at[e] = kv * __expf(gsh[1][t]);
-                bhat[e] = -gsh[2][t] * kv * __expf(gL - gsh[1][t]);
-                khat[e] = kv * __expf(gL - gsh[0][t]);
+                const float kv = t < L ? io<TI>::ld(krow[e], 16 * tj) * gsh[3][t] : 0.f;
+                at[e] = kv * ea[e];
+                bhat[e] = kv * eb[e];
+                khat[e] = kv * ek[e];
             }
             const Pk pA = pk(at);
             const f32x4_t Pt = mm16s(pTiT, pA);   // P tile [t][j]
