@@ -37,11 +37,11 @@
 //    state in registers (value rows never interact) and advances them by one
 //    chunk per tick from the operands the producers left in a 5-slot LDS ring
 //    (chunk x in slot x % 5, free from tick x-4 since its last reader was
-//    chunk x-5).  Their outputs leave in whole 128-byte rows: y through LDS,
-//    stored a tick late by all four waves, and each wave's saved-state rows
-//    regrouped eight at a time; the saved states S_c straight from the
-//    registers in the tiled order, in chunk c's tick while its first products
-//    run.
+//    chunk x-5).  Their outputs leave in whole lines: y through LDS in
+//    128-byte rows, stored a tick late by all four waves; the saved states S_c
+//    straight from the registers in a tiled order (whole KBs), in chunk c's tick
+//    while its first products run; the final saved state in [value][key] rows
+//    regrouped through LDS eight at a time.
 #include "wkv7_launch.h"
 #include "wkv7_io.h"
 #include "wkv7_sched.h"
@@ -71,15 +71,16 @@ struct Slot {
     Plane V;       // V [t][i], exact bf16 (SwDma)
     float egL[NK]; // e^{gL} per key
 };
-// Outputs leave in whole rows: a wave's own pieces are 32-byte (y) and 64-byte (saved
-// states) parts of 128-byte lines, and stores of such parts cost far more than their
-// bytes (measured: the forward ran 7 % and 6 % faster with each regrouped).
-constexpr int LDR = NK + 4;  // padded row (floats) of the saved-state regrouping planes
+// Outputs leave in whole lines: a wave's own pieces of y are 32-byte parts of 128-byte
+// lines, and stores of such parts cost far more than their bytes (the forward ran 7 %
+// faster with y regrouped, 6 % with the saved states regrouped, before those were stored
+// in the tiled order instead).
+constexpr int LDR = NK + 4;  // padded row (floats) of the final state's regrouping planes
 struct FwdLds {
     Slot slot[NSLOT];
     Plane raw[NPROD][5];     // producer input staging: r, w, k, a, b (SwDma)
     uint16_t yq[2][CH * NK]; // y tiles of the last two ticks [t][i], stored a tick late
-    float sq[4][8 * LDR];    // per consumer wave: 8 of its 16 saved-state rows at a time
+    float sq[4][8 * LDR];    // per consumer wave: 8 of its 16 final-state rows at a time
 };
 static_assert(sizeof(FwdLds) <= 160 * 1024, "forward LDS budget");
 
