@@ -4,9 +4,10 @@
  * recurrence in TimeMix.forward (theseus/timemix.py:66-89); the reference has no
  * native counterpart (it runs ~20 separate torch kernels there).
  *
- * Activations are [B,T,C] contiguous bf16 except `a` (float32, the dtype
- * sigmoid(a0 + ...) has under bf16 autocast with float32 parameters); per-channel
- * parameters are float32 [C] (r_k is [H,N] = [C]).  Parameter gradients are
+ * Activations are [B,T,C] contiguous bf16; the gate a = sigmoid(a0 + za) of
+ * theseus/timemix.py:75 is formed inside the kernels from za (the bf16 LoRA output
+ * (x_a @ a1) @ a2) and the parameter a0, in float32 as bf16 autocast over float32
+ * parameters computes it; per-channel parameters are float32 [C] (r_k is [H,N] = [C]).  Parameter gradients are
  * reduced over B*T in a fixed order through a caller-provided float32 workspace
  * (theseus_tm_*_workspace gives its size), then written to [C] outputs.
  * Head size N must be 64 (8 lanes x 8 channels per head row), and B*T at most
@@ -36,30 +37,37 @@ int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dmixed, co
                               float* dcoef, float* workspace, size_t workspace_bytes,
                               hipStream_t stream);
 
-/* WKV operands (theseus/timemix.py:78-80): kk = normalize(k * k_k) per head (eps 1e-12),
- * kw = k * (1 + (a - 1) * k_a), aw = -kk, bw = kk * a, all written as bf16. */
-int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const float* a, const float* k_k,
+/* WKV operands (theseus/timemix.py:75, 78-80): a = sigmoid(a0 + za), kk = normalize(k * k_k)
+ * per head (eps 1e-12), kw = k * (1 + (a - 1) * k_a), aw = -kk, bw = kk * a, all written as
+ * bf16. */
+int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const void* za, const float* a0, const float* k_k,
                       const float* k_a, void* kw, void* aw, void* bw, hipStream_t stream);
 size_t theseus_tm_kk_workspace(int B, int T, int C);
-/* writes dk (bf16), da (f32), dk_k, dk_a ([C] f32) */
+/* writes dk (bf16), dza (bf16) = dL/d(a0 + za) and [C] f32 da0, dk_k, dk_a.  dzg
+ * (float32 [B,T,C], or NULL for zero) is the rest of dL/da times a (1 - a), as
+ * theseus_tm_gn_bwd writes it: the two parts are added in float32 before dza is rounded. */
 int theseus_tm_kk_bwd(int B, int T, int C, const void* dkw, const void* daw, const void* dbw,
-                      const void* k, const float* a, const float* k_k, const float* k_a, void* dk,
-                      float* da, float* dk_k, float* dk_a, float* workspace,
-                      size_t workspace_bytes, hipStream_t stream);
+                      const void* k, const void* za, const float* a0, const float* dzg,
+                      const float* k_k, const float* k_a, void* dk, void* dza, float* da0,
+                      float* dk_k, float* dk_a, float* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
 
 /* out = (GroupNorm_H(y; ln_w, ln_b, eps) + (sum_n r*kmod*r_k) v) * g, all float32
- * arithmetic, written as bf16 (theseus/timemix.py:83-88); kmod = k * (1 + (a-1) * k_a). */
+ * arithmetic, written as bf16 (theseus/timemix.py:83-88); kmod = k * (1 + (a - 1) * k_a),
+ * a = sigmoid(a0 + za). */
 int theseus_tm_gn_fwd(int B, int T, int C, const void* y, const void* r, const void* k,
-                      const float* a, const float* k_a, const void* v, const void* g,
-                      const float* r_k, const float* ln_w, const float* ln_b, float eps, void* out,
-                      hipStream_t stream);
+                      const void* za, const float* a0, const float* k_a, const void* v,
+                      const void* g, const float* r_k, const float* ln_w, const float* ln_b,
+                      float eps, void* out, hipStream_t stream);
 size_t theseus_tm_gn_workspace(int B, int T, int C);
-/* writes dy, dr, dk, dv, dg (bf16), da (f32), and [C] f32 dr_k, dln_w, dln_b, dk_a */
+/* writes dy, dr, dk, dv, dg (bf16), dzg (f32: this term's dL/da times a (1 - a), for
+ * theseus_tm_kk_bwd), and [C] f32 dr_k, dln_w, dln_b, dk_a */
 int theseus_tm_gn_bwd(int B, int T, int C, const void* dout, const void* y, const void* r,
-                      const void* k, const float* a, const float* k_a, const void* v, const void* g,
-                      const float* r_k, const float* ln_w, const float* ln_b, float eps, void* dy,
-                      void* dr, void* dk, void* dv, void* dg, float* da, float* dr_k, float* dln_w,
-                      float* dln_b, float* dk_a, float* workspace, size_t workspace_bytes,
+                      const void* k, const void* za, const float* a0, const float* k_a,
+                      const void* v, const void* g, const float* r_k, const float* ln_w,
+                      const float* ln_b, float eps, void* dy, void* dr, void* dk, void* dv,
+                      void* dg, float* dzg, float* dr_k, float* dln_w, float* dln_b,
+                      float* dk_a, float* workspace, size_t workspace_bytes,
                       hipStream_t stream);
 
 #ifdef __cplusplus

@@ -6,6 +6,8 @@
 //   shift-lerp     mixed_n = x + (x[t-1] - x) * coef_n, six outputs   (:70-71)
 //   kk / k-mod     kk = normalize(k*k_k), kw = k*(1+(a-1)k_a), -kk, kk*a  (:78-80)
 //   GN+bonus+gate  ((GroupNorm(y) + (sum r*kmod*r_k) v) * g)        (:83-88)
+// with a = sigmoid(a0 + za) (:75) formed inside the kernels that read it, from the bf16
+// LoRA output za and the parameter a0; its backward is folded into theirs.
 // Head rows of 64 channels are handled by 8 lanes x 8 channels (16-byte bf16
 // vectors); row sums are 8-lane butterflies.  Parameter gradients are
 // accumulated per (head, token block) and reduced over token blocks by
@@ -68,6 +70,16 @@ __device__ __forceinline__ void st_f8(float* p, const V8& v) {
     *reinterpret_cast<float4*>(p + 4) = make_float4(v.x[4], v.x[5], v.x[6], v.x[7]);
 }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+// a = sigmoid(a0 + za) of theseus/timemix.py:75 in float32 (za, the LoRA output, is bf16 and
+// the parameter a0 float32 under bf16 autocast): formed in every kernel that reads `a`, so
+// no [B,T,C] float32 `a` is written or read
+__device__ __forceinline__ V8 gate_a(const V8& a0, uint4 za) {
+    const V8 z = cvt_bf8(za);
+    V8 r;
+#pragma unroll
+    for (int e = 0; e < 8; e++) r.x[e] = 1.f / (1.f + expf(-(a0.x[e] + z.x[e])));
+    return r;
+}
 __device__ __forceinline__ float sum8(float x) {  // over the 8 lanes of a head row
     x += __shfl_xor(x, 1, 8);
     x += __shfl_xor(x, 2, 8);
@@ -244,27 +256,26 @@ __global__ __launch_bounds__(256) void reduce_blocks(const float* __restrict__ p
 // config 3 against one (token, head) row per 8 lanes).
 constexpr int KU = 4;  // tokens per wave of kk_fwd
 __global__ __launch_bounds__(256) void kk_fwd(long M, int H, int C, const uint16_t* __restrict__ k,
-                                              const float* __restrict__ a, const float* __restrict__ kkp,
-                                              const float* __restrict__ kap, uint16_t* kw, uint16_t* aw,
-                                              uint16_t* bw) {
+                                              const uint16_t* __restrict__ za, const float* __restrict__ a0p,
+                                              const float* __restrict__ kkp, const float* __restrict__ kap,
+                                              uint16_t* kw, uint16_t* aw, uint16_t* bw) {
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, sub = l & 7;
     const int ng = (H + 7) / 8, h = (int)(blockIdx.x % ng) * 8 + (l >> 3);
     const bool hok = h < H;
     const int c = (hok ? h : 0) * HN + 8 * sub;
     const long mb = ((long)(blockIdx.x / ng) * 4 + w) * KU;
-    uint4 kr[KU];
-    V8 av[KU];
+    uint4 kr[KU], zr[KU];
 #pragma unroll
     for (int u = 0; u < KU; u++) {
         const bool ok = hok && mb + u < M;
         const long o = ok ? (mb + u) * C + c : c;
         kr[u] = ld_str8(k + o);
-        av[u] = ld_f8s(a + o);
+        zr[u] = ld_str8(za + o);
     }
-    const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c);
+    const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c), a0 = ld_f8(a0p + c);
 #pragma unroll
     for (int u = 0; u < KU; u++) {
-        const V8 kv = cvt_bf8(kr[u]);
+        const V8 kv = cvt_bf8(kr[u]), av = gate_a(a0, zr[u]);
         float uu[8], ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -277,9 +288,9 @@ __global__ __launch_bounds__(256) void kk_fwd(long M, int H, int C, const uint16
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const float kkv = uu[e] * inv;
-            ow.x[e] = kv.x[e] * (1.f + (av[u].x[e] - 1.f) * ka.x[e]);
+            ow.x[e] = kv.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e]);
             oa.x[e] = -kkv;
-            ob.x[e] = kkv * av[u].x[e];
+            ob.x[e] = kkv * av.x[e];
         }
         if (hok && mb + u < M) {
             const long o = (mb + u) * C + c;
@@ -291,39 +302,44 @@ __global__ __launch_bounds__(256) void kk_fwd(long M, int H, int C, const uint16
 }
 
 // grid (ceil(H/HG), ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
+// dza = (this kernel's part of dL/da) a (1 - a) + dzg, where dzg is gn_bwd's part, already
+// times a (1 - a) (float32, or null): the two parts meet in float32 and dza (bf16) is
+// rounded once; partials dk_k, dk_a and a0's gradient (the sum of dza over tokens)
 __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16_t* __restrict__ dkw,
                                               const uint16_t* __restrict__ daw,
                                               const uint16_t* __restrict__ dbw, const uint16_t* __restrict__ k,
-                                              const float* __restrict__ a, const float* __restrict__ kkp,
-                                              const float* __restrict__ kap, uint16_t* dk, float* da,
+                                              const uint16_t* __restrict__ za, const float* __restrict__ a0p,
+                                              const float* __restrict__ dzg, const float* __restrict__ kkp,
+                                              const float* __restrict__ kap, uint16_t* dk, uint16_t* dza,
                                               float* __restrict__ part) {
-    __shared__ float red[2][32][HN + 1];
+    __shared__ float red[3][32][HN + 1];
     // 32 rows = 4 tokens x HG consecutive heads, so a wave reads whole 1 KB runs of a token;
     // the next step's rows are loaded before this step's arithmetic
     const int rs = threadIdx.x >> 3, sub = threadIdx.x & 7, hh = rs % HG, tt = rs / HG;
     const int h = blockIdx.x * HG + hh;
     const bool hok = h < H;
     const int c = (hok ? h : 0) * HN + 8 * sub;
-    const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c);
-    float acc_kk[8] = {}, acc_ka[8] = {};
-    uint4 nk, nw, na, nb;
-    V8 nav;
+    const V8 kk_ = ld_f8(kkp + c), ka = ld_f8(kap + c), a0 = ld_f8(a0p + c);
+    float acc_kk[8] = {}, acc_ka[8] = {}, acc_a0[8] = {};
+    uint4 nk, nz, nw, na, nb;
+    V8 ngz;
     auto fetch = [&](int it) {
         const long m = (long)blockIdx.y * TB + it * 4 + tt;
         const long o = hok && m < M ? m * C + c : c;
         nk = ld_str8(k + o);
-        nav = ld_f8s(a + o);
+        nz = ld_str8(za + o);
         nw = ld_str8(dkw + o);
         na = ld_str8(daw + o);
         nb = ld_str8(dbw + o);
+        ngz = dzg ? ld_f8s(dzg + o) : V8{};
     };
     fetch(0);
     for (int it = 0; it < TB / 4; it++) {
         const long m = (long)blockIdx.y * TB + it * 4 + tt;
         const bool ok = hok && m < M;
         const long o = m * C + c;
-        V8 kv = cvt_bf8(nk), av = nav, gw = cvt_bf8(nw), ga = cvt_bf8(na), gb = cvt_bf8(nb);
-        if (!ok) kv = av = gw = ga = gb = V8{};
+        V8 kv = cvt_bf8(nk), av = gate_a(a0, nz), gw = cvt_bf8(nw), ga = cvt_bf8(na), gb = cvt_bf8(nb), gz = ngz;
+        if (!ok) kv = gw = ga = gb = gz = V8{};
         if (it + 1 < TB / 4) fetch(it + 1);
         float u[8], ss = 0.f;
 #pragma unroll
@@ -343,32 +359,36 @@ __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16
             dot += kkv[e] * dkk[e];
         }
         dot = sum8(dot);
-        V8 gk, gav;
+        V8 gk, gz_out;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const float du = clamped ? dkk[e] * inv : (dkk[e] - kkv[e] * dot) * inv;
             gk.x[e] = du * kk_.x[e] + gw.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e]);
-            gav.x[e] = gb.x[e] * kkv[e] + gw.x[e] * kv.x[e] * ka.x[e];
+            const float gav = gb.x[e] * kkv[e] + gw.x[e] * kv.x[e] * ka.x[e];  // dL/da, this part
+            const float dz = gav * (av.x[e] * (1.f - av.x[e])) + gz.x[e];
+            gz_out.x[e] = dz;
             acc_kk[e] += du * kv.x[e];
             acc_ka[e] += gw.x[e] * kv.x[e] * (av.x[e] - 1.f);
+            acc_a0[e] += dz;
         }
         if (ok) {
             st_bf8(dk + o, gk);
-            st_f8(da + o, gav);
+            st_bf8(dza + o, gz_out);
         }
     }
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         red[0][rs][8 * sub + e] = acc_kk[e];
         red[1][rs][8 * sub + e] = acc_ka[e];
+        red[2][rs][8 * sub + e] = acc_a0[e];
     }
     __syncthreads();
-    for (int q = threadIdx.x; q < 2 * HG * HN; q += 256) {  // sum the 4 token rows of each head
+    for (int q = threadIdx.x; q < 3 * HG * HN; q += 256) {  // sum the 4 token rows of each head
         const int p = q / (HG * HN), hq = (q / HN) % HG, n = q % HN, hd = blockIdx.x * HG + hq;
         if (hd < H) {
             float s = 0.f;
             for (int i = 0; i < 32 / HG; i++) s += red[p][i * HG + hq][n];
-            part[((long)blockIdx.y * 2 + p) * C + hd * HN + n] = s;
+            part[((long)blockIdx.y * 3 + p) * C + hd * HN + n] = s;
         }
     }
 }
@@ -377,7 +397,8 @@ __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16
 constexpr int FU = 4;  // tokens per wave of gn_fwd (mapped as kk_fwd)
 __global__ __launch_bounds__(256) void gn_fwd(long M, int H, int C, const uint16_t* __restrict__ y,
                                               const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
-                                              const float* __restrict__ a, const float* __restrict__ kap,
+                                              const uint16_t* __restrict__ za, const float* __restrict__ a0p,
+                                              const float* __restrict__ kap,
                                               const uint16_t* __restrict__ v, const uint16_t* __restrict__ g,
                                               const float* __restrict__ rkp, const float* __restrict__ lwp,
                                               const float* __restrict__ lbp, float eps, uint16_t* out) {
@@ -386,8 +407,7 @@ __global__ __launch_bounds__(256) void gn_fwd(long M, int H, int C, const uint16
     const bool hok = h < H;
     const int c = (hok ? h : 0) * HN + 8 * sub;
     const long mb = ((long)(blockIdx.x / ng) * 4 + w) * FU;
-    uint4 yr[FU], rr[FU], kr[FU], vr[FU], gr[FU];
-    V8 av[FU];
+    uint4 yr[FU], rr[FU], kr[FU], vr[FU], gr[FU], zr[FU];
 #pragma unroll
     for (int u = 0; u < FU; u++) {
         const bool ok = hok && mb + u < M;
@@ -397,17 +417,19 @@ __global__ __launch_bounds__(256) void gn_fwd(long M, int H, int C, const uint16
         kr[u] = ld_str8(k + o);
         vr[u] = ld_str8(v + o);
         gr[u] = ld_str8(g + o);
-        av[u] = ld_f8s(a + o);
+        zr[u] = ld_str8(za + o);
     }
     const V8 ka = ld_f8(kap + c), rk = ld_f8(rkp + c), lw = ld_f8(lwp + c), lb = ld_f8(lbp + c);
+    const V8 a0 = ld_f8(a0p + c);
 #pragma unroll
     for (int u = 0; u < FU; u++) {
         const V8 yv = cvt_bf8(yr[u]), rv = cvt_bf8(rr[u]), kv = cvt_bf8(kr[u]), vv = cvt_bf8(vr[u]), gv = cvt_bf8(gr[u]);
+        const V8 av = gate_a(a0, zr[u]);
         float s = 0.f, cd = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             s += yv.x[e];
-            cd += rv.x[e] * (kv.x[e] * (1.f + (av[u].x[e] - 1.f) * ka.x[e])) * rk.x[e];
+            cd += rv.x[e] * (kv.x[e] * (1.f + (av.x[e] - 1.f) * ka.x[e])) * rk.x[e];
         }
         const float mean = sum8(s) * (1.f / HN);
         cd = sum8(cd);
@@ -424,14 +446,16 @@ __global__ __launch_bounds__(256) void gn_fwd(long M, int H, int C, const uint16
 }
 
 // grid (ceil(H/HG), ceil(M/TB)), 256 lanes = 32 rows x 8 lanes
+// dzg = this kernel's part of dL/da times a (1 - a), float32, for kk_bwd to finish dza
 __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16_t* __restrict__ dout,
                                               const uint16_t* __restrict__ y, const uint16_t* __restrict__ r,
-                                              const uint16_t* __restrict__ k, const float* __restrict__ a,
-                                              const float* __restrict__ kap, const uint16_t* __restrict__ v,
-                                              const uint16_t* __restrict__ g, const float* __restrict__ rkp,
-                                              const float* __restrict__ lwp, const float* __restrict__ lbp,
-                                              float eps, uint16_t* dy, uint16_t* dr, uint16_t* dk,
-                                              uint16_t* dv, uint16_t* dg, float* da, float* __restrict__ part) {
+                                              const uint16_t* __restrict__ k, const uint16_t* __restrict__ za,
+                                              const float* __restrict__ a0p, const float* __restrict__ kap,
+                                              const uint16_t* __restrict__ v, const uint16_t* __restrict__ g,
+                                              const float* __restrict__ rkp, const float* __restrict__ lwp,
+                                              const float* __restrict__ lbp, float eps, uint16_t* dy,
+                                              uint16_t* dr, uint16_t* dk, uint16_t* dv, uint16_t* dg,
+                                              float* dzg, float* __restrict__ part) {
     __shared__ float red[4][32][HN + 1];
     // 32 rows = 4 tokens x HG consecutive heads, as kk_bwd
     const int rs = threadIdx.x >> 3, sub = threadIdx.x & 7, hh = rs % HG, tt = rs / HG;
@@ -439,16 +463,16 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
     const bool hok = h < H;
     const int c = (hok ? h : 0) * HN + 8 * sub;
     const V8 ka = ld_f8(kap + c), rk = ld_f8(rkp + c), lw = ld_f8(lwp + c), lb = ld_f8(lbp + c);
+    const V8 a0 = ld_f8(a0p + c);
     float acc[4][8] = {};  // dr_k, dln_w, dln_b, dk_a
-    uint4 ny, nr, nk, nv, ng, no;
-    V8 nav;
+    uint4 ny, nr, nk, nz, nv, ng, no;
     auto fetch = [&](int it) {
         const long m = (long)blockIdx.y * TB + it * 4 + tt;
         const long o = hok && m < M ? m * C + c : c;
         ny = ld_str8(y + o);
         nr = ld_str8(r + o);
         nk = ld_str8(k + o);
-        nav = ld_f8s(a + o);
+        nz = ld_str8(za + o);
         nv = ld_str8(v + o);
         ng = ld_str8(g + o);
         no = ld_str8(dout + o);
@@ -458,7 +482,8 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
         const long m = (long)blockIdx.y * TB + it * 4 + tt;
         const bool ok = hok && m < M;
         const long o = m * C + c;
-        V8 yv = cvt_bf8(ny), rv = cvt_bf8(nr), kv = cvt_bf8(nk), av = nav, vv = cvt_bf8(nv), gv = cvt_bf8(ng), go = cvt_bf8(no);
+        V8 yv = cvt_bf8(ny), rv = cvt_bf8(nr), kv = cvt_bf8(nk), av = gate_a(a0, nz), vv = cvt_bf8(nv), gv = cvt_bf8(ng),
+           go = cvt_bf8(no);
         if (!ok) yv = rv = kv = av = vv = gv = go = V8{};
         if (it + 1 < TB / 4) fetch(it + 1);
         float km[8], s = 0.f, cd = 0.f;
@@ -500,7 +525,7 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
             ogr.x[e] = dc * km[e] * rk.x[e];
             const float dkm = dc * rv.x[e] * rk.x[e];
             ogk.x[e] = dkm * (1.f + (av.x[e] - 1.f) * ka.x[e]);
-            oga.x[e] = dkm * kv.x[e] * ka.x[e];
+            oga.x[e] = dkm * kv.x[e] * ka.x[e] * (av.x[e] * (1.f - av.x[e]));  // dL/da a (1 - a)
             acc[0][e] += dc * rv.x[e] * km[e];
             acc[3][e] += dkm * kv.x[e] * (av.x[e] - 1.f);
         }
@@ -510,7 +535,7 @@ __global__ __launch_bounds__(256) void gn_bwd(long M, int H, int C, const uint16
             st_bf8(dk + o, ogk);
             st_bf8(dv + o, ogv);
             st_bf8(dg + o, ogg);
-            st_f8(da + o, oga);
+            st_f8(dzg + o, oga);
         }
     }
 #pragma unroll
@@ -580,47 +605,49 @@ int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const 
     return tm_status();
 }
 
-int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const float* a, const float* k_k, const float* k_a,
-                      void* kw, void* aw, void* bw, hipStream_t stream) {
+int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const void* za, const float* a0, const float* k_k,
+                      const float* k_a, void* kw, void* aw, void* bw, hipStream_t stream) {
     if (int e = tm_check(B, T, C)) return e;
-    if (!k || !a || !k_k || !k_a || !kw || !aw || !bw) return THESEUS_WKV7_ERR_NULL;
+    if (!k || !za || !a0 || !k_k || !k_a || !kw || !aw || !bw) return THESEUS_WKV7_ERR_NULL;
     const int H = C / tmix::HN;
     const long M = (long)B * T;
     hipLaunchKernelGGL(tmix::kk_fwd, dim3((unsigned)((M + 4 * tmix::KU - 1) / (4 * tmix::KU) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
-                       (const uint16_t*)k, a, k_k, k_a, (uint16_t*)kw, (uint16_t*)aw, (uint16_t*)bw);
+                       (const uint16_t*)k, (const uint16_t*)za, a0, k_k, k_a, (uint16_t*)kw, (uint16_t*)aw, (uint16_t*)bw);
     return tm_status();
 }
 
 size_t theseus_tm_kk_workspace(int B, int T, int C) {
-    return tm_check(B, T, C) ? 0 : (size_t)nblk_t(B, T) * 2 * C * sizeof(float);
+    return tm_check(B, T, C) ? 0 : (size_t)nblk_t(B, T) * 3 * C * sizeof(float);
 }
 
 int theseus_tm_kk_bwd(int B, int T, int C, const void* dkw, const void* daw, const void* dbw, const void* k,
-                      const float* a, const float* k_k, const float* k_a, void* dk, float* da, float* dk_k,
-                      float* dk_a, float* ws, size_t ws_bytes, hipStream_t stream) {
+                      const void* za, const float* a0, const float* dzg, const float* k_k, const float* k_a,
+                      void* dk, void* dza, float* da0, float* dk_k, float* dk_a, float* ws, size_t ws_bytes,
+                      hipStream_t stream) {
     if (int e = tm_check(B, T, C)) return e;
-    if (!dkw || !daw || !dbw || !k || !a || !k_k || !k_a || !dk || !da || !dk_k || !dk_a)
+    if (!dkw || !daw || !dbw || !k || !za || !a0 || !k_k || !k_a || !dk || !dza || !da0 || !dk_k || !dk_a)
         return THESEUS_WKV7_ERR_NULL;
     if (!ws || ws_bytes < theseus_tm_kk_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
     const int H = C / tmix::HN, nb = (int)nblk_t(B, T);
     hipLaunchKernelGGL(tmix::kk_bwd, dim3((H + tmix::HG - 1) / tmix::HG, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dkw,
-                       (const uint16_t*)daw, (const uint16_t*)dbw, (const uint16_t*)k, a, k_k, k_a,
-                       (uint16_t*)dk, da, ws);
-    tmix::Outs o2{{dk_k, dk_a, nullptr, nullptr, nullptr, nullptr}};
-    hipLaunchKernelGGL(tmix::reduce_blocks, dim3((2 * C + 255) / 256), dim3(256), 0, stream, ws, nb, 2, C, o2);
+                       (const uint16_t*)daw, (const uint16_t*)dbw, (const uint16_t*)k, (const uint16_t*)za, a0, dzg,
+                       k_k, k_a, (uint16_t*)dk, (uint16_t*)dza, ws);
+    tmix::Outs o3{{dk_k, dk_a, da0, nullptr, nullptr, nullptr}};
+    hipLaunchKernelGGL(tmix::reduce_blocks, dim3((3 * C + 255) / 256), dim3(256), 0, stream, ws, nb, 3, C, o3);
     return tm_status();
 }
 
-int theseus_tm_gn_fwd(int B, int T, int C, const void* y, const void* r, const void* k, const float* a,
-                      const float* k_a, const void* v, const void* g, const float* r_k, const float* ln_w,
-                      const float* ln_b, float eps, void* out, hipStream_t stream) {
+int theseus_tm_gn_fwd(int B, int T, int C, const void* y, const void* r, const void* k, const void* za,
+                      const float* a0, const float* k_a, const void* v, const void* g, const float* r_k,
+                      const float* ln_w, const float* ln_b, float eps, void* out, hipStream_t stream) {
     if (int e = tm_check(B, T, C)) return e;
-    if (!y || !r || !k || !a || !k_a || !v || !g || !r_k || !ln_w || !ln_b || !out) return THESEUS_WKV7_ERR_NULL;
+    if (!y || !r || !k || !za || !a0 || !k_a || !v || !g || !r_k || !ln_w || !ln_b || !out)
+        return THESEUS_WKV7_ERR_NULL;
     const int H = C / tmix::HN;
     const long M = (long)B * T;
     hipLaunchKernelGGL(tmix::gn_fwd, dim3((unsigned)((M + 4 * tmix::FU - 1) / (4 * tmix::FU) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
-                       (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, a, k_a, (const uint16_t*)v,
-                       (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)out);
+                       (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)za, a0, k_a,
+                       (const uint16_t*)v, (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)out);
     return tm_status();
 }
 
@@ -629,20 +656,20 @@ size_t theseus_tm_gn_workspace(int B, int T, int C) {
 }
 
 int theseus_tm_gn_bwd(int B, int T, int C, const void* dout, const void* y, const void* r, const void* k,
-                      const float* a, const float* k_a, const void* v, const void* g, const float* r_k,
-                      const float* ln_w, const float* ln_b, float eps, void* dy, void* dr, void* dk, void* dv,
-                      void* dg, float* da, float* dr_k, float* dln_w, float* dln_b, float* dk_a, float* ws,
-                      size_t ws_bytes, hipStream_t stream) {
+                      const void* za, const float* a0, const float* k_a, const void* v, const void* g,
+                      const float* r_k, const float* ln_w, const float* ln_b, float eps, void* dy, void* dr,
+                      void* dk, void* dv, void* dg, float* dzg, float* dr_k, float* dln_w, float* dln_b,
+                      float* dk_a, float* ws, size_t ws_bytes, hipStream_t stream) {
     if (int e = tm_check(B, T, C)) return e;
-    if (!dout || !y || !r || !k || !a || !k_a || !v || !g || !r_k || !ln_w || !ln_b || !dy || !dr || !dk ||
-        !dv || !dg || !da || !dr_k || !dln_w || !dln_b || !dk_a)
+    if (!dout || !y || !r || !k || !za || !a0 || !k_a || !v || !g || !r_k || !ln_w || !ln_b || !dy || !dr ||
+        !dk || !dv || !dg || !dzg || !dr_k || !dln_w || !dln_b || !dk_a)
         return THESEUS_WKV7_ERR_NULL;
     if (!ws || ws_bytes < theseus_tm_gn_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
     const int H = C / tmix::HN, nb = (int)nblk_t(B, T);
     hipLaunchKernelGGL(tmix::gn_bwd, dim3((H + tmix::HG - 1) / tmix::HG, nb), dim3(256), 0, stream, (long)B * T, H, C, (const uint16_t*)dout,
-                       (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, a, k_a, (const uint16_t*)v,
-                       (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)dy, (uint16_t*)dr, (uint16_t*)dk,
-                       (uint16_t*)dv, (uint16_t*)dg, da, ws);
+                       (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)za, a0, k_a,
+                       (const uint16_t*)v, (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)dy, (uint16_t*)dr,
+                       (uint16_t*)dk, (uint16_t*)dv, (uint16_t*)dg, dzg, ws);
     tmix::Outs o4{{dr_k, dln_w, dln_b, dk_a, nullptr, nullptr}};
     hipLaunchKernelGGL(tmix::reduce_blocks, dim3((4 * C + 255) / 256), dim3(256), 0, stream, ws, nb, 4, C, o4);
     return tm_status();

@@ -2,16 +2,21 @@
 (C ABI: include/theseus_timemix.h).
 
 Each Function replaces one torch op chain of TimeMix.forward
-(theseus/timemix.py:70-71, 78-80, 83-88) and returns the same values and
+(theseus/timemix.py:70-71, 75, 78-80, 83-88) and returns the same values and
 gradients (to bf16 rounding) with bf16 activations:
 
 * ``shift_lerp(x, shift, coefs)`` -> 6 mixes (r, w, k, v, a, g order);
-* ``kk_kmod(k, a, k_k, k_a, N, dtype)`` -> (kw, aw, bw, k) where kw, aw, bw are
-  the WKV operands k*(1+(a-1)k_a), -kk, kk*a as [B,T,H,N] tensors of ``dtype``
-  and k is passed through unchanged (the bonus term recomputes the modulation
-  from it);
-* ``gn_bonus_gate(y, r, k, v, g, r_k, ln_w, ln_b, eps, out_dtype)`` -> fp32
+* ``kk_kmod(k, za, a0, k_k, k_a, N, dtype)`` -> (kw, aw, bw, kmod) where, with the gate
+  a = sigmoid(a0 + za) (za the LoRA output (x_a @ a1) @ a2), kw, aw, bw are the WKV
+  operands k*(1+(a-1)k_a), -kk, kk*a as [B,T,H,N] tensors of ``dtype`` and kmod carries
+  what the bonus term needs to recompute the modulation;
+* ``gn_bonus_gate(y, r, kmod, v, g, r_k, ln_w, ln_b, eps, out_dtype)`` -> fp32
   GroupNorm over heads + (sum r*kmod*r_k) v, times g, as ``out_dtype``.
+
+The gate is never materialised: both kernels that read it form it from za and a0, and
+the GroupNorm backward hands its part of dL/da (times a (1 - a), float32) to the kk
+backward through a float32 ``carrier`` output of kk_kmod, so that dL/dza is summed in
+float32 and rounded to bf16 once, as autograd does for the reference's chain.
 
 Parameters are handed to the kernels as float32 and their gradients come back
 in the parameter's dtype.
@@ -38,14 +43,14 @@ def _lib():
             lib.theseus_tm_shift_lerp_workspace.argtypes = [i32] * 3
             lib.theseus_tm_shift_lerp_workspace.restype = sz
             lib.theseus_tm_shift_lerp_bwd.argtypes = [i32] * 3 + [vp] * 8 + [sz, vp]
-            lib.theseus_tm_kk_fwd.argtypes = [i32] * 3 + [vp] * 7 + [vp]
+            lib.theseus_tm_kk_fwd.argtypes = [i32] * 3 + [vp] * 8 + [vp]
             lib.theseus_tm_kk_workspace.argtypes = [i32] * 3
             lib.theseus_tm_kk_workspace.restype = sz
-            lib.theseus_tm_kk_bwd.argtypes = [i32] * 3 + [vp] * 12 + [sz, vp]
-            lib.theseus_tm_gn_fwd.argtypes = [i32] * 3 + [vp] * 10 + [f32, vp, vp]
+            lib.theseus_tm_kk_bwd.argtypes = [i32] * 3 + [vp] * 15 + [sz, vp]
+            lib.theseus_tm_gn_fwd.argtypes = [i32] * 3 + [vp] * 11 + [f32, vp, vp]
             lib.theseus_tm_gn_workspace.argtypes = [i32] * 3
             lib.theseus_tm_gn_workspace.restype = sz
-            lib.theseus_tm_gn_bwd.argtypes = [i32] * 3 + [vp] * 11 + [f32] + [vp] * 11 + [sz, vp]
+            lib.theseus_tm_gn_bwd.argtypes = [i32] * 3 + [vp] * 12 + [f32] + [vp] * 11 + [sz, vp]
             for n in ("shift_lerp_fwd", "shift_lerp_bwd", "kk_fwd", "kk_bwd", "gn_fwd", "gn_bwd"):
                 getattr(lib, "theseus_tm_" + n).restype = i32
             _ready = True
@@ -153,91 +158,102 @@ def shift_lerp(x, shift, coefs):
 
 class _KkKmod(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, k, a, k_k, k_a, N, dtype):
+    def forward(ctx, k, za, a0, k_k, k_a, N, dtype):
         B, T, C = k.shape
         k = k.to(torch.bfloat16).contiguous()
-        af = a.float().contiguous()
-        kk_, ka = _vec(k_k, C), _vec(k_a, C)
+        zs = za.to(torch.bfloat16).contiguous()
+        a0v, kk_, ka = _vec(a0, C), _vec(k_k, C), _vec(k_a, C)
         kw, aw, bw = (torch.empty((B, T, C // N, N), dtype=torch.bfloat16, device=k.device) for _ in range(3))
         with torch.cuda.device(k.device):
-            _check(_lib().theseus_tm_kk_fwd(B, T, C, _p(k), _p(af), _p(kk_), _p(ka), _p(kw), _p(aw), _p(bw),
-                                            _s(k.device)))
-        ctx.save_for_backward(k, af, kk_, ka)
-        ctx.meta = (a.dtype, k_k.shape, k_k.dtype, k_a.shape, k_a.dtype)
+            _check(_lib().theseus_tm_kk_fwd(B, T, C, _p(k), _p(zs), _p(a0v), _p(kk_), _p(ka), _p(kw), _p(aw),
+                                            _p(bw), _s(k.device)))
+        ctx.save_for_backward(k, zs, a0v, kk_, ka)
+        ctx.meta = (za.dtype, a0.shape, a0.dtype, k_k.shape, k_k.dtype, k_a.shape, k_a.dtype)
         if dtype != torch.bfloat16:
             kw, aw, bw = kw.to(dtype), aw.to(dtype), bw.to(dtype)
-        return kw, aw, bw
+        # the channel through which gn_bonus_gate's backward returns its part of dL/da
+        # (times a (1 - a)): a [B,T,C] float32 placeholder that holds no data
+        carrier = torch.zeros((), dtype=torch.float32, device=k.device).expand(B, T, C)
+        return kw, aw, bw, carrier
 
     @staticmethod
-    def backward(ctx, dkw, daw, dbw):
-        k, af, kk_, ka = ctx.saved_tensors
+    def backward(ctx, dkw, daw, dbw, dzg):
+        k, zs, a0v, kk_, ka = ctx.saved_tensors
         B, T, C = k.shape
         z = torch.zeros(B, T, C, dtype=torch.bfloat16, device=k.device)
         g = [(d.to(torch.bfloat16).reshape(B, T, C).contiguous() if d is not None else z) for d in (dkw, daw, dbw)]
+        gz = dzg.float().contiguous() if dzg is not None else None
         dk = torch.empty_like(k)
-        da = torch.empty_like(af)
-        dkk, dka = (torch.empty(C, dtype=torch.float32, device=k.device) for _ in range(2))
+        dza = torch.empty_like(zs)
+        da0, dkk, dka = (torch.empty(C, dtype=torch.float32, device=k.device) for _ in range(3))
         lib = _lib()
         ws_bytes = int(lib.theseus_tm_kk_workspace(B, T, C))
         ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device=k.device)
         with torch.cuda.device(k.device):
-            _check(lib.theseus_tm_kk_bwd(B, T, C, *map(_p, g), _p(k), _p(af), _p(kk_), _p(ka), _p(dk), _p(da),
-                                         _p(dkk), _p(dka), _p(ws), ctypes.c_size_t(ws_bytes), _s(k.device)))
-        a_dt, kk_shape, kk_dt, ka_shape, ka_dt = ctx.meta
-        return dk, da.to(a_dt), dkk.reshape(kk_shape).to(kk_dt), dka.reshape(ka_shape).to(ka_dt), None, None
+            _check(lib.theseus_tm_kk_bwd(B, T, C, *map(_p, g), _p(k), _p(zs), _p(a0v),
+                                         _p(gz) if gz is not None else ctypes.c_void_p(0), _p(kk_), _p(ka),
+                                         _p(dk), _p(dza), _p(da0), _p(dkk), _p(dka), _p(ws),
+                                         ctypes.c_size_t(ws_bytes), _s(k.device)))
+        z_dt, a0_shape, a0_dt, kk_shape, kk_dt, ka_shape, ka_dt = ctx.meta
+        return (dk, dza.to(z_dt), da0.reshape(a0_shape).to(a0_dt), dkk.reshape(kk_shape).to(kk_dt),
+                dka.reshape(ka_shape).to(ka_dt), None, None)
 
 
-def kk_kmod(k, a, k_k, k_a, N, dtype):
-    """WKV operands (kw, aw, bw) as [B,T,H,N] plus k itself for the bonus term."""
-    kw, aw, bw = _KkKmod.apply(k, a, k_k, k_a, N, dtype)
-    return kw, aw, bw, _KMod(k, a, k_a)
+def kk_kmod(k, za, a0, k_k, k_a, N, dtype):
+    """WKV operands (kw, aw, bw) as [B,T,H,N], with a = sigmoid(a0 + za), plus what the
+    bonus term needs (gn_bonus_gate)."""
+    kw, aw, bw, carrier = _KkKmod.apply(k, za, a0, k_k, k_a, N, dtype)
+    return kw, aw, bw, _KMod(k, za, a0, k_a, carrier)
 
 
 class _KMod:
-    """Carries (k, a, k_a) to gn_bonus_gate, which recomputes k*(1+(a-1)k_a) itself."""
+    """Carries (k, za, a0, k_a) to gn_bonus_gate, which recomputes a and k*(1+(a-1)k_a)
+    itself, and the carrier through which its part of dL/da reaches kk_kmod's backward."""
 
-    def __init__(self, k, a, k_a):
-        self.k, self.a, self.k_a = k, a, k_a
+    def __init__(self, k, za, a0, k_a, carrier):
+        self.k, self.za, self.a0, self.k_a, self.carrier = k, za, a0, k_a, carrier
 
 
 class _GnBonusGate(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, y, r, k, a, k_a, v, g, r_k, ln_w, ln_b, eps, out_dtype):
+    def forward(ctx, y, r, k, carrier, za, a0, k_a, v, g, r_k, ln_w, ln_b, eps, out_dtype):
         B, T, C = r.shape
         bf = torch.bfloat16
         ys = y.reshape(B, T, C).to(bf).contiguous()
-        rs, ks, vs, gs = (t.to(bf).contiguous() for t in (r, k, v, g))
-        af = a.float().contiguous()
-        ka, rk, lw, lb = _vec(k_a, C), _vec(r_k, C), _vec(ln_w, C), _vec(ln_b, C)
+        rs, ks, zs, vs, gs = (t.to(bf).contiguous() for t in (r, k, za, v, g))
+        a0v, ka, rk, lw, lb = _vec(a0, C), _vec(k_a, C), _vec(r_k, C), _vec(ln_w, C), _vec(ln_b, C)
         out = torch.empty(B, T, C, dtype=bf, device=r.device)
         with torch.cuda.device(r.device):
-            _check(_lib().theseus_tm_gn_fwd(B, T, C, _p(ys), _p(rs), _p(ks), _p(af), _p(ka), _p(vs), _p(gs),
-                                            _p(rk), _p(lw), _p(lb), ctypes.c_float(eps), _p(out), _s(r.device)))
-        ctx.save_for_backward(ys, rs, ks, af, ka, vs, gs, rk, lw, lb)
+            _check(_lib().theseus_tm_gn_fwd(B, T, C, _p(ys), _p(rs), _p(ks), _p(zs), _p(a0v), _p(ka), _p(vs),
+                                            _p(gs), _p(rk), _p(lw), _p(lb), ctypes.c_float(eps), _p(out),
+                                            _s(r.device)))
+        ctx.save_for_backward(ys, rs, ks, zs, a0v, ka, vs, gs, rk, lw, lb)
         ctx.eps = eps
-        ctx.meta = [(t.shape, t.dtype) for t in (y, r, k, a, k_a, v, g, r_k, ln_w, ln_b)]
+        ctx.meta = [(t.shape, t.dtype) for t in (y, r, k, k_a, v, g, r_k, ln_w, ln_b)]
         return out if out_dtype == bf else out.to(out_dtype)
 
     @staticmethod
     def backward(ctx, dout):
-        ys, rs, ks, af, ka, vs, gs, rk, lw, lb = ctx.saved_tensors
+        ys, rs, ks, zs, a0v, ka, vs, gs, rk, lw, lb = ctx.saved_tensors
         B, T, C = rs.shape
         do = dout.to(torch.bfloat16).contiguous()
         dy, dr, dk, dv, dg = (torch.empty_like(rs) for _ in range(5))
-        da = torch.empty_like(af)
+        dzg = torch.empty(B, T, C, dtype=torch.float32, device=rs.device)
         drk, dlw, dlb, dka = (torch.empty(C, dtype=torch.float32, device=rs.device) for _ in range(4))
         lib = _lib()
         ws_bytes = int(lib.theseus_tm_gn_workspace(B, T, C))
         ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device=rs.device)
         with torch.cuda.device(rs.device):
-            _check(lib.theseus_tm_gn_bwd(B, T, C, _p(do), _p(ys), _p(rs), _p(ks), _p(af), _p(ka), _p(vs), _p(gs),
-                                         _p(rk), _p(lw), _p(lb), ctypes.c_float(ctx.eps), _p(dy), _p(dr), _p(dk),
-                                         _p(dv), _p(dg), _p(da), _p(drk), _p(dlw), _p(dlb), _p(dka), _p(ws),
-                                         ctypes.c_size_t(ws_bytes), _s(rs.device)))
-        grads = [dy, dr, dk, da, dka, dv, dg, drk, dlw, dlb]
-        outs = [gr.reshape(shape).to(dt) for gr, (shape, dt) in zip(grads, ctx.meta)]
-        return (*outs, None, None)
+            _check(lib.theseus_tm_gn_bwd(B, T, C, _p(do), _p(ys), _p(rs), _p(ks), _p(zs), _p(a0v), _p(ka), _p(vs),
+                                         _p(gs), _p(rk), _p(lw), _p(lb), ctypes.c_float(ctx.eps), _p(dy), _p(dr),
+                                         _p(dk), _p(dv), _p(dg), _p(dzg), _p(drk), _p(dlw), _p(dlb), _p(dka),
+                                         _p(ws), ctypes.c_size_t(ws_bytes), _s(rs.device)))
+        y_, r_, k_, ka_, v_, g_, rk_, lw_, lb_ = [gr.reshape(shape).to(dt) for gr, (shape, dt) in
+                                                  zip([dy, dr, dk, dka, dv, dg, drk, dlw, dlb], ctx.meta)]
+        # za's and a0's share of the gradient goes to kk_kmod's backward through the carrier
+        return y_, r_, k_, dzg, None, None, ka_, v_, g_, rk_, lw_, lb_, None, None
 
 
 def gn_bonus_gate(y, r, kmod, v, g, r_k, ln_w, ln_b, eps, out_dtype):
-    return _GnBonusGate.apply(y, r, kmod.k, kmod.a, kmod.k_a, v, g, r_k, ln_w, ln_b, eps, out_dtype)
+    return _GnBonusGate.apply(y, r, kmod.k, kmod.carrier, kmod.za, kmod.a0, kmod.k_a, v, g, r_k, ln_w, ln_b,
+                              eps, out_dtype)

@@ -163,14 +163,16 @@ class TimeMix(nn.Module):
         r = self.receptance(mixed["r"])
         w = self.w0 + torch.tanh(mixed["w"] @ self.w1) @ self.w2
         k, v = self.key(mixed["k"]), self.value(mixed["v"])
-        a = torch.sigmoid(self.a0 + (mixed["a"] @ self.a1) @ self.a2)
+        za = (mixed["a"] @ self.a1) @ self.a2
         g = torch.sigmoid(mixed["g"] @ self.g1) @ self.g2
         if fused_ok:
             from . import fused
-            kw, aw, bw, kmod = fused.kk_kmod(k, a, self.k_k, self.k_a, self.head_size, r.dtype)
+            # a = sigmoid(a0 + za) (the reference's theseus/timemix.py:75) is formed inside the kernels
+            kw, aw, bw, kmod = fused.kk_kmod(k, za, self.a0, self.k_k, self.k_a, self.head_size, r.dtype)
             args = [r.reshape(shape).to(r.dtype).contiguous(), w.reshape(shape).to(r.dtype).contiguous(),
                     kw, v.reshape(shape).to(r.dtype).contiguous(), aw, bw]
         else:
+            a = torch.sigmoid(self.a0 + za)
             kk = F.normalize((k.float() * self.k_k).reshape(shape), dim=-1, eps=1e-12)
             k = k * (1 + (a - 1) * self.k_a)
             args = [z.reshape(shape).to(r.dtype).contiguous()

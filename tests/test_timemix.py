@@ -128,12 +128,14 @@ def test_fused_shift_lerp_matches_torch(B, T, H):
 
 
 def _kk_gn_chain(leaves, B, T, H, N, out_dtype):
-    """The reference's op chains around the recurrence (theseus/timemix.py:78-80, 83-88):
-    the WKV operands k*(1+(a-1)k_a), -kk, kk*a and the GroupNorm/bonus/gate output."""
-    k, a, k_k, k_a, r, v, g, y, r_k, ln_w, ln_b = leaves
+    """The reference's op chains around the recurrence (theseus/timemix.py:75, 78-80, 83-88):
+    the gate a = sigmoid(a0 + za), the WKV operands k*(1+(a-1)k_a), -kk, kk*a and the
+    GroupNorm/bonus/gate output."""
+    k, za, a0, k_k, k_a, r, v, g, y, r_k, ln_w, ln_b = leaves
     C = H * N
     f = torch.float64 if out_dtype == torch.float64 else torch.float32
     shape = (B, T, H, N)
+    a = torch.sigmoid(a0 + za.to(f))
     kk = F.normalize((k.to(f) * k_k).reshape(shape), dim=-1, eps=1e-12)
     kmod = k * (1 + (a - 1) * k_a)
     ops = [z.reshape(shape).to(out_dtype) for z in (kmod, -kk, kk * a.reshape(shape))]
@@ -146,8 +148,8 @@ def _kk_gn_chain(leaves, B, T, H, N, out_dtype):
 @gpu
 @pytest.mark.parametrize("B,T,H", OP_SIZES)
 def test_fused_kk_and_gn_match_torch(B, T, H):
-    """The fused kk/k-mod and GroupNorm/bonus/gate kernels against the same op chain in
-    float64 on the CPU (outputs and all 11 input gradients at rel-L2 5e-3).  The torch
+    """The fused gate/kk/k-mod and GroupNorm/bonus/gate kernels against the same op chain in
+    float64 on the CPU (outputs and all 12 input gradients at rel-L2 5e-3).  The torch
     chain on the GPU (bf16/fp32, as TimeMix runs it unfused) is measured against the same
     float64 truth and printed beside it."""
     from theseus import fused
@@ -157,7 +159,8 @@ def test_fused_kk_and_gn_match_torch(B, T, H):
     bf = torch.bfloat16
     mk = lambda *s, dt=bf: torch.randn(*s, device="cuda", dtype=dt)  # noqa: E731
     k = mk(B, T, C).requires_grad_()
-    a = torch.sigmoid(mk(B, T, C, dt=torch.float32)).requires_grad_()
+    za = mk(B, T, C).requires_grad_()  # the LoRA output; the gate is sigmoid(a0 + za)
+    a0 = (.3 * torch.randn(1, 1, C, device="cuda")).requires_grad_()
     k_k = (.71 + .1 * torch.rand(1, 1, C, device="cuda")).requires_grad_()
     k_a = torch.full((1, 1, C), 1.02, device="cuda").requires_grad_()
     r, v, g = (mk(B, T, C).requires_grad_() for _ in range(3))
@@ -165,11 +168,11 @@ def test_fused_kk_and_gn_match_torch(B, T, H):
     r_k = torch.full((H, N), -.04, device="cuda").requires_grad_()
     ln_w = (1 + .1 * torch.randn(C, device="cuda")).requires_grad_()
     ln_b = (.1 * torch.randn(C, device="cuda")).requires_grad_()
-    leaves = [k, a, k_k, k_a, r, v, g, y, r_k, ln_w, ln_b]
+    leaves = [k, za, a0, k_k, k_a, r, v, g, y, r_k, ln_w, ln_b]
     refl = [t.detach().clone().requires_grad_() for t in leaves]
     truthl = [t.detach().cpu().double().requires_grad_() for t in leaves]
 
-    kw, aw, bw, km = fused.kk_kmod(k, a, k_k, k_a, N, bf)
+    kw, aw, bw, km = fused.kk_kmod(k, za, a0, k_k, k_a, N, bf)
     out = fused.gn_bonus_gate(y, r, km, v, g, r_k, ln_w, ln_b, 64e-5, bf)
     got = (kw, aw, bw, out)
     refs = _kk_gn_chain(refl, B, T, H, N, bf)
@@ -182,7 +185,7 @@ def test_fused_kk_and_gn_match_torch(B, T, H):
     torch.autograd.backward(got, gs)
     torch.autograd.backward(refs, gs)
     torch.autograd.backward(truth, [gg.cpu().double() for gg in gs])
-    names = ["k", "a", "k_k", "k_a", "r", "v", "g", "y", "r_k", "ln_w", "ln_b"]
+    names = ["k", "za", "a0", "k_k", "k_a", "r", "v", "g", "y", "r_k", "ln_w", "ln_b"]
     bad = []
     for n, t, tr, tt in zip(names, leaves, refl, truthl):
         e = rel_l2(t.grad.float().cpu(), tt.grad)
