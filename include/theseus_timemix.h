@@ -37,6 +37,12 @@ int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dmixed, co
                               float* dcoef, float* workspace, size_t workspace_bytes,
                               hipStream_t stream);
 
+/* The decay input w = (w0 + zw).to(bf16) (theseus/timemix.py:73, 80): float32 parameter w0
+ * [C] plus the bf16 LoRA output zw [B,T,C], rounded once to bf16.  Its backward needs no
+ * kernel: dL/dzw is dL/dw itself and dL/dw0 its sum over B*T. */
+int theseus_tm_add_param_fwd(int B, int T, int C, const void* zw, const float* w0, void* w,
+                             hipStream_t stream);
+
 /* WKV operands (theseus/timemix.py:75, 78-80): a = sigmoid(a0 + za), kk = normalize(k * k_k)
  * per head (eps 1e-12), kw = k * (1 + (a - 1) * k_a), aw = -kk, bw = kk * a, all written as
  * bf16. */

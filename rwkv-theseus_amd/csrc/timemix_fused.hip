@@ -247,6 +247,22 @@ __global__ __launch_bounds__(256) void reduce_blocks(const float* __restrict__ p
     outs.p[j / C][j % C] = s;
 }
 
+// ---------------------------------------------------------------- decay input
+// w = (w0 + zw).to(bf16) of theseus/timemix.py:73, 80: the float32 parameter w0 plus the bf16
+// LoRA output zw, rounded to bf16 once (the reference adds in float32 and casts); 8 channels
+// per thread, whole rows of threads over whole rows of w.
+__global__ __launch_bounds__(256) void add_param_bf16(long n8, int C, const uint16_t* __restrict__ z,
+                                                      const float* __restrict__ p, uint16_t* __restrict__ out) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const int c = (int)(i % (C / 8)) * 8;
+    const V8 zv = cvt_bf8(ld_str8(z + 8 * i)), pv = ld_f8(p + c);
+    V8 o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) o.x[e] = pv.x[e] + zv.x[e];
+    st_bf8(out + 8 * i, o);
+}
+
 // ---------------------------------------------------------------- kk / k-mod
 // The forward kernels: ceil(H / 8) x ceil(M / (4 U)) workgroups of 256 lanes, head groups
 // first (workgroups next in line read neighbouring 1 KB runs of the same tokens; token-first
@@ -602,6 +618,15 @@ int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const 
                        (const uint16_t*)x, (const uint16_t*)st, coef, (uint16_t*)dx, (uint16_t*)dshift, ws);
     tmix::Outs o6{{dcoef, dcoef + C, dcoef + 2 * C, dcoef + 3 * C, dcoef + 4 * C, dcoef + 5 * C}};
     hipLaunchKernelGGL(tmix::reduce_blocks, dim3((6 * C + 255) / 256), dim3(256), 0, stream, ws, nb, 6, C, o6);
+    return tm_status();
+}
+
+int theseus_tm_add_param_fwd(int B, int T, int C, const void* z, const float* p, void* out, hipStream_t stream) {
+    if (int e = tm_check(B, T, C)) return e;
+    if (!z || !p || !out) return THESEUS_WKV7_ERR_NULL;
+    const long n8 = (long)B * T * C / 8;
+    hipLaunchKernelGGL(tmix::add_param_bf16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream, n8, C,
+                       (const uint16_t*)z, p, (uint16_t*)out);
     return tm_status();
 }
 

@@ -6,6 +6,8 @@ Each Function replaces one torch op chain of TimeMix.forward
 gradients (to bf16 rounding) with bf16 activations:
 
 * ``shift_lerp(x, shift, coefs)`` -> 6 mixes (r, w, k, v, a, g order);
+* ``add_param(z, p)`` -> (p + z).to(bf16), the decay input w = w0 + zw as the recurrence
+  takes it (theseus/timemix.py:73, 80), without the float32 [B,T,C] sum;
 * ``kk_kmod(k, za, a0, k_k, k_a, N, dtype)`` -> (kw, aw, bw, kmod) where, with the gate
   a = sigmoid(a0 + za) (za the LoRA output (x_a @ a1) @ a2), kw, aw, bw are the WKV
   operands k*(1+(a-1)k_a), -kk, kk*a as [B,T,H,N] tensors of ``dtype`` and kmod carries
@@ -43,6 +45,7 @@ def _lib():
             lib.theseus_tm_shift_lerp_workspace.argtypes = [i32] * 3
             lib.theseus_tm_shift_lerp_workspace.restype = sz
             lib.theseus_tm_shift_lerp_bwd.argtypes = [i32] * 3 + [vp] * 8 + [sz, vp]
+            lib.theseus_tm_add_param_fwd.argtypes = [i32] * 3 + [vp] * 3 + [vp]
             lib.theseus_tm_kk_fwd.argtypes = [i32] * 3 + [vp] * 8 + [vp]
             lib.theseus_tm_kk_workspace.argtypes = [i32] * 3
             lib.theseus_tm_kk_workspace.restype = sz
@@ -51,7 +54,7 @@ def _lib():
             lib.theseus_tm_gn_workspace.argtypes = [i32] * 3
             lib.theseus_tm_gn_workspace.restype = sz
             lib.theseus_tm_gn_bwd.argtypes = [i32] * 3 + [vp] * 12 + [f32] + [vp] * 11 + [sz, vp]
-            for n in ("shift_lerp_fwd", "shift_lerp_bwd", "kk_fwd", "kk_bwd", "gn_fwd", "gn_bwd"):
+            for n in ("shift_lerp_fwd", "shift_lerp_bwd", "add_param_fwd", "kk_fwd", "kk_bwd", "gn_fwd", "gn_bwd"):
                 getattr(lib, "theseus_tm_" + n).restype = i32
             _ready = True
         except AttributeError:
@@ -154,6 +157,30 @@ class _ShiftLerp(torch.autograd.Function):
 
 def shift_lerp(x, shift, coefs):
     return _ShiftLerp.apply(x, shift, *coefs)
+
+
+class _AddParam(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, z, p):
+        B, T, C = z.shape
+        zs = z.to(torch.bfloat16).contiguous()
+        out = torch.empty_like(zs)
+        with torch.cuda.device(z.device):
+            _check(_lib().theseus_tm_add_param_fwd(B, T, C, _p(zs), _p(_vec(p, C)), _p(out), _s(z.device)))
+        ctx.meta = (z.dtype, p.shape, p.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        # as the reference's float32 add and cast: dL/dz is dL/dw, dL/dp its float32 sum
+        z_dt, p_shape, p_dt = ctx.meta
+        dp = torch.sum(dout, dim=(0, 1), dtype=torch.float32)
+        return dout.to(z_dt), dp.reshape(p_shape).to(p_dt)
+
+
+def add_param(z, p):
+    """(p + z).to(bf16) for a bf16 [B,T,C] tensor z and a parameter p with C elements."""
+    return _AddParam.apply(z, p)
 
 
 class _KkKmod(torch.autograd.Function):

@@ -161,7 +161,12 @@ class TimeMix(nn.Module):
             mixed = dict(zip("rwkvag", _shift_lerp_ops(
                 x, state["shift"], [getattr(self, "x_" + n) for n in "rwkvag"])))
         r = self.receptance(mixed["r"])
-        w = self.w0 + torch.tanh(mixed["w"] @ self.w1) @ self.w2
+        zw = torch.tanh(mixed["w"] @ self.w1) @ self.w2
+        if fused_ok:
+            from . import fused
+            w = fused.add_param(zw, self.w0)  # (w0 + zw) in the recurrence's bf16, in one pass
+        else:
+            w = self.w0 + zw
         k, v = self.key(mixed["k"]), self.value(mixed["v"])
         za = (mixed["a"] @ self.a1) @ self.a2
         g = torch.sigmoid(mixed["g"] @ self.g1) @ self.g2

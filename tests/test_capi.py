@@ -61,7 +61,7 @@ def test_timemix_abi_exported_and_bound_with_header_arity():
     lib = fused._lib()
     assert lib is not None
     arity = declared_arity(ROOT / "include" / "theseus_timemix.h")
-    assert len(arity) == 9
+    assert len(arity) == 10
     for name, n in arity.items():
         fn = getattr(lib, name)
         assert fn.argtypes is not None and len(fn.argtypes) == n, (name, n)
@@ -73,8 +73,8 @@ def test_timemix_abi_rejects_shapes_before_launching():
     along the grid's y dimension.  Null pointers are never reached."""
     from theseus import fused
     lib = fused._lib()
-    names = ["theseus_tm_shift_lerp_fwd", "theseus_tm_shift_lerp_bwd", "theseus_tm_kk_fwd",
-             "theseus_tm_kk_bwd", "theseus_tm_gn_fwd", "theseus_tm_gn_bwd"]
+    names = ["theseus_tm_shift_lerp_fwd", "theseus_tm_shift_lerp_bwd", "theseus_tm_add_param_fwd",
+             "theseus_tm_kk_fwd", "theseus_tm_kk_bwd", "theseus_tm_gn_fwd", "theseus_tm_gn_bwd"]
     for B, T, C in [(1 << 16, 1 << 13, 64), (65535, 65, 64), (1, 4, 96), (0, 4, 64), (1, 0, 64)]:
         for name in names:
             fn = getattr(lib, name)

@@ -147,6 +147,26 @@ def _kk_gn_chain(leaves, B, T, H, N, out_dtype):
 
 @gpu
 @pytest.mark.parametrize("B,T,H", OP_SIZES)
+def test_fused_decay_input_matches_torch(B, T, H):
+    """w = (w0 + zw).to(bf16) (theseus/timemix.py:73, 80) in one kernel: the same bits as
+    torch's float32 add and cast; dL/dzw is dL/dw, dL/dw0 its float32 sum over tokens."""
+    from theseus import fused
+    torch.manual_seed(4)
+    C = 64 * H
+    zw = torch.randn(B, T, C, device="cuda", dtype=torch.bfloat16).requires_grad_()
+    w0 = torch.randn(1, 1, C, device="cuda").requires_grad_()
+    z2, p2 = zw.detach().clone().requires_grad_(), w0.detach().clone().requires_grad_()
+    got, ref = fused.add_param(zw, w0), (p2 + z2).to(torch.bfloat16)
+    assert got.dtype == torch.bfloat16 and torch.equal(got, ref)
+    dw = torch.randn_like(got)
+    got.backward(dw)
+    ref.backward(dw)
+    assert torch.equal(zw.grad, z2.grad)
+    torch.testing.assert_close(w0.grad, p2.grad, rtol=1e-5, atol=1e-4)
+
+
+@gpu
+@pytest.mark.parametrize("B,T,H", OP_SIZES)
 def test_fused_kk_and_gn_match_torch(B, T, H):
     """The fused gate/kk/k-mod and GroupNorm/bonus/gate kernels against the same op chain in
     float64 on the CPU (outputs and all 12 input gradients at rel-L2 5e-3).  The torch
