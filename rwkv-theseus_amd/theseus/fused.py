@@ -199,8 +199,9 @@ class _KkKmod(torch.autograd.Function):
         if dtype != torch.bfloat16:
             kw, aw, bw = kw.to(dtype), aw.to(dtype), bw.to(dtype)
         # the channel through which gn_bonus_gate's backward returns its part of dL/da
-        # (times a (1 - a)): a [B,T,C] float32 placeholder that holds no data
-        carrier = torch.zeros((), dtype=torch.float32, device=k.device).expand(B, T, C)
+        # (times a (1 - a)): a [B,T,C] float32 placeholder whose one element is never read
+        # (so nothing is launched to fill it)
+        carrier = torch.empty((), dtype=torch.float32, device=k.device).expand(B, T, C)
         return kw, aw, bw, carrier
 
     @staticmethod
