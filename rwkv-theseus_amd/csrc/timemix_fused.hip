@@ -270,7 +270,10 @@ __global__ __launch_bounds__(256) void add_param_bf16(long n8, int C, const uint
 // of a token per load) of the tokens 4 U tb + U w + u, u < U, all U tokens' loads issued
 // before any is used and the parameter vectors loaded once (gn_fwd: 127 -> 121 µs at
 // config 3 against one (token, head) row per 8 lanes).
-constexpr int KU = 4;  // tokens per wave of kk_fwd
+// KU / FU tokens per wave: 4 for long inputs, 1 for short ones (a serving step's 64 tokens
+// would fill only 40 workgroups with 4: 7.3 against 4.5 µs per gn_fwd call)
+constexpr int U_LONG = 4;
+template <int KU>
 __global__ __launch_bounds__(256) void kk_fwd(long M, int H, int C, const uint16_t* __restrict__ k,
                                               const uint16_t* __restrict__ za, const float* __restrict__ a0p,
                                               const float* __restrict__ kkp, const float* __restrict__ kap,
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(256) void kk_bwd(long M, int H, int C, const uint16
 }
 
 // ---------------------------------------------------------------- GroupNorm + bonus + gate
-constexpr int FU = 4;  // tokens per wave of gn_fwd (mapped as kk_fwd)
+template <int FU>  // tokens per wave (mapped as kk_fwd)
 __global__ __launch_bounds__(256) void gn_fwd(long M, int H, int C, const uint16_t* __restrict__ y,
                                               const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                                               const uint16_t* __restrict__ za, const float* __restrict__ a0p,
@@ -636,7 +639,9 @@ int theseus_tm_kk_fwd(int B, int T, int C, const void* k, const void* za, const 
     if (!k || !za || !a0 || !k_k || !k_a || !kw || !aw || !bw) return THESEUS_WKV7_ERR_NULL;
     const int H = C / tmix::HN;
     const long M = (long)B * T;
-    hipLaunchKernelGGL(tmix::kk_fwd, dim3((unsigned)((M + 4 * tmix::KU - 1) / (4 * tmix::KU) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
+    const int U = M >= 4096 ? tmix::U_LONG : 1;
+    hipLaunchKernelGGL(U == 1 ? tmix::kk_fwd<1> : tmix::kk_fwd<tmix::U_LONG>,
+                       dim3((unsigned)((M + 4 * U - 1) / (4 * U) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
                        (const uint16_t*)k, (const uint16_t*)za, a0, k_k, k_a, (uint16_t*)kw, (uint16_t*)aw, (uint16_t*)bw);
     return tm_status();
 }
@@ -670,7 +675,9 @@ int theseus_tm_gn_fwd(int B, int T, int C, const void* y, const void* r, const v
         return THESEUS_WKV7_ERR_NULL;
     const int H = C / tmix::HN;
     const long M = (long)B * T;
-    hipLaunchKernelGGL(tmix::gn_fwd, dim3((unsigned)((M + 4 * tmix::FU - 1) / (4 * tmix::FU) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
+    const int U = M >= 4096 ? tmix::U_LONG : 1;
+    hipLaunchKernelGGL(U == 1 ? tmix::gn_fwd<1> : tmix::gn_fwd<tmix::U_LONG>,
+                       dim3((unsigned)((M + 4 * U - 1) / (4 * U) * ((H + 7) / 8))), dim3(256), 0, stream, M, H, C,
                        (const uint16_t*)y, (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)za, a0, k_a,
                        (const uint16_t*)v, (const uint16_t*)g, r_k, ln_w, ln_b, eps, (uint16_t*)out);
     return tm_status();

@@ -159,16 +159,20 @@ def shift_lerp(x, shift, coefs):
     return _ShiftLerp.apply(x, shift, *coefs)
 
 
+def _add_param_fwd(z, p):
+    B, T, C = z.shape
+    zs = z.to(torch.bfloat16).contiguous()
+    out = torch.empty_like(zs)
+    with torch.cuda.device(z.device):
+        _check(_lib().theseus_tm_add_param_fwd(B, T, C, _p(zs), _p(_vec(p, C)), _p(out), _s(z.device)))
+    return out
+
+
 class _AddParam(torch.autograd.Function):
     @staticmethod
     def forward(ctx, z, p):
-        B, T, C = z.shape
-        zs = z.to(torch.bfloat16).contiguous()
-        out = torch.empty_like(zs)
-        with torch.cuda.device(z.device):
-            _check(_lib().theseus_tm_add_param_fwd(B, T, C, _p(zs), _p(_vec(p, C)), _p(out), _s(z.device)))
         ctx.meta = (z.dtype, p.shape, p.dtype)
-        return out
+        return _add_param_fwd(z, p)
 
     @staticmethod
     def backward(ctx, dout):
@@ -180,24 +184,36 @@ class _AddParam(torch.autograd.Function):
 
 def add_param(z, p):
     """(p + z).to(bf16) for a bf16 [B,T,C] tensor z and a parameter p with C elements."""
-    return _AddParam.apply(z, p)
+    if torch.is_grad_enabled() and (z.requires_grad or p.requires_grad):
+        return _AddParam.apply(z, p)
+    return _add_param_fwd(z, p)  # (serving: no autograd node per token)
+
+
+def _needs_grad(*ts):
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts)
+
+
+def _kk_fwd(k, za, a0, k_k, k_a, N, dtype):
+    B, T, C = k.shape
+    k = k.to(torch.bfloat16).contiguous()
+    zs = za.to(torch.bfloat16).contiguous()
+    a0v, kk_, ka = _vec(a0, C), _vec(k_k, C), _vec(k_a, C)
+    kw, aw, bw = (torch.empty((B, T, C // N, N), dtype=torch.bfloat16, device=k.device) for _ in range(3))
+    with torch.cuda.device(k.device):
+        _check(_lib().theseus_tm_kk_fwd(B, T, C, _p(k), _p(zs), _p(a0v), _p(kk_), _p(ka), _p(kw), _p(aw),
+                                        _p(bw), _s(k.device)))
+    if dtype != torch.bfloat16:
+        kw, aw, bw = kw.to(dtype), aw.to(dtype), bw.to(dtype)
+    return (k, zs, a0v, kk_, ka), (kw, aw, bw)
 
 
 class _KkKmod(torch.autograd.Function):
     @staticmethod
     def forward(ctx, k, za, a0, k_k, k_a, N, dtype):
         B, T, C = k.shape
-        k = k.to(torch.bfloat16).contiguous()
-        zs = za.to(torch.bfloat16).contiguous()
-        a0v, kk_, ka = _vec(a0, C), _vec(k_k, C), _vec(k_a, C)
-        kw, aw, bw = (torch.empty((B, T, C // N, N), dtype=torch.bfloat16, device=k.device) for _ in range(3))
-        with torch.cuda.device(k.device):
-            _check(_lib().theseus_tm_kk_fwd(B, T, C, _p(k), _p(zs), _p(a0v), _p(kk_), _p(ka), _p(kw), _p(aw),
-                                            _p(bw), _s(k.device)))
-        ctx.save_for_backward(k, zs, a0v, kk_, ka)
+        saved, (kw, aw, bw) = _kk_fwd(k, za, a0, k_k, k_a, N, dtype)
+        ctx.save_for_backward(*saved)
         ctx.meta = (za.dtype, a0.shape, a0.dtype, k_k.shape, k_k.dtype, k_a.shape, k_a.dtype)
-        if dtype != torch.bfloat16:
-            kw, aw, bw = kw.to(dtype), aw.to(dtype), bw.to(dtype)
         # the channel through which gn_bonus_gate's backward returns its part of dL/da
         # (times a (1 - a)): a [B,T,C] float32 placeholder whose one element is never read
         # (so nothing is launched to fill it)
@@ -230,6 +246,8 @@ class _KkKmod(torch.autograd.Function):
 def kk_kmod(k, za, a0, k_k, k_a, N, dtype):
     """WKV operands (kw, aw, bw) as [B,T,H,N], with a = sigmoid(a0 + za), plus what the
     bonus term needs (gn_bonus_gate)."""
+    if not _needs_grad(k, za, a0, k_k, k_a):  # (serving: no autograd node, no carrier)
+        return (*_kk_fwd(k, za, a0, k_k, k_a, N, dtype)[1], _KMod(k, za, a0, k_a, None))
     kw, aw, bw, carrier = _KkKmod.apply(k, za, a0, k_k, k_a, N, dtype)
     return kw, aw, bw, _KMod(k, za, a0, k_a, carrier)
 
@@ -242,20 +260,26 @@ class _KMod:
         self.k, self.za, self.a0, self.k_a, self.carrier = k, za, a0, k_a, carrier
 
 
+def _gn_fwd(y, r, k, za, a0, k_a, v, g, r_k, ln_w, ln_b, eps):
+    B, T, C = r.shape
+    bf = torch.bfloat16
+    ys = y.reshape(B, T, C).to(bf).contiguous()
+    rs, ks, zs, vs, gs = (t.to(bf).contiguous() for t in (r, k, za, v, g))
+    a0v, ka, rk, lw, lb = _vec(a0, C), _vec(k_a, C), _vec(r_k, C), _vec(ln_w, C), _vec(ln_b, C)
+    out = torch.empty(B, T, C, dtype=bf, device=r.device)
+    with torch.cuda.device(r.device):
+        _check(_lib().theseus_tm_gn_fwd(B, T, C, _p(ys), _p(rs), _p(ks), _p(zs), _p(a0v), _p(ka), _p(vs),
+                                        _p(gs), _p(rk), _p(lw), _p(lb), ctypes.c_float(eps), _p(out),
+                                        _s(r.device)))
+    return (ys, rs, ks, zs, a0v, ka, vs, gs, rk, lw, lb), out
+
+
 class _GnBonusGate(torch.autograd.Function):
     @staticmethod
     def forward(ctx, y, r, k, carrier, za, a0, k_a, v, g, r_k, ln_w, ln_b, eps, out_dtype):
-        B, T, C = r.shape
         bf = torch.bfloat16
-        ys = y.reshape(B, T, C).to(bf).contiguous()
-        rs, ks, zs, vs, gs = (t.to(bf).contiguous() for t in (r, k, za, v, g))
-        a0v, ka, rk, lw, lb = _vec(a0, C), _vec(k_a, C), _vec(r_k, C), _vec(ln_w, C), _vec(ln_b, C)
-        out = torch.empty(B, T, C, dtype=bf, device=r.device)
-        with torch.cuda.device(r.device):
-            _check(_lib().theseus_tm_gn_fwd(B, T, C, _p(ys), _p(rs), _p(ks), _p(zs), _p(a0v), _p(ka), _p(vs),
-                                            _p(gs), _p(rk), _p(lw), _p(lb), ctypes.c_float(eps), _p(out),
-                                            _s(r.device)))
-        ctx.save_for_backward(ys, rs, ks, zs, a0v, ka, vs, gs, rk, lw, lb)
+        saved, out = _gn_fwd(y, r, k, za, a0, k_a, v, g, r_k, ln_w, ln_b, eps)
+        ctx.save_for_backward(*saved)
         ctx.eps = eps
         ctx.meta = [(t.shape, t.dtype) for t in (y, r, k, k_a, v, g, r_k, ln_w, ln_b)]
         return out if out_dtype == bf else out.to(out_dtype)
@@ -279,9 +303,13 @@ class _GnBonusGate(torch.autograd.Function):
         y_, r_, k_, ka_, v_, g_, rk_, lw_, lb_ = [gr.reshape(shape).to(dt) for gr, (shape, dt) in
                                                   zip([dy, dr, dk, dka, dv, dg, drk, dlw, dlb], ctx.meta)]
         # za's and a0's share of the gradient goes to kk_kmod's backward through the carrier
-        return y_, r_, k_, dzg, None, None, ka_, v_, g_, rk_, lw_, lb_, None, None
+        return (y_, r_, k_, dzg if ctx.needs_input_grad[3] else None, None, None, ka_, v_, g_, rk_, lw_, lb_,
+                None, None)
 
 
 def gn_bonus_gate(y, r, kmod, v, g, r_k, ln_w, ln_b, eps, out_dtype):
+    if not _needs_grad(y, r, kmod.k, kmod.za, kmod.a0, kmod.k_a, v, g, r_k, ln_w, ln_b):
+        out = _gn_fwd(y, r, kmod.k, kmod.za, kmod.a0, kmod.k_a, v, g, r_k, ln_w, ln_b, eps)[1]
+        return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
     return _GnBonusGate.apply(y, r, kmod.k, kmod.carrier, kmod.za, kmod.a0, kmod.k_a, v, g, r_k, ln_w, ln_b,
                               eps, out_dtype)
