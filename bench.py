@@ -413,6 +413,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-ms", type=float, default=100.0,
+                    help="untimed steps after the warmup steps until this much time under load has "
+                         "passed, before the timed steps (the GPU's clock transient)")
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-slice", type=int, default=256, help="T of each CPU baseline slice (0: skip)")
     ap.add_argument("--timemix-unfused", action="store_true",
@@ -489,16 +492,31 @@ def main():
                 _, st, _ = ext.forward(*pc, st, False)
             return st
 
+    def timed(k):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(k):
+            one_step()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t
+
+    # -- W warmup steps, then K steps timed right after them ------------------------------
+    t_warm = time.perf_counter()
     for _ in range(args.warmup):
         one_step()
+    ms_after_w = timed(args.steps) * 1e3 / args.steps
+    # The MI355X's clocks go through a transient in the first ~20 ms of sustained load
+    # (kernel trace of this bench: the same kernels run up to 30 % longer there, with no
+    # gap between launches), so the K steps right after W short warmup steps time part of
+    # it.  The reported steps come after untimed steps that fill --settle-ms of load.
+    settle = args.warmup + args.steps
+    while (time.perf_counter() - t_warm) * 1e3 < args.settle_ms:
+        one_step()
+        settle += 1
     torch.cuda.synchronize()
 
     # -- timed region: exactly K steps ---------------------------------------------------
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        one_step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    elapsed = timed(args.steps)
     ms_per_step = elapsed * 1e3 / args.steps
     tokens = B * T
     value = tokens * args.steps / elapsed
@@ -604,6 +622,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "untimed_steps_before_timing": settle,
+        "ms_per_step_right_after_warmup": round(ms_after_w, 4),
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

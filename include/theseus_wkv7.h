@@ -198,7 +198,10 @@ int theseus_wkv7_decode_step(int B, int H, int N, int dtype,
  * return THESEUS_WKV7_ERR_SCRATCH without enqueuing anything.  The call
  * allocates nothing (no hipMalloc/hipFree).  All calls on one device share
  * that array: calls that may run at the same time on one device (different
- * streams) race and must be serialised by the caller. */
+ * streams, or graphs holding this call replayed concurrently) race on its
+ * handoff counters and carried states and give silently wrong or NaN results,
+ * not an error.  Call it from one stream per device, or order the streams
+ * (an event or stream wait between two such calls). */
 int theseus_wkv7_forward_noalloc(int B, int T, int H, int N, int dtype,
                                  const void* r, const void* w, const void* k, const void* v,
                                  const void* a, const void* b, const float* s0,

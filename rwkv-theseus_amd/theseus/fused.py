@@ -25,8 +25,8 @@ in the parameter's dtype.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
-import weakref
 
 import torch
 
@@ -86,27 +86,54 @@ def _check(status):
         raise RuntimeError("theseus_timemix: " + extension().lib.theseus_wkv7_error_string(status).decode())
 
 
-# float32 copies of parameters kept in another dtype (bf16 serving weights) and the
-# stacked shift-lerp coefficients, reused while every source tensor is unchanged (same
-# version counter and storage), so a serving step does not convert its parameters again
-# on every token.  Never filled while a stream is being captured into a graph: a copy
+# Derived parameter tensors -- float32 copies of parameters kept in another dtype (bf16
+# serving weights) and the stacked shift-lerp coefficients -- are made afresh on every
+# call, so they always hold the parameters' current values, however those were updated
+# (optimizer kernels that write through raw pointers change no version counter).  Only
+# inside ``param_cache(store)`` are they made once and kept in the caller's ``store``:
+# a serving loop or a captured graph (theseus.serving.CapturedStep) that owns the store
+# then reuses them on every token, and calls ``refresh_param_cache(store)`` after a
+# weight update.  Never filled while a stream is being captured into a graph: a copy
 # made under capture holds its values only once the graph has run.
-_derived = {}  # id(first source) -> {slot: (ids of the sources, their stamps, value)}
+_store = None  # the store of the innermost param_cache, or None
+
+
+@contextlib.contextmanager
+def param_cache(store):
+    """Keep the derived parameter tensors made inside this context in ``store`` (a dict
+    the caller owns) and reuse them; they live as long as ``store``."""
+    global _store
+    prev, _store = _store, store
+    try:
+        yield store
+    finally:
+        _store = prev
+
+
+def refresh_param_cache(store):
+    """Rewrite every derived tensor held in ``store`` in place from its parameters'
+    current values (same addresses, so graphs captured over them stay valid)."""
+    global _store
+    prev, _store = _store, None
+    try:
+        with torch.no_grad():
+            for _srcs, make, out in store.values():
+                out.copy_(make())
+    finally:
+        _store = prev
 
 
 def _cached(slot, srcs, make):
-    ids = tuple(id(t) for t in srcs)
-    stamp = tuple((t._version, t.data_ptr()) for t in srcs)
-    slots = _derived.get(ids[0])
-    hit = slots.get(slot) if slots is not None else None
-    if hit is not None and hit[0] == ids and hit[1] == stamp:
+    store = _store
+    if store is None:
+        return make()
+    key = (slot,) + tuple(id(t) for t in srcs)
+    hit = store.get(key)
+    if hit is not None:
         return hit[2]
     out = make()
     if not (out.is_cuda and torch.cuda.is_current_stream_capturing()):
-        if slots is None:
-            slots = _derived[ids[0]] = {}
-            weakref.finalize(srcs[0], _derived.pop, ids[0], None)  # forget it with its source
-        slots[slot] = (ids, stamp, out)
+        store[key] = (tuple(srcs), make, out)  # (the sources stay alive with the store)
     return out
 
 

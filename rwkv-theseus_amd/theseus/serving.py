@@ -12,13 +12,18 @@ adds what a serving loop needs around it:
 * ``CapturedStep``: one ``step_`` captured into a HIP graph (``torch.cuda.CUDAGraph``),
   so a token costs one graph launch instead of ~20 kernel launches from Python.  The
   state tensors and the input/output buffers keep fixed addresses, which is what makes
-  the capture valid; every replay advances the captured state by one token.
+  the capture valid; every replay advances the captured state by one token.  The graph
+  also reads float32 copies of the layer's small parameters (the stacked shift-lerp
+  coefficients; bf16 vectors), which the CapturedStep owns (theseus.fused.param_cache):
+  after an in-place weight update call ``refresh_params()`` before the next replay.
 """
 from __future__ import annotations
 
 import contextlib
 
 import torch
+
+from . import fused
 
 
 def serving_state(state):
@@ -47,6 +52,13 @@ class CapturedStep:
 
     Capture runs the step twice eagerly first (on a side stream, as torch's capture
     requires) and then restores ``state`` to its value at construction.
+
+    The graph reads the parameters in place -- the projection weights directly, the
+    small parameters through float32 copies held by this object (``self.params``,
+    made during the eager steps, so none is allocated under capture and none can be
+    freed while the graph may still replay).  Weights must be updated in place (same
+    storage); after such an update, ``refresh_params()`` rewrites the copies, so the
+    next replay computes with the new weights.
     """
 
     def __init__(self, model, state, x_example, autocast=torch.bfloat16):
@@ -54,10 +66,11 @@ class CapturedStep:
             raise ValueError("CapturedStep takes a CUDA x of shape [B,1,C]")
         self.model, self.state, self.autocast = model, state, autocast
         self.x = x_example.detach().clone()
+        self.params = {}  # derived parameter tensors the graph reads (fused.param_cache)
         saved = {k: v.clone() for k, v in state.items()}
         side = torch.cuda.Stream(device=self.x.device)
         side.wait_stream(torch.cuda.current_stream(self.x.device))
-        with torch.cuda.stream(side), torch.no_grad(), _autocast(autocast):
+        with torch.cuda.stream(side), torch.no_grad(), _autocast(autocast), fused.param_cache(self.params):
             for _ in range(2):
                 model.step_(self.x, state)
         torch.cuda.current_stream(self.x.device).wait_stream(side)
@@ -65,9 +78,14 @@ class CapturedStep:
             for k, v in state.items():
                 v.copy_(saved[k])
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph), torch.no_grad(), _autocast(autocast):
+        with torch.cuda.graph(self.graph), torch.no_grad(), _autocast(autocast), fused.param_cache(self.params):
             self.out = model.step_(self.x, state)
         torch.cuda.synchronize(self.x.device)
+
+    def refresh_params(self):
+        """Rewrite the graph's parameter copies from the model's current (in place
+        updated) weights; the next replay uses them."""
+        fused.refresh_param_cache(self.params)
 
     def __call__(self, x):
         with torch.no_grad():

@@ -155,6 +155,12 @@ class Extension:
             raise RuntimeError(msg)
         warnings.warn(msg, RuntimeWarning, stacklevel=4)
 
+    def _layout(self, B, T, H, N, dt, flags):
+        """Order of the saved states a forward writes: "tiled" on the chunked kernels
+        (every state but the last in their register tiling), "rows" ([value][key]) on the
+        step-serial kernels.  The backward must read them with the family that wrote them."""
+        return "rows" if flags or self.kernel_family(B, T, H, N, dt) else "tiled"
+
     def _raise(self, status):
         if status:
             msg = self.lib.theseus_wkv7_error_string(status).decode()
@@ -209,6 +215,8 @@ class Extension:
                     B, T, H, N, dt, *map(_ptr, (r, w, k, v, a, b, s0, y, end)), ck, _ptr(ws),
                     ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)
+        if save_history:
+            saved.theseus_layout = self._layout(B, T, H, N, dt, flags)
         return [y, end, saved]
 
     def gdn_forward(self, q, k, v, g, beta, s0, qk_l2norm=False):
@@ -240,11 +248,19 @@ class Extension:
                 p(o), p(sT), None if ws is None else p(ws), nbytes, _stream(q.device)))
         return o, sT
 
-    def backward(self, r, w, k, v, a, b, saved, dy, dend, flags=0):
+    def backward(self, r, w, k, v, a, b, saved, dy, dend, flags=0, layout=None):
         """-> [dr, dw, dk, dv, da, db, ds0] (cpp:26-37).  dend may be None (zero).
-        ``flags`` must be those of the forward that made ``saved``."""
+        ``flags`` must be those of the forward that made ``saved``; ``layout`` (default:
+        the one that forward recorded on ``saved``) is the saved states' order, and a
+        call that would read them with the other kernel family (THESEUS_WKV7_FAMILY
+        changed in between) raises instead of returning wrong gradients."""
         self._check(r, (w, k, v, a, b, dy))
         B, T, H, N = r.shape
+        layout = layout if layout is not None else getattr(saved, "theseus_layout", None)
+        if layout is not None and layout != self._layout(B, T, H, N, _BF16 if r.dtype == torch.bfloat16 else _FP32,
+                                                         flags):
+            raise RuntimeError("saved states were written by the other kernel family (their order differs); "
+                               "run the backward with the forward's THESEUS_WKV7_FAMILY")
         if not (saved.device == r.device and saved.dtype == torch.float32
                 and saved.is_contiguous()
                 and tuple(saved.shape) == (B, H, self.checkpoint_count(T), N, N)):
@@ -315,6 +331,7 @@ class _WKV(torch.autograd.Function):
         state = state.float().contiguous()
         y, end, saved = extension().forward(*xs, state, True)
         ctx.save_for_backward(*xs, saved)
+        ctx.layout = saved.theseus_layout
         return y, end
 
     @staticmethod
@@ -323,7 +340,7 @@ class _WKV(torch.autograd.Function):
         if dy is None:
             dy = torch.zeros_like(xs[0])
         dend = None if dend is None else dend.float().contiguous()
-        grads = extension().backward(*xs, saved, dy.to(xs[0].dtype).contiguous(), dend)
+        grads = extension().backward(*xs, saved, dy.to(xs[0].dtype).contiguous(), dend, layout=ctx.layout)
         return tuple(g.to(x.dtype) for g, x in zip(grads[:6], xs)) + (grads[6],)
 
 
@@ -351,6 +368,7 @@ class _WKVFlags(torch.autograd.Function):
         y, end, saved = extension().forward(*xs, state.float().contiguous(), True, flags=flags)
         ctx.save_for_backward(*xs, saved)
         ctx.flags = flags
+        ctx.layout = saved.theseus_layout
         return y, end
 
     @staticmethod
@@ -359,7 +377,8 @@ class _WKVFlags(torch.autograd.Function):
         if dy is None:
             dy = torch.zeros_like(xs[0])
         dend = None if dend is None else dend.float().contiguous()
-        grads = extension().backward(*xs, saved, dy.to(xs[0].dtype).contiguous(), dend, flags=ctx.flags)
+        grads = extension().backward(*xs, saved, dy.to(xs[0].dtype).contiguous(), dend, flags=ctx.flags,
+                                     layout=ctx.layout)
         return (None,) + tuple(g.to(x.dtype) for g, x in zip(grads[:6], xs)) + (grads[6],)
 
 

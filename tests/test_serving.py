@@ -106,22 +106,72 @@ def test_captured_step_replays_match_eager_steps(autocast):
         assert torch.equal(s_graph["shift"], s_eager["shift"])
 
 
-def test_cached_parameter_copies_follow_updates():
-    """The fused wrappers reuse float32 copies of bf16 parameters (and the stacked lerp
-    coefficients) across calls, and make new ones after any in-place update."""
+def test_parameter_copies_follow_every_update():
+    """Outside a caller-owned store the fused wrappers make their float32 parameter copies
+    (and the stacked lerp coefficients) afresh on every call, so even an update written
+    through a raw pointer -- as optimizer kernels do, with no version-counter bump -- is
+    seen by the next call.  Inside ``param_cache(store)`` the copies are reused, and
+    ``refresh_param_cache`` rewrites them in place."""
+    import ctypes
     from theseus import fused
     p = torch.nn.Parameter(torch.randn(1, 1, 8).to(torch.bfloat16))
     a = fused._vec(p, 8)
-    assert fused._vec(p, 8) is a and torch.equal(a, p.detach().float().reshape(8))
-    with torch.no_grad():
-        p.mul_(2)
-    b = fused._vec(p, 8)
-    assert b is not a and torch.equal(b, p.detach().float().reshape(8))
+    assert torch.equal(a, p.detach().float().reshape(8))
+    v0 = p._version
+    new = torch.randn(1, 1, 8).to(torch.bfloat16)
+    ctypes.memmove(p.data_ptr(), new.data_ptr(), 16)  # a raw-pointer write
+    assert p._version == v0
+    assert torch.equal(fused._vec(p, 8), new.float().reshape(8))
     cs = [torch.nn.Parameter(torch.randn(1, 1, 8)) for _ in range(6)]
     m1 = fused._coef_matrix(cs, 8)
-    assert fused._coef_matrix(cs, 8) is m1
-    with torch.no_grad():
-        cs[3].add_(1)
+    ctypes.memmove(cs[3].data_ptr(), torch.ones(8).data_ptr(), 32)
     m2 = fused._coef_matrix(cs, 8)
-    assert m2 is not m1 and torch.equal(m2, torch.stack([c.detach().reshape(8) for c in cs]))
-    assert fused._coef_matrix(cs[:5] + [cs[0]], 8) is not m2  # other sources, other copy
+    assert torch.equal(m2, torch.stack([c.detach().reshape(8) for c in cs])) and not torch.equal(m1, m2)
+
+    store = {}
+    with fused.param_cache(store):
+        c1 = fused._coef_matrix(cs, 8)
+        assert fused._coef_matrix(cs, 8) is c1 and len(store) == 1
+        b1 = fused._vec(p, 8)
+        assert fused._vec(p, 8) is b1
+    assert fused._coef_matrix(cs, 8) is not c1  # the store is used only inside the context
+    with torch.no_grad():
+        cs[0].add_(1)
+        p.mul_(2)
+    fused.refresh_param_cache(store)
+    assert torch.equal(c1, torch.stack([c.detach().reshape(8) for c in cs]))
+    assert torch.equal(b1, p.detach().float().reshape(8))
+    with fused.param_cache(store):
+        assert fused._coef_matrix(cs, 8) is c1
+
+
+@pytest.mark.gpu
+def test_captured_step_follows_refreshed_weights():
+    """The graph reads parameter copies that the CapturedStep owns: an in-place weight
+    update and eager calls with the new weights leave them alone (a replay still computes
+    with the old small parameters), and after ``refresh_params()`` a replay equals an
+    eager step with the new weights."""
+    B, C = 2, 256
+    m = _model(C, seed=13)
+    x = torch.randn(B, 3, C, device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad():
+        st0 = {"shift": torch.randn(B, C, device="cuda", dtype=torch.bfloat16),
+               "wkv": .1 * torch.randn(B, C // 64, 64, 64, device="cuda")}
+        s_graph = serving_state(st0)
+        step = CapturedStep(m, s_graph, x[:, :1], autocast=None)
+        step(x[:, :1])
+        s1 = serving_state(s_graph)  # the state after token 0 (old weights)
+        gen = torch.Generator(device="cuda").manual_seed(3)
+        for p in m.parameters():
+            if p.numel() == C:  # the small parameters (the graph reads float32 copies of them)
+                p.add_((.2 * torch.randn(p.shape, generator=gen, device="cuda")).to(p.dtype))
+        s_e = serving_state(s1)
+        y_new = m.step_(x[:, 1:2], s_e).clone()  # eager, new weights
+        y_stale = step(x[:, 1:2]).clone()        # replay before the refresh
+        for k in s_graph:
+            s_graph[k].copy_(s1[k])
+        step.refresh_params()
+        y_ref = step(x[:, 1:2]).clone()
+    assert rel_l2(y_ref.float().cpu(), y_new.float().cpu()) < 1e-3
+    assert rel_l2(s_graph["wkv"].cpu(), s_e["wkv"].cpu()) < 1e-4
+    assert rel_l2(y_stale.float().cpu(), y_new.float().cpu()) > 2e-2  # (the update matters)

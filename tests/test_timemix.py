@@ -244,6 +244,49 @@ def test_fused_timemix_layer_matches_reference_backend():
         assert e < 2e-2, (n, e)
 
 
+@gpu
+@pytest.mark.parametrize("optim", ["FusedAdamW", "AdamW-fused"])
+def test_fused_layer_computes_with_the_updated_parameters(optim):
+    """Training: forward, backward and two optimizer steps on backend="cuda" -- through
+    this build's FusedAdamW (it writes the parameters through raw pointers) or torch's
+    AdamW(fused=True), as the reference's stage.py:42 -- then the next forward and backward
+    against the reference backend on the same, updated parameters.  The steps move the
+    shift-lerp coefficients far enough that the old values are detectably wrong."""
+    from theseus.optim import FusedAdamW
+    torch.manual_seed(8)
+    C, N = 256, 64
+    m = TimeMix(C, 2, 6, head_size=N, backend="cuda").cuda()
+    for p in (m.w1, m.a1, m.g1, m.output.weight):
+        torch.nn.init.normal_(p, std=.05)
+    before = TimeMix(C, 2, 6, head_size=N, backend="reference").cuda()
+    before.load_state_dict(m.state_dict())
+    opt = (FusedAdamW(m.parameters(), lr=.05) if optim == "FusedAdamW"
+           else torch.optim.AdamW(m.parameters(), lr=.05, fused=True))
+    x = torch.randn(2, 33, C, device="cuda", dtype=torch.bfloat16)
+    for _ in range(2):
+        opt.zero_grad()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y, _ = m(x)
+        y.float().square().mean().backward()
+        opt.step()
+    ref = TimeMix(C, 2, 6, head_size=N, backend="reference").cuda()
+    ref.load_state_dict(m.state_dict())
+    opt.zero_grad()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y, _ = m(x)
+        yr, _ = ref(x)
+        with torch.no_grad():
+            yb, _ = before(x)
+    assert rel_l2(y.float().cpu(), yr.float().cpu()) < 1e-2
+    assert rel_l2(yb.float().cpu(), yr.float().cpu()) > 5e-2  # (the steps changed the layer)
+    gy = torch.randn_like(y)
+    (y.float() * gy.float()).sum().backward()
+    (yr.float() * gy.float()).sum().backward()
+    for (n, p), (_, pr) in zip(m.named_parameters(), ref.named_parameters()):
+        e = rel_l2(p.grad.float().cpu(), pr.grad.float().cpu())
+        assert e < 2e-2, (n, e)
+
+
 # ---------------------------------------------------------------- GPU: the reference's own tests
 @gpu
 def test_cuda_inference_chunking_and_current_stream():

@@ -129,9 +129,18 @@ def test_shapes_and_tails_against_oracle(B, T, H, N, dtype):
     _parity(B, T, H, N, dtype, seed=1000 + T + N)
 
 
-def test_config2_training_shape_against_oracle():
-    """Config 2 at full size: B=4, T=2048, H=80, N=64, bf16, s0 ~ N(0,0.1), dsT = 0."""
-    _parity(4, 2048, 80, 64, torch.bfloat16, seed=20262, s0_std=0.1, with_dsT=False)
+@pytest.mark.parametrize("with_dsT", [False, True], ids=["dsT0", "dsT"])
+def test_config2_training_shape_against_oracle(with_dsT):
+    """Config 2 at full size: B=4, T=2048, H=80, N=64, bf16, s0 ~ N(0,0.1); dsT = 0 (the
+    training case) and dsT ~ N(0,1) (the contract, as the reference's own test uses)."""
+    _parity(4, 2048, 80, 64, torch.bfloat16, seed=20262, s0_std=0.1, with_dsT=with_dsT)
+
+
+def test_config3_recurrence_geometry_against_oracle():
+    """The recurrence inside config 3's TimeMix layer: B=2, T=4096, H=80, N=64, bf16 --
+    160 heads, fewer than the CUs, so every head runs uncut through 256 chunks and 257
+    saved states -- forward and backward with dsT ~ N(0,1), against the C oracle."""
+    _parity(2, 4096, 80, 64, torch.bfloat16, seed=20263, s0_std=0.1, with_dsT=True)
 
 
 def test_config2_nonzero_dsT_reduced_length():
@@ -292,6 +301,28 @@ def test_chunked_and_step_serial_families_agree(T, monkeypatch):
         rl = rel_l2(x, z)
         print(f"    {name:4s} chunk-vs-seq rel_l2={rl:.2e}", flush=True)
         assert rl < 5e-3, (name, rl)
+
+
+@pytest.mark.parametrize("fwd_fam,bwd_fam", [("auto", "seq"), ("seq", "auto")])
+def test_backward_refuses_saved_states_of_the_other_family(fwd_fam, bwd_fam, monkeypatch):
+    """The chunked kernels keep saved states in their own tiled order, the step-serial ones
+    in [value][key] rows: a backward on the other family than the forward raises (through
+    the Extension and through autograd) instead of returning wrong gradients."""
+    inp = wkv7_inputs(1, 40, 2, 64, seed=77, dtype=torch.bfloat16, s0_std=0.1)
+    ext = W.extension()
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    monkeypatch.setenv("THESEUS_WKV7_FAMILY", fwd_fam)
+    y, end, saved = ext.forward(*xs, inp["s0"].cuda(), True)
+    xg = [x.clone().requires_grad_() for x in xs]
+    yg, _ = W.wkv7(*xg, inp["s0"].cuda())
+    monkeypatch.setenv("THESEUS_WKV7_FAMILY", bwd_fam)
+    with pytest.raises(RuntimeError, match="other kernel family"):
+        ext.backward(*xs, saved, inp["dy"].cuda(), None)
+    with pytest.raises(RuntimeError, match="other kernel family"):
+        yg.backward(inp["dy"].cuda())
+    monkeypatch.setenv("THESEUS_WKV7_FAMILY", fwd_fam)
+    ext.backward(*xs, saved, inp["dy"].cuda(), None)  # the forward's family reads them
+    torch.cuda.synchronize()
 
 
 # -- the load-balanced schedule: heads cut between workgroups ---------------------------

@@ -100,3 +100,41 @@ def test_noalloc_forward_refuses_sizes_beyond_its_scratch():
     assert st == ERR_SCRATCH
     assert b"THESEUS_WKV7_NOALLOC_SCRATCH_BYTES" in lib.theseus_wkv7_error_string(st)
     assert bool((y == 7.0).all()) and bool((sT == 7.0).all())
+
+
+def test_noalloc_forward_on_two_ordered_streams():
+    """The single-stream rule, as a caller on two streams keeps it: calls on stream A,
+    then (after B waits for A) on stream B share the scratch array in order, and each
+    result equals the caller-workspace forward bitwise."""
+    if torch.cuda.get_device_properties(0).multi_processor_count >= 320:
+        pytest.skip("sizes below assume fewer than 320 CUs (cut heads)")
+    B, T, H, N = 4, 300, 72, 64
+    ext = W.extension()
+    lib = ext.lib
+    need = int(lib.theseus_wkv7_forward_workspace_size(B, T, H, N, 0))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    cases = []
+    for seed in (11, 12):
+        inp = wkv7_inputs(B, T, H, N, seed=seed, dtype=torch.bfloat16, s0_std=0.1)
+        xs = [inp[n].cuda() for n in "rwkvab"]
+        s0 = inp["s0"].cuda()
+        y, s, c = _outputs(B, T, H, N, True, ext)
+        assert lib.theseus_wkv7_forward(B, T, H, N, 0, *map(_p, (*xs, s0, y, s, c, ws)),
+                                        ctypes.c_size_t(need), _stream()) == 0
+        cases.append((xs, s0, (y, s, c)))
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    got = []
+    for st, (xs, s0, _) in zip((sa, sb), cases):
+        st.wait_stream(torch.cuda.current_stream())
+        if st is sb:
+            sb.wait_stream(sa)  # the ordering the shared scratch array requires
+        with torch.cuda.stream(st):
+            outs = _outputs(B, T, H, N, True, ext)
+            assert lib.theseus_wkv7_forward_noalloc(B, T, H, N, 0, *map(_p, (*xs, s0, *outs)),
+                                                    ctypes.c_void_p(st.cuda_stream)) == 0
+        got.append(outs)
+    torch.cuda.synchronize()
+    for (_, _, want), outs in zip(cases, got):
+        for a, b in zip(want, outs):
+            assert torch.equal(a, b)
