@@ -39,6 +39,7 @@ Algorithmic bytes (compulsory contract I/O; E = H*N, S_l = H*N*N*4 bytes):
 """
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -509,10 +510,10 @@ def main():
     # (kernel trace of this bench: the same kernels run up to 30 % longer there, with no
     # gap between launches), so the K steps right after W short warmup steps time part of
     # it.  The reported steps come after untimed steps that fill --settle-ms of load.
-    settle = args.warmup + args.steps
-    while (time.perf_counter() - t_warm) * 1e3 < args.settle_ms:
+    extra = max(0, math.ceil((args.settle_ms - (time.perf_counter() - t_warm) * 1e3) / ms_after_w))
+    for _ in range(extra):
         one_step()
-        settle += 1
+    settle = args.warmup + args.steps + extra
     torch.cuda.synchronize()
 
     # -- timed region: exactly K steps ---------------------------------------------------

@@ -89,6 +89,20 @@ const char* theseus_wkv7_error_string(int status);
  * reference (its kernel is step-serial for every call, kernels/wkv7_state.cu:81-92). */
 int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype);
 
+/* Time-outs of the chunked kernels' bounded waits on the current device since the
+ * last reset: the cross-workgroup handoffs (heads cut between workgroups) and the
+ * backward's in-workgroup rendezvous.  A wait that times out (about a second) writes
+ * NaN in place of what depends on it instead of hanging; this count tells such a
+ * result from NaN inputs.  Synchronous (waits for the device); reset != 0 zeroes the
+ * count.  Not safe to call while such kernels run.  No counterpart in the reference,
+ * whose kernel has no cross-wave waits (kernels/wkv7_state.cu:12-79). */
+int theseus_wkv7_wait_timeouts(unsigned int* count, int reset);
+/* Test hook: on = 0 makes every bounded wait of the chunked kernels give up at once
+ * (each such wait then counts a time-out and poisons its outputs with NaN), so the
+ * failure path can be exercised without any wave waiting; on = 1 restores them.
+ * Synchronous; affects the current device only.  No counterpart in the reference. */
+int theseus_wkv7_set_waits(int on);
+
 /* Steps between saved states (16); the saved-state tensor of a T-step
  * forward holds theseus_wkv7_checkpoint_count(T) states
  * [B,H,count,N,N] float32: state after steps 0,16,32,... and, last, the final

@@ -26,7 +26,7 @@ constexpr int HG = 8;    // heads per block of the kk / GroupNorm backward kerne
 struct V8 {
     float x[8];
 };
-// Inputs read exactly once are loaded non-temporally (ld_str8, ld_str4, ld_f8s): measured at
+// Inputs read exactly once are loaded non-temporally (ld_str8, ld_row, ld_f8s): measured at
 // config 3, kk_bwd 156 -> 138 µs and kk_fwd 91 -> 82 µs with them; the shift-lerp forward,
 // whose threads re-read the row before their first token, keeps ordinary loads (it ran 4 %
 // slower with them).  Stores stay ordinary: their results are read by the next kernel.
@@ -131,98 +131,142 @@ __global__ __launch_bounds__(256) void shift_lerp_fwd(long M, int T, int C, cons
     }
 }
 
-// grid (ceil(C/256), ceil(M/TB)), 64 lanes, 4 channels per lane (8-byte rows pieces, so
-// that a group's loads fit in registers with two waves per SIMD).  A wave walks its TB
-// tokens in order (the parameter-gradient partials are sums over them), UG tokens at a
-// time: all loads of a group -- the six gradient rows of tokens m+1 .. m+UG (token m's
-// are carried over) and the x rows of m .. m+UG-1 (x[m-1] is carried) -- are issued
-// before any is used, so a group costs one memory latency instead of one per token.
-constexpr int UG = 4;
-struct V4 {
-    float x[4];
+// 1-D grid of ceil(C/(64 SV)) x ceil(M/SLB) waves (channel blocks fastest), SV channels
+// per lane.  A wave walks its SLB tokens in order (the parameter-gradient partials are sums
+// over them), UG tokens at a time: all loads of a group -- the six gradient rows of tokens
+// m+1 .. m+UG (token m's are carried over) and the x rows of m .. m+UG-1 (x[m-1] is
+// carried) -- are issued before any is used, and with PF the next group's loads are issued
+// before the current group is used, so the wave waits on memory about once per group pair.
+// Loads past the end of the tensors re-read its last row (their values are not used), so
+// every group issues the same sequence of loads.  Measured at config 3 (B=2, T=4096,
+// C=5120) against other shapes of the same kernel: 16-byte rows, 2 tokens per group,
+// prefetch and 48 tokens per wave 146 µs (with the partials' reduction), 4-byte rows 152-171,
+// 8-byte rows 149-167, 16-byte rows without prefetch 166-180; forcing more waves per SIMD
+// than the registers allow spills.
+constexpr int SV = 8, UG = 2, SLB = 48;
+constexpr bool SPF = true;
+template <int V>
+struct RowT;
+template <>
+struct RowT<4> {
+    typedef u32x2_t type;
 };
-__device__ __forceinline__ uint2 ld_str4(const uint16_t* p) {
-    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
-    return make_uint2(v.x, v.y);
+template <>
+struct RowT<8> {
+    typedef u32x4_t type;
+};
+template <int V>
+__device__ __forceinline__ typename RowT<V>::type ld_row(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const typename RowT<V>::type*>(p));
 }
-__device__ __forceinline__ V4 cvt_bf4(uint2 u) {
-    return V4{{bf16_to_f32((uint16_t)(u.x & 0xffffu)), bf16_to_f32((uint16_t)(u.x >> 16)),
-               bf16_to_f32((uint16_t)(u.y & 0xffffu)), bf16_to_f32((uint16_t)(u.y >> 16))}};
+template <int V>
+__device__ __forceinline__ float el(const typename RowT<V>::type& u, int e) {  // channel e
+    const uint32_t w = u[e >> 1];
+    return (e & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
 }
-__device__ __forceinline__ void st_bf4(uint16_t* p, const V4& v) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(f32x2_to_bf16x2(v.x[0], v.x[1]), f32x2_to_bf16x2(v.x[2], v.x[3]));
+template <int V>
+__device__ __forceinline__ void st_row(uint16_t* p, const float (&v)[V]) {
+    typename RowT<V>::type u;
+#pragma unroll
+    for (int w = 0; w < V / 2; w++) u[w] = f32x2_to_bf16x2(v[2 * w], v[2 * w + 1]);
+    *reinterpret_cast<typename RowT<V>::type*>(p) = u;
 }
-__global__ __launch_bounds__(64) void shift_lerp_bwd(long M, int T, int C, const uint16_t* d0,
+template <int V, int G, bool PF>
+__global__ __launch_bounds__(64) void shift_lerp_bwd(long M, int T, int C, int TBk, const uint16_t* d0,
                                                      const uint16_t* d1, const uint16_t* d2,
                                                      const uint16_t* d3, const uint16_t* d4,
                                                      const uint16_t* d5, const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ st,
                                                      const float* __restrict__ coef, uint16_t* dx,
                                                      uint16_t* dshift, float* __restrict__ part) {
-    const int c = (blockIdx.x * 64 + threadIdx.x) * 4;
+    static_assert(V % 4 == 0, "coefficients and partials move as float4");
+    typedef typename RowT<V>::type row_t;
+    const int nbx = (C + 64 * V - 1) / (64 * V), bx = blockIdx.x % nbx, by = blockIdx.x / nbx;
+    const int c = (bx * 64 + threadIdx.x) * V;
     if (c >= C) return;
-    const long m0 = (long)blockIdx.y * TB, m1 = min(M, m0 + TB);
+    const long m0 = (long)by * TBk, m1 = min(M, m0 + TBk);
     const uint16_t* dn[6] = {d0, d1, d2, d3, d4, d5};
-    V4 cf[6];
-#pragma unroll
-    for (int n = 0; n < 6; n++) {
-        const float4 f = *reinterpret_cast<const float4*>(coef + n * C + c);
-        cf[n] = V4{{f.x, f.y, f.z, f.w}};
-    }
-    float acc[6][4];
+    float cf[6][V], acc[6][V];
 #pragma unroll
     for (int n = 0; n < 6; n++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) acc[n][e] = 0.f;
-    const uint2 zero = make_uint2(0, 0);
-    uint2 dcur[6];  // gradient rows of the group's first token
-#pragma unroll
-    for (int n = 0; n < 6; n++) dcur[n] = ld_str4(dn[n] + m0 * C + c);
-    uint2 xprev = (m0 % T) > 0 ? ld_str4(x + (m0 - 1) * C + c) : ld_str4(st + (m0 / T) * C + c);
-    for (long m = m0; m < m1; m += UG) {
-        uint2 dr[UG][6], xr[UG];
-#pragma unroll
-        for (int u = 0; u < UG; u++) {
-            const long row = m + 1 + u;  // (the last token's successor may lie past m1)
-#pragma unroll
-            for (int n = 0; n < 6; n++) dr[u][n] = row < M ? ld_str4(dn[n] + row * C + c) : zero;
-            xr[u] = m + u < m1 ? ld_str4(x + (m + u) * C + c) : zero;
+        for (int e = 0; e < V; e += 4) {
+            const float4 f = *reinterpret_cast<const float4*>(coef + n * C + c + e);
+            cf[n][e] = f.x, cf[n][e + 1] = f.y, cf[n][e + 2] = f.z, cf[n][e + 3] = f.w;
         }
 #pragma unroll
-        for (int u = 0; u < UG; u++) {
+    for (int n = 0; n < 6; n++)
+#pragma unroll
+        for (int e = 0; e < V; e++) acc[n][e] = 0.f;
+    row_t dcur[6];  // gradient rows of the group's first token
+#pragma unroll
+    for (int n = 0; n < 6; n++) dcur[n] = ld_row<V>(dn[n] + m0 * C + c);
+    row_t xprev = ld_row<V>((m0 % T) > 0 ? x + (m0 - 1) * C + c : st + (m0 / T) * C + c);
+    auto load = [&](long m, row_t (&dr)[G][6], row_t (&xr)[G]) {
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            const long row = min(m + 1 + u, M - 1);  // (the last token's successor may lie past m1)
+#pragma unroll
+            for (int n = 0; n < 6; n++) dr[u][n] = ld_row<V>(dn[n] + row * C + c);
+            xr[u] = ld_row<V>(x + min(m + u, M - 1) * C + c);
+        }
+    };
+    auto compute = [&](long m, const row_t (&dr)[G][6], const row_t (&xr)[G]) {
+#pragma unroll
+        for (int u = 0; u < G; u++) {
             const long mm = m + u;
             if (mm < m1) {
                 const int t = (int)(mm % T), b = (int)(mm / T);
-                const V4 xv = cvt_bf4(xr[u]);
-                const V4 pv = cvt_bf4(t > 0 ? (u == 0 ? xprev : xr[u - 1]) : ld_str4(st + (long)b * C + c));
-                V4 gx, gs;
+                const row_t pr = t > 0 ? (u == 0 ? xprev : xr[u - 1]) : ld_row<V>(st + (long)b * C + c);
+                const bool nxt = t + 1 < T;
+                float gx[V], gs[V];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float delta = round_bf16(pv.x[e] - xv.x[e]);
+                for (int e = 0; e < V; e++) {
+                    const float delta = round_bf16(el<V>(pr, e) - el<V>(xr[u], e));
                     float dsum = 0.f, dc = 0.f, nx = 0.f;
 #pragma unroll
                     for (int n = 0; n < 6; n++) {
-                        const float cu = cvt_bf4(u == 0 ? dcur[n] : dr[u - 1][n]).x[e];
+                        const float cu = el<V>(u == 0 ? dcur[n] : dr[u - 1][n], e);
                         dsum += cu;
-                        dc += cu * cf[n].x[e];
-                        nx += cvt_bf4(dr[u][n]).x[e] * cf[n].x[e];
+                        dc += cu * cf[n][e];
+                        nx += el<V>(dr[u][n], e) * cf[n][e];
                         acc[n][e] += cu * delta;
                     }
-                    gx.x[e] = dsum - dc + (t + 1 < T ? nx : 0.f);
-                    gs.x[e] = dc;
+                    gx[e] = dsum - dc + (nxt ? nx : 0.f);
+                    gs[e] = dc;
                 }
-                st_bf4(dx + mm * C + c, gx);
-                if (t == 0) st_bf4(dshift + (long)b * C + c, gs);
+                st_row<V>(dx + mm * C + c, gx);
+                if (t == 0) st_row<V>(dshift + (long)b * C + c, gs);
             }
         }
-        xprev = xr[UG - 1];
+        xprev = xr[G - 1];
 #pragma unroll
-        for (int n = 0; n < 6; n++) dcur[n] = dr[UG - 1][n];
+        for (int n = 0; n < 6; n++) dcur[n] = dr[G - 1][n];
+    };
+    if (!PF) {
+        for (long m = m0; m < m1; m += G) {
+            row_t dr[G][6], xr[G];
+            load(m, dr, xr);
+            compute(m, dr, xr);
+        }
+    } else {
+        row_t da[G][6], xa[G], db[G][6], xb[G];
+        load(m0, da, xa);
+        for (long m = m0; m < m1; m += 2 * G) {
+            load(m + G, db, xb);
+            compute(m, da, xa);
+            if (m + G >= m1) break;
+            load(m + 2 * G, da, xa);
+            compute(m + G, db, xb);
+        }
     }
-    float* pb = part + (long)blockIdx.y * 6 * C;
+    float* pb = part + (long)by * 6 * C;
 #pragma unroll
     for (int n = 0; n < 6; n++)
-        *reinterpret_cast<float4*>(pb + n * C + c) = make_float4(acc[n][0], acc[n][1], acc[n][2], acc[n][3]);
+#pragma unroll
+        for (int e = 0; e < V; e += 4)
+            *reinterpret_cast<float4*>(pb + n * C + c + e) =
+                make_float4(acc[n][e], acc[n][e + 1], acc[n][e + 2], acc[n][e + 3]);
 }
 
 // part is [nblk][P][C]; outs[p][c] = sum_b part[b][p][c], summed in block order
@@ -584,6 +628,7 @@ int tm_check(int B, int T, int C) {
 }
 int tm_status() { return hipGetLastError() == hipSuccess ? THESEUS_WKV7_OK : THESEUS_WKV7_ERR_LAUNCH; }
 long nblk_t(int B, int T) { return ((long)B * T + tmix::TB - 1) / tmix::TB; }
+long nblk_sl(int B, int T) { return ((long)B * T + tmix::SLB - 1) / tmix::SLB; }
 }  // namespace
 
 extern "C" {
@@ -602,7 +647,7 @@ int theseus_tm_shift_lerp_fwd(int B, int T, int C, const void* x, const void* st
 }
 
 size_t theseus_tm_shift_lerp_workspace(int B, int T, int C) {
-    return tm_check(B, T, C) ? 0 : (size_t)nblk_t(B, T) * 6 * C * sizeof(float);
+    return tm_check(B, T, C) ? 0 : (size_t)nblk_sl(B, T) * 6 * C * sizeof(float);
 }
 
 int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const void* x, const void* st,
@@ -614,9 +659,10 @@ int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const 
         if (!dm[n]) return THESEUS_WKV7_ERR_NULL;
     if (!ws || ws_bytes < theseus_tm_shift_lerp_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
     const long M = (long)B * T;
-    const int nb = (int)nblk_t(B, T);
-    hipLaunchKernelGGL(tmix::shift_lerp_bwd, dim3((C + 255) / 256, nb), dim3(64), 0, stream, M, T, C,
-                       (const uint16_t*)dm[0], (const uint16_t*)dm[1], (const uint16_t*)dm[2],
+    const int nb = (int)nblk_sl(B, T);
+    hipLaunchKernelGGL((tmix::shift_lerp_bwd<tmix::SV, tmix::UG, tmix::SPF>),
+                       dim3((unsigned)((C + 64 * tmix::SV - 1) / (64 * tmix::SV) * (long)nb)), dim3(64), 0, stream, M,
+                       T, C, tmix::SLB, (const uint16_t*)dm[0], (const uint16_t*)dm[1], (const uint16_t*)dm[2],
                        (const uint16_t*)dm[3], (const uint16_t*)dm[4], (const uint16_t*)dm[5],
                        (const uint16_t*)x, (const uint16_t*)st, coef, (uint16_t*)dx, (uint16_t*)dshift, ws);
     tmix::Outs o6{{dcoef, dcoef + C, dcoef + 2 * C, dcoef + 3 * C, dcoef + 4 * C, dcoef + 5 * C}};

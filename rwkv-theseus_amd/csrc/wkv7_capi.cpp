@@ -141,6 +141,20 @@ int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype) {
     return wkv7::chunk_refusal(B, T, H, N, dtype, 0);
 }
 
+int theseus_wkv7_wait_timeouts(unsigned int* count, int reset) {
+    if (!count) return THESEUS_WKV7_ERR_NULL;
+    uint32_t f = 0, b = 0;
+    if (wkv7::chunk_forward_wait_timeouts(&f, reset) || wkv7::chunk_backward_wait_timeouts(&b, reset))
+        return THESEUS_WKV7_ERR_LAUNCH;
+    *count = f + b;
+    return THESEUS_WKV7_OK;
+}
+
+int theseus_wkv7_set_waits(int on) {
+    if (wkv7::chunk_forward_waits(on) || wkv7::chunk_backward_waits(on)) return THESEUS_WKV7_ERR_LAUNCH;
+    return THESEUS_WKV7_OK;
+}
+
 int theseus_wkv7_checkpoint_interval(void) { return wkv7::kCkptInterval; }
 
 long long theseus_wkv7_checkpoint_count(int T) {

@@ -123,11 +123,12 @@ __device__ __forceinline__ Pk mat_n(const Mat& m, int lane) {  // A operand of M
 // never pass for a result.  The count is read through readfirstlane, so the
 // outcome is wave-uniform and the poisoning is a scalar branch.
 constexpr int NCONS = 8;
-__device__ __forceinline__ bool consumer_sync(uint32_t* cnt, uint32_t target) {
+// `lim` is the spin bound, wait_bound(1 << 22) read once per kernel.
+__device__ __forceinline__ bool consumer_sync(uint32_t* cnt, uint32_t target, int lim) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are done
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     bool ok = false;
-    for (int i = 0; i < (1 << 22); i++) {
+    for (int i = 0; i < lim; i++) {
         if (__builtin_amdgcn_readfirstlane(
                 __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) >= target) {
             ok = true;
@@ -136,6 +137,7 @@ __device__ __forceinline__ bool consumer_sync(uint32_t* cnt, uint32_t target) {
         __builtin_amdgcn_s_sleep(1);
     }
     asm volatile("" ::: "memory");
+    if (!ok) note_timeout();
     return ok;
 }
 __device__ __forceinline__ f32x4_t nan4() {
@@ -473,6 +475,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         // ======================= H side: rows i_own of H and dV; key strip j_own: dK, dB =======================
         f32x4_t Ht[4];  // H^T tiles Ht[tj][e] = H[i_own][16tj + 4q + e] (H' within a tick)
         bool bad = false;  // a rendezvous timed out: every later output is NaN
+        const int slim = wait_bound(1 << 22);
         lds_barrier();
         lds_barrier();
         for (int n = -NPROD; n < 0; n++) lds_barrier();
@@ -549,7 +552,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 st8(&sm.QT[0][pl16(i_own, 4 * q)], pq.h);
                 st8(&sm.QT[1][pl16(i_own, 4 * q)], pq.l);
             }
-            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 1));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 1), slim);
             // ---- stage C: key strip j_own of dK, dB (all value rows, fixed order); dV rows i_own; new H ----
             const Strip st = strip(S);
             // The masked 16x16 products XM = dY SA^T (keep s <= t), M1^T = Q V^T and N1 = SA Q^T
@@ -597,7 +600,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     gB = mma32(gB, sl, hh);
                 }
             }
-            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 2));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 2), slim);
             // (put_mat of a D tile of M: mat_t reads the A operand of M^T, mat_n that of M)
             const Pk m2n = mat_n(S.M2, lane), pm1 = mat_t(sm.Mq[1], lane), pn1 = mat_n(sm.Mq[2], lane),
                      pxm = mat_t(sm.Mq[0], lane);
@@ -667,6 +670,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         float S0s[16];
         float carry = 0.f;  // the dlogd carry for key j_own
         bool bad = false;   // a rendezvous timed out: every later output is NaN
+        const int slim = wait_bound(1 << 22);
         // buffer loads from a head's saved states: one lane offset, the rest in
         // scalar and immediate offsets (no per-load address arithmetic)
         auto ck_rsrc = [&](int j) { return make_rsrc(ckpt + (long)j * ncp * NN, (uint32_t)(ncp * NN * 4)); };
@@ -804,7 +808,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                 const uint4 ya = fragp_sw<SwDma>(S.dY, r16, 32 * s, lane);
                 gR = mma32(mma32(gR, ya, oh[s]), ya, ol[s]);
             }
-            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 1));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 1), slim);
             // ---- stage C: key strip j_own of dR, dA and this chunk's dlogd terms (this side's
             //      wave 2 forms N1 for all eight consumer waves; XM and M1^T come from the H side) ----
             if (cw == 2) {
@@ -832,7 +836,7 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
                     gA = mma32(gA, ql, oh[s]);
                 }
             }
-            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 2));
+            bad |= !consumer_sync(&sm.csync, NCONS * (2 * n + 2), slim);
             const Pk m2t = mat_t(S.M2, lane), pm1 = mat_n(sm.Mq[1], lane), pn1 = mat_t(sm.Mq[2], lane),
                      pxm = mat_n(sm.Mq[0], lane);
             const f32x4_t cR = mm32s(cat(pxm.h, m2t.h), cat(pxm.l, m2t.l), st.bkh, st.bkl);  // [tril(dY SA^T) | tril(dY V^T)]
@@ -866,6 +870,9 @@ __global__ __launch_bounds__(704) void chunk_backward_bf16(
         if (hand_prev) hand_carry();
     }
 }
+
+int chunk_backward_wait_timeouts(uint32_t* out, int reset) { return wait_timeouts_read(out, reset != 0); }
+int chunk_backward_waits(int on) { return wait_switch(on); }
 
 size_t chunk_backward_workspace(int B, int T, int H, int cus) {
     return sched_workspace(plan_schedule(B * H, (T + CH - 1) / CH, cus), NK * NK + NK);

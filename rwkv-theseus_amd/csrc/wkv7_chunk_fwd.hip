@@ -541,6 +541,9 @@ __global__ __launch_bounds__(512) void chunk_forward_bf16(
     }
 }
 
+int chunk_forward_wait_timeouts(uint32_t* out, int reset) { return wait_timeouts_read(out, reset != 0); }
+int chunk_forward_waits(int on) { return wait_switch(on); }
+
 size_t chunk_forward_workspace(int B, int T, int H, int cus) {
     return sched_workspace(plan_schedule(B * H, (T + CH - 1) / CH, cus), NK * NK);
 }

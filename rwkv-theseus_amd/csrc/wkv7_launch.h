@@ -56,6 +56,12 @@ void launch_decode(const Dec& p);
 // bf16, N == 64; `cus` = CUs the schedule spreads the heads over
 void launch_chunk_forward(const Fwd& p, int cus);
 void launch_chunk_backward(const Bwd& p, int cus);
+// time-outs of the chunked kernels' bounded waits on the current device (read, optionally
+// zeroed), and the host switch that makes those waits give up at once (tests); 0 on success
+int chunk_forward_wait_timeouts(uint32_t* out, int reset);
+int chunk_backward_wait_timeouts(uint32_t* out, int reset);
+int chunk_forward_waits(int on);
+int chunk_backward_waits(int on);
 size_t chunk_forward_workspace(int B, int T, int H, int cus);
 size_t chunk_backward_workspace(int B, int T, int H, int cus);
 // The time-split forward (no saved states, few heads): each head's chunks cut into

@@ -132,16 +132,46 @@ __device__ __forceinline__ void handoff_signal(uint32_t* cnt) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Bounded waits that time out poison what depends on them with NaN, and count the
+// time-out here (one word per file that includes this header, per device), so that the
+// host can tell a time-out from a NaN input (wait_timeouts_read, theseus_wkv7_wait_timeouts).
+// g_wait_on = 0 (set from the host for tests, theseus_wkv7_set_waits) makes every bounded
+// wait give up at once, which forces the time-out path without any wave waiting forever.
+static __device__ uint32_t g_wait_timeouts;
+static __device__ int g_wait_on = 1;
+__device__ __forceinline__ void note_timeout() {
+    if ((threadIdx.x & 63) == 0)
+        __hip_atomic_fetch_add(&g_wait_timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// the spin bound of a wait (n, or 0 while the host has switched waits off), read once
+__device__ __forceinline__ int wait_bound(int n) {
+    return __builtin_amdgcn_readfirstlane(*(volatile const int*)&g_wait_on) ? n : 0;
+}
+// host side: read this file's time-out count on the current device (and zero it), or
+// switch its waits on / off; synchronous
+static inline int wait_timeouts_read(uint32_t* out, bool reset) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(g_wait_timeouts), sizeof(uint32_t)) != hipSuccess) return -1;
+    const uint32_t zero = 0;
+    if (reset && hipMemcpyToSymbol(HIP_SYMBOL(g_wait_timeouts), &zero, sizeof(uint32_t)) != hipSuccess) return -1;
+    return 0;
+}
+static inline int wait_switch(int on) {
+    const int v = on ? 1 : 0;
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_wait_on), &v, sizeof(int)) == hipSuccess ? 0 : -1;
+}
+
 // Wait (bounded, about a second) until `target` waves have counted in; the
 // handoff loads come after it in program order (and the compiler may not move
-// them above it).  Returns false on time-out.
+// them above it).  Returns false on time-out (counted).
 __device__ __forceinline__ bool handoff_wait(const uint32_t* cnt, uint32_t target) {
     bool ok = false;
-    for (int i = 0; i < (1 << 21) && !ok; i++) {
+    const int lim = wait_bound(1 << 21);
+    for (int i = 0; i < lim && !ok; i++) {
         ok = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
         if (!ok) __builtin_amdgcn_s_sleep(8);
     }
     asm volatile("" ::: "memory");
+    if (!ok) note_timeout();
     return ok;
 }
 

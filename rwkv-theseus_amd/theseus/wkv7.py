@@ -125,6 +125,10 @@ class Extension:
         lib.theseus_wkv7_workspace_size_ex.restype = sz
         lib.theseus_wkv7_kernel_family.argtypes = [i32] * 5
         lib.theseus_wkv7_kernel_family.restype = i32
+        lib.theseus_wkv7_wait_timeouts.argtypes = [ctypes.POINTER(ctypes.c_uint), i32]
+        lib.theseus_wkv7_wait_timeouts.restype = i32
+        lib.theseus_wkv7_set_waits.argtypes = [i32]
+        lib.theseus_wkv7_set_waits.restype = i32
         # chunked gated-delta-rule forward (include/theseus_gdn.h)
         lib.theseus_gdn_forward.argtypes = [i32] * 6 + [vp] * 8 + [vp, sz, vp]
         lib.theseus_gdn_forward.restype = i32
@@ -165,6 +169,29 @@ class Extension:
         if status:
             msg = self.lib.theseus_wkv7_error_string(status).decode()
             raise RuntimeError(f"theseus_wkv7: {msg}")
+
+    def wait_timeouts(self, reset=True):
+        """Time-outs of the chunked kernels' bounded waits on the current device since the
+        last reset (theseus_wkv7_wait_timeouts; synchronises the device).  A time-out
+        leaves NaN where the result depended on the wait."""
+        n = ctypes.c_uint(0)
+        self._raise(self.lib.theseus_wkv7_wait_timeouts(ctypes.byref(n), 1 if reset else 0))
+        return int(n.value)
+
+    def set_waits(self, on):
+        """Test hook (theseus_wkv7_set_waits): with on=False every bounded wait of the
+        chunked kernels gives up at once, forcing the time-out path."""
+        self._raise(self.lib.theseus_wkv7_set_waits(1 if on else 0))
+
+    def _check_waits(self, device):
+        """THESEUS_WKV7_CHECK_WAITS=1: after each call, synchronise and raise if a bounded
+        wait timed out (a debug mode: it stalls the host on every call)."""
+        if os.environ.get("THESEUS_WKV7_CHECK_WAITS", "") == "1":
+            with _on(device):
+                n = self.wait_timeouts(reset=True)
+            if n:
+                raise RuntimeError(f"theseus_wkv7: {n} bounded wait(s) timed out in the chunked kernels; "
+                                   "the outputs hold NaN where they depended on them")
 
     @staticmethod
     def _check(r, xs):
@@ -215,6 +242,7 @@ class Extension:
                     B, T, H, N, dt, *map(_ptr, (r, w, k, v, a, b, s0, y, end)), ck, _ptr(ws),
                     ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)
+        self._check_waits(r.device)
         if save_history:
             saved.theseus_layout = self._layout(B, T, H, N, dt, flags)
         return [y, end, saved]
@@ -286,6 +314,7 @@ class Extension:
                 status = self.lib.theseus_wkv7_backward(B, T, H, N, dt, *ptrs, _ptr(ws),
                                                         ctypes.c_size_t(ws_bytes), _stream(r.device))
         self._raise(status)
+        self._check_waits(r.device)
         return grads + [ds0]
 
     def decode_step(self, r, w, k, v, a, b, state):

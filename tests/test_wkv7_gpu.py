@@ -393,6 +393,40 @@ def _ext_fwd_bwd_async(inp):
     return [y, end, saved] + list(grads) + [y_ng, end_ng]
 
 
+def test_wait_timeouts_are_counted_and_poison_the_outputs(monkeypatch):
+    """The time-out path of the chunked kernels' bounded waits, forced from the host
+    (theseus_wkv7_set_waits(0): every wait gives up at once, no wave waits): the
+    time-outs are counted (theseus_wkv7_wait_timeouts), the outputs that depended on
+    the waits are NaN, THESEUS_WKV7_CHECK_WAITS=1 turns them into an error, and with
+    the waits back on the same calls are clean again.  Heads are cut (5 CUs planned),
+    so the forward and backward hand states over between workgroups."""
+    monkeypatch.setenv("THESEUS_WKV7_CUS", "5")
+    inp = wkv7_inputs(2, 100, 3, 64, seed=777, dtype=torch.bfloat16, s0_std=0.1, with_dsT=True)
+    ext = W.extension()
+    ext.wait_timeouts(reset=True)
+    good = _ext_fwd_bwd(inp)
+    assert ext.wait_timeouts(reset=True) == 0
+    ext.set_waits(False)
+    try:
+        bad = _ext_fwd_bwd(inp)
+        n = ext.wait_timeouts(reset=True)
+        monkeypatch.setenv("THESEUS_WKV7_CHECK_WAITS", "1")
+        with pytest.raises(RuntimeError, match="timed out"):
+            _ext_fwd_bwd(inp)
+        monkeypatch.delenv("THESEUS_WKV7_CHECK_WAITS")
+    finally:
+        ext.set_waits(True)
+    print(f"    forced time-outs: {n}", flush=True)
+    assert n > 0
+    names = ["y", "end", "saved", "dr", "dw", "dk", "dv", "da", "db", "ds0", "y_ng", "end_ng"]
+    for name in ("end", "dr", "dk", "ds0", "end_ng"):  # (each depends on a handoff or rendezvous)
+        assert torch.isnan(bad[names.index(name)].float()).any(), name
+    again = _ext_fwd_bwd(inp)
+    assert ext.wait_timeouts(reset=True) == 0
+    for name, a, b in zip(names, good, again):
+        assert torch.equal(a, b), name
+
+
 def test_cut_schedule_against_oracle(monkeypatch):
     monkeypatch.setenv("THESEUS_WKV7_CUS", "5")
     _parity(2, 100, 3, 64, torch.bfloat16, seed=777)
