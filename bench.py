@@ -132,6 +132,7 @@ def bench_serving(args, cfg):
     step replays the graph 256 times.  Per-token HBM bytes: the layer's bf16 weights once
     plus the fp32 WKV state read and written (2*B*S_l) plus activations."""
     import torch
+    from theseus import fused
     from theseus.serving import CapturedStep, serving_state
     from theseus.timemix import TimeMix
 
@@ -150,21 +151,29 @@ def bench_serving(args, cfg):
     st_ip = serving_state(st0)
     graph = CapturedStep(m, serving_state(st0), toks[0], autocast=None)
 
+    # the eager modes run as a serving loop that keeps the layer's derived parameter copies
+    # (float32 vectors, stacked lerp coefficients, transposed LoRAs) in a store of its own,
+    # as the captured graph does (theseus.fused.param_cache)
+    store = {}
+
     def run(mode):
         if mode == "out_of_place":
             st = st0
-            for t in range(T):
-                _, st = m(toks[t], st)
+            with fused.param_cache(store):
+                for t in range(T):
+                    _, st = m(toks[t], st)
         elif mode == "in_place":
-            for t in range(T):
-                m.step_(toks[t], st_ip)
+            with fused.param_cache(store):
+                for t in range(T):
+                    m.step_(toks[t], st_ip)
         else:
             for t in range(T):
                 graph(toks[t])
 
     per_token = {}
+    modes = [md for md in args.serving_modes.split(",") if md]
     with torch.no_grad():
-        for mode in ("out_of_place", "in_place", "graph"):
+        for mode in modes:
             for _ in range(max(1, args.warmup // 5)):
                 run(mode)
             torch.cuda.synchronize()
@@ -174,7 +183,7 @@ def bench_serving(args, cfg):
                 run(mode)
             torch.cuda.synchronize()
             per_token[mode] = (time.perf_counter() - t0) * 1e3 / (n * T)
-    ms_tok = per_token["graph"]
+    ms_tok = per_token["graph"] if "graph" in per_token else min(per_token.values())
     weight_bytes = sum(p.numel() * p.element_size() for p in m.parameters())
     state_bytes = 2 * B * H * N * N * 4
     act_bytes = B * C * 2 * 8  # x in, out, and the mixes / WKV operands that stay small at T=1
@@ -421,6 +430,8 @@ def main():
     ap.add_argument("--cpu-slice", type=int, default=256, help="T of each CPU baseline slice (0: skip)")
     ap.add_argument("--timemix-unfused", action="store_true",
                     help="config c3 only: run TimeMix's elementwise parts as torch ops (comparison)")
+    ap.add_argument("--serving-modes", default="out_of_place,in_place,graph",
+                    help="config c4tm only: which of out_of_place,in_place,graph to run")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (3 launches), to scale rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against known traffic")

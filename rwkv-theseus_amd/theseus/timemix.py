@@ -112,6 +112,18 @@ class TimeMix(nn.Module):
         from . import fused
         return fused.available(x, self.head_size)
 
+    def _few_rows(self, x):
+        """Projections on the few-row GEMM kernel (theseus.gemm): a no-grad call with at
+        most gemm.MAX_ROWS tokens in all (a serving step: one token per lane) and
+        kernel-compatible widths and LoRA ranks."""
+        from . import gemm
+        C = self.width
+        ranks = (self.w1.shape[1], self.a1.shape[1], self.g1.shape[1])
+        if not (all(gemm.supported(1, C, C) and gemm.supported(1, r, C) and gemm.supported(1, C, r) for r in ranks)):
+            return False
+        return gemm.usable(x, self.receptance.weight, self.key.weight, self.value.weight, self.output.weight,
+                           self.w1, self.w2, self.a1, self.a2, self.g1, self.g2)
+
     def forward(self, x, state=None):
         """x [B,T,C] -> (out [B,T,C] in x.dtype, {"shift": x[:, -1], "wkv": end state})."""
         if state is None:
@@ -160,16 +172,34 @@ class TimeMix(nn.Module):
         else:
             mixed = dict(zip("rwkvag", _shift_lerp_ops(
                 x, state["shift"], [getattr(self, "x_" + n) for n in "rwkvag"])))
-        r = self.receptance(mixed["r"])
-        zw = torch.tanh(mixed["w"] @ self.w1) @ self.w2
+        rows = fused_ok and self._few_rows(x)
+        if rows:
+            # (as the torch products under bf16 autocast, with each activation applied to the
+            # float32 accumulator before the bf16 rounding)
+            from . import fused, gemm
+            r = gemm.linear(mixed["r"], self.receptance.weight)
+            k, v = gemm.linear(mixed["k"], self.key.weight), gemm.linear(mixed["v"], self.value.weight)
+            if fused._store is not None or self.w1.dtype != torch.bfloat16:
+                # the LoRAs too where their [out][in] bf16 copies are kept (a serving store) or
+                # a float32 -> bf16 copy is made anyway (autocast would make one per call)
+                zw = gemm.lora(mixed["w"], self.w1, self.w2, gemm.TANH)
+                za = gemm.lora(mixed["a"], self.a1, self.a2)
+                g = gemm.lora(mixed["g"], self.g1, self.g2, gemm.SIGMOID)
+            else:
+                zw = torch.tanh(mixed["w"] @ self.w1) @ self.w2
+                za = (mixed["a"] @ self.a1) @ self.a2
+                g = torch.sigmoid(mixed["g"] @ self.g1) @ self.g2
+        else:
+            r = self.receptance(mixed["r"])
+            zw = torch.tanh(mixed["w"] @ self.w1) @ self.w2
+            k, v = self.key(mixed["k"]), self.value(mixed["v"])
+            za = (mixed["a"] @ self.a1) @ self.a2
+            g = torch.sigmoid(mixed["g"] @ self.g1) @ self.g2
         if fused_ok:
             from . import fused
             w = fused.add_param(zw, self.w0)  # (w0 + zw) in the recurrence's bf16, in one pass
         else:
             w = self.w0 + zw
-        k, v = self.key(mixed["k"]), self.value(mixed["v"])
-        za = (mixed["a"] @ self.a1) @ self.a2
-        g = torch.sigmoid(mixed["g"] @ self.g1) @ self.g2
         if fused_ok:
             from . import fused
             # a = sigmoid(a0 + za) (the reference's theseus/timemix.py:75) is formed inside the kernels
@@ -201,7 +231,11 @@ class TimeMix(nn.Module):
                 bonus = ((r.float().reshape(shape) * kmod.float().reshape(shape) * self.r_k)
                          .sum(-1, keepdim=True) * v.float().reshape(shape)).reshape(B, T, self.width)
                 out = ((yn + bonus) * g.float()).to(x.dtype)
-        out = self.output(out).to(x.dtype)
+        if rows:
+            from . import gemm
+            out = gemm.linear(out, self.output.weight).to(x.dtype)
+        else:
+            out = self.output(out).to(x.dtype)
         if inplace:
             state["shift"].copy_(x[:, -1])
             return out, state
