@@ -17,6 +17,11 @@ moves dx and the shift gradient by 5e-3 to 2e-2 from the float32 sum.  The refer
 therefore runs the chain's lerp through a twin with bitwise the same forward values whose
 gradients accumulate in float32 (straight-through bf16 rounding of the difference): the
 rest of the op sequence is the reference's, unchanged.
+
+A second test measures both against the truth instead: the same layer in float64 (up to
+config 3's size), the fused layer and the reference's own unmodified bf16 chain
+(backend="reference") each compared with it; the fused layer must be as close as the
+reference chain is (its float32 gradient sums make dx and dshift closer).
 """
 import pytest
 import torch
@@ -99,3 +104,51 @@ def test_fp32_grad_twin_has_the_reference_chain_forward():
     for a, b in zip(TM._shift_lerp_ops(x, sh, coefs), _shift_lerp_fp32_grad(x, sh, coefs)):
         assert a.dtype == b.dtype == torch.bfloat16 and torch.equal(a, b)
 
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,T,H", [(2, 256, 16), (2, 4096, 80)], ids=["C1024", "config3"])
+def test_fused_layer_is_as_close_to_float64_as_the_reference_chain(B, T, H):
+    """Against the truth rather than against each other: the same layer and inputs in
+    float64 (backend="reference", no autocast) give the exact values; the fused layer
+    (backend="cuda", bf16 autocast) and the reference's own unmodified bf16 chain
+    (backend="reference": its torch op sequence and its float32 recurrence loop, bf16
+    autocast) are each measured against them.  Every output and all 23 parameter gradients
+    of the fused layer must be within 1.25 times the reference chain's own error, or within
+    2e-3 rel-L2 where that error is smaller."""
+    print(f"  layer vs float64: B={B} T={T} H={H}", flush=True)
+    torch.manual_seed(31)
+    N = 64
+    C = H * N
+    m = TimeMix(C, 3, 8, head_size=N, backend="cuda").cuda()
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if p.dim() == 2 and name != "r_k":
+                p.normal_(0, .02)
+    bf = torch.bfloat16
+    x = torch.randn(B, T, C, device="cuda", dtype=bf)
+    st = {"shift": torch.randn(B, C, device="cuda", dtype=bf), "wkv": .1 * torch.randn(B, H, N, N, device="cuda")}
+    gy = torch.randn(B, T, C, device="cuda", dtype=bf)
+    gS = torch.randn(B, H, N, N, device="cuda")
+    fused_out = _run(m, x, st, gy, gS)
+    m.backend = "reference"
+    ref_out = _run(m, x, st, gy, gS)
+    m64 = TimeMix(C, 3, 8, head_size=N, backend="reference").cuda().double()
+    m64.load_state_dict({k: v.double() for k, v in m.state_dict().items()})
+    xx = x.double().requires_grad_()
+    sh = st["shift"].double().requires_grad_()
+    s0 = st["wkv"].double().requires_grad_()
+    y, s = m64(xx, {"shift": sh, "wkv": s0})
+    torch.autograd.backward((y, s["wkv"]), (gy.double(), gS.double()))
+    truth = {"y": y.detach(), "state.wkv": s["wkv"].detach(), "state.shift": s["shift"].detach(),
+             "dx": xx.grad, "dshift0": sh.grad, "dwkv0": s0.grad}
+    for n, p in m64.named_parameters():
+        truth["grad." + n] = p.grad.detach()
+    bad = []
+    for k, t in truth.items():
+        ef = rel_l2(fused_out[k].double().cpu(), t.cpu())
+        er = rel_l2(ref_out[k].double().cpu(), t.cpu())
+        print(f"    {k}: fused {ef:.2e}  reference chain {er:.2e}", flush=True)
+        if not ef <= max(1.25 * er, 2e-3):
+            bad.append((k, ef, er))
+    assert not bad, bad
