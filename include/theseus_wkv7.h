@@ -71,8 +71,13 @@ enum theseus_wkv7_family {
     THESEUS_WKV7_FAMILY_HEAD_SIZE = 3,  /* step-serial: N != 64                              */
     THESEUS_WKV7_FAMILY_SIZE = 4,       /* step-serial: a token tensor >= 2 GiB or one head's
                                            saved states >= 4 GiB (32-bit buffer offsets)     */
-    THESEUS_WKV7_FAMILY_FLAGS = 5       /* step-serial: a call of the *_ex entry points with
+    THESEUS_WKV7_FAMILY_FLAGS = 5,      /* step-serial: a call of the *_ex entry points with
                                            flags (exp decay or key-value states)             */
+    THESEUS_WKV7_FAMILY_RECORDS = 6     /* bf16, N = 128: the forward on the chunk-record
+                                           kernels when the workspace holds the records
+                                           (theseus_wkv7_forward_workspace_size counts
+                                           them), else step-serial; the backward
+                                           step-serial                                       */
 };
 
 /* ABI version of this header; bumped on any incompatible change. */

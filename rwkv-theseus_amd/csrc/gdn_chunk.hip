@@ -47,8 +47,10 @@ namespace {
 
 constexpr int GC = 16;  // chunk length
 
-// One chunk's record in the workspace (byte offsets; 256-byte aligned records).
-template <int NK>
+// One chunk's record in the workspace (byte offsets; 256-byte aligned records).  PK: the
+// WKV7 operator's records (wkv7_rec_prep), whose decay is one per key, so EL holds
+// e^{g_L} for every key instead of one e^{gamma_L}.
+template <int NK, bool PK = false>
 struct GdnRec {
     static constexpr int KS = NK / 32, TJ = NK / 16;
     static constexpr size_t PF = 0;                                // [KS][hi, lo][64 lanes] uint4
@@ -56,11 +58,12 @@ struct GdnRec {
     static constexpr size_t UF = P2F + (size_t)KS * 2 * 64 * 16;   // [TJ][hi, lo][64] uint4
     static constexpr size_t QF = UF + (size_t)TJ * 2 * 64 * 16;    // [Q'^T hi, lo, Q2^T hi, lo][64] uint2
     static constexpr size_t VF = QF + 4 * 64 * 8;                  // [TJ row blocks][hi, lo][64] uint2
-    static constexpr size_t EL = VF + (size_t)TJ * 2 * 64 * 8;     // e^{gamma_L}
-    static constexpr size_t BYTES = EL + 256;
+    static constexpr size_t EL = VF + (size_t)TJ * 2 * 64 * 8;     // e^{gamma_L} (PK: [NK] per key)
+    static constexpr size_t BYTES = EL + (PK ? ((size_t)NK * 4 + 255) / 256 * 256 : 256);
     static constexpr int DMA_BLOCKS = (int)((BYTES + 1023) / 1024);  // 1 KB LDS DMA blocks
 };
-static_assert(GdnRec<128>::BYTES % 256 == 0 && GdnRec<64>::BYTES % 256 == 0, "record alignment");
+static_assert(GdnRec<128>::BYTES % 256 == 0 && GdnRec<64>::BYTES % 256 == 0 && GdnRec<128, true>::BYTES % 256 == 0,
+              "record alignment");
 
 // four consecutive elements as float
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -263,6 +266,152 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
 }
 
 // ---------------------------------------------------------------------------
+// The WKV7 operator's records (bf16 r, w, k, v, a, b; kernels/wkv7_state.cu:12-40's
+// recurrence, chunk algebra of wkv7_chunk_fwd.hip).  The decay is one per key, so the
+// decay ratios ride on the operands rather than on a 16x16 matrix: per key, with g the
+// chunk's inclusive cumulative log-decay (|g| < 16 e^{-1/2}, so e^{-g} < 2e4 stays
+// finite and every product below is of moderate size), gp = g_{t-1} and gL = g_{L-1},
+//   A~ = a e^{gp}, R~ = r e^{g}, B- = b e^{-g}, K- = k e^{-g}, B^ = b e^{gL-g}, K^ = k e^{gL-g}
+//   Aab = tril_s(A~ B-^T), Aak = tril_s(A~ K-^T), Brb = tril(R~ B-^T), Brk = tril(R~ K-^T)
+// (contractions over the keys on the matrix cores), V = v, and e^{gL} per key.  One wave
+// per chunk as gdn_prep, writing the same record layout (GdnRec<NK, true>).  Lane (q4,
+// r16) holds token r16's keys 32ks + 4q4 + e and 32ks + 16 + 4q4 + e; the D-layout tiles
+// of A~, B^ and K^ ([t][j], rows t = 4q4 + e) are read back from LDS planes.
+// ---------------------------------------------------------------------------
+template <int NK>
+__global__ __launch_bounds__(64) void wkv7_rec_prep(int Tn, int H, const bf16_t* __restrict__ r,
+                                                    const bf16_t* __restrict__ w, const bf16_t* __restrict__ k,
+                                                    const bf16_t* __restrict__ v, const bf16_t* __restrict__ a,
+                                                    const bf16_t* __restrict__ b, uint8_t* __restrict__ ws) {
+    using R = GdnRec<NK, true>;
+    constexpr int KS = R::KS, LP = NK + 4;
+    const int c = blockIdx.x, bh = blockIdx.y, nchunk = gridDim.x;
+    const int bb = bh / H, h = bh - bb * H;
+    const int lane = threadIdx.x, q4 = lane >> 4, r16 = lane & 15;
+    const int t0 = c * GC, L = min(GC, Tn - t0);
+    const long tok0 = (long)bb * Tn + t0;
+    const long row = ((tok0 + r16) * H + h) * (long)NK;  // token r16's row (read only when r16 < L)
+    const bool tv = r16 < L;
+    // A~, B^, K^ as rows [t][j] for the D-layout reads; v as rows [t][i]
+    __shared__ __attribute__((aligned(16))) float pa[GC][LP], pb[GC][LP], pkh[GC][LP], vsh[GC][LP];
+    uint8_t* const rec = ws + ((size_t)bh * nchunk + c) * R::BYTES;
+    f32x4_t Aab = zero4(), AabT = zero4(), Aak = zero4(), BrbT = zero4(), BrkT = zero4();
+    float rt[KS][8];  // R~ of the lane's keys, kept for P2
+    auto ld8 = [&](const bf16_t* x, int c0, float (&o)[8]) {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 p = tv ? ld4(x + row + c0) : z, q = tv ? ld4(x + row + c0 + 16) : z;
+        o[0] = p.x, o[1] = p.y, o[2] = p.z, o[3] = p.w, o[4] = q.x, o[5] = q.y, o[6] = q.z, o[7] = q.w;
+    };
+    auto st8 = [&](float (*pl)[LP], int c0, const float (&x)[8]) {
+        *reinterpret_cast<float4*>(&pl[r16][c0]) = make_float4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<float4*>(&pl[r16][c0 + 16]) = make_float4(x[4], x[5], x[6], x[7]);
+    };
+    // split products over one K=32 step: acc += X Y^T (X, Y: the lanes' token rows)
+    auto mm3 = [](f32x4_t acc, uint4 xh, uint4 xl, uint4 yh, uint4 yl) {
+        return mma32(mma32(mma32(acc, xh, yh), xh, yl), xl, yh);
+    };
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        const int c0 = 32 * ks + 4 * q4;
+        float wv[8], av[8], bv[8], kv[8], vv[8];
+        ld8(w, c0, wv), ld8(a, c0, av), ld8(b, c0, bv), ld8(k, c0, kv), ld8(r, c0, rt[ks]), ld8(v, c0, vv);
+        st8(vsh, c0, vv);
+        float At[8], Bm[8], Km[8], Bh[8], Kh[8], eL[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float g = row_prefix_sum(tv ? log_decay(wv[e]) : 0.f);  // (0 past the end)
+            const float gp = row_prev(g, 0.f), gL = row_last(g);
+            const float em = __expf(-g), eh = __expf(gL - g);
+            At[e] = av[e] * __expf(gp);
+            rt[ks][e] *= __expf(g);
+            Bm[e] = bv[e] * em, Km[e] = kv[e] * em;
+            Bh[e] = bv[e] * eh, Kh[e] = kv[e] * eh;
+            eL[e] = __expf(gL);
+        }
+        st8(pa, c0, At), st8(pb, c0, Bh), st8(pkh, c0, Kh);
+        if (r16 == 0) {
+            float* el = reinterpret_cast<float*>(rec + R::EL);
+            *reinterpret_cast<float4*>(el + c0) = make_float4(eL[0], eL[1], eL[2], eL[3]);
+            *reinterpret_cast<float4*>(el + c0 + 16) = make_float4(eL[4], eL[5], eL[6], eL[7]);
+        }
+        uint4 ah, al, bh_, bl, kh, kl, rh, rl;
+        pack8(At, ah, al), pack8(Bm, bh_, bl), pack8(Km, kh, kl), pack8(rt[ks], rh, rl);
+        Aab = mm3(Aab, ah, al, bh_, bl);     // [rr][cc] = A~_rr . B-_cc
+        AabT = mm3(AabT, bh_, bl, ah, al);   // B-_rr . A~_cc
+        Aak = mm3(Aak, ah, al, kh, kl);      // A~_rr . K-_cc
+        BrbT = mm3(BrbT, bh_, bl, rh, rl);   // B-_rr . R~_cc
+        BrkT = mm3(BrkT, kh, kl, rh, rl);    // K-_rr . R~_cc
+    }
+    // the chunk matrices in D layout (element [rr][cc], rr = 4q4 + e, cc = r16), masked
+    const int cc = r16;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = 4 * q4 + e;
+        Aab[e] = cc < rr ? Aab[e] : 0.f;     // Aab[rr][cc]
+        AabT[e] = rr < cc ? AabT[e] : 0.f;   // Aab[cc][rr]
+        Aak[e] = cc < rr ? Aak[e] : 0.f;     // Aak[rr][cc]
+        BrbT[e] = rr <= cc ? BrbT[e] : 0.f;  // Brb[cc][rr]
+        BrkT[e] = rr <= cc ? BrkT[e] : 0.f;  // Brk[cc][rr]
+    }
+    f32x4_t Ti, TiT;
+    tri_inverse(Aab, AabT, lane, Ti, TiT);
+    const Pk pTiT = pk(TiT), pAak = pk(Aak), pBrbT = pk(BrbT);
+    const f32x4_t Q1 = mm16s(pTiT, pAak);                      // Q' = Ti Aak        [t][s]
+    const Pk pQ1T = pk(mm16s(pAak, pTiT));                      // Q'^T               [s][t]
+    const Pk pQ2T = pk(BrkT + mm16s(pk(Q1), pBrbT));            // Q2^T = Brk^T + Q'^T Brb^T
+    {
+        uint2* qf = reinterpret_cast<uint2*>(rec + R::QF) + lane;
+        qf[0] = pQ1T.h, qf[64] = pQ1T.l, qf[128] = pQ2T.h, qf[192] = pQ2T.l;
+    }
+    __syncthreads();  // the planes
+    // V as the K=16 B operand of each block of 16 value rows (lane: value 16rb + r16,
+    // steps 4q4 + e; zero past the end), split
+#pragma unroll
+    for (int rb = 0; rb < R::TJ; rb++) {
+        f32x4_t vq;
+#pragma unroll
+        for (int e = 0; e < 4; e++) vq[e] = vsh[4 * q4 + e][16 * rb + r16];
+        const Pk pv = pk(vq);
+        uint2* vf = reinterpret_cast<uint2*>(rec + R::VF) + (size_t)(2 * rb) * 64 + lane;
+        vf[0] = pv.h;
+        vf[64] = pv.l;
+    }
+    // per pair of 16-key tiles (one K-step): P, P2 and the update operands
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        Pk pPT[2], pP2T[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int tj = 2 * ks + u;
+            f32x4_t at, bhat, khat;  // D layout [t][j], t = 4q4 + e, j = 16tj + r16
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                at[e] = pa[4 * q4 + e][16 * tj + r16];
+                bhat[e] = pb[4 * q4 + e][16 * tj + r16];
+                khat[e] = pkh[4 * q4 + e][16 * tj + r16];
+            }
+            const Pk pA = pk(at);
+            const f32x4_t Pt = mm16s(pTiT, pA);   // P tile [t][j]
+            pPT[u] = pk(mm16s(pA, pTiT));          // P^T tile [j][t]
+            f32x4_t rr4;                            // R~[t = r16][16tj + 4q4 + e]
+#pragma unroll
+            for (int e = 0; e < 4; e++) rr4[e] = rt[ks][4 * u + e];
+            pP2T[u] = pk(rr4 + mm16s(pk(Pt), pBrbT));  // P2^T = R~^T + P^T Brb^T
+            const Pk pb4 = pk(bhat), pk4 = pk(khat);
+            uint4* uf = reinterpret_cast<uint4*>(rec + R::UF) + (size_t)(2 * tj) * 64 + lane;
+            uf[0] = cat(pb4.h, pk4.h);
+            uf[64] = cat(pb4.l, pk4.l);
+        }
+        uint4* pf = reinterpret_cast<uint4*>(rec + R::PF) + (size_t)(2 * ks) * 64 + lane;
+        pf[0] = cat(pPT[0].h, pPT[1].h);
+        pf[64] = cat(pPT[0].l, pPT[1].l);
+        uint4* p2 = reinterpret_cast<uint4*>(rec + R::P2F) + (size_t)(2 * ks) * 64 + lane;
+        p2[0] = cat(pP2T[0].h, pP2T[1].h);
+        p2[64] = cat(pP2T[0].l, pP2T[1].l);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Each head's chunks in order.  A head's value rows are split over `row groups`
 // (workgroups rg * BH + bh, so that with BH a multiple of 8 a head's groups share an
 // XCD and its L2); wave w of group rg keeps the 16 rows of block rb = rg * NW + w,
@@ -280,11 +429,15 @@ struct GdnSplit {
     float *send0 = nullptr, *uend = nullptr, *phi = nullptr, *y0 = nullptr, *z = nullptr;
 };
 
-template <int NK, typename TO, bool SPLIT>
+// PK: WKV7 records (a decay per key: the state's key columns scale by e^{g_L} each);
+// ckpt (not with SPLIT; may be null): the state at every chunk's start and the final one,
+// [bh][count][value][key] as the step-serial kernels keep saved states.
+template <int NK, typename TO, bool SPLIT, bool PK = false>
 __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, const float* __restrict__ s0,
                                                    TO* __restrict__ o, float* __restrict__ sT,
-                                                   const uint8_t* __restrict__ ws, GdnSplit sp) {
-    using R = GdnRec<NK>;
+                                                   const uint8_t* __restrict__ ws, GdnSplit sp,
+                                                   float* __restrict__ ckpt) {
+    using R = GdnRec<NK, PK>;
     constexpr int KS = R::KS, TJ = R::TJ;
     __shared__ __attribute__((aligned(1024))) uint8_t recs[2][R::DMA_BLOCKS * 1024];
     // workgroup (segment * row groups + rg) * BH + bh (SPLIT; else rg * BH + bh)
@@ -321,9 +474,17 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
         }
     vm_wait0();
     __syncthreads();
+    const long ncp = nchunk + 1;  // saved states per head
+    auto save = [&](int slot) {     // (whole float4 rows of the state)
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++)
+            *reinterpret_cast<float4*>(ckpt + ((long)bh * ncp + slot) * NN + (long)i_own * NK + 16 * tj + 4 * q4) =
+                make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+    };
     for (int c = c0; c < c1; c++) {
         if (c + 1 < c1) fetch(c + 1, (c - c0 + 1) & 1);
         const uint8_t* const rec = recs[(c - c0) & 1];
+        if (!SPLIT && ckpt) save(c);
         const int t0 = c * GC, L = min(GC, Tn - t0);
         const long tok0 = (long)bb * Tn + t0;
         // SA = P X0^T and Y = P2 X0^T over the keys (permuted K=32 steps)
@@ -379,13 +540,17 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
         for (int tj = 0; tj < TJ; tj++) {
             const uint4* uf = reinterpret_cast<const uint4*>(rec + R::UF) + (2 * tj) * 64 + lane;
             const uint4 ah = uf[0], al = uf[64];
-            St[tj] = mma32(mma32(mma32(St[tj] * egL, ah, bhi), ah, blo), al, bhi);
-            if (dual) Sp[tj] = mma32(mma32(mma32(Sp[tj] * egL, ah, bhi2), ah, blo2), al, bhi2);
+            // the decay of the lane's keys 16 tj + 4 q4 + e (one for all keys unless PK)
+            const f32x4_t eg = PK ? *reinterpret_cast<const f32x4_t*>(rec + R::EL + 4 * (16 * tj + 4 * q4))
+                                  : f32x4_t{egL, egL, egL, egL};
+            St[tj] = mma32(mma32(mma32(St[tj] * eg, ah, bhi), ah, blo), al, bhi);
+            if (dual) Sp[tj] = mma32(mma32(mma32(Sp[tj] * eg, ah, bhi2), ah, blo2), al, bhi2);
         }
         vm_wait0();      // this wave's part of the next record is in LDS
         __syncthreads();  // every wave's part is, and nobody still reads this one
     }
     if (!SPLIT) {
+        if (ckpt) save(nchunk);
 #pragma unroll
         for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
@@ -590,10 +755,12 @@ void gdn_split_lengths(int n, int k, int& m0, int& m) {
 }
 }  // namespace
 
-size_t gdn_forward_workspace(int B, int T, int H, int N) {
-    const size_t rec = N == 128 ? GdnRec<128>::BYTES : GdnRec<64>::BYTES;
+template <bool PK>
+static size_t records(int B, int T, int H, int N) {
+    const size_t rec = N == 128 ? GdnRec<128, PK>::BYTES : GdnRec<64, PK>::BYTES;
     return (size_t)B * H * ((T + GC - 1) / GC) * rec;
 }
+size_t gdn_forward_workspace(int B, int T, int H, int N) { return records<false>(B, T, H, N); }
 // Segments of the time-split scan: with at least 8 chunks, as many as fit one workgroup
 // per CU (B*H*N/64 per segment), at most 4, each with at least one chunk; 1 = no split.
 int gdn_split_segments(int B, int T, int H, int N, int cus) {
@@ -601,31 +768,40 @@ int gdn_split_segments(int B, int T, int H, int N, int cus) {
     if (n < 8 || per < 1) return 1;
     return max(1, min(min(4, cus / per), n));
 }
-size_t gdn_forward_workspace_split(int B, int T, int H, int N, int cus) {
+template <bool PK>
+static size_t split_workspace(int B, int T, int H, int N, int cus) {
     const int k = gdn_split_segments(B, T, H, N, cus);
-    if (k < 2) return gdn_forward_workspace(B, T, H, N);
+    if (k < 2) return records<PK>(B, T, H, N);
     int m0, mi;
     gdn_split_lengths((T + GC - 1) / GC, k, m0, mi);
     const size_t m = mi, BH = (size_t)B * H, NN = (size_t)N * N;
-    const size_t recs = (gdn_forward_workspace(B, T, H, N) + 255) / 256 * 256;
+    const size_t recs = (records<PK>(B, T, H, N) + 255) / 256 * 256;
     return recs + BH * ((2 * k - 1) * NN + 2 * (k - 1) * m * GC * N) * sizeof(float);
 }
+size_t gdn_forward_workspace_split(int B, int T, int H, int N, int cus) {
+    return split_workspace<false>(B, T, H, N, cus);
+}
+size_t wkv7_rec_workspace(int B, int T, int H, int N) { return records<true>(B, T, H, N); }
+size_t wkv7_rec_workspace_split(int B, int T, int H, int N, int cus) { return split_workspace<true>(B, T, H, N, cus); }
+
 // Row groups per head for the scan: groups of four waves (64 value rows).  Measured at
 // B=1, T=2048 (MI355X): N=128 in 2 groups 0.248 ms against 0.279 (1), 0.292 (4) and
 // 0.380 (8); N=64 in 1 group 0.168 ms against 0.192 (2) -- every group moves the whole
 // record into its LDS, and groups of fewer waves wait on that more than they gain.
 static int gdn_row_groups(int N) { return N / 64; }  // (256 lanes each: the kernel's bound)
-template <int NK, typename TI>
-static void launch_gdn(const Gdn& p) {
-    const int nchunk = (p.T + GC - 1) / GC, BH = p.B * p.H;
+
+// The scan over the records at ws: in one pass (with saved states when ckpt), or cut in
+// time when cus allows at least two segments and ws_bytes covers the split's buffers.
+template <int NK, typename TO, bool PK>
+static void scan_records(int B, int T, int H, int kv, const float* s0, TO* o, float* sT, float* ckpt, void* ws,
+                         size_t ws_bytes, int cus, hipStream_t stream) {
+    const int nchunk = (T + GC - 1) / GC, BH = B * H;
     const int rgs = gdn_row_groups(NK), lanes = 64 * (NK / 16) / rgs;
-    hipLaunchKernelGGL((gdn_prep<NK, TI>), dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, p.qk_norm,
-                       static_cast<const TI*>(p.q), static_cast<const TI*>(p.k), static_cast<const TI*>(p.v), p.g,
-                       p.beta, static_cast<uint8_t*>(p.ws));
-    const int k = gdn_split_segments(p.B, p.T, p.H, NK, p.cus);
-    if (k < 2 || p.ws_bytes < gdn_forward_workspace_split(p.B, p.T, p.H, NK, p.cus)) {
-        hipLaunchKernelGGL((gdn_scan<NK, TI, false>), dim3(BH * rgs), dim3(lanes), 0, p.stream, p.T, p.H, BH, p.kv,
-                           p.s0, static_cast<TI*>(p.o), p.sT, static_cast<const uint8_t*>(p.ws), GdnSplit{});
+    const uint8_t* const recs = static_cast<const uint8_t*>(ws);
+    const int k = ckpt ? 1 : gdn_split_segments(B, T, H, NK, cus);
+    if (k < 2 || ws_bytes < split_workspace<PK>(B, T, H, NK, cus)) {
+        hipLaunchKernelGGL((gdn_scan<NK, TO, false, PK>), dim3(BH * rgs), dim3(lanes), 0, stream, T, H, BH, kv, s0, o,
+                           sT, recs, GdnSplit{}, ckpt);
         return;
     }
     // the time split: buffers after the records
@@ -633,16 +809,24 @@ static void launch_gdn(const Gdn& p) {
     sp.k = k;
     gdn_split_lengths(nchunk, k, sp.m0, sp.m);
     const size_t NN = (size_t)NK * NK, per = (size_t)(k - 1) * BH;
-    float* const base = reinterpret_cast<float*>(static_cast<uint8_t*>(p.ws) +
-                                                 (gdn_forward_workspace(p.B, p.T, p.H, NK) + 255) / 256 * 256);
+    float* const base = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (records<PK>(B, T, H, NK) + 255) / 256 * 256);
     sp.send0 = base, sp.uend = base + BH * NN, sp.phi = sp.uend + per * NN;
     sp.y0 = sp.phi + per * NN, sp.z = sp.y0 + per * sp.m * GC * NK;
-    hipLaunchKernelGGL((gdn_scan<NK, TI, true>), dim3(k * BH * rgs), dim3(lanes), 0, p.stream, p.T, p.H, BH, p.kv,
-                       p.s0, static_cast<TI*>(p.o), p.sT, static_cast<const uint8_t*>(p.ws), sp);
-    hipLaunchKernelGGL((gdn_split_chain<NK>), dim3(BH), dim3(64 * (NK / 16)), 0, p.stream, BH, p.kv, sp, p.sT);
+    hipLaunchKernelGGL((gdn_scan<NK, TO, true, PK>), dim3(k * BH * rgs), dim3(lanes), 0, stream, T, H, BH, kv, s0, o,
+                       sT, recs, sp, nullptr);
+    hipLaunchKernelGGL((gdn_split_chain<NK>), dim3(BH), dim3(64 * (NK / 16)), 0, stream, BH, kv, sp, sT);
     // chunk groups of segments 1 .. k-1; heads along y
-    hipLaunchKernelGGL((gdn_split_y<NK, TI>), dim3((k - 1) * ((sp.m + GFY - 1) / GFY), BH), dim3(64 * (NK / 16)), 0,
-                       p.stream, p.T, p.H, BH, sp, static_cast<TI*>(p.o));
+    hipLaunchKernelGGL((gdn_split_y<NK, TO>), dim3((k - 1) * ((sp.m + GFY - 1) / GFY), BH), dim3(64 * (NK / 16)), 0,
+                       stream, T, H, BH, sp, o);
+}
+template <int NK, typename TI>
+static void launch_gdn(const Gdn& p) {
+    const int nchunk = (p.T + GC - 1) / GC, BH = p.B * p.H;
+    hipLaunchKernelGGL((gdn_prep<NK, TI>), dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, p.qk_norm,
+                       static_cast<const TI*>(p.q), static_cast<const TI*>(p.k), static_cast<const TI*>(p.v), p.g,
+                       p.beta, static_cast<uint8_t*>(p.ws));
+    scan_records<NK, TI, false>(p.B, p.T, p.H, p.kv, p.s0, static_cast<TI*>(p.o), p.sT, nullptr, p.ws, p.ws_bytes,
+                                p.cus, p.stream);
 }
 void launch_gdn_forward(const Gdn& p) {
     if (p.N == 128) {
@@ -652,6 +836,19 @@ void launch_gdn_forward(const Gdn& p) {
         if (p.dtype == 0) launch_gdn<64, bf16_t>(p);
         else launch_gdn<64, float>(p);
     }
+}
+
+// The WKV7 forward on records: bf16, N = 128, flags 0 ([value][key] states), a
+// workspace of at least wkv7_rec_workspace bytes; saved states (ckpt) in the step-serial
+// kernels' [value][key] order.
+void launch_wkv7_rec_forward(const Fwd& p, int cus) {
+    const int nchunk = (p.T + GC - 1) / GC, BH = p.B * p.H;
+    hipLaunchKernelGGL((wkv7_rec_prep<128>), dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H,
+                       static_cast<const bf16_t*>(p.r), static_cast<const bf16_t*>(p.w), static_cast<const bf16_t*>(p.k),
+                       static_cast<const bf16_t*>(p.v), static_cast<const bf16_t*>(p.a), static_cast<const bf16_t*>(p.b),
+                       static_cast<uint8_t*>(p.ws));
+    scan_records<128, bf16_t, true>(p.B, p.T, p.H, 0, p.s0, static_cast<bf16_t*>(p.y), p.sT, p.ckpt, p.ws, p.ws_bytes,
+                                    cus, p.stream);
 }
 
 }  // namespace wkv7

@@ -57,6 +57,19 @@ static bool chunk_ok(int B, int T, int H, int N, int dtype, int flags) {
     return chunk_refusal(B, T, H, N, dtype, flags) == 0;
 }
 
+// bf16, N = 128 and no flags: the forward on the chunk-record kernels (gdn_chunk.hip)
+// when the caller's workspace holds the records -- theseus_wkv7_forward_workspace_size
+// counts them, theseus_wkv7_forward_noalloc brings none and stays step-serial.  One
+// head's records stay under 4 GiB (32-bit DMA offsets), B*H within the prep's grid y.
+static bool rec_shape(int B, int T, int H, int N, int dtype, int flags) {
+    return chunk_refusal(B, T, H, N, dtype, flags) == THESEUS_WKV7_FAMILY_HEAD_SIZE && N == 128 &&
+           (long long)B * H <= 65535 && wkv7_rec_workspace(1, T, 1, N) < (1ull << 32);
+}
+static bool rec_ok(const Fwd& p) {
+    return rec_shape(p.B, p.T, p.H, p.N, p.dtype, p.flags) && p.ws &&
+           p.ws_bytes >= wkv7_rec_workspace(p.B, p.T, p.H, p.N);
+}
+
 // CUs of the current device, which the chunked kernels' schedule spreads the
 // heads over (one workgroup each).  THESEUS_WKV7_CUS=<n> plans for n instead
 // (the tests use it to cut heads at small sizes).
@@ -92,6 +105,7 @@ void launch_forward(const Fwd& p) {
         launch_decode(d);
     } else if (split_ok(p)) launch_chunk_forward_split(p, cu_count());
     else if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype, p.flags)) launch_chunk_forward(p, cu_count());
+    else if (rec_ok(p)) launch_wkv7_rec_forward(p, cu_count());
     else launch_seq_forward(p);
 }
 void launch_backward(const Bwd& p) {
@@ -104,6 +118,7 @@ size_t forward_workspace(int B, int T, int H, int N, int dtype, int flags) {
     return chunk_ok(B, T, H, N, dtype, flags) ? chunk_forward_workspace(B, T, H, cu_count()) : 0;
 }
 size_t forward_workspace_fast(int B, int T, int H, int N, int dtype, int flags) {
+    if (rec_shape(B, T, H, N, dtype, flags)) return wkv7_rec_workspace_split(B, T, H, N, cu_count());
     const size_t need = forward_workspace(B, T, H, N, dtype, flags);
     if (!split_shape(B, T, H, N, dtype, flags)) return need;
     const size_t split = chunk_forward_split_workspace(B, T, H, cu_count());
@@ -138,6 +153,7 @@ const char* theseus_wkv7_error_string(int status) {
 
 int theseus_wkv7_kernel_family(int B, int T, int H, int N, int dtype) {
     if (int e = check_dims(B, T, H, N, dtype)) return -e;
+    if (wkv7::rec_shape(B, T, H, N, dtype, 0)) return THESEUS_WKV7_FAMILY_RECORDS;
     return wkv7::chunk_refusal(B, T, H, N, dtype, 0);
 }
 

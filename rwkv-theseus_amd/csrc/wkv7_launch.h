@@ -94,6 +94,12 @@ size_t gdn_forward_workspace(int B, int T, int H, int N);
 size_t gdn_forward_workspace_split(int B, int T, int H, int N, int cus);
 int gdn_split_segments(int B, int T, int H, int N, int cus);
 void launch_gdn_forward(const Gdn& p);
+// The WKV7 forward for bf16, N = 128 and flags 0 on the same two kernels (per-key
+// decays in the records): wkv7_rec_workspace bytes of records, or
+// wkv7_rec_workspace_split with the time split's buffers (few heads, no saved states).
+size_t wkv7_rec_workspace(int B, int T, int H, int N);
+size_t wkv7_rec_workspace_split(int B, int T, int H, int N, int cus);
+void launch_wkv7_rec_forward(const Fwd& p, int cus);
 
 // Family dispatch (wkv7_capi.cpp): the chunked MFMA kernels when they cover
 // the call, else the step-serial ones.
