@@ -73,11 +73,12 @@ enum theseus_wkv7_family {
                                            saved states >= 4 GiB (32-bit buffer offsets)     */
     THESEUS_WKV7_FAMILY_FLAGS = 5,      /* step-serial: a call of the *_ex entry points with
                                            flags (exp decay or key-value states)             */
-    THESEUS_WKV7_FAMILY_RECORDS = 6     /* bf16, N = 128: the forward on the chunk-record
-                                           kernels when the workspace holds the records
+    THESEUS_WKV7_FAMILY_RECORDS = 6     /* bf16, N = 128: chunk-record kernels -- the forward
+                                           when the workspace holds the records
                                            (theseus_wkv7_forward_workspace_size counts
-                                           them), else step-serial; the backward
-                                           step-serial                                       */
+                                           them; else step-serial), the backward always.
+                                           Saved states in [value][key] order, as the
+                                           step-serial kernels keep them                     */
 };
 
 /* ABI version of this header; bumped on any incompatible change. */

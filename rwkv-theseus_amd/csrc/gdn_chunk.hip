@@ -65,26 +65,6 @@ struct GdnRec {
 static_assert(GdnRec<128>::BYTES % 256 == 0 && GdnRec<64>::BYTES % 256 == 0 && GdnRec<128, true>::BYTES % 256 == 0,
               "record alignment");
 
-// four consecutive elements as float
-__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-__device__ __forceinline__ float4 ld4(const bf16_t* p) {
-    const uint2 u = *reinterpret_cast<const uint2*>(p);
-    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
-                       __uint_as_float(u.y & 0xffff0000u));
-}
-
-// LDS DMA of 1 KB: lane l moves 16 bytes from the buffer at soff + voff to lds_off + 16 l
-// (lds_off: byte address in LDS, made scalar for M0).  Issued from inline asm like
-// wkv7_io.h's dma16, so the compiler does not wait for it; vm_wait0 does.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_kb(uint32_t lds_off, i32x4_t rs, uint32_t voff, uint32_t soff) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_off);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :: "s"(m0), "v"(voff), "s"(rs), "s"(soff) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 // ---------------------------------------------------------------------------
 // Operands of chunk blockIdx.x of head blockIdx.y (one wave).
 // Lane (q4, r16) holds token t = r16's keys of K-step ks in the permuted K=32
@@ -124,8 +104,8 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
     for (int ks = 0; ks < KS; ks++) {
         const int c0 = 32 * ks + 4 * q4;
         const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4*>(&vsh[r16][c0]) = tv ? ld4(v + row(r16) + c0) : z;
-        *reinterpret_cast<float4*>(&vsh[r16][c0 + 16]) = tv ? ld4(v + row(r16) + c0 + 16) : z;
+        *reinterpret_cast<float4*>(&vsh[r16][c0]) = tv ? ld4f(v + row(r16) + c0) : z;
+        *reinterpret_cast<float4*>(&vsh[r16][c0 + 16]) = tv ? ld4f(v + row(r16) + c0 + 16) : z;
     }
     float kr[KS][8], qr[KS][8];
     float ssk = 0.f, ssq = 0.f;
@@ -133,8 +113,8 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
     for (int ks = 0; ks < KS; ks++) {
         const int c0 = 32 * ks + 4 * q4;
         if (tv) {
-            const float4 a = ld4(k + row(r16) + c0), b = ld4(k + row(r16) + c0 + 16);
-            const float4 x = ld4(q + row(r16) + c0), y = ld4(q + row(r16) + c0 + 16);
+            const float4 a = ld4f(k + row(r16) + c0), b = ld4f(k + row(r16) + c0 + 16);
+            const float4 x = ld4f(q + row(r16) + c0), y = ld4f(q + row(r16) + c0 + 16);
             kr[ks][0] = a.x, kr[ks][1] = a.y, kr[ks][2] = a.z, kr[ks][3] = a.w;
             kr[ks][4] = b.x, kr[ks][5] = b.y, kr[ks][6] = b.z, kr[ks][7] = b.w;
             qr[ks][0] = x.x, qr[ks][1] = x.y, qr[ks][2] = x.z, qr[ks][3] = x.w;
@@ -299,7 +279,7 @@ __global__ __launch_bounds__(64) void wkv7_rec_prep(int Tn, int H, const bf16_t*
     float rt[KS][8];  // R~ of the lane's keys, kept for P2
     auto ld8 = [&](const bf16_t* x, int c0, float (&o)[8]) {
         const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 p = tv ? ld4(x + row + c0) : z, q = tv ? ld4(x + row + c0 + 16) : z;
+        const float4 p = tv ? ld4f(x + row + c0) : z, q = tv ? ld4f(x + row + c0 + 16) : z;
         o[0] = p.x, o[1] = p.y, o[2] = p.z, o[3] = p.w, o[4] = q.x, o[5] = q.y, o[6] = q.z, o[7] = q.w;
     };
     auto st8 = [&](float (*pl)[LP], int c0, const float (&x)[8]) {

@@ -59,8 +59,9 @@ static bool chunk_ok(int B, int T, int H, int N, int dtype, int flags) {
 
 // bf16, N = 128 and no flags: the forward on the chunk-record kernels (gdn_chunk.hip)
 // when the caller's workspace holds the records -- theseus_wkv7_forward_workspace_size
-// counts them, theseus_wkv7_forward_noalloc brings none and stays step-serial.  One
-// head's records stay under 4 GiB (32-bit DMA offsets), B*H within the prep's grid y.
+// counts them, theseus_wkv7_forward_noalloc brings none and stays step-serial -- and the
+// backward on wkv7_rec_bwd.hip's (its workspace is required).  One head's records stay
+// under 4 GiB (32-bit DMA offsets), B*H within the preps' grid y.
 static bool rec_shape(int B, int T, int H, int N, int dtype, int flags) {
     return chunk_refusal(B, T, H, N, dtype, flags) == THESEUS_WKV7_FAMILY_HEAD_SIZE && N == 128 &&
            (long long)B * H <= 65535 && wkv7_rec_workspace(1, T, 1, N) < (1ull << 32);
@@ -110,6 +111,7 @@ void launch_forward(const Fwd& p) {
 }
 void launch_backward(const Bwd& p) {
     if (chunk_ok(p.B, p.T, p.H, p.N, p.dtype, p.flags)) launch_chunk_backward(p, cu_count());
+    else if (rec_shape(p.B, p.T, p.H, p.N, p.dtype, p.flags)) launch_wkv7_rec_backward(p);
     else launch_seq_backward(p);
 }
 // The chunked kernels' handoffs; the step-serial backward replays each
@@ -125,8 +127,9 @@ size_t forward_workspace_fast(int B, int T, int H, int N, int dtype, int flags) 
     return split > need ? split : need;
 }
 size_t backward_workspace(int B, int T, int H, int N, int dtype, int flags) {
-    return chunk_ok(B, T, H, N, dtype, flags) ? chunk_backward_workspace(B, T, H, cu_count())
-                                              : seq_backward_workspace(B, H, N);
+    if (chunk_ok(B, T, H, N, dtype, flags)) return chunk_backward_workspace(B, T, H, cu_count());
+    if (rec_shape(B, T, H, N, dtype, flags)) return wkv7_rec_bwd_workspace(B, T, H);
+    return seq_backward_workspace(B, H, N);
 }
 
 }  // namespace wkv7

@@ -64,6 +64,25 @@ __device__ __forceinline__ void dma16(const uint16_t* lds, i32x4_t rs, uint32_t 
 }
 #pragma clang diagnostic pop
 
+// LDS DMA of 1 KB: lane l moves 16 bytes from the buffer at soff + voff to lds_off + 16 l
+// (lds_off: byte address in LDS, made scalar for M0), issued like dma16 above.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_kb(uint32_t lds_off, i32x4_t rs, uint32_t voff, uint32_t soff) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_off);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(m0), "v"(voff), "s"(rs), "s"(soff) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// four consecutive elements as float
+__device__ __forceinline__ float4 ld4f(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 ld4f(const bf16_t* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
+
 // Per-lane DMA offsets for a [16][64] SwDma plane: lane l fills physical
 // 16-byte chunk l%8 of row 8m + l/8 with the logical chunk that belongs there
 // (rstride = elements between consecutive tokens of one head).

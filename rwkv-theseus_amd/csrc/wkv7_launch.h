@@ -100,6 +100,11 @@ void launch_gdn_forward(const Gdn& p);
 size_t wkv7_rec_workspace(int B, int T, int H, int N);
 size_t wkv7_rec_workspace_split(int B, int T, int H, int N, int cus);
 void launch_wkv7_rec_forward(const Fwd& p, int cus);
+// Its backward (wkv7_rec_bwd.hip), every chunk at once from the [value][key] saved
+// states: a workspace of wkv7_rec_bwd_workspace bytes (the scan's records and dL/dS at
+// every chunk's end).
+size_t wkv7_rec_bwd_workspace(int B, int T, int H);
+void launch_wkv7_rec_backward(const Bwd& p);
 
 // Family dispatch (wkv7_capi.cpp): the chunked MFMA kernels when they cover
 // the call, else the step-serial ones.

@@ -1,0 +1,520 @@
+// WKV7 backward for head size 128 (bf16) on the matrix cores, every chunk at once.
+//
+// The chunk form of the recurrence (kernels/wkv7_state.cu:12-79; operands A~, R~, B-, K-,
+// B^, K^, Aab, Aak, Brb, Brk, Ti, P, P2 as in wkv7_chunk_fwd.hip, decays per key) gives,
+// with H = dL/dS at a chunk's end, H' = H diag(e^{gL}), S0 the state at its start (a
+// saved state) and dY its output gradient,
+//   SA = Ti (A~ S0^T + Aak V),  Q = Ti^T (B^ H^T + Brb^T dY)
+//   dV = K^ H^T + Aak^T Q + Brk^T dY
+//   dK = e^{-g} o [V H' + triu_s(V Q^T) A~ + triu(V dY^T) R~]
+//   dB = e^{-g} o [SA H' + triu_s(SA Q^T) A~ + triu(SA dY^T) R~]
+//   dR = e^{g}  o [dY S0 + tril(dY SA^T) B- + tril(dY V^T) K-]
+//   dA = e^{gp} o [Q S0 + tril_s(Q SA^T) B- + tril_s(Q V^T) K-]
+//   H at the chunk's start = H diag(e^{gL}) + (H B^^T) P + dY^T P2
+// and the log-decay gradient dlogd_t = sum_{s>=t} (r dR - b dB - k dK)_s +
+// sum_{s>t} (a dA)_s + colsum(H_end o S_end) over the chunk's own steps: the gradients of
+// the steps up to a boundary are those of the sequence cut there with dL/dS_end = H_end,
+// so the carry from every later step is the column sum of H_end o S_end at the chunk's
+// end (S_end: the next saved state).  dw = dlogd * (-e^{-1/2}) sig(w) (1 - sig(w)).
+// (Checked in float64 against the oracle's step adjoint before the kernels.)
+//
+// Three kernels.  wkv7_bwd_prep (one wave per chunk, all at once) writes each chunk's
+// record for the scan: B^ as the K=32 A operand over the keys, [P | P2] per 16-key tile
+// as the A operand of the K=32 update, e^{gL} per key.  wkv7_bwd_scan walks each head's
+// chunks backwards (one workgroup per 64 value rows of H, fp32 in registers, records
+// double-buffered in LDS by DMA as gdn_scan's), storing H at every chunk's end in the
+// workspace and the first chunk's start as ds0.  wkv7_bwd_chunk then forms every
+// chunk's gradients independently (eight waves; wave w owns value rows 16w..16w+15 for
+// SA, Q, dV and keys 16w..16w+15 for dK, dB, dR, dA, dw).
+#include "wkv7_io.h"
+#include "wkv7_launch.h"
+
+namespace wkv7 {
+namespace {
+
+constexpr int BC = 16;        // chunk length
+constexpr int BNK = 128;      // head size
+constexpr int BKS = BNK / 32, BTJ = BNK / 16;
+constexpr long BNN = (long)BNK * BNK;
+
+// One chunk's record for the scan (byte offsets).
+struct BwdRec {
+    static constexpr size_t BF = 0;                                // B^ [KS][hi, lo][64 lanes] uint4
+    static constexpr size_t PP = BF + (size_t)BKS * 2 * 64 * 16;   // [P | P2] [TJ][hi, lo][64] uint4
+    static constexpr size_t EL = PP + (size_t)BTJ * 2 * 64 * 16;   // e^{gL} [NK]
+    static constexpr size_t BYTES = EL + (size_t)BNK * 4;
+    static constexpr int DMA_BLOCKS = (int)((BYTES + 1023) / 1024);
+};
+static_assert(BwdRec::BYTES % 256 == 0, "record alignment");
+
+__device__ __forceinline__ f32x4_t mm3(f32x4_t acc, uint4 xh, uint4 xl, uint4 yh, uint4 yl) {
+    return mma32(mma32(mma32(acc, xh, yh), xh, yl), xl, yh);
+}
+// M^T of a D-layout tile, by the product M^T I on the K=16 instruction (I exact in bf16)
+__device__ __forceinline__ f32x4_t transpose16(const f32x4_t& m, int lane) {
+    f32x4_t id;
+#pragma unroll
+    for (int e = 0; e < 4; e++) id[e] = (4 * (lane >> 4) + e) == (lane & 15) ? 1.f : 0.f;
+    const Pk pm = pk(m), pi = pk(id);
+    return mma16(mma16(zero4(), pm.h, pi.h), pm.l, pi.h);
+}
+__device__ __forceinline__ float bf2f(const bf16_t* p, long i) { return io<bf16_t>::ld(p, i); }
+
+// ---------------------------------------------------------------------------
+// Records of chunk blockIdx.x of head blockIdx.y (one wave; lane (q4, r16): token r16's
+// keys 32ks + 4q4 + e and 32ks + 16 + 4q4 + e, as wkv7_rec_prep).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void wkv7_bwd_prep(int Tn, int H, const bf16_t* __restrict__ r,
+                                                    const bf16_t* __restrict__ w, const bf16_t* __restrict__ k,
+                                                    const bf16_t* __restrict__ a, const bf16_t* __restrict__ b,
+                                                    uint8_t* __restrict__ ws) {
+    using R = BwdRec;
+    constexpr int LP = BNK + 4;
+    const int c = blockIdx.x, bh = blockIdx.y, nchunk = gridDim.x;
+    const int bb = bh / H, h = bh - bb * H;
+    const int lane = threadIdx.x, q4 = lane >> 4, r16 = lane & 15;
+    const int t0 = c * BC, L = min(BC, Tn - t0);
+    const long row = (((long)bb * Tn + t0 + r16) * H + h) * (long)BNK;
+    const bool tv = r16 < L;
+    __shared__ __attribute__((aligned(16))) float pa[BC][LP], pr[BC][LP];  // A~, R~ [t][j]
+    uint8_t* const rec = ws + ((size_t)bh * nchunk + c) * R::BYTES;
+    auto ld8 = [&](const bf16_t* x, int c0, float (&o)[8]) {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 p = tv ? ld4f(x + row + c0) : z, q = tv ? ld4f(x + row + c0 + 16) : z;
+        o[0] = p.x, o[1] = p.y, o[2] = p.z, o[3] = p.w, o[4] = q.x, o[5] = q.y, o[6] = q.z, o[7] = q.w;
+    };
+    auto st8 = [&](float (*pl)[LP], int c0, const float (&x)[8]) {
+        *reinterpret_cast<float4*>(&pl[r16][c0]) = make_float4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<float4*>(&pl[r16][c0 + 16]) = make_float4(x[4], x[5], x[6], x[7]);
+    };
+    f32x4_t Aab = zero4(), AabT = zero4(), BrbT = zero4();
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) {
+        const int c0 = 32 * ks + 4 * q4;
+        float wv[8], av[8], bv[8], rv[8];
+        ld8(w, c0, wv), ld8(a, c0, av), ld8(b, c0, bv), ld8(r, c0, rv);
+        float At[8], Bm[8], Rt[8], Bh[8], eL[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float g = row_prefix_sum(tv ? log_decay(wv[e]) : 0.f);
+            const float gp = row_prev(g, 0.f), gL = row_last(g);
+            At[e] = av[e] * __expf(gp);
+            Rt[e] = rv[e] * __expf(g);
+            Bm[e] = bv[e] * __expf(-g);
+            Bh[e] = bv[e] * __expf(gL - g);
+            eL[e] = __expf(gL);
+        }
+        st8(pa, c0, At), st8(pr, c0, Rt);
+        if (r16 == 0) {
+            float* el = reinterpret_cast<float*>(rec + R::EL);
+            *reinterpret_cast<float4*>(el + c0) = make_float4(eL[0], eL[1], eL[2], eL[3]);
+            *reinterpret_cast<float4*>(el + c0 + 16) = make_float4(eL[4], eL[5], eL[6], eL[7]);
+        }
+        uint4 ah, al, bh_, bl, rh, rl, hh, hl;
+        pack8(At, ah, al), pack8(Bm, bh_, bl), pack8(Rt, rh, rl), pack8(Bh, hh, hl);
+        uint4* bf = reinterpret_cast<uint4*>(rec + R::BF) + (size_t)(2 * ks) * 64 + lane;
+        bf[0] = hh;
+        bf[64] = hl;
+        Aab = mm3(Aab, ah, al, bh_, bl);    // A~_rr . B-_cc
+        AabT = mm3(AabT, bh_, bl, ah, al);  // B-_rr . A~_cc
+        BrbT = mm3(BrbT, bh_, bl, rh, rl);  // B-_rr . R~_cc
+    }
+    const int cc = r16;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = 4 * q4 + e;
+        Aab[e] = cc < rr ? Aab[e] : 0.f;
+        AabT[e] = rr < cc ? AabT[e] : 0.f;
+        BrbT[e] = rr <= cc ? BrbT[e] : 0.f;  // Brb[cc][rr]
+    }
+    f32x4_t Ti, TiT;
+    tri_inverse(Aab, AabT, lane, Ti, TiT);
+    const Pk pTiT = pk(TiT), pBrbT = pk(BrbT);
+    __syncthreads();  // the planes
+#pragma unroll
+    for (int tj = 0; tj < BTJ; tj++) {
+        f32x4_t at, rt;  // D layout [t][j], t = 4q4 + e, j = 16tj + r16
+#pragma unroll
+        for (int e = 0; e < 4; e++) at[e] = pa[4 * q4 + e][16 * tj + r16], rt[e] = pr[4 * q4 + e][16 * tj + r16];
+        const f32x4_t Pt = mm16s(pTiT, pk(at));          // P = Ti A~
+        const Pk pP = pk(Pt);
+        const Pk pP2 = pk(rt + mm16s(pBrbT, pP));        // P2 = R~ + Brb P
+        uint4* pp = reinterpret_cast<uint4*>(rec + R::PP) + (size_t)(2 * tj) * 64 + lane;
+        pp[0] = cat(pP.h, pP2.h);
+        pp[64] = cat(pP.l, pP2.l);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Each head's chunks backwards: workgroup rg * BH + bh, four waves, wave wv of group rg
+// keeps value rows i_own = 16 (4 rg + wv) + r16 of H as Ht[tj][e] = H[i_own][16tj + 4q4 + e].
+// Per chunk: H is stored (the chunk kernel's H_end), U^T = B^ H^T over the keys, then
+// H^T <- e^{gL} o H^T + [P^T | P2^T] [U^T; dY] on the K=32 instruction.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, const float* __restrict__ dsT,
+                                                     const bf16_t* __restrict__ dy, float* __restrict__ ds0,
+                                                     float* __restrict__ hbuf, const uint8_t* __restrict__ ws) {
+    using R = BwdRec;
+    __shared__ __attribute__((aligned(1024))) uint8_t recs[2][R::DMA_BLOCKS * 1024];
+    const int bh = blockIdx.x % BH, rg = blockIdx.x / BH, bb = bh / H, h = bh - bb * H;
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+    const int i_own = 16 * (4 * rg + wv) + r16;
+    const int nchunk = (Tn + BC - 1) / BC;
+    const i32x4_t rs = dma_rsrc(ws + (size_t)bh * nchunk * R::BYTES, (uint32_t)((size_t)nchunk * R::BYTES));
+    auto fetch = [&](int c, int buf) {
+        uint32_t so = (uint32_t)((size_t)c * R::BYTES);
+        asm volatile("" : "+s"(so));
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)recs[buf];
+        for (int j = wv; j < R::DMA_BLOCKS; j += 4) dma_kb(base + 1024 * j, rs, (uint32_t)(1024 * j + 16 * lane), so);
+    };
+    // dY[t0 + 4q4 + e][i_own] (zero past the end)
+    auto load_dy = [&](int c, float (&o)[4]) {
+        const int t0 = c * BC, L = min(BC, Tn - t0);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 4 * q4 + e;
+            o[e] = t < L ? bf2f(dy, (((long)bb * Tn + t0 + t) * H + h) * BNK + i_own) : 0.f;
+        }
+    };
+    fetch(nchunk - 1, 0);
+    f32x4_t Ht[BTJ];
+#pragma unroll
+    for (int tj = 0; tj < BTJ; tj++) {
+        const float4 x = dsT ? *reinterpret_cast<const float4*>(dsT + bh * BNN + (long)i_own * BNK + 16 * tj + 4 * q4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
+    }
+    float dyn[4];
+    load_dy(nchunk - 1, dyn);
+    vm_wait0();
+    __syncthreads();
+    for (int c = nchunk - 1, it = 0; c >= 0; c--, it++) {
+        if (c > 0) fetch(c - 1, (it + 1) & 1);
+        const uint8_t* const rec = recs[it & 1];
+        const f32x4_t dyc = {dyn[0], dyn[1], dyn[2], dyn[3]};
+        if (c > 0) load_dy(c - 1, dyn);
+        float* const hout = hbuf + ((long)bh * nchunk + c) * BNN + (long)i_own * BNK + 4 * q4;
+#pragma unroll
+        for (int tj = 0; tj < BTJ; tj++)
+            *reinterpret_cast<float4*>(hout + 16 * tj) = make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+        // U^T [t][i_own] = sum_j B^[t][j] H[i_own][j]
+        f32x4_t u = zero4();
+#pragma unroll
+        for (int ks = 0; ks < BKS; ks++) {
+            const float sv[8] = {Ht[2 * ks][0], Ht[2 * ks][1], Ht[2 * ks][2], Ht[2 * ks][3],
+                                 Ht[2 * ks + 1][0], Ht[2 * ks + 1][1], Ht[2 * ks + 1][2], Ht[2 * ks + 1][3]};
+            uint4 sh, sl;
+            pack8(sv, sh, sl);
+            const uint4* bf = reinterpret_cast<const uint4*>(rec + R::BF) + (2 * ks) * 64 + lane;
+            u = mm3(u, bf[0], bf[64], sh, sl);
+        }
+        uint2 uh, ul, dh, dl;
+        pack4(u, uh, ul);
+        pack4(dyc, dh, dl);  // (exact in bf16: dl = 0)
+        const uint4 bhi = cat(uh, dh), blo = cat(ul, dl);
+#pragma unroll
+        for (int tj = 0; tj < BTJ; tj++) {
+            const uint4* pp = reinterpret_cast<const uint4*>(rec + R::PP) + (2 * tj) * 64 + lane;
+            const uint4 ah = pp[0], al = pp[64];
+            const f32x4_t eg = *reinterpret_cast<const f32x4_t*>(rec + R::EL + 4 * (16 * tj + 4 * q4));
+            Ht[tj] = mma32(mma32(mma32(Ht[tj] * eg, ah, bhi), ah, blo), al, bhi);
+        }
+        vm_wait0();
+        __syncthreads();
+    }
+#pragma unroll
+    for (int tj = 0; tj < BTJ; tj++)
+        *reinterpret_cast<float4*>(ds0 + bh * BNN + (long)i_own * BNK + 16 * tj + 4 * q4) =
+            make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+}
+
+// ---------------------------------------------------------------------------
+// The gradients of one chunk (512 lanes).  Workgroups map to (head, chunk) so that a
+// head's consecutive chunks share an XCD (chunk c's S_end is chunk c + 1's S0 in L2).
+// ---------------------------------------------------------------------------
+constexpr int CLP = BNK + 4;  // padded plane row (floats)
+struct ChunkLds {
+    float At[BC][CLP], Bm[BC][CLP], Km[BC][CLP], Rt[BC][CLP];  // [t][j], written by the key owners
+    float SA[BC][CLP], Q[BC][CLP];                             // [t][i], written by the value-row owners
+    float eL[BNK];
+    float csum[BTJ][BNK];  // per wave: column sums of H_end o S_end over its 16 value rows
+};
+
+__global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int per_xcd,
+                                                      const bf16_t* __restrict__ r, const bf16_t* __restrict__ w,
+                                                      const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                                                      const bf16_t* __restrict__ a, const bf16_t* __restrict__ b,
+                                                      const bf16_t* __restrict__ dy, const float* __restrict__ ckpt,
+                                                      const float* __restrict__ hbuf, bf16_t* __restrict__ dr,
+                                                      bf16_t* __restrict__ dw, bf16_t* __restrict__ dk,
+                                                      bf16_t* __restrict__ dv, bf16_t* __restrict__ da,
+                                                      bf16_t* __restrict__ db) {
+    __shared__ __attribute__((aligned(16))) ChunkLds sm;
+    const int nchunk = (Tn + BC - 1) / BC;
+    const int job = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (job >= nchunk * BH) return;  // (whole workgroup)
+    const int bh = job / nchunk, c = job - bh * nchunk, bb = bh / H, h = bh - bb * H;
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+    const int t0 = c * BC, L = min(BC, Tn - t0);
+    const long tok0 = (long)bb * Tn + t0;
+    const int col = 16 * wv + r16;  // the lane's key (dK ...) and value column (dV ...)
+    auto at_tok = [&](int t) { return ((tok0 + t) * H + h) * (long)BNK; };
+    const long ncp = nchunk + 1;
+    const float* const S0 = ckpt + ((long)bh * ncp + c) * BNN;
+    const float* const Se = S0 + BNN;
+    const float* const Hm = hbuf + ((long)bh * nchunk + c) * BNN;
+    const int irow = 16 * wv + r16;  // value row of the row-strip loads
+
+    // ---- the wave's value rows of H_end, S_end and S0 (keys 32ks + 4q4 + e, +16) ----
+    float hr[BKS][8], sr[BKS][8];
+    auto rows = [&](const float* M, float (&o)[BKS][8]) {
+#pragma unroll
+        for (int ks = 0; ks < BKS; ks++) {
+            const float4 x = *reinterpret_cast<const float4*>(M + (long)irow * BNK + 32 * ks + 4 * q4);
+            const float4 y = *reinterpret_cast<const float4*>(M + (long)irow * BNK + 32 * ks + 16 + 4 * q4);
+            o[ks][0] = x.x, o[ks][1] = x.y, o[ks][2] = x.z, o[ks][3] = x.w;
+            o[ks][4] = y.x, o[ks][5] = y.y, o[ks][6] = y.z, o[ks][7] = y.w;
+        }
+    };
+    rows(Hm, hr);
+    rows(Se, sr);
+
+    // ---- the chunk operands of the wave's keys in D layout ([t][col], t = 4q4 + e) ----
+    float xr[4], xw[4], xk[4], xa[4], xb[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = 4 * q4 + e;
+        const bool ok = t < L;
+        const long o = at_tok(ok ? t : 0) + col;
+        xr[e] = ok ? bf2f(r, o) : 0.f, xw[e] = ok ? bf2f(w, o) : 0.f, xk[e] = ok ? bf2f(k, o) : 0.f;
+        xa[e] = ok ? bf2f(a, o) : 0.f, xb[e] = ok ? bf2f(b, o) : 0.f;
+    }
+    float ld[4], p[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) ld[e] = (4 * q4 + e) < L ? log_decay(xw[e]) : 0.f;
+    p[0] = ld[0], p[1] = p[0] + ld[1], p[2] = p[1] + ld[2], p[3] = p[2] + ld[3];
+    // cumulative over the four lane groups (tokens 4q'..4q'+3 of the same key)
+    const float T0 = __shfl(p[3], r16), T1 = __shfl(p[3], 16 + r16), T2 = __shfl(p[3], 32 + r16),
+                T3 = __shfl(p[3], 48 + r16);
+    const float excl = (q4 > 0 ? T0 : 0.f) + (q4 > 1 ? T1 : 0.f) + (q4 > 2 ? T2 : 0.f);
+    const float eLj = __expf(T0 + T1 + T2 + T3);
+    f32x4_t At, Rt, Bm, Km, eA, eR, eM;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float g = excl + p[e], gp = e ? excl + p[e - 1] : excl;
+        eA[e] = __expf(gp), eR[e] = __expf(g), eM[e] = __expf(-g);
+        At[e] = xa[e] * eA[e], Rt[e] = xr[e] * eR[e], Bm[e] = xb[e] * eM[e], Km[e] = xk[e] * eM[e];
+        const int t = 4 * q4 + e;
+        sm.At[t][col] = At[e], sm.Bm[t][col] = Bm[e], sm.Km[t][col] = Km[e], sm.Rt[t][col] = Rt[e];
+    }
+    if (q4 == 0) sm.eL[col] = eLj;
+    // the carry's partial column sums over this wave's value rows
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float s = row_sum16(hr[ks][e] * sr[ks][e]);
+            if (r16 == 0) sm.csum[wv][32 * ks + (e < 4 ? 4 * q4 + e : 16 + 4 * q4 + e - 4)] = s;
+        }
+    uint4 Hh[BKS], Hl[BKS], Sh[BKS], Sl[BKS];
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) pack8(hr[ks], Hh[ks], Hl[ks]);
+    rows(S0, sr);
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) pack8(sr[ks], Sh[ks], Sl[ks]);
+    __syncthreads();
+
+    // ---- chunk matrices (every wave) and the wave's [t][i] products over the keys ----
+    f32x4_t Aab = zero4(), AabT = zero4(), Aak = zero4(), Brb = zero4(), Brk = zero4();
+    f32x4_t P1 = zero4(), P2 = zero4(), P3 = zero4();
+    auto trow = [&](float (*pl)[CLP], int ks, float (&o)[8]) {
+        const float4 x = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 4 * q4]);
+        const float4 y = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 16 + 4 * q4]);
+        o[0] = x.x, o[1] = x.y, o[2] = x.z, o[3] = x.w, o[4] = y.x, o[5] = y.y, o[6] = y.z, o[7] = y.w;
+    };
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) {
+        float fa[8], fb[8], fk[8], fr[8], el[8];
+        trow(sm.At, ks, fa), trow(sm.Bm, ks, fb), trow(sm.Km, ks, fk), trow(sm.Rt, ks, fr);
+        {
+            const float4 x = *reinterpret_cast<const float4*>(&sm.eL[32 * ks + 4 * q4]);
+            const float4 y = *reinterpret_cast<const float4*>(&sm.eL[32 * ks + 16 + 4 * q4]);
+            el[0] = x.x, el[1] = x.y, el[2] = x.z, el[3] = x.w, el[4] = y.x, el[5] = y.y, el[6] = y.z, el[7] = y.w;
+        }
+        uint4 ah, al, bh_, bl, kh, kl, rh, rl;
+        pack8(fa, ah, al), pack8(fb, bh_, bl), pack8(fk, kh, kl), pack8(fr, rh, rl);
+        Aab = mm3(Aab, ah, al, bh_, bl);
+        AabT = mm3(AabT, bh_, bl, ah, al);
+        Aak = mm3(Aak, ah, al, kh, kl);
+        Brb = mm3(Brb, rh, rl, bh_, bl);   // R~_rr . B-_cc
+        Brk = mm3(Brk, rh, rl, kh, kl);    // R~_rr . K-_cc
+        P1 = mm3(P1, ah, al, Sh[ks], Sl[ks]);  // A~ S0^T
+#pragma unroll
+        for (int e = 0; e < 8; e++) fb[e] *= el[e], fk[e] *= el[e];  // B^, K^
+        pack8(fb, bh_, bl), pack8(fk, kh, kl);
+        P2 = mm3(P2, bh_, bl, Hh[ks], Hl[ks]);  // B^ H^T
+        P3 = mm3(P3, kh, kl, Hh[ks], Hl[ks]);   // K^ H^T
+    }
+    const int cc = r16;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = 4 * q4 + e;
+        Aab[e] = cc < rr ? Aab[e] : 0.f;
+        AabT[e] = rr < cc ? AabT[e] : 0.f;
+        Aak[e] = cc < rr ? Aak[e] : 0.f;
+        Brb[e] = cc <= rr ? Brb[e] : 0.f;
+        Brk[e] = cc <= rr ? Brk[e] : 0.f;
+    }
+    f32x4_t Ti, TiT;
+    tri_inverse(Aab, AabT, lane, Ti, TiT);
+    const Pk pAak = pk(Aak), pBrb = pk(Brb), pBrk = pk(Brk), pTi = pk(Ti), pTiT = pk(TiT);
+    const Pk pAakT = pk(transpose16(Aak, lane));
+
+    // ---- SA, Q, dV for the wave's value columns ----
+    f32x4_t vD, dyD;  // [t][col]
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = 4 * q4 + e;
+        vD[e] = t < L ? bf2f(v, at_tok(t) + col) : 0.f;
+        dyD[e] = t < L ? bf2f(dy, at_tok(t) + col) : 0.f;
+    }
+    const Pk pV = pk(vD), pdY = pk(dyD);
+    const f32x4_t SA = mm16s(pTiT, pk(P1 + mm16s(pAakT, pV)));  // Ti (A~ S0^T + Aak V)
+    const f32x4_t Q = mm16s(pTi, pk(P2 + mm16s(pBrb, pdY)));    // Ti^T (B^ H^T + Brb^T dY)
+    const f32x4_t dV = P3 + mm16s(pAak, pk(Q)) + mm16s(pBrk, pdY);
+#pragma unroll
+    for (int e = 0; e < 4; e++) sm.SA[4 * q4 + e][col] = SA[e], sm.Q[4 * q4 + e][col] = Q[e];
+    {
+        const int tr = 4 * q4 + (lane & 3);  // the row quad_rows_bf16 gives this lane
+        const uint2 q = quad_rows_bf16(dV, lane);  // (cross-lane: every lane takes part)
+        if (tr < L) *reinterpret_cast<uint2*>(dv + at_tok(tr) + 16 * wv + 4 * ((lane >> 2) & 3)) = q;
+    }
+    // the key columns of H_end and S0 (value rows 32ks + 4q4 + e, +16) for the products over
+    // the value rows
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int i = 32 * ks + (e < 4 ? 4 * q4 + e : 16 + 4 * q4 + e - 4);
+            hr[ks][e] = Hm[(long)i * BNK + col];
+            sr[ks][e] = S0[(long)i * BNK + col];
+        }
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) pack8(hr[ks], Hh[ks], Hl[ks]), pack8(sr[ks], Sh[ks], Sl[ks]);
+    __syncthreads();  // SA, Q, csum
+
+    // ---- dK, dB, dR, dA, dw for the wave's keys ----
+    f32x4_t VH = zero4(), SAH = zero4(), dYS = zero4(), QS = zero4();
+    f32x4_t Gqv = zero4(), Gyv = zero4(), Gqs = zero4(), Gys = zero4();  // Gram matrices over the value rows
+    const bool tv = r16 < L;
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) {
+        float fs[8], fq[8], fv[8], fy[8];
+        trow(sm.SA, ks, fs), trow(sm.Q, ks, fq);
+        {
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const long o = at_tok(tv ? r16 : 0) + 32 * ks + 4 * q4;
+            const float4 v0 = tv ? ld4f(v + o) : z, v1 = tv ? ld4f(v + o + 16) : z;
+            const float4 y0 = tv ? ld4f(dy + o) : z, y1 = tv ? ld4f(dy + o + 16) : z;
+            fv[0] = v0.x, fv[1] = v0.y, fv[2] = v0.z, fv[3] = v0.w, fv[4] = v1.x, fv[5] = v1.y, fv[6] = v1.z, fv[7] = v1.w;
+            fy[0] = y0.x, fy[1] = y0.y, fy[2] = y0.z, fy[3] = y0.w, fy[4] = y1.x, fy[5] = y1.y, fy[6] = y1.z, fy[7] = y1.w;
+        }
+        uint4 sh, sl, qh, ql, vh, vl, yh, yl;
+        pack8(fs, sh, sl), pack8(fq, qh, ql), pack8(fv, vh, vl), pack8(fy, yh, yl);  // (vl = yl = 0)
+        VH = mma32(mma32(VH, vh, Hh[ks]), vh, Hl[ks]);
+        SAH = mm3(SAH, sh, sl, Hh[ks], Hl[ks]);
+        dYS = mma32(mma32(dYS, yh, Sh[ks]), yh, Sl[ks]);
+        QS = mm3(QS, qh, ql, Sh[ks], Sl[ks]);
+        Gqv = mma32(mma32(Gqv, qh, vh), ql, vh);   // Q_rr . V_cc
+        Gyv = mma32(Gyv, yh, vh);                  // dY_rr . V_cc
+        Gqs = mm3(Gqs, qh, ql, sh, sl);            // Q_rr . SA_cc
+        Gys = mma32(mma32(Gys, yh, sh), yh, sl);   // dY_rr . SA_cc
+    }
+    const f32x4_t Gvq = transpose16(Gqv, lane), Gvy = transpose16(Gyv, lane);
+    const f32x4_t Gsq = transpose16(Gqs, lane), Gsy = transpose16(Gys, lane);
+    // masked transposes of the intra-chunk matrices, element [rr][cc] (rr = 4q4 + e, cc = r16)
+    f32x4_t M1, M2, M3, M4, M5, M6, M7, M8;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = 4 * q4 + e;
+        M1[e] = rr > cc ? Gqv[e] : 0.f;   // triu_s(V Q^T)^T
+        M2[e] = rr >= cc ? Gyv[e] : 0.f;  // triu(V dY^T)^T
+        M3[e] = rr > cc ? Gqs[e] : 0.f;   // triu_s(SA Q^T)^T
+        M4[e] = rr >= cc ? Gys[e] : 0.f;  // triu(SA dY^T)^T
+        M5[e] = rr <= cc ? Gsy[e] : 0.f;  // tril(dY SA^T)^T
+        M6[e] = rr <= cc ? Gvy[e] : 0.f;  // tril(dY V^T)^T
+        M7[e] = rr < cc ? Gsq[e] : 0.f;   // tril_s(Q SA^T)^T
+        M8[e] = rr < cc ? Gvq[e] : 0.f;   // tril_s(Q V^T)^T
+    }
+    const Pk pAt = pk(At), pRt = pk(Rt), pBm = pk(Bm), pKm = pk(Km);
+    const f32x4_t gK = eM * (VH * eLj + mm16s(pk(M1), pAt) + mm16s(pk(M2), pRt));
+    const f32x4_t gB = eM * (SAH * eLj + mm16s(pk(M3), pAt) + mm16s(pk(M4), pRt));
+    const f32x4_t gR = eR * (dYS + mm16s(pk(M5), pBm) + mm16s(pk(M6), pKm));
+    const f32x4_t gA = eA * (QS + mm16s(pk(M7), pBm) + mm16s(pk(M8), pKm));
+    // dlogd_t = sum_{s>=t} (r dR - b dB - k dK)_s + sum_{s>t} (a dA)_s + carry
+    float sx[4], sy[4];
+    {
+        float x[4], y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = xr[e] * gR[e] - xb[e] * gB[e] - xk[e] * gK[e], y[e] = xa[e] * gA[e];
+        sx[3] = x[3], sy[3] = 0.f;
+#pragma unroll
+        for (int e = 2; e >= 0; e--) sx[e] = sx[e + 1] + x[e], sy[e] = sy[e + 1] + y[e + 1];
+        const float ytot = sy[0] + y[0];
+        const float X1 = __shfl(sx[0], 16 + r16), X2 = __shfl(sx[0], 32 + r16), X3 = __shfl(sx[0], 48 + r16);
+        const float Y1 = __shfl(ytot, 16 + r16), Y2 = __shfl(ytot, 32 + r16), Y3 = __shfl(ytot, 48 + r16);
+        const float xa_ = (q4 < 1 ? X1 : 0.f) + (q4 < 2 ? X2 : 0.f) + (q4 < 3 ? X3 : 0.f);
+        const float ya_ = (q4 < 1 ? Y1 : 0.f) + (q4 < 2 ? Y2 : 0.f) + (q4 < 3 ? Y3 : 0.f);
+        float carry = 0.f;
+#pragma unroll
+        for (int u = 0; u < BTJ; u++) carry += sm.csum[u][col];
+#pragma unroll
+        for (int e = 0; e < 4; e++) sx[e] += xa_ + carry, sy[e] += ya_;
+    }
+    f32x4_t gW;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float s = sigmoidf_(xw[e]);
+        gW[e] = (sx[e] + sy[e]) * (-DECAY_SCALE) * s * (1.f - s);
+    }
+    const int tr = 4 * q4 + (lane & 3);
+    const uint2 qk = quad_rows_bf16(gK, lane), qb = quad_rows_bf16(gB, lane), qr = quad_rows_bf16(gR, lane),
+                qa = quad_rows_bf16(gA, lane), qw = quad_rows_bf16(gW, lane);
+    if (tr < L) {
+        const long o = at_tok(tr) + 16 * wv + 4 * ((lane >> 2) & 3);
+        *reinterpret_cast<uint2*>(dk + o) = qk;
+        *reinterpret_cast<uint2*>(db + o) = qb;
+        *reinterpret_cast<uint2*>(dr + o) = qr;
+        *reinterpret_cast<uint2*>(da + o) = qa;
+        *reinterpret_cast<uint2*>(dw + o) = qw;
+    }
+}
+
+}  // namespace
+
+size_t wkv7_rec_bwd_workspace(int B, int T, int H) {
+    const size_t n = (size_t)B * H * ((T + BC - 1) / BC);
+    return (n * BwdRec::BYTES + 255) / 256 * 256 + n * BNN * sizeof(float);
+}
+
+void launch_wkv7_rec_backward(const Bwd& p) {
+    const int nchunk = (p.T + BC - 1) / BC, BH = p.B * p.H;
+    uint8_t* const recs = static_cast<uint8_t*>(p.ws);
+    float* const hbuf = reinterpret_cast<float*>(recs + ((size_t)BH * nchunk * BwdRec::BYTES + 255) / 256 * 256);
+    const bf16_t *r = static_cast<const bf16_t*>(p.r), *w = static_cast<const bf16_t*>(p.w),
+                 *k = static_cast<const bf16_t*>(p.k), *v = static_cast<const bf16_t*>(p.v),
+                 *a = static_cast<const bf16_t*>(p.a), *b = static_cast<const bf16_t*>(p.b),
+                 *dy = static_cast<const bf16_t*>(p.dy);
+    hipLaunchKernelGGL(wkv7_bwd_prep, dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, r, w, k, a, b, recs);
+    hipLaunchKernelGGL(wkv7_bwd_scan, dim3(BH * (BNK / 64)), dim3(256), 0, p.stream, p.T, p.H, BH, p.dsT, dy, p.ds0,
+                       hbuf, recs);
+    const int jobs = nchunk * BH, per_xcd = (jobs + 7) / 8;
+    hipLaunchKernelGGL(wkv7_bwd_chunk, dim3(8 * per_xcd), dim3(512), 0, p.stream, p.T, p.H, BH, per_xcd, r, w, k, v,
+                       a, b, dy, p.ckpt, hbuf, static_cast<bf16_t*>(p.dr), static_cast<bf16_t*>(p.dw),
+                       static_cast<bf16_t*>(p.dk), static_cast<bf16_t*>(p.dv), static_cast<bf16_t*>(p.da),
+                       static_cast<bf16_t*>(p.db));
+}
+
+}  // namespace wkv7

@@ -41,7 +41,7 @@ STATE_KEY_VALUE = 2     # states [B,H,key,value] (GDN's layout) instead of [B,H,
 
 # theseus_wkv7_family codes (include/theseus_wkv7.h) -> why the step-serial kernels run
 _FAMILY_FORCED = 1
-_FAMILY_RECORDS = 6  # bf16, N=128: chunk-record forward, step-serial backward
+_FAMILY_RECORDS = 6  # bf16, N=128: the chunk-record kernels
 _FALLBACK_REASON = {
     2: "float32 token tensors",
     3: "a head size other than 64 or 128",
@@ -146,19 +146,16 @@ class Extension:
         """theseus_wkv7_family code of a call (0: chunked MFMA kernels)."""
         return int(self.lib.theseus_wkv7_kernel_family(B, T, H, N, dtype))
 
-    def _warn_fallback(self, B, T, H, N, dt, backward=False):
+    def _warn_fallback(self, B, T, H, N, dt):
         """Say so when a call runs on the step-serial kernels (exact, but one step at a
         time: ~75x slower than the chunked kernels at config 2).  THESEUS_WKV7_STRICT=1
         turns the warning into an error; THESEUS_WKV7_FAMILY=seq (an explicit request)
         is silent."""
-        family = self.kernel_family(B, T, H, N, dt)
-        reason = _FALLBACK_REASON.get(family)
-        if family == _FAMILY_RECORDS and backward:
-            reason = "a head size of 128 (its forward runs on the chunk-record kernels)"
+        reason = _FALLBACK_REASON.get(self.kernel_family(B, T, H, N, dt))
         if reason is None:
             return
         msg = (f"theseus_wkv7: {reason} -> the step-serial kernels run this call "
-               f"(B={B} T={T} H={H} N={N}); bf16 with N=64 runs on the chunked MFMA kernels")
+               f"(B={B} T={T} H={H} N={N}); bf16 with N=64 or N=128 runs on the chunked MFMA kernels")
         if os.environ.get("THESEUS_WKV7_STRICT", "") == "1":
             raise RuntimeError(msg)
         warnings.warn(msg, RuntimeWarning, stacklevel=4)
@@ -312,7 +309,7 @@ class Extension:
                 status = self.lib.theseus_wkv7_backward_ex(B, T, H, N, dt, flags, *ptrs, _ptr(ws),
                                                            ctypes.c_size_t(ws_bytes), _stream(r.device))
             else:
-                self._warn_fallback(B, T, H, N, dt, backward=True)
+                self._warn_fallback(B, T, H, N, dt)
                 ws, ws_bytes = _workspace(int(self.lib.theseus_wkv7_backward_workspace_size(B, T, H, N, dt)),
                                           r.device)
                 status = self.lib.theseus_wkv7_backward(B, T, H, N, dt, *ptrs, _ptr(ws),

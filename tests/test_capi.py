@@ -207,7 +207,7 @@ def test_kernel_family_dispatch_predicate(monkeypatch):
     assert fam(4, 2048, 80, 64, 0) == 0
     assert fam(4, 2048, 80, 64, 1) == 2   # fp32
     assert fam(4, 2048, 80, 32, 0) == 3   # head size
-    assert fam(1, 2048, 32, 128, 0) == 6  # N = 128, bf16: the chunk-record forward
+    assert fam(1, 2048, 32, 128, 0) == 6  # N = 128, bf16: the chunk-record kernels
     assert fam(1, 2048, 32, 128, 1) == 2
     assert fam(1, 16 * 98689, 1, 128, 0) == 6   # one head's records (43520 B per chunk) < 4 GiB
     assert fam(1, 16 * 98690, 1, 128, 0) == 3
@@ -233,13 +233,11 @@ def test_step_serial_fallback_warns_and_strict_mode_refuses(monkeypatch):
         ext._warn_fallback(1, 32, 2, 64, 1)
     with pytest.warns(RuntimeWarning, match="head size other than 64"):
         ext._warn_fallback(1, 32, 2, 8, 0)
-    with pytest.warns(RuntimeWarning, match="head size of 128"):
-        ext._warn_fallback(1, 32, 2, 128, 0, backward=True)
     import warnings
     with warnings.catch_warnings():
         warnings.simplefilter("error")
         ext._warn_fallback(1, 32, 2, 64, 0)  # chunked: silent
-        ext._warn_fallback(1, 32, 2, 128, 0)  # the record forward: silent
+        ext._warn_fallback(1, 32, 2, 128, 0)  # the chunk-record kernels: silent
         monkeypatch.setenv("THESEUS_WKV7_FAMILY", "seq")
         ext._warn_fallback(1, 32, 2, 64, 0)  # an explicit request: silent
     monkeypatch.delenv("THESEUS_WKV7_FAMILY")

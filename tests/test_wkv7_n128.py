@@ -4,9 +4,11 @@ The reference's operator takes any head size from 2 to 128 (kernels/wkv7_state.c
 theseus/config.py:53-59 exposes head_size up to 128).  Here a bf16 forward with N = 128
 runs on two kernels of gdn_chunk.hip -- every chunk's operands formed at once, then one
 scan per head on the matrix cores -- when the caller's workspace holds the chunk records
-(theseus_wkv7_forward_workspace_size counts them); the backward stays step-serial and
-reads the saved states that forward writes.  Bars as in test_wkv7_gpu.py: rel-L2 <= 5e-3,
-fp32 outputs max-abs <= 2e-2, bf16 outputs |err| <= 2e-2 + 2^-7 |ref| elementwise.
+(theseus_wkv7_forward_workspace_size counts them); the backward runs on the three of
+wkv7_rec_bwd.hip (records, a reverse scan of dL/dS over the chunks, then every chunk's
+gradients at once) from the [value][key] saved states either forward writes.  Bars as in
+test_wkv7_gpu.py: rel-L2 <= 5e-3, fp32 outputs max-abs <= 2e-2, bf16 outputs
+|err| <= 2e-2 + 2^-7 |ref| elementwise.
 """
 import ctypes
 
@@ -14,7 +16,7 @@ import pytest
 import torch
 
 from oracle import wkv7_oracle as O
-from test_wkv7_gpu import _check, _parity, _split_vs_one_pass
+from test_wkv7_gpu import _check, _gpu_fwd_bwd, _oracle, _parity, _split_vs_one_pass
 from theseus import wkv7 as W
 from theseus.synthetic import wkv7_inputs
 
@@ -79,11 +81,51 @@ def test_record_forward_against_oracle(B, T, H, monkeypatch):
     torch.testing.assert_close(sT, s_q, atol=1e-4, rtol=1e-4)
 
 
-@pytest.mark.parametrize("B,T,H", [(1, 18, 1), (2, 100, 2), (1, 257, 3)])
-def test_record_forward_with_step_serial_backward_against_oracle(B, T, H):
-    """Training calls: the forward with saved states on the records, the step-serial
-    backward from those saved states; all nine outputs against the oracle (dsT ~ N(0,1))."""
+@pytest.mark.parametrize("B,T,H", [(1, 1, 1), (1, 15, 2), (2, 16, 1), (1, 18, 1), (2, 100, 2), (1, 257, 3),
+                                   (3, 48, 4)])
+def test_record_backward_against_oracle(B, T, H):
+    """Training calls through autograd: all nine outputs (y, sT, the six input gradients
+    and ds0) against the oracle, dsT ~ N(0,1), tails of every length."""
     _parity(B, T, H, N, torch.bfloat16, seed=5100 + T)
+
+
+def test_record_backward_without_state_gradient():
+    """dsT = 0 (the training case: the final state is not used), B=2, T=200, H=3."""
+    _parity(2, 200, 3, N, torch.bfloat16, seed=5150, with_dsT=False)
+
+
+@pytest.mark.parametrize("fwd_fam", ["auto", "seq"])
+def test_record_backward_reads_either_forwards_saved_states(fwd_fam, monkeypatch):
+    """Both forwards keep [value][key] saved states: the record backward given the
+    step-serial forward's (and the step-serial backward given the record forward's) gives
+    the gradients of the all-record call to fp32 rounding, nothing raises."""
+    B, T, H = 1, 90, 2
+    inp = _inputs(B, T, H, seed=5170)
+    ext = W.extension()
+    xs = [inp[n].cuda() for n in "rwkvab"]
+    s0, dy, dsT = inp["s0"].cuda(), inp["dy"].cuda(), inp["dsT"].cuda()
+    _, _, saved = ext.forward(*xs, s0, True)
+    ref = ext.backward(*xs, saved, dy, dsT)
+    monkeypatch.setenv("THESEUS_WKV7_FAMILY", fwd_fam)
+    _, _, saved2 = ext.forward(*xs, s0, True)
+    monkeypatch.setenv("THESEUS_WKV7_FAMILY", "seq" if fwd_fam == "auto" else "auto")
+    got = ext.backward(*xs, saved2, dy, dsT)
+    torch.cuda.synchronize()
+    for name, x, z in zip(["dr", "dw", "dk", "dv", "da", "db", "ds0"], got, ref):
+        rel = ((x.float() - z.float()).norm() / z.float().norm()).item()
+        print(f"    {name} rel {rel:.2e}", flush=True)
+        assert rel < 5e-3, (name, rel)
+
+
+def test_record_backward_at_the_ends_of_the_decay_range():
+    """w ~ N(0, 8^2) (decays from none to the strongest within a chunk), fwd+bwd against
+    the oracle."""
+    B, T, H = 1, 120, 2
+    inp = _inputs(B, T, H, seed=5180, w_mode="wide")
+    got = _gpu_fwd_bwd(inp, torch.bfloat16, inp["dsT"])
+    ref = _oracle(inp, inp["dsT"])
+    for name, g, r in zip(["y", "sT", "dr", "dw", "dk", "dv", "da", "db", "ds0"], got, ref):
+        _check(name, g, r, torch.bfloat16)
 
 
 def test_saved_states_equal_the_step_serial_forwards(monkeypatch):
@@ -156,18 +198,9 @@ def test_record_forward_at_the_ends_of_the_decay_range(mode, monkeypatch):
 
 
 def test_teacher_geometry_against_oracle():
-    """B=1, T=2048, H=32 (a 4096-wide layer of 128-key heads) with saved states: y and the
-    final state against the oracle; the last saved state is the final state."""
-    B, T, H = 1, 2048, 32
-    inp = _inputs(B, T, H, seed=5500)
-    ext = W.extension()
-    xs = [inp[n].cuda() for n in "rwkvab"]
-    y, end, saved = ext.forward(*xs, inp["s0"].cuda(), True)
-    torch.cuda.synchronize()
-    y_ref, s_ref = _oracle_fwd(inp)
-    _check("y", y, y_ref, torch.bfloat16)
-    _check("sT", end, s_ref, torch.bfloat16)
-    assert torch.equal(saved[:, :, -1], end)
+    """B=1, T=2048, H=32 (a 4096-wide layer of 128-key heads), forward with saved states
+    and backward, all nine outputs against the oracle."""
+    _parity(1, 2048, 32, N, torch.bfloat16, seed=5500)
 
 
 def test_noalloc_forward_stays_step_serial():
