@@ -31,7 +31,9 @@ float32 parameters (gradient scale, clip_grad_norm_, AdamW), fused
 (theseus.optim.FusedAdamW) against the reference's torch sequence; gdn = the teacher's
 gated delta rule (Qwen3.5 GDN geometry: 32 value heads, K = V = 128) through the WKV7
 kernels' exp-decay mode (theseus.gdn), forward and forward+backward, against
-transformers' torch_chunk_gated_delta_rule on the same GPU.
+transformers' torch_chunk_gated_delta_rule on the same GPU; n128 = config 2's training
+step at head size 128 (B=4, T=2048, H=32: a 4096-wide layer), on the chunk-record kernels,
+with one step on the step-serial kernels timed beside it.
 
 Algorithmic bytes (compulsory contract I/O; E = H*N, S_l = H*N*N*4 bytes):
   forward  = B*T*E*2*7  + 2*B*S_l   (r,w,k,v,a,b in, y out; s0 in, sT out)
@@ -61,6 +63,7 @@ CONFIGS = {
     "c4tm": dict(B=64, T=256, H=80, N=64, s0_std=0.0, seed=20264),
     "optim": dict(B=0, T=0, H=80, N=64, s0_std=0.0, seed=20265),
     "gdn": dict(B=1, T=2048, H=32, N=128, s0_std=0.0, seed=20266),
+    "n128": dict(B=4, T=2048, H=32, N=128, s0_std=0.1, seed=20267),
 }
 
 
@@ -488,7 +491,7 @@ def main():
         def one_step():
             for t in range(T):
                 ext.decode_step(*steps_in[t], state)
-    elif args.config == "c2":
+    elif args.config in ("c2", "n128"):
         def one_step():
             y, end, saved = ext.forward(*xs, s0, True)
             ext.backward(*xs, saved, dy, None)
@@ -626,7 +629,16 @@ def main():
     if args.cpu_slice and args.config == "c2":
         cpu = cpu_baseline(B, H, N, args.cpu_slice, cfg["seed"])
 
-    workload = {"c2": "wkv7_fwd_bwd", "c1": "wkv7_fwd_8x512_chained", "c4": "wkv7_decode"}[args.config]
+    serial_ms = None
+    if args.config == "n128":
+        # one step on the step-serial kernels (after an untimed one), for comparison
+        os.environ["THESEUS_WKV7_FAMILY"] = "seq"
+        one_step()
+        serial_ms = timed(1) * 1e3
+        del os.environ["THESEUS_WKV7_FAMILY"]
+
+    workload = {"c2": "wkv7_fwd_bwd", "n128": "wkv7_fwd_bwd_n128", "c1": "wkv7_fwd_8x512_chained",
+                "c4": "wkv7_decode"}[args.config]
     line = {
         "metric": METRIC if args.config == "c2" else f"WKV7 {workload} tokens/s ({args.config})",
         "value": round(value, 1),
@@ -660,6 +672,9 @@ def main():
         # the full 8 TB/s with these bytes (the saved-state traffic the config mandates)
         line["hbm_frac_counted"] = round(counted / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
         line["alg_frac_cap_at_peak"] = round(step_bytes / counted, 4)
+    if serial_ms is not None:
+        line["step_serial_ms_per_step"] = round(serial_ms, 2)
+        line["speedup_vs_step_serial"] = round(serial_ms / ms_per_step, 1)
     if args.config == "c1":
         line["config"].update(calls=NSPLIT, T_per_call=Tc, saved_states=False)
         line["call_ms"] = round(kern["fwd"][0], 4)
