@@ -282,10 +282,11 @@ def bench_optim(args, cfg):
 def bench_gdn(args, cfg):
     """GDN forward (no grad) and forward+backward at B=1, T=2048, H=32, K=V=128, bf16 q/k/v
     with the layers' in-kernel q/k L2 norm, through theseus.gdn: the forward on the chunked
-    MFMA kernels (theseus_gdn_forward: gdn_prep, gdn_scan), forward+backward on the WKV7
-    step-serial kernels in exp-decay mode; beside transformers' torch_chunk_gated_delta_rule
-    (its torch fallback, the function the reference's teacher runs without FLA) and the
-    step-serial forward of the same call."""
+    MFMA kernels (theseus_gdn_forward: gdn_prep, gdn_scan), forward+backward on the chunked
+    kernels too (theseus_gdn_forward_train with saved states, theseus_gdn_backward:
+    gdn_bwd_prep, wkv7_bwd_scan, gdn_bwd_chunk; float32 operands as transformers computes);
+    beside transformers' torch_chunk_gated_delta_rule (its torch fallback, the function the
+    reference's teacher runs without FLA) and the step-serial forward of the same call."""
     import inspect
 
     import torch
@@ -373,10 +374,12 @@ def bench_gdn(args, cfg):
         "warmup": 2, "ms_per_step": round(ms["ours_fwd"], 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16 I/O, fp32 compute", "data": "synthetic",
         "config": {"workload": "gdn_forward", "B": B, "T": T, "H": H, "K": N, "V": N,
-                   "kernels": "forward: chunked MFMA GDN (gdn_prep + gdn_scan); fwd+bwd: step-serial WKV7, "
-                              "exp decay, key-value states"},
+                   "kernels": "forward: chunked MFMA GDN (gdn_prep + gdn_scan); fwd+bwd: the same with saved "
+                              "states, then gdn_bwd_prep + wkv7_bwd_scan + gdn_bwd_chunk (float32 operands)"},
         "ms_by_impl": {k2: round(v2, 4) for k2, v2 in ms.items()},
         "speedup_vs_transformers_torch_chunk": round(ms["transformers_torch_chunk_fwd"] / ms["ours_fwd"], 2),
+        "speedup_fwd_bwd_vs_transformers_torch_chunk": round(ms["transformers_torch_chunk_fwd_bwd"] /
+                                                             ms["ours_fwd_bwd"], 2),
         "roofline": {"kernel": "forward", "bound": "latency (chunk-to-chunk chain)", "achieved": round(gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                      "traffic": None, "alg_bytes_per_launch": fwd_bytes}}), flush=True)

@@ -9,8 +9,9 @@
  *   S_t = e^{g_t} S_{t-1} + beta_t k_t (v_t - e^{g_t} S_{t-1}^T k_t)^T,
  *   o_t = S_t^T q_t / sqrt(N)                  (S: [key][value], N = K = V)
  *
- * q is scaled by 1/sqrt(N) inside.  Forward only, no saved states: the reference's
- * teacher runs these layers without gradients.
+ * q is scaled by 1/sqrt(N) inside.  theseus_gdn_forward is the forward without
+ * gradients (how the reference's teacher runs these layers); theseus_gdn_forward_train
+ * and theseus_gdn_backward are the pair for calls that need them.
  * Status codes are those of theseus_wkv7.h.
  */
 #ifndef THESEUS_GDN_H
@@ -45,6 +46,33 @@ int theseus_gdn_forward(int B, int T, int H, int N, int dtype, int qk_l2norm, co
                         size_t workspace_bytes, hipStream_t stream);
 /* Workspace bytes of theseus_gdn_forward (0 for invalid sizes). */
 size_t theseus_gdn_forward_workspace_size(int B, int T, int H, int N);
+
+/* The forward of a call that needs gradients: as theseus_gdn_forward with q and k used as
+ * given (a layer that normalises them does so before, differentiably), and also the saved
+ * states ckpt [B,H,ceil(T/16)+1,N,N] float32 (the state after steps 0, 16, 32, ... and the
+ * final one, in the library's own [value][key] order) for theseus_gdn_backward; the scan
+ * runs in one pass (no time split).  Replaces the forward of transformers'
+ * torch_chunk_gated_delta_rule under autograd (theseus/hf_model.py:37-48 keeps it for
+ * such calls). */
+int theseus_gdn_forward_train(int B, int T, int H, int N, int dtype, const void* q, const void* k,
+                              const void* v, const float* g, const float* beta, const float* s0,
+                              void* o, float* sT, float* ckpt, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
+/* Backward of theseus_gdn_forward_train, N = 128 (else THESEUS_WKV7_ERR_SHAPE), on the
+ * caller's stream: q, k, v, g, beta and ckpt as that forward had them, dout [B,T,H,N] in
+ * dtype, dsT [B,H,key,value] float32 (may be NULL: zero); writes dq, dk, dv [B,T,H,N] in
+ * dtype, dg, dbeta [B,T,H] float32 and ds0 [B,H,key,value] float32.  Workspace of
+ * theseus_gdn_backward_workspace_size bytes (24.5 KB of scan records and a 64 KB float32
+ * dL/dS per 16-step chunk and head), not shared with a call that can run at the same
+ * time.  Replaces the backward of transformers' torch_chunk_gated_delta_rule. */
+int theseus_gdn_backward(int B, int T, int H, int N, int dtype, const void* q, const void* k,
+                         const void* v, const float* g, const float* beta, const float* ckpt,
+                         const void* dout, const float* dsT, void* dq, void* dk, void* dv,
+                         float* dg, float* dbeta, float* ds0, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+/* Workspace bytes of theseus_gdn_backward (0 for invalid sizes or N != 128). */
+size_t theseus_gdn_backward_workspace_size(int B, int T, int H, int N);
 
 #ifdef __cplusplus
 }

@@ -805,7 +805,7 @@ static void launch_gdn(const Gdn& p) {
     hipLaunchKernelGGL((gdn_prep<NK, TI>), dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, p.qk_norm,
                        static_cast<const TI*>(p.q), static_cast<const TI*>(p.k), static_cast<const TI*>(p.v), p.g,
                        p.beta, static_cast<uint8_t*>(p.ws));
-    scan_records<NK, TI, false>(p.B, p.T, p.H, p.kv, p.s0, static_cast<TI*>(p.o), p.sT, nullptr, p.ws, p.ws_bytes,
+    scan_records<NK, TI, false>(p.B, p.T, p.H, p.kv, p.s0, static_cast<TI*>(p.o), p.sT, p.ckpt, p.ws, p.ws_bytes,
                                 p.cus, p.stream);
 }
 void launch_gdn_forward(const Gdn& p) {

@@ -283,4 +283,37 @@ int theseus_gdn_forward(int B, int T, int H, int N, int dtype, int qk_l2norm, co
     return launch_status();
 }
 
+int theseus_gdn_forward_train(int B, int T, int H, int N, int dtype, const void* q, const void* k, const void* v,
+                              const float* g, const float* beta, const float* s0, void* o, float* sT, float* ckpt,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (int e = gdn_dims(B, T, H, N)) return e;
+    if (dtype != THESEUS_WKV7_BF16 && dtype != THESEUS_WKV7_FP32) return THESEUS_WKV7_ERR_DTYPE;
+    if (!q || !k || !v || !g || !beta || !s0 || !o || !sT || !ckpt) return THESEUS_WKV7_ERR_NULL;
+    if (!workspace || workspace_bytes < wkv7::gdn_forward_workspace(B, T, H, N)) return THESEUS_WKV7_ERR_WORKSPACE;
+    wkv7::Gdn p{B, T, H, N, dtype, 0, q, k, v, g, beta, s0, o, sT, workspace, 1, stream};
+    p.ws_bytes = workspace_bytes;
+    p.ckpt = ckpt;
+    wkv7::launch_gdn_forward(p);
+    return launch_status();
+}
+
+size_t theseus_gdn_backward_workspace_size(int B, int T, int H, int N) {
+    return gdn_dims(B, T, H, N) || N != 128 ? 0 : wkv7::gdn_backward_workspace(B, T, H);
+}
+
+int theseus_gdn_backward(int B, int T, int H, int N, int dtype, const void* q, const void* k, const void* v,
+                         const float* g, const float* beta, const float* ckpt, const void* dout, const float* dsT,
+                         void* dq, void* dk, void* dv, float* dg, float* dbeta, float* ds0, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
+    if (int e = gdn_dims(B, T, H, N)) return e;
+    if (N != 128) return THESEUS_WKV7_ERR_SHAPE;
+    if (dtype != THESEUS_WKV7_BF16 && dtype != THESEUS_WKV7_FP32) return THESEUS_WKV7_ERR_DTYPE;
+    if (!q || !k || !v || !g || !beta || !ckpt || !dout || !dq || !dk || !dv || !dg || !dbeta || !ds0)
+        return THESEUS_WKV7_ERR_NULL;
+    if (!workspace || workspace_bytes < wkv7::gdn_backward_workspace(B, T, H)) return THESEUS_WKV7_ERR_WORKSPACE;
+    wkv7::GdnBwd p{B, T, H, N, dtype, q, k, v, g, beta, ckpt, dout, dsT, dq, dk, dv, dg, dbeta, ds0, workspace, stream};
+    wkv7::launch_gdn_backward(p);
+    return launch_status();
+}
+
 }  // extern "C"

@@ -87,7 +87,26 @@ struct Gdn {
     hipStream_t stream;
     size_t ws_bytes = 0;  // bytes at ws: the time-split scan runs when they cover its buffers
     int cus = 0;          // CUs the time split may spread the segments over (0: no split)
+    float* ckpt = nullptr;  // saved states for gdn backward ([value][key], every 16 steps + final); no split
 };
+// Its backward for N = 128 (wkv7_rec_bwd.hip): q, k as the forward used them (normalised
+// by the caller), dout [B,T,H,N] and the gradients of q, k, v in dtype; g, beta and their
+// gradients [B,T,H] float32; dsT (may be null) and ds0 [B,H,key,value]; the forward's
+// saved states; a workspace of gdn_backward_workspace bytes.
+struct GdnBwd {
+    int B, T, H, N, dtype;
+    const void *q, *k, *v;
+    const float *g, *beta;
+    const float* ckpt;
+    const void* dout;
+    const float* dsT;
+    void *dq, *dk, *dv;
+    float *dg, *dbeta, *ds0;
+    void* ws;
+    hipStream_t stream;
+};
+size_t gdn_backward_workspace(int B, int T, int H);
+void launch_gdn_backward(const GdnBwd& p);
 // the operand records (the least a call needs); with the time split's buffers when it
 // applies (gdn_split_segments >= 2)
 size_t gdn_forward_workspace(int B, int T, int H, int N);

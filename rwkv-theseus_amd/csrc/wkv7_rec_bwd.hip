@@ -149,10 +149,13 @@ __global__ __launch_bounds__(64) void wkv7_bwd_prep(int Tn, int H, const bf16_t*
 // Each head's chunks backwards: workgroup rg * BH + bh, four waves, wave wv of group rg
 // keeps value rows i_own = 16 (4 rg + wv) + r16 of H as Ht[tj][e] = H[i_own][16tj + 4q4 + e].
 // Per chunk: H is stored (the chunk kernel's H_end), U^T = B^ H^T over the keys, then
-// H^T <- e^{gL} o H^T + [P^T | P2^T] [U^T; dY] on the K=32 instruction.
+// H^T <- e^{gL} o H^T + [P^T | P2^T] [U^T; dY] on the K=32 instruction.  dY of dtype TI;
+// dsT (may be null) and ds0 [key][value] when kv (GDN's layout), else [value][key]; H in
+// the workspace always [value][key].
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, const float* __restrict__ dsT,
-                                                     const bf16_t* __restrict__ dy, float* __restrict__ ds0,
+template <typename TI>
+__global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, int kv, const float* __restrict__ dsT,
+                                                     const TI* __restrict__ dy, float* __restrict__ ds0,
                                                      float* __restrict__ hbuf, const uint8_t* __restrict__ ws) {
     using R = BwdRec;
     __shared__ __attribute__((aligned(1024))) uint8_t recs[2][R::DMA_BLOCKS * 1024];
@@ -174,16 +177,22 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, cons
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int t = 4 * q4 + e;
-            o[e] = t < L ? bf2f(dy, (((long)bb * Tn + t0 + t) * H + h) * BNK + i_own) : 0.f;
+            o[e] = t < L ? io<TI>::ld(dy, (((long)bb * Tn + t0 + t) * H + h) * BNK + i_own) : 0.f;
         }
     };
     fetch(nchunk - 1, 0);
     f32x4_t Ht[BTJ];
 #pragma unroll
     for (int tj = 0; tj < BTJ; tj++) {
-        const float4 x = dsT ? *reinterpret_cast<const float4*>(dsT + bh * BNN + (long)i_own * BNK + 16 * tj + 4 * q4)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-        Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
+        if (!dsT) {
+            Ht[tj] = zero4();
+        } else if (kv) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) Ht[tj][e] = dsT[bh * BNN + (long)(16 * tj + 4 * q4 + e) * BNK + i_own];
+        } else {
+            const float4 x = *reinterpret_cast<const float4*>(dsT + bh * BNN + (long)i_own * BNK + 16 * tj + 4 * q4);
+            Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
+        }
     }
     float dyn[4];
     load_dy(nchunk - 1, dyn);
@@ -211,7 +220,7 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, cons
         }
         uint2 uh, ul, dh, dl;
         pack4(u, uh, ul);
-        pack4(dyc, dh, dl);  // (exact in bf16: dl = 0)
+        pack4(dyc, dh, dl);  // (bf16 dY: dl = 0)
         const uint4 bhi = cat(uh, dh), blo = cat(ul, dl);
 #pragma unroll
         for (int tj = 0; tj < BTJ; tj++) {
@@ -224,9 +233,15 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, cons
         __syncthreads();
     }
 #pragma unroll
-    for (int tj = 0; tj < BTJ; tj++)
-        *reinterpret_cast<float4*>(ds0 + bh * BNN + (long)i_own * BNK + 16 * tj + 4 * q4) =
-            make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+    for (int tj = 0; tj < BTJ; tj++) {
+        if (kv) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) ds0[bh * BNN + (long)(16 * tj + 4 * q4 + e) * BNK + i_own] = Ht[tj][e];
+        } else {
+            *reinterpret_cast<float4*>(ds0 + bh * BNN + (long)i_own * BNK + 16 * tj + 4 * q4) =
+                make_float4(Ht[tj][0], Ht[tj][1], Ht[tj][2], Ht[tj][3]);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -492,6 +507,367 @@ __global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// The gated delta rule's backward (GDN layers: one decay e^{g_t} per token and head,
+// r = q/sqrt(N), a = k, b = -e^{g} beta k, v' = beta v; q and k as the forward used them).
+// With gamma the chunk's inclusive cumulative g, the per-key factors above become 16x16
+// decay-ratio masks, every one of them e^{(a later gamma) - (an earlier one)} <= 1, so
+// nothing overflows for any decay (as gdn_prep in the forward):
+//   Aab[t][s] = -beta_s (k_t.k_s) e^{gm1_t - gm1_s} (s < t)   Aak = (k_t.k_s) e^{gm1_t - gam_s}
+//   Brb[t][s] = -beta_s (r_t.k_s) e^{gam_t - gm1_s} (s <= t)  Brk = (r_t.k_s) e^{gam_t - gam_s}
+//   A~ S0^T = e^{gm1_t} (k S0^T),  B^ H^T = -beta_t e^{gL - gm1_t} (k H^T),  K^ H^T = e^{gL - gam_t} (k H^T)
+//   dK = e^{gL - gam_t} V'H + M1 k + M2 r,   dB = e^{gL - gam_t} SA H + M3 k + M4 r
+//   dR = e^{gam_t} dY S0 + (M5 + M6) k,      dA = e^{gm1_t} Q S0 + (M7 + M8) k
+// with M1 = triu_s(V'Q^T) e^{gm1_s - gam_t}, M2 = triu(V'dY^T) e^{gam_s - gam_t}, M3, M4 the
+// same for SA, M5 = tril(dY SA^T) (-beta_s) e^{gam_t - gm1_s}, M6 = tril(dY V'^T)
+// e^{gam_t - gam_s}, M7 = tril_s(Q SA^T) (-beta_s) e^{gm1_t - gm1_s}, M8 = tril_s(Q V'^T)
+// e^{gm1_t - gam_s}; then dq = dR/sqrt(N), dk = dK + dA - e^{g} beta dB, dv = beta dV',
+// dbeta = sum_i v dV' - e^{g} sum_j k dB, dg = sum_j dlogd - e^{g} beta sum_j k dB.
+// (Checked in float64 against the oracle's exp-mode step adjoint, strong decays included,
+// before the kernels.)  The reverse scan's records are the WKV7 ones (e^{gL} repeated
+// per key), so wkv7_bwd_scan runs them unchanged.
+// ---------------------------------------------------------------------------
+template <typename TI>
+__global__ __launch_bounds__(64) void gdn_bwd_prep(int Tn, int H, const TI* __restrict__ q, const TI* __restrict__ k,
+                                                   const float* __restrict__ g, const float* __restrict__ beta,
+                                                   uint8_t* __restrict__ ws) {
+    using R = BwdRec;
+    const int c = blockIdx.x, bh = blockIdx.y, nchunk = gridDim.x;
+    const int bb = bh / H, h = bh - bb * H;
+    const int lane = threadIdx.x, q4 = lane >> 4, r16 = lane & 15;
+    const int t0 = c * BC, L = min(BC, Tn - t0);
+    const long tok0 = (long)bb * Tn + t0;
+    auto row = [&](int t) { return ((tok0 + t) * H + h) * (long)BNK; };
+    const float rs = 1.f / __builtin_sqrtf((float)BNK);
+    __shared__ float gsh[3][BC];  // gamma_t, gamma_{t-1}, beta_t (past the end: 0)
+    const bool tv = r16 < L;
+    const float gt = tv ? g[(tok0 + r16) * H + h] : 0.f;
+    const float bt = tv ? beta[(tok0 + r16) * H + h] : 0.f;
+    const float gam = row_prefix_sum(gt), gm1 = row_prev(gam, 0.f), gL = row_last(gam);
+    if (q4 == 0) gsh[0][r16] = gam, gsh[1][r16] = gm1, gsh[2][r16] = bt;
+    uint8_t* const rec = ws + ((size_t)bh * nchunk + c) * R::BYTES;
+    const float sb = -bt * __expf(gL - gm1);  // B^ = sb k for the lane's token
+    f32x4_t KK = zero4(), KR = zero4();
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) {
+        const int c0 = 32 * ks + 4 * q4;
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 ka = tv ? ld4f(k + row(r16) + c0) : z, kb = tv ? ld4f(k + row(r16) + c0 + 16) : z;
+        const float4 qa = tv ? ld4f(q + row(r16) + c0) : z, qb = tv ? ld4f(q + row(r16) + c0 + 16) : z;
+        const float kr[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+        const float qr[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        float br8[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) br8[e] = kr[e] * sb;
+        uint4 kh, kl, qh, ql, bh_, bl;
+        pack8(kr, kh, kl), pack8(qr, qh, ql), pack8(br8, bh_, bl);
+        uint4* bf = reinterpret_cast<uint4*>(rec + R::BF) + (size_t)(2 * ks) * 64 + lane;
+        bf[0] = bh_;
+        bf[64] = bl;
+        KK = mm3(KK, kh, kl, kh, kl);  // k_rr . k_cc
+        KR = mm3(KR, kh, kl, qh, ql);  // k_rr . q_cc
+    }
+    __syncthreads();  // gsh
+    const int cc = r16;
+    f32x4_t Aab, AabT, BrbT;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = 4 * q4 + e;
+        const float gm1r = gsh[1][rr], br = gsh[2][rr];
+        const float kk = KK[e], kq = KR[e] * rs;  // k_rr.k_cc, k_rr.r_cc
+        Aab[e] = cc < rr ? -bt * kk * __expf(gm1r - gm1) : 0.f;    // Aab[rr][cc]
+        AabT[e] = rr < cc ? -br * kk * __expf(gm1 - gm1r) : 0.f;   // Aab[cc][rr]
+        BrbT[e] = rr <= cc ? -br * kq * __expf(gam - gm1r) : 0.f;  // Brb[cc][rr]
+    }
+    f32x4_t Ti, TiT;
+    tri_inverse(Aab, AabT, lane, Ti, TiT);
+    const Pk pTiT = pk(TiT), pBrbT = pk(BrbT);
+    float ea[4], er[4];
+    const TI *krow[4], *qrow[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = 4 * q4 + e;
+        krow[e] = k + row(t < L ? t : 0) + r16;
+        qrow[e] = q + row(t < L ? t : 0) + r16;
+        ea[e] = t < L ? __expf(gsh[1][t]) : 0.f;
+        er[e] = t < L ? rs * __expf(gsh[0][t]) : 0.f;
+    }
+#pragma unroll
+    for (int tj = 0; tj < BTJ; tj++) {
+        f32x4_t at, rt;  // A~, R~ in D layout [t][j], j = 16tj + r16
+#pragma unroll
+        for (int e = 0; e < 4; e++) at[e] = io<TI>::ld(krow[e], 16 * tj) * ea[e], rt[e] = io<TI>::ld(qrow[e], 16 * tj) * er[e];
+        const f32x4_t Pt = mm16s(pTiT, pk(at));
+        const Pk pP = pk(Pt);
+        const Pk pP2 = pk(rt + mm16s(pBrbT, pP));
+        uint4* pp = reinterpret_cast<uint4*>(rec + R::PP) + (size_t)(2 * tj) * 64 + lane;
+        pp[0] = cat(pP.h, pP2.h);
+        pp[64] = cat(pP.l, pP2.l);
+    }
+    if (lane < BNK / 4) {
+        const float egL = __expf(gL);
+        reinterpret_cast<float4*>(rec + R::EL)[lane] = make_float4(egL, egL, egL, egL);
+    }
+}
+
+struct GdnChunkLds {
+    float K[BC][CLP], R[BC][CLP];  // k, r = q / sqrt(N) [t][j], written by the key owners
+    float SA[BC][CLP], Q[BC][CLP];  // [t][i], written by the value-row owners
+    float gam[BC], gm1[BC], beta[BC];
+    float csum[BTJ][BNK];
+    float pv[BTJ][BC], pd[BTJ][BC], pk[BTJ][BC];  // per wave and token: sum v dV', sum dlogd, sum k dB
+};
+
+template <typename TI>
+__global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int per_xcd, const TI* __restrict__ q,
+                                                     const TI* __restrict__ k, const TI* __restrict__ v,
+                                                     const float* __restrict__ g, const float* __restrict__ beta,
+                                                     const TI* __restrict__ dy, const float* __restrict__ ckpt,
+                                                     const float* __restrict__ hbuf, TI* __restrict__ dq,
+                                                     TI* __restrict__ dk, TI* __restrict__ dv, float* __restrict__ dg,
+                                                     float* __restrict__ dbeta) {
+    __shared__ __attribute__((aligned(16))) GdnChunkLds sm;
+    const int nchunk = (Tn + BC - 1) / BC;
+    const int job = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (job >= nchunk * BH) return;  // (whole workgroup)
+    const int bh = job / nchunk, c = job - bh * nchunk, bb = bh / H, h = bh - bb * H;
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, q4 = lane >> 4, r16 = lane & 15;
+    const int t0 = c * BC, L = min(BC, Tn - t0);
+    const long tok0 = (long)bb * Tn + t0;
+    const int col = 16 * wv + r16;
+    const float rs = 1.f / __builtin_sqrtf((float)BNK);
+    auto at_tok = [&](int t) { return ((tok0 + t) * H + h) * (long)BNK; };
+    const long ncp = nchunk + 1;
+    const float* const S0 = ckpt + ((long)bh * ncp + c) * BNN;
+    const float* const Se = S0 + BNN;
+    const float* const Hm = hbuf + ((long)bh * nchunk + c) * BNN;
+    const int irow = 16 * wv + r16;
+    // the token scalars (wave 0)
+    if (wv == 0) {
+        const bool tv = r16 < L;
+        const float gt = tv ? g[(tok0 + r16) * H + h] : 0.f, bt = tv ? beta[(tok0 + r16) * H + h] : 0.f;
+        const float gam = row_prefix_sum(gt), gm1 = row_prev(gam, 0.f);
+        if (q4 == 0) sm.gam[r16] = gam, sm.gm1[r16] = gm1, sm.beta[r16] = bt;
+    }
+    float hr[BKS][8], sr[BKS][8];
+    auto rows = [&](const float* M, float (&o)[BKS][8]) {
+#pragma unroll
+        for (int ks = 0; ks < BKS; ks++) {
+            const float4 x = *reinterpret_cast<const float4*>(M + (long)irow * BNK + 32 * ks + 4 * q4);
+            const float4 y = *reinterpret_cast<const float4*>(M + (long)irow * BNK + 32 * ks + 16 + 4 * q4);
+            o[ks][0] = x.x, o[ks][1] = x.y, o[ks][2] = x.z, o[ks][3] = x.w;
+            o[ks][4] = y.x, o[ks][5] = y.y, o[ks][6] = y.z, o[ks][7] = y.w;
+        }
+    };
+    rows(Hm, hr);
+    rows(Se, sr);
+    // k and r of the wave's keys in D layout ([t][col], t = 4q4 + e)
+    f32x4_t kD, rD;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = 4 * q4 + e;
+        const bool ok = t < L;
+        kD[e] = ok ? io<TI>::ld(k, at_tok(t) + col) : 0.f;
+        rD[e] = ok ? io<TI>::ld(q, at_tok(t) + col) * rs : 0.f;
+        sm.K[t][col] = kD[e], sm.R[t][col] = rD[e];
+    }
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float s = row_sum16(hr[ks][e] * sr[ks][e]);
+            if (r16 == 0) sm.csum[wv][32 * ks + (e < 4 ? 4 * q4 + e : 16 + 4 * q4 + e - 4)] = s;
+        }
+    uint4 Hh[BKS], Hl[BKS], Sh[BKS], Sl[BKS];
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) pack8(hr[ks], Hh[ks], Hl[ks]);
+    rows(S0, sr);
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) pack8(sr[ks], Sh[ks], Sl[ks]);
+    __syncthreads();
+
+    // token scalars: rows rr = 4q4 + e, column token cc = r16
+    const int cc = r16;
+    float gr[4], gm1r[4], br[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) gr[e] = sm.gam[4 * q4 + e], gm1r[e] = sm.gm1[4 * q4 + e], br[e] = sm.beta[4 * q4 + e];
+    const float gc = sm.gam[cc], gm1c = sm.gm1[cc], bc = sm.beta[cc], gL = sm.gam[BC - 1];
+    // Gram matrices over the keys and the wave's products k S0^T, k H^T
+    f32x4_t KK = zero4(), RK = zero4(), kS = zero4(), kH = zero4();
+    auto trow = [&](float (*pl)[CLP], int ks, float (&o)[8]) {
+        const float4 x = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 4 * q4]);
+        const float4 y = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 16 + 4 * q4]);
+        o[0] = x.x, o[1] = x.y, o[2] = x.z, o[3] = x.w, o[4] = y.x, o[5] = y.y, o[6] = y.z, o[7] = y.w;
+    };
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) {
+        float fk[8], fr[8];
+        trow(sm.K, ks, fk), trow(sm.R, ks, fr);
+        uint4 kh, kl, rh, rl;
+        pack8(fk, kh, kl), pack8(fr, rh, rl);
+        KK = mm3(KK, kh, kl, kh, kl);
+        RK = mm3(RK, rh, rl, kh, kl);  // r_rr . k_cc
+        kS = mm3(kS, kh, kl, Sh[ks], Sl[ks]);
+        kH = mm3(kH, kh, kl, Hh[ks], Hl[ks]);
+    }
+    f32x4_t Aab, AabT, Aak, Brb, Brk, P1, P2, P3;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = 4 * q4 + e;
+        Aab[e] = cc < rr ? -bc * KK[e] * __expf(gm1r[e] - gm1c) : 0.f;
+        AabT[e] = rr < cc ? -br[e] * KK[e] * __expf(gm1c - gm1r[e]) : 0.f;
+        Aak[e] = cc < rr ? KK[e] * __expf(gm1r[e] - gc) : 0.f;
+        Brb[e] = cc <= rr ? -bc * RK[e] * __expf(gr[e] - gm1c) : 0.f;
+        Brk[e] = cc <= rr ? RK[e] * __expf(gr[e] - gc) : 0.f;
+        P1[e] = kS[e] * __expf(gm1r[e]);
+        P2[e] = kH[e] * (-br[e] * __expf(gL - gm1r[e]));
+        P3[e] = kH[e] * __expf(gL - gr[e]);
+    }
+    f32x4_t Ti, TiT;
+    tri_inverse(Aab, AabT, lane, Ti, TiT);
+    const Pk pAak = pk(Aak), pBrb = pk(Brb), pBrk = pk(Brk), pTi = pk(Ti), pTiT = pk(TiT);
+    const Pk pAakT = pk(transpose16(Aak, lane));
+
+    auto put = [&](TI* dst, const f32x4_t& x) {
+        if constexpr (sizeof(TI) == 2) {
+            const int tr = 4 * q4 + (lane & 3);
+            const uint2 qv = quad_rows_bf16(x, lane);  // (cross-lane: every lane takes part)
+            if (tr < L) *reinterpret_cast<uint2*>(dst + at_tok(tr) + 16 * wv + 4 * ((lane >> 2) & 3)) = qv;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (4 * q4 + e < L) dst[at_tok(4 * q4 + e) + col] = x[e];
+        }
+    };
+    // ---- SA, Q, dV' for the wave's value columns ----
+    f32x4_t vraw, vD, dyD;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int t = 4 * q4 + e;
+        vraw[e] = t < L ? io<TI>::ld(v, at_tok(t) + col) : 0.f;
+        vD[e] = br[e] * vraw[e];
+        dyD[e] = t < L ? io<TI>::ld(dy, at_tok(t) + col) : 0.f;
+    }
+    const Pk pV = pk(vD), pdY = pk(dyD);
+    const f32x4_t SA = mm16s(pTiT, pk(P1 + mm16s(pAakT, pV)));
+    const f32x4_t Q = mm16s(pTi, pk(P2 + mm16s(pBrb, pdY)));
+    const f32x4_t dVp = P3 + mm16s(pAak, pk(Q)) + mm16s(pBrk, pdY);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        sm.SA[4 * q4 + e][col] = SA[e], sm.Q[4 * q4 + e][col] = Q[e];
+        const float s = row_sum16(vraw[e] * dVp[e]);
+        if (r16 == 0) sm.pv[wv][4 * q4 + e] = s;
+    }
+    put(dv, f32x4_t{br[0] * dVp[0], br[1] * dVp[1], br[2] * dVp[2], br[3] * dVp[3]});
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int i = 32 * ks + (e < 4 ? 4 * q4 + e : 16 + 4 * q4 + e - 4);
+            hr[ks][e] = Hm[(long)i * BNK + col];
+            sr[ks][e] = S0[(long)i * BNK + col];
+        }
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) pack8(hr[ks], Hh[ks], Hl[ks]), pack8(sr[ks], Sh[ks], Sl[ks]);
+    __syncthreads();  // SA, Q, csum, pv
+
+    // ---- dq, dk and the token sums for the wave's keys ----
+    f32x4_t VH = zero4(), SAH = zero4(), dYS = zero4(), QS = zero4();
+    f32x4_t Gqv = zero4(), Gyv = zero4(), Gqs = zero4(), Gys = zero4();
+    const bool tv = r16 < L;
+#pragma unroll
+    for (int ks = 0; ks < BKS; ks++) {
+        float fs[8], fq[8], fv[8], fy[8];
+        trow(sm.SA, ks, fs), trow(sm.Q, ks, fq);
+        {
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const long o = at_tok(tv ? r16 : 0) + 32 * ks + 4 * q4;
+            const float4 v0 = tv ? ld4f(v + o) : z, v1 = tv ? ld4f(v + o + 16) : z;
+            const float4 y0 = tv ? ld4f(dy + o) : z, y1 = tv ? ld4f(dy + o + 16) : z;
+            fv[0] = v0.x, fv[1] = v0.y, fv[2] = v0.z, fv[3] = v0.w, fv[4] = v1.x, fv[5] = v1.y, fv[6] = v1.z, fv[7] = v1.w;
+            fy[0] = y0.x, fy[1] = y0.y, fy[2] = y0.z, fy[3] = y0.w, fy[4] = y1.x, fy[5] = y1.y, fy[6] = y1.z, fy[7] = y1.w;
+#pragma unroll
+            for (int e = 0; e < 8; e++) fv[e] *= bc;  // V' = beta v (the lane's token r16)
+        }
+        uint4 sh, sl, qh, ql, vh, vl, yh, yl;
+        pack8(fs, sh, sl), pack8(fq, qh, ql), pack8(fv, vh, vl), pack8(fy, yh, yl);
+        VH = mm3(VH, vh, vl, Hh[ks], Hl[ks]);
+        SAH = mm3(SAH, sh, sl, Hh[ks], Hl[ks]);
+        dYS = mm3(dYS, yh, yl, Sh[ks], Sl[ks]);
+        QS = mm3(QS, qh, ql, Sh[ks], Sl[ks]);
+        Gqv = mm3(Gqv, qh, ql, vh, vl);  // Q_rr . V'_cc
+        Gyv = mm3(Gyv, yh, yl, vh, vl);  // dY_rr . V'_cc
+        Gqs = mm3(Gqs, qh, ql, sh, sl);  // Q_rr . SA_cc
+        Gys = mm3(Gys, yh, yl, sh, sl);  // dY_rr . SA_cc
+    }
+    const f32x4_t Gvq = transpose16(Gqv, lane), Gvy = transpose16(Gyv, lane);
+    const f32x4_t Gsq = transpose16(Gqs, lane), Gsy = transpose16(Gys, lane);
+    f32x4_t M1, M2, M3, M4, M56, M78;  // transposes, element [rr][cc]
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = 4 * q4 + e;
+        M1[e] = rr > cc ? Gqv[e] * __expf(gm1r[e] - gc) : 0.f;
+        M2[e] = rr >= cc ? Gyv[e] * __expf(gr[e] - gc) : 0.f;
+        M3[e] = rr > cc ? Gqs[e] * __expf(gm1r[e] - gc) : 0.f;
+        M4[e] = rr >= cc ? Gys[e] * __expf(gr[e] - gc) : 0.f;
+        M56[e] = rr <= cc ? -br[e] * Gsy[e] * __expf(gc - gm1r[e]) + Gvy[e] * __expf(gc - gr[e]) : 0.f;
+        M78[e] = rr < cc ? -br[e] * Gsq[e] * __expf(gm1c - gm1r[e]) + Gvq[e] * __expf(gm1c - gr[e]) : 0.f;
+    }
+    const Pk pkD = pk(kD), prD = pk(rD);
+    const f32x4_t tK = mm16s(pk(M1), pkD) + mm16s(pk(M2), prD);
+    const f32x4_t tB = mm16s(pk(M3), pkD) + mm16s(pk(M4), prD);
+    const f32x4_t tR = mm16s(pk(M56), pkD), tA = mm16s(pk(M78), pkD);
+    f32x4_t gK, gB, gR, gA, egb;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float fL = __expf(gL - gr[e]);
+        gK[e] = fL * VH[e] + tK[e];
+        gB[e] = fL * SAH[e] + tB[e];
+        gR[e] = __expf(gr[e]) * dYS[e] + tR[e];
+        gA[e] = __expf(gm1r[e]) * QS[e] + tA[e];
+        egb[e] = __expf(gr[e] - gm1r[e]) * br[e];  // e^{g_t} beta_t
+    }
+    float sx[4], sy[4];
+    {
+        float x[4], y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            x[e] = rD[e] * gR[e] + egb[e] * kD[e] * gB[e] - kD[e] * gK[e], y[e] = kD[e] * gA[e];
+        sx[3] = x[3], sy[3] = 0.f;
+#pragma unroll
+        for (int e = 2; e >= 0; e--) sx[e] = sx[e + 1] + x[e], sy[e] = sy[e + 1] + y[e + 1];
+        const float ytot = sy[0] + y[0];
+        const float X1 = __shfl(sx[0], 16 + r16), X2 = __shfl(sx[0], 32 + r16), X3 = __shfl(sx[0], 48 + r16);
+        const float Y1 = __shfl(ytot, 16 + r16), Y2 = __shfl(ytot, 32 + r16), Y3 = __shfl(ytot, 48 + r16);
+        const float xa_ = (q4 < 1 ? X1 : 0.f) + (q4 < 2 ? X2 : 0.f) + (q4 < 3 ? X3 : 0.f);
+        const float ya_ = (q4 < 1 ? Y1 : 0.f) + (q4 < 2 ? Y2 : 0.f) + (q4 < 3 ? Y3 : 0.f);
+        float carry = 0.f;
+#pragma unroll
+        for (int u = 0; u < BTJ; u++) carry += sm.csum[u][col];
+#pragma unroll
+        for (int e = 0; e < 4; e++) sx[e] += xa_ + carry, sy[e] += ya_;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float sd = row_sum16(sx[e] + sy[e]), skb = row_sum16(kD[e] * gB[e]);
+        if (r16 == 0) sm.pd[wv][4 * q4 + e] = sd, sm.pk[wv][4 * q4 + e] = skb;
+    }
+    put(dq, gR * rs);
+    put(dk, gK + gA - egb * gB);
+    __syncthreads();  // pd, pk
+    if (wv == 0 && lane < L) {
+        float spv = 0.f, spd = 0.f, spk = 0.f;
+#pragma unroll
+        for (int u = 0; u < BTJ; u++) spv += sm.pv[u][lane], spd += sm.pd[u][lane], spk += sm.pk[u][lane];
+        const float eg = __expf(sm.gam[lane] - sm.gm1[lane]);
+        const long o = (tok0 + lane) * H + h;
+        dg[o] = spd - eg * sm.beta[lane] * spk;
+        dbeta[o] = spv - eg * spk;
+    }
+}
+
 }  // namespace
 
 size_t wkv7_rec_bwd_workspace(int B, int T, int H) {
@@ -508,13 +884,35 @@ void launch_wkv7_rec_backward(const Bwd& p) {
                  *a = static_cast<const bf16_t*>(p.a), *b = static_cast<const bf16_t*>(p.b),
                  *dy = static_cast<const bf16_t*>(p.dy);
     hipLaunchKernelGGL(wkv7_bwd_prep, dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, r, w, k, a, b, recs);
-    hipLaunchKernelGGL(wkv7_bwd_scan, dim3(BH * (BNK / 64)), dim3(256), 0, p.stream, p.T, p.H, BH, p.dsT, dy, p.ds0,
-                       hbuf, recs);
+    hipLaunchKernelGGL(wkv7_bwd_scan<bf16_t>, dim3(BH * (BNK / 64)), dim3(256), 0, p.stream, p.T, p.H, BH, 0, p.dsT,
+                       dy, p.ds0, hbuf, recs);
     const int jobs = nchunk * BH, per_xcd = (jobs + 7) / 8;
     hipLaunchKernelGGL(wkv7_bwd_chunk, dim3(8 * per_xcd), dim3(512), 0, p.stream, p.T, p.H, BH, per_xcd, r, w, k, v,
                        a, b, dy, p.ckpt, hbuf, static_cast<bf16_t*>(p.dr), static_cast<bf16_t*>(p.dw),
                        static_cast<bf16_t*>(p.dk), static_cast<bf16_t*>(p.dv), static_cast<bf16_t*>(p.da),
                        static_cast<bf16_t*>(p.db));
+}
+
+size_t gdn_backward_workspace(int B, int T, int H) { return wkv7_rec_bwd_workspace(B, T, H); }
+
+template <typename TI>
+static void launch_gdn_bwd(const GdnBwd& p) {
+    const int nchunk = (p.T + BC - 1) / BC, BH = p.B * p.H;
+    uint8_t* const recs = static_cast<uint8_t*>(p.ws);
+    float* const hbuf = reinterpret_cast<float*>(recs + ((size_t)BH * nchunk * BwdRec::BYTES + 255) / 256 * 256);
+    const TI *q = static_cast<const TI*>(p.q), *k = static_cast<const TI*>(p.k), *v = static_cast<const TI*>(p.v),
+             *dout = static_cast<const TI*>(p.dout);
+    hipLaunchKernelGGL(gdn_bwd_prep<TI>, dim3(nchunk, BH), dim3(64), 0, p.stream, p.T, p.H, q, k, p.g, p.beta, recs);
+    hipLaunchKernelGGL(wkv7_bwd_scan<TI>, dim3(BH * (BNK / 64)), dim3(256), 0, p.stream, p.T, p.H, BH, 1, p.dsT, dout,
+                       p.ds0, hbuf, recs);
+    const int jobs = nchunk * BH, per_xcd = (jobs + 7) / 8;
+    hipLaunchKernelGGL(gdn_bwd_chunk<TI>, dim3(8 * per_xcd), dim3(512), 0, p.stream, p.T, p.H, BH, per_xcd, q, k, v,
+                       p.g, p.beta, dout, p.ckpt, hbuf, static_cast<TI*>(p.dq), static_cast<TI*>(p.dk),
+                       static_cast<TI*>(p.dv), p.dg, p.dbeta);
+}
+void launch_gdn_backward(const GdnBwd& p) {
+    if (p.dtype == 0) launch_gdn_bwd<bf16_t>(p);
+    else launch_gdn_bwd<float>(p);
 }
 
 }  // namespace wkv7

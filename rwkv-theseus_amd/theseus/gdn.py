@@ -15,7 +15,9 @@ theseus/hf_model.py:28-52).  Its converter states the same recurrence as a WKV7 
 THESEUS_WKV7_STATE_KEY_VALUE (no state transpose); the mapping is torch ops, so autograd
 carries the kernels' gradients back to q, k, v, g and beta.  When no gradient is wanted
 (the teacher's forward) and the head size is 64 or 128, it runs the chunked MFMA forward
-of the gated delta rule instead (``theseus_gdn_forward``, include/theseus_gdn.h).  Like transformers'
+of the gated delta rule instead (``theseus_gdn_forward``, include/theseus_gdn.h); with
+gradients at head size 128, the chunked forward with saved states and the chunked backward
+(``theseus_gdn_forward_train`` / ``theseus_gdn_backward``).  Like transformers'
 functions it computes in float32 (the operands are passed to the kernels as float32)
 and returns the output in the query's dtype.  The state must be square (K == V, the
 kernels' N, 2..128).
@@ -35,6 +37,28 @@ from .wkv7 import DECAY_EXP, STATE_KEY_VALUE, extension, wkv7_ex
 
 # head sizes of the chunked forward (theseus_gdn_forward); others use the step-serial kernels
 CHUNKED_HEAD_SIZES = (64, 128)
+# head sizes of the chunked forward+backward (theseus_gdn_forward_train, theseus_gdn_backward)
+CHUNKED_GRAD_HEAD_SIZES = (128,)
+
+
+class _GDN(torch.autograd.Function):
+    """The gated delta rule on the chunked kernels with gradients: q, k (as the layer
+    normalised them), v, g, beta, s0 float32 or q/k/v bfloat16; saved states between
+    the two calls."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, s0):
+        ctx.set_materialize_grads(False)
+        o, sT, saved = extension().gdn_forward_train(q, k, v, g, beta, s0)
+        ctx.save_for_backward(q, k, v, g, beta, saved)
+        return o, sT
+
+    @staticmethod
+    def backward(ctx, do, dsT):
+        q, k, v, g, beta, saved = ctx.saved_tensors
+        do = torch.zeros_like(q) if do is None else do.to(q.dtype).contiguous()
+        dsT = None if dsT is None else dsT.float().contiguous()
+        return extension().gdn_backward(q, k, v, g, beta, saved, do, dsT)
 
 
 def l2norm(x, dim=-1, eps=1e-6):
@@ -69,6 +93,13 @@ def gated_delta_rule(query, key, value, g, beta, initial_state=None, output_fina
         return o.to(out_dtype), (sT if output_final_state else None)
     if use_qk_l2norm_in_kernel:
         query, key = l2norm(query), l2norm(key)
+    if (K in CHUNKED_GRAD_HEAD_SIZES and query.is_cuda
+            and extension().lib.theseus_gdn_backward_workspace_size(B, T, H, K) > 0):
+        # gradients wanted: the chunked forward with saved states and the chunked backward,
+        # in float32 as transformers' functions compute
+        q, k, v, gf, bf = (x.float().contiguous() for x in (query, key, value, g, beta))
+        o, sT = _GDN.apply(q, k, v, gf, bf, s0)
+        return o.to(out_dtype), (sT if output_final_state else None)
     q, k, v, gf, bf = (x.float() for x in (query, key, value, g, beta))
     eg = torch.exp(gf)
     r = q * (K ** -0.5)
@@ -107,20 +138,21 @@ def _wants_grad(args, kwargs):
 
 def patch_transformers(module):
     """Route ``module.torch_chunk_gated_delta_rule`` / ``torch_recurrent_gated_delta_rule``
-    to the HIP kernels for CUDA tensors with a square state (K == V <= 128), no packed
-    sequences (cu_seqlens) and no gradient wanted (the teacher's forward, on the chunked
-    kernels); any other call goes to the function that was there -- with gradients,
-    transformers' own chunked torch function (37 ms forward+backward at B=1, T=2048,
-    H=32, K=V=128 on MI355X) beats the step-serial backward (190 ms).  Returns the
+    to the HIP kernels for CUDA tensors with a square state and no packed sequences
+    (cu_seqlens): without gradients for K == V <= 128 (the teacher's forward, on the
+    chunked kernels for 64 and 128), with gradients for K == V == 128 (the chunked forward
+    and backward); any other call goes to the function that was there -- with gradients
+    at other head sizes, transformers' own chunked torch function (37 ms forward+backward
+    at B=1, T=2048, H=32, K=V=128 on MI355X) beats the step-serial backward.  Returns the
     previous pair."""
     old = (module.torch_chunk_gated_delta_rule, module.torch_recurrent_gated_delta_rule)
 
     def route(ours, theirs):
         @functools.wraps(theirs)
         def call(query, key, value, *args, **kwargs):
-            if (query.is_cuda and 2 <= query.shape[-1] == value.shape[-1] <= 128
-                    and kwargs.get("cu_seqlens") is None
-                    and not _wants_grad((query, key, value) + args, kwargs)):
+            K = query.shape[-1]
+            if (query.is_cuda and 2 <= K == value.shape[-1] <= 128 and kwargs.get("cu_seqlens") is None
+                    and (K in CHUNKED_GRAD_HEAD_SIZES or not _wants_grad((query, key, value) + args, kwargs))):
                 return ours(query, key, value, *args, **kwargs)
             return theirs(query, key, value, *args, **kwargs)
         return call

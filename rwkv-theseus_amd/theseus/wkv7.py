@@ -135,6 +135,12 @@ class Extension:
         lib.theseus_gdn_forward.restype = i32
         lib.theseus_gdn_forward_workspace_size.argtypes = [i32] * 4
         lib.theseus_gdn_forward_workspace_size.restype = sz
+        lib.theseus_gdn_forward_train.argtypes = [i32] * 5 + [vp] * 9 + [vp, sz, vp]
+        lib.theseus_gdn_forward_train.restype = i32
+        lib.theseus_gdn_backward.argtypes = [i32] * 5 + [vp] * 14 + [vp, sz, vp]
+        lib.theseus_gdn_backward.restype = i32
+        lib.theseus_gdn_backward_workspace_size.argtypes = [i32] * 4
+        lib.theseus_gdn_backward_workspace_size.restype = sz
         self.abi_version = lib.theseus_wkv7_abi_version()
         self.checkpoint_interval = lib.theseus_wkv7_checkpoint_interval()
 
@@ -276,6 +282,63 @@ class Extension:
                 B, T, H, N, _BF16 if q.dtype == torch.bfloat16 else _FP32, 1 if qk_l2norm else 0, p(q), p(k), p(v), p(g), p(beta), p(s0),
                 p(o), p(sT), None if ws is None else p(ws), nbytes, _stream(q.device)))
         return o, sT
+
+    @staticmethod
+    def _gdn_check(q, k, v, g, beta, s0):
+        B, T, H, N = q.shape
+        if q.dtype not in (torch.bfloat16, torch.float32):
+            raise RuntimeError("theseus_gdn: expected bfloat16 or float32 q, k, v")
+        for x in (q, k, v):
+            if not (x.is_cuda and x.dtype == q.dtype and x.is_contiguous() and x.shape == q.shape):
+                raise RuntimeError("theseus_gdn: expected contiguous CUDA q, k, v [B,T,H,N] of one dtype")
+        for x in (g, beta):
+            if not (x.device == q.device and x.dtype == torch.float32 and x.is_contiguous()
+                    and tuple(x.shape) == (B, T, H)):
+                raise RuntimeError("theseus_gdn: expected contiguous float32 g, beta [B,T,H]")
+        if s0 is not None and not (s0.device == q.device and s0.dtype == torch.float32 and s0.is_contiguous()
+                                   and tuple(s0.shape) == (B, H, N, N)):
+            raise RuntimeError("theseus_gdn: expected contiguous float32 state [B,H,N,N]")
+
+    def gdn_forward_train(self, q, k, v, g, beta, s0):
+        """The gated delta rule forward of a call that needs gradients
+        (theseus_gdn_forward_train): q and k used as given, and the saved states for
+        ``gdn_backward``.  Returns (o in q's dtype, sT, saved [B,H,ceil(T/16)+1,N,N])."""
+        self._gdn_check(q, k, v, g, beta, s0)
+        B, T, H, N = q.shape
+        with _on(q.device):
+            o = torch.empty_like(q)
+            sT = torch.empty_like(s0)
+            saved = torch.empty((B, H, self.checkpoint_count(T), N, N), dtype=torch.float32, device=q.device)
+            ws, nbytes = _workspace(self.lib.theseus_gdn_forward_workspace_size(B, T, H, N), q.device)
+            p = lambda t: t.data_ptr()  # noqa: E731
+            self._raise(self.lib.theseus_gdn_forward_train(
+                B, T, H, N, _BF16 if q.dtype == torch.bfloat16 else _FP32, p(q), p(k), p(v), p(g), p(beta), p(s0),
+                p(o), p(sT), p(saved), None if ws is None else p(ws), nbytes, _stream(q.device)))
+        return o, sT, saved
+
+    def gdn_backward(self, q, k, v, g, beta, saved, dout, dsT):
+        """Backward of ``gdn_forward_train`` (theseus_gdn_backward, N = 128): dout in q's
+        dtype, dsT [B,H,key,value] float32 or None.  Returns (dq, dk, dv in q's dtype, dg,
+        dbeta [B,T,H] and ds0 [B,H,key,value] float32)."""
+        self._gdn_check(q, k, v, g, beta, dsT)
+        B, T, H, N = q.shape
+        if not (dout.dtype == q.dtype and dout.is_contiguous() and dout.shape == q.shape
+                and dout.device == q.device):
+            raise RuntimeError("theseus_gdn: expected a contiguous output gradient like q")
+        if not (saved.dtype == torch.float32 and saved.is_contiguous() and saved.device == q.device
+                and tuple(saved.shape) == (B, H, self.checkpoint_count(T), N, N)):
+            raise RuntimeError("theseus_gdn: invalid saved states")
+        with _on(q.device):
+            dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+            dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
+            ds0 = torch.empty((B, H, N, N), dtype=torch.float32, device=q.device)
+            ws, nbytes = _workspace(self.lib.theseus_gdn_backward_workspace_size(B, T, H, N), q.device)
+            p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+            self._raise(self.lib.theseus_gdn_backward(
+                B, T, H, N, _BF16 if q.dtype == torch.bfloat16 else _FP32, p(q), p(k), p(v), p(g), p(beta),
+                p(saved), p(dout), p(dsT), p(dq), p(dk), p(dv), p(dg), p(dbeta), p(ds0), p(ws), nbytes,
+                _stream(q.device)))
+        return dq, dk, dv, dg, dbeta, ds0
 
     def backward(self, r, w, k, v, a, b, saved, dy, dend, flags=0, layout=None):
         """-> [dr, dw, dk, dv, da, db, ds0] (cpp:26-37).  dend may be None (zero).

@@ -265,7 +265,9 @@ def test_gdn_abi_exported_bound_and_validated():
     arity; sizes are checked before anything is enqueued (N must be 64 or 128)."""
     ext = W.extension()
     arity = declared_arity(ROOT / "include" / "theseus_gdn.h")
-    assert arity == {"theseus_gdn_forward": 17, "theseus_gdn_forward_workspace_size": 4}
+    assert arity == {"theseus_gdn_forward": 17, "theseus_gdn_forward_workspace_size": 4,
+                     "theseus_gdn_forward_train": 17, "theseus_gdn_backward": 22,
+                     "theseus_gdn_backward_workspace_size": 4}
     for name, n in arity.items():
         fn = getattr(ext.lib, name)
         assert fn.argtypes is not None and len(fn.argtypes) == n, (name, n)
@@ -281,3 +283,12 @@ def test_gdn_abi_exported_bound_and_validated():
         assert lib.theseus_gdn_forward(B, T, H, N, 1, 0, *[None] * 8, None, 0, None) == 1
     assert lib.theseus_gdn_forward(1, 4, 1, 64, 5, 0, *[None] * 8, None, 0, None) == 2  # dtype
     assert lib.theseus_gdn_forward(1, 4, 1, 64, 0, 1, *[None] * 8, None, 0, None) == 3  # null pointers
+    # the training pair: saved states required; the backward takes N = 128 only, its
+    # workspace 25088 bytes of scan record and a 64 KiB float32 dL/dS per chunk
+    assert lib.theseus_gdn_forward_train(1, 4, 1, 64, 1, *[None] * 9, None, 0, None) == 3
+    assert lib.theseus_gdn_forward_train(1, 4, 1, 100, 1, *[None] * 9, None, 0, None) == 1
+    assert lib.theseus_gdn_backward_workspace_size(1, 2048, 32, 128) == 32 * 128 * (25088 + 65536)
+    assert lib.theseus_gdn_backward_workspace_size(1, 2048, 32, 64) == 0
+    assert lib.theseus_gdn_backward(1, 4, 1, 64, 1, *[None] * 14, None, 0, None) == 1
+    assert lib.theseus_gdn_backward(1, 4, 1, 128, 5, *[None] * 14, None, 0, None) == 2
+    assert lib.theseus_gdn_backward(1, 4, 1, 128, 1, *[None] * 14, None, 0, None) == 3

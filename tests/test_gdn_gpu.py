@@ -144,7 +144,14 @@ def test_gdn_dropin_matches_transformers(N, T):
     for n, x, y in zip(["q", "k", "v", "g", "beta", "s0"], a, b):
         e = rel_l2(x.grad.cpu(), y.grad.cpu())
         print(f"    d{n}: rel_l2 {e:.2e}", flush=True)
-        assert e <= 1e-4, (n, e)
+        assert e <= (DG_BAR if n == "g" and N in gdn.CHUNKED_GRAD_HEAD_SIZES else 1e-4), (n, e)
+
+
+# dg on the chunked backward (N = 128): every other output is within ~2e-5 of float64, but
+# dg is a sum over the 128 keys of dlogd, itself a reverse sum of per-token terms that
+# cancel down to e^{g} times their size, so the products' split-bf16 rounding (~2^-16 of
+# the terms) shows there several times larger: 5e-5 - 1e-4 measured at ordinary decays.
+DG_BAR = 3e-4
 
 
 def test_gdn_dropin_bf16_and_float64_oracle():
@@ -223,15 +230,105 @@ def test_chunked_gdn_forward_against_oracle(B, T, H, N, g_scale):
 
 def test_chunked_gdn_matches_the_step_serial_path():
     """No-grad calls of theseus.gdn take the chunked forward, calls that need gradients the
-    WKV7 kernels in exp mode: the two agree (both fp32 I/O, different summation orders)."""
-    B, T, H, N = 1, 100, 4, 128
-    q, k, v, g, beta, s0 = (x.float().cuda() for x in _chunked_inputs(B, T, H, N, seed=11))
-    with torch.no_grad():
-        o1, s1 = gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0, output_final_state=True)
-    leaves = [x.clone().requires_grad_() for x in (q, k, v, g, beta, s0)]
-    o2, s2 = gdn.chunk_gated_delta_rule(*leaves[:5], initial_state=leaves[5], output_final_state=True)
-    assert rel_l2(o1.cpu(), o2.detach().cpu()) <= 1e-4
-    assert rel_l2(s1.cpu(), s2.detach().cpu()) <= 1e-4
+    chunked forward with saved states (N = 128) or the WKV7 kernels in exp mode (N = 64):
+    each agrees with the step-serial exp-mode kernels (fp32 I/O, different summation
+    orders)."""
+    B, T, H = 1, 100, 4
+    for N in (128, 64):
+        q, k, v, g, beta, s0 = (x.float().cuda() for x in _chunked_inputs(B, T, H, N, seed=11))
+        with torch.no_grad():
+            o1, s1 = gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0, output_final_state=True)
+            r = q * N ** -0.5
+            w = g.unsqueeze(-1).expand(B, T, H, N).contiguous()
+            o0, s_0 = W.wkv7_ex(r, w, k, v * beta.unsqueeze(-1), k, -(torch.exp(g) * beta).unsqueeze(-1) * k, s0,
+                                flags=W.DECAY_EXP | W.STATE_KEY_VALUE)
+        leaves = [x.clone().requires_grad_() for x in (q, k, v, g, beta, s0)]
+        o2, s2 = gdn.chunk_gated_delta_rule(*leaves[:5], initial_state=leaves[5], output_final_state=True)
+        for x, y in [(o1, o0), (s1, s_0), (o2.detach(), o0), (s2.detach(), s_0)]:
+            assert rel_l2(x.cpu(), y.cpu()) <= 1e-4
+
+
+def _gdn_oracle_grads(q, k, v, g, beta, s0_kv, do, dsT_kv):
+    """float64 gradients of the gated delta rule: the oracle's exp-mode step adjoint on the
+    converter's WKV operands (oracle.gdn_operands), chained back to q, k, v, g, beta and the
+    [key][value] initial state."""
+    q, k, v, g, beta, s0_kv, do, dsT_kv = (np.asarray(x, dtype=np.float64) for x in
+                                            (q, k, v, g, beta, s0_kv, do, dsT_kv))
+    N = q.shape[-1]
+    ops = O.gdn_operands(q, k, v, g, beta)
+    tr = lambda s: np.ascontiguousarray(np.swapaxes(s, -1, -2))  # noqa: E731
+    y, sT = O.forward_c(*ops, tr(s0_kv), mode="exp")
+    dr, dw, dk, dv, da, db, ds0 = O.backward_c(*ops, tr(s0_kv), do, tr(dsT_kv), mode="exp")
+    eg, bt = np.exp(g)[..., None], beta[..., None]
+    return dict(o=y, sT=tr(sT), dq=dr / np.sqrt(N), dk=dk + da - eg * bt * db, dv=bt * dv,
+                dg=dw.sum(-1) + (ops[5] * db).sum(-1), dbeta=(v * dv).sum(-1) - (eg * k * db).sum(-1), ds0=tr(ds0))
+
+
+@pytest.mark.parametrize("B,T,H,dtype,g_scale", [
+    (1, 1, 1, torch.float32, 1.0), (2, 15, 2, torch.float32, 1.0), (1, 16, 3, torch.float32, 1.0),
+    (2, 70, 3, torch.float32, 1.0), (1, 100, 2, torch.float32, 20.0), (1, 333, 2, torch.float32, 0.01),
+    (2, 70, 3, torch.bfloat16, 1.0),
+])
+def test_chunked_gdn_backward_against_oracle(B, T, H, dtype, g_scale):
+    """theseus_gdn_forward_train + theseus_gdn_backward (N = 128) on given q, k (unit
+    rows, as a layer's normalisation leaves them), against the float64 oracle: output,
+    final state and the gradients of q, k, v, g, beta and s0, dsT ~ N(0,1); tails of every
+    length; decays from e^{-0.01 e^x} to e^{-20 e^x} per step (the chunk's decay ratios stay
+    at most 1, however strong).  fp32 I/O: rel-L2 <= 1e-4, dg <= DG_BAR; bf16 I/O: <= 5e-3
+    on the bf16 inputs exactly as the kernels see them.  At the strongest decays dg itself
+    is ~e^{-20} times the terms it is summed from, so there it keeps the other gradients'
+    absolute accuracy rather than a relative one (rel-L2 2.2e-3, max-abs 7.6e-5 measured,
+    against 2.7e-4 on dk): that case is held to the north star's 5e-3."""
+    N = 128
+    print(f"  gdn backward B={B} T={T} H={H} {dtype} g_scale={g_scale}", flush=True)
+    q, k, v, g, beta, s0 = _chunked_inputs(B, T, H, N, seed=T + 7 * H, g_scale=g_scale)
+    gen = torch.Generator().manual_seed(T + 1)
+    do = torch.randn(B, T, H, N, generator=gen, dtype=torch.float64)
+    dsT = torch.randn(B, H, N, N, generator=gen, dtype=torch.float64)
+    qd, kd, vd, dod = (x.to(dtype) for x in (q, k, v, do))
+    ext = W.extension()
+    cu = lambda x: x.cuda().contiguous()  # noqa: E731
+    o, sT, saved = ext.gdn_forward_train(cu(qd), cu(kd), cu(vd), cu(g.float()), cu(beta.float()), cu(s0.float()))
+    grads = ext.gdn_backward(cu(qd), cu(kd), cu(vd), cu(g.float()), cu(beta.float()), saved, cu(dod),
+                             cu(dsT.float()))
+    torch.cuda.synchronize()
+    ref = _gdn_oracle_grads(*(x.double().numpy() for x in (qd, kd, vd)), g.float().double().numpy(),
+                            beta.float().double().numpy(), s0.float().double().numpy(), dod.double().numpy(),
+                            dsT.float().double().numpy())
+    bar = 1e-4 if dtype == torch.float32 else 5e-3
+    for name, got in zip(["o", "sT", "dq", "dk", "dv", "dg", "dbeta", "ds0"], (o, sT) + tuple(grads)):
+        got = got.double().cpu().numpy()
+        rl = rel_l2(got, ref[name])
+        print(f"    {name:5s} rel_l2={rl:.2e} max_abs={max_abs(got, ref[name]):.2e}", flush=True)
+        b = bar if name != "dg" else (5e-3 if g_scale >= 10 else max(bar, DG_BAR))
+        assert np.isfinite(got).all() and rl <= b, (name, rl)
+
+
+def test_chunked_gdn_backward_teacher_geometry_matches_transformers():
+    """B=1, T=2048, 32 value heads, K=V=128 (the teacher's GDN layers), float32, in-kernel
+    q/k norm: theseus.gdn's chunked forward+backward against transformers'
+    torch_chunk_gated_delta_rule with autograd, output, state and all six gradients at
+    rel-L2 <= 1e-4 (dg: DG_BAR)."""
+    import inspect
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as M
+    hf = inspect.unwrap(M.torch_chunk_gated_delta_rule)
+    B, T, H, N = 1, 2048, 32, 128
+    ins = _gdn_inputs(B, T, H, N, seed=2048)
+    a = [t.clone().requires_grad_() for t in ins]
+    b = [t.clone().requires_grad_() for t in ins]
+    oa, sa = gdn.chunk_gated_delta_rule(*a[:5], initial_state=a[5], output_final_state=True,
+                                        use_qk_l2norm_in_kernel=True)
+    ob, sb = hf(*b[:5], initial_state=b[5], output_final_state=True, use_qk_l2norm_in_kernel=True)
+    go, gs = torch.randn_like(ob), torch.randn_like(sb)
+    torch.autograd.backward((oa, sa), (go, gs))
+    torch.autograd.backward((ob, sb), (go, gs))
+    torch.cuda.synchronize()
+    assert rel_l2(oa.detach().cpu(), ob.detach().cpu()) <= 1e-4
+    assert rel_l2(sa.detach().cpu(), sb.detach().cpu()) <= 1e-4
+    for n, x, y in zip(["q", "k", "v", "g", "beta", "s0"], a, b):
+        e = rel_l2(x.grad.cpu(), y.grad.cpu())
+        print(f"    d{n}: rel_l2 {e:.2e}", flush=True)
+        assert e <= (DG_BAR if n == "g" else 1e-4), (n, e)
 
 
 def test_chunked_gdn_bf16_io_and_in_kernel_norm():
@@ -255,8 +352,10 @@ def test_chunked_gdn_bf16_io_and_in_kernel_norm():
 
 
 def test_patch_routes_gradient_calls_to_transformers():
-    """patch_transformers sends no-grad CUDA calls to the chunked kernels and calls that need
-    gradients back to the function it replaced (transformers' own is faster there)."""
+    """patch_transformers sends no-grad CUDA calls to the chunked kernels, calls that need
+    gradients at K = V = 128 to the chunked forward and backward, and other calls that need
+    gradients back to the function it replaced (transformers' own beats the step-serial
+    backward there)."""
     import types
     calls = []
 
@@ -273,6 +372,11 @@ def test_patch_routes_gradient_calls_to_transformers():
     qg = q.clone().requires_grad_()
     mod.torch_chunk_gated_delta_rule(qg, k, v, g, beta, initial_state=s0)
     assert calls == ["theirs"]
+    q, k, v, g, beta, s0 = _gdn_inputs(1, 20, 2, 128, seed=5)
+    qg = q.clone().requires_grad_()
+    o, _ = mod.torch_chunk_gated_delta_rule(qg, k, v, g, beta, initial_state=s0)
+    o.sum().backward()
+    assert calls == ["theirs"] and qg.grad is not None and bool(torch.isfinite(qg.grad).all())
 
 
 def _gdn_capi(lib, q, k, v, g, beta, s0, qk_norm, ws_bytes):
