@@ -220,8 +220,10 @@ __device__ __forceinline__ float row_prev(float x, float first) { return dpp_f<0
 // (q, 4m + jj) holds row 4q + jj, columns 4m..4m+3: an 8-byte piece of a row,
 // stored with one instruction instead of four 2-byte ones.  Two DPP exchanges
 // (quad_perm) and byte permutes, no LDS.
-__device__ __forceinline__ uint2 quad_rows_bf16(const f32x4_t& d, int lane) {
-    const uint32_t d0 = f32x2_to_bf16x2(d[0], d[1]), d1 = f32x2_to_bf16x2(d[2], d[3]);  // rows (0,1), (2,3)
+// quad_regroup does the regrouping for a tile already packed as bf16 row pairs (d0: rows
+// 0, 1 and d1: rows 2, 3 of the lane's column), quad_rows_split for both halves of the
+// tile's split-bf16 pair (split2's hi and lo).
+__device__ __forceinline__ uint2 quad_regroup(uint32_t d0, uint32_t d1, int lane) {
     const bool lo2 = (lane & 2) == 0, odd = lane & 1;
     // lanes jj, jj^2 swap halves of the column: jj < 2 keeps rows 0,1 of columns jj, jj+2,
     // jj >= 2 keeps rows 2,3 of columns jj-2, jj (a0: the even column, a1: the odd+2 one)
@@ -232,6 +234,16 @@ __device__ __forceinline__ uint2 quad_rows_bf16(const f32x4_t& d, int lane) {
     const uint32_t rb = __builtin_amdgcn_update_dpp(0, sb, 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
     return make_uint2(__builtin_amdgcn_perm(rb, a0, odd ? 0x03020504u : 0x05040100u),
                       __builtin_amdgcn_perm(rb, a1, odd ? 0x03020706u : 0x07060100u));
+}
+__device__ __forceinline__ uint2 quad_rows_bf16(const f32x4_t& d, int lane) {
+    return quad_regroup(f32x2_to_bf16x2(d[0], d[1]), f32x2_to_bf16x2(d[2], d[3]), lane);  // rows (0,1), (2,3)
+}
+__device__ __forceinline__ void quad_rows_split(const f32x4_t& d, int lane, uint2& hi, uint2& lo) {
+    uint32_t h01, l01, h23, l23;
+    split2(d[0], d[1], h01, l01);
+    split2(d[2], d[3], h23, l23);
+    hi = quad_regroup(h01, h23, lane);
+    lo = quad_regroup(l01, l23, lane);
 }
 __device__ __forceinline__ float row_last(float x) {  // ds_swizzle, and_mask 0x10, or_mask 0x0f
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f0));

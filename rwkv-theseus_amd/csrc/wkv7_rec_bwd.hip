@@ -248,11 +248,39 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, int 
 // The gradients of one chunk (512 lanes).  Workgroups map to (head, chunk) so that a
 // head's consecutive chunks share an XCD (chunk c's S_end is chunk c + 1's S0 in L2).
 // ---------------------------------------------------------------------------
-constexpr int CLP = BNK + 4;  // padded plane row (floats)
+// The operands every wave reads as K=32 A/B fragments over the keys or value rows are
+// split into bf16 hi/lo once, by the wave that owns their 16 columns, and kept so in LDS
+// (splitting them in every reader had been most of the kernel's VALU work).
+constexpr int CLB = BNK + 8;  // padded split-plane row (bf16)
+struct SplitPlane {
+    uint16_t h[BC][CLB], l[BC][CLB];
+};
+// a D-layout tile ([t][16 wv + c], rows t = 4q4 + e) into a split plane, 8-byte rows per lane
+__device__ __forceinline__ void put_split(SplitPlane& P, const f32x4_t& d, int lane, int wv) {
+    uint2 h, l;
+    quad_rows_split(d, lane, h, l);  // (cross-lane: every lane takes part)
+    const int tr = 4 * (lane >> 4) + (lane & 3), c = 16 * wv + 4 * ((lane >> 2) & 3);
+    *reinterpret_cast<uint2*>(&P.h[tr][c]) = h;
+    *reinterpret_cast<uint2*>(&P.l[tr][c]) = l;
+}
+// the K=32 fragment of row r16, columns 32ks + 4q4 .. +3 and 32ks + 16 + 4q4 .. +3
+__device__ __forceinline__ void get_split(const SplitPlane& P, int lane, int ks, uint4& h, uint4& l) {
+    const int r = lane & 15, c = 32 * ks + 4 * (lane >> 4);
+    const uint2 a = *reinterpret_cast<const uint2*>(&P.h[r][c]), b = *reinterpret_cast<const uint2*>(&P.h[r][c + 16]);
+    const uint2 x = *reinterpret_cast<const uint2*>(&P.l[r][c]), y = *reinterpret_cast<const uint2*>(&P.l[r][c + 16]);
+    h = make_uint4(a.x, a.y, b.x, b.y);
+    l = make_uint4(x.x, x.y, y.x, y.y);
+}
+// the same fragment of a bf16 row in memory (exact: no lo part), zero when !ok
+__device__ __forceinline__ uint4 bf16_frag(const bf16_t* row, int ks, int q4, bool ok) {
+    if (!ok) return make_uint4(0, 0, 0, 0);
+    const uint2 a = *reinterpret_cast<const uint2*>(row + 32 * ks + 4 * q4);
+    const uint2 b = *reinterpret_cast<const uint2*>(row + 32 * ks + 16 + 4 * q4);
+    return make_uint4(a.x, a.y, b.x, b.y);
+}
 struct ChunkLds {
-    float At[BC][CLP], Bm[BC][CLP], Km[BC][CLP], Rt[BC][CLP];  // [t][j], written by the key owners
-    float SA[BC][CLP], Q[BC][CLP];                             // [t][i], written by the value-row owners
-    float eL[BNK];
+    SplitPlane At, Bm, Km, Rt, Bh, Kh;  // [t][j], written by the key owners
+    SplitPlane SA, Q;                   // [t][i], written by the value-row owners
     float csum[BTJ][BNK];  // per wave: column sums of H_end o S_end over its 16 value rows
 };
 
@@ -321,10 +349,9 @@ __global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int
         const float g = excl + p[e], gp = e ? excl + p[e - 1] : excl;
         eA[e] = __expf(gp), eR[e] = __expf(g), eM[e] = __expf(-g);
         At[e] = xa[e] * eA[e], Rt[e] = xr[e] * eR[e], Bm[e] = xb[e] * eM[e], Km[e] = xk[e] * eM[e];
-        const int t = 4 * q4 + e;
-        sm.At[t][col] = At[e], sm.Bm[t][col] = Bm[e], sm.Km[t][col] = Km[e], sm.Rt[t][col] = Rt[e];
     }
-    if (q4 == 0) sm.eL[col] = eLj;
+    put_split(sm.At, At, lane, wv), put_split(sm.Bm, Bm, lane, wv), put_split(sm.Km, Km, lane, wv);
+    put_split(sm.Rt, Rt, lane, wv), put_split(sm.Bh, Bm * eLj, lane, wv), put_split(sm.Kh, Km * eLj, lane, wv);
     // the carry's partial column sums over this wave's value rows
 #pragma unroll
     for (int ks = 0; ks < BKS; ks++)
@@ -344,33 +371,20 @@ __global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int
     // ---- chunk matrices (every wave) and the wave's [t][i] products over the keys ----
     f32x4_t Aab = zero4(), AabT = zero4(), Aak = zero4(), Brb = zero4(), Brk = zero4();
     f32x4_t P1 = zero4(), P2 = zero4(), P3 = zero4();
-    auto trow = [&](float (*pl)[CLP], int ks, float (&o)[8]) {
-        const float4 x = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 4 * q4]);
-        const float4 y = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 16 + 4 * q4]);
-        o[0] = x.x, o[1] = x.y, o[2] = x.z, o[3] = x.w, o[4] = y.x, o[5] = y.y, o[6] = y.z, o[7] = y.w;
-    };
 #pragma unroll
     for (int ks = 0; ks < BKS; ks++) {
-        float fa[8], fb[8], fk[8], fr[8], el[8];
-        trow(sm.At, ks, fa), trow(sm.Bm, ks, fb), trow(sm.Km, ks, fk), trow(sm.Rt, ks, fr);
-        {
-            const float4 x = *reinterpret_cast<const float4*>(&sm.eL[32 * ks + 4 * q4]);
-            const float4 y = *reinterpret_cast<const float4*>(&sm.eL[32 * ks + 16 + 4 * q4]);
-            el[0] = x.x, el[1] = x.y, el[2] = x.z, el[3] = x.w, el[4] = y.x, el[5] = y.y, el[6] = y.z, el[7] = y.w;
-        }
-        uint4 ah, al, bh_, bl, kh, kl, rh, rl;
-        pack8(fa, ah, al), pack8(fb, bh_, bl), pack8(fk, kh, kl), pack8(fr, rh, rl);
+        uint4 ah, al, bh_, bl, kh, kl, rh, rl, hh, hl, xh, xl;
+        get_split(sm.At, lane, ks, ah, al), get_split(sm.Bm, lane, ks, bh_, bl);
+        get_split(sm.Km, lane, ks, kh, kl), get_split(sm.Rt, lane, ks, rh, rl);
+        get_split(sm.Bh, lane, ks, hh, hl), get_split(sm.Kh, lane, ks, xh, xl);
         Aab = mm3(Aab, ah, al, bh_, bl);
         AabT = mm3(AabT, bh_, bl, ah, al);
         Aak = mm3(Aak, ah, al, kh, kl);
         Brb = mm3(Brb, rh, rl, bh_, bl);   // R~_rr . B-_cc
         Brk = mm3(Brk, rh, rl, kh, kl);    // R~_rr . K-_cc
         P1 = mm3(P1, ah, al, Sh[ks], Sl[ks]);  // A~ S0^T
-#pragma unroll
-        for (int e = 0; e < 8; e++) fb[e] *= el[e], fk[e] *= el[e];  // B^, K^
-        pack8(fb, bh_, bl), pack8(fk, kh, kl);
-        P2 = mm3(P2, bh_, bl, Hh[ks], Hl[ks]);  // B^ H^T
-        P3 = mm3(P3, kh, kl, Hh[ks], Hl[ks]);   // K^ H^T
+        P2 = mm3(P2, hh, hl, Hh[ks], Hl[ks]);  // B^ H^T
+        P3 = mm3(P3, xh, xl, Hh[ks], Hl[ks]);  // K^ H^T
     }
     const int cc = r16;
 #pragma unroll
@@ -399,8 +413,7 @@ __global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int
     const f32x4_t SA = mm16s(pTiT, pk(P1 + mm16s(pAakT, pV)));  // Ti (A~ S0^T + Aak V)
     const f32x4_t Q = mm16s(pTi, pk(P2 + mm16s(pBrb, pdY)));    // Ti^T (B^ H^T + Brb^T dY)
     const f32x4_t dV = P3 + mm16s(pAak, pk(Q)) + mm16s(pBrk, pdY);
-#pragma unroll
-    for (int e = 0; e < 4; e++) sm.SA[4 * q4 + e][col] = SA[e], sm.Q[4 * q4 + e][col] = Q[e];
+    put_split(sm.SA, SA, lane, wv), put_split(sm.Q, Q, lane, wv);
     {
         const int tr = 4 * q4 + (lane & 3);  // the row quad_rows_bf16 gives this lane
         const uint2 q = quad_rows_bf16(dV, lane);  // (cross-lane: every lane takes part)
@@ -426,18 +439,10 @@ __global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int
     const bool tv = r16 < L;
 #pragma unroll
     for (int ks = 0; ks < BKS; ks++) {
-        float fs[8], fq[8], fv[8], fy[8];
-        trow(sm.SA, ks, fs), trow(sm.Q, ks, fq);
-        {
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            const long o = at_tok(tv ? r16 : 0) + 32 * ks + 4 * q4;
-            const float4 v0 = tv ? ld4f(v + o) : z, v1 = tv ? ld4f(v + o + 16) : z;
-            const float4 y0 = tv ? ld4f(dy + o) : z, y1 = tv ? ld4f(dy + o + 16) : z;
-            fv[0] = v0.x, fv[1] = v0.y, fv[2] = v0.z, fv[3] = v0.w, fv[4] = v1.x, fv[5] = v1.y, fv[6] = v1.z, fv[7] = v1.w;
-            fy[0] = y0.x, fy[1] = y0.y, fy[2] = y0.z, fy[3] = y0.w, fy[4] = y1.x, fy[5] = y1.y, fy[6] = y1.z, fy[7] = y1.w;
-        }
-        uint4 sh, sl, qh, ql, vh, vl, yh, yl;
-        pack8(fs, sh, sl), pack8(fq, qh, ql), pack8(fv, vh, vl), pack8(fy, yh, yl);  // (vl = yl = 0)
+        uint4 sh, sl, qh, ql;
+        get_split(sm.SA, lane, ks, sh, sl), get_split(sm.Q, lane, ks, qh, ql);
+        const long o = at_tok(tv ? r16 : 0);
+        const uint4 vh = bf16_frag(v + o, ks, q4, tv), yh = bf16_frag(dy + o, ks, q4, tv);  // (exact in bf16)
         VH = mma32(mma32(VH, vh, Hh[ks]), vh, Hl[ks]);
         SAH = mm3(SAH, sh, sl, Hh[ks], Hl[ks]);
         dYS = mma32(mma32(dYS, yh, Sh[ks]), yh, Sl[ks]);
@@ -612,8 +617,8 @@ __global__ __launch_bounds__(64) void gdn_bwd_prep(int Tn, int H, const TI* __re
 }
 
 struct GdnChunkLds {
-    float K[BC][CLP], R[BC][CLP];  // k, r = q / sqrt(N) [t][j], written by the key owners
-    float SA[BC][CLP], Q[BC][CLP];  // [t][i], written by the value-row owners
+    SplitPlane K, R;   // k, r = q / sqrt(N) [t][j], written by the key owners
+    SplitPlane SA, Q;  // [t][i], written by the value-row owners
     float gam[BC], gm1[BC], beta[BC];
     float csum[BTJ][BNK];
     float pv[BTJ][BC], pd[BTJ][BC], pk[BTJ][BC];  // per wave and token: sum v dV', sum dlogd, sum k dB
@@ -671,8 +676,8 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
         const bool ok = t < L;
         kD[e] = ok ? io<TI>::ld(k, at_tok(t) + col) : 0.f;
         rD[e] = ok ? io<TI>::ld(q, at_tok(t) + col) * rs : 0.f;
-        sm.K[t][col] = kD[e], sm.R[t][col] = rD[e];
     }
+    put_split(sm.K, kD, lane, wv), put_split(sm.R, rD, lane, wv);
 #pragma unroll
     for (int ks = 0; ks < BKS; ks++)
 #pragma unroll
@@ -696,17 +701,10 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
     const float gc = sm.gam[cc], gm1c = sm.gm1[cc], bc = sm.beta[cc], gL = sm.gam[BC - 1];
     // Gram matrices over the keys and the wave's products k S0^T, k H^T
     f32x4_t KK = zero4(), RK = zero4(), kS = zero4(), kH = zero4();
-    auto trow = [&](float (*pl)[CLP], int ks, float (&o)[8]) {
-        const float4 x = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 4 * q4]);
-        const float4 y = *reinterpret_cast<const float4*>(&pl[r16][32 * ks + 16 + 4 * q4]);
-        o[0] = x.x, o[1] = x.y, o[2] = x.z, o[3] = x.w, o[4] = y.x, o[5] = y.y, o[6] = y.z, o[7] = y.w;
-    };
 #pragma unroll
     for (int ks = 0; ks < BKS; ks++) {
-        float fk[8], fr[8];
-        trow(sm.K, ks, fk), trow(sm.R, ks, fr);
         uint4 kh, kl, rh, rl;
-        pack8(fk, kh, kl), pack8(fr, rh, rl);
+        get_split(sm.K, lane, ks, kh, kl), get_split(sm.R, lane, ks, rh, rl);
         KK = mm3(KK, kh, kl, kh, kl);
         RK = mm3(RK, rh, rl, kh, kl);  // r_rr . k_cc
         kS = mm3(kS, kh, kl, Sh[ks], Sl[ks]);
@@ -754,9 +752,9 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
     const f32x4_t SA = mm16s(pTiT, pk(P1 + mm16s(pAakT, pV)));
     const f32x4_t Q = mm16s(pTi, pk(P2 + mm16s(pBrb, pdY)));
     const f32x4_t dVp = P3 + mm16s(pAak, pk(Q)) + mm16s(pBrk, pdY);
+    put_split(sm.SA, SA, lane, wv), put_split(sm.Q, Q, lane, wv);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        sm.SA[4 * q4 + e][col] = SA[e], sm.Q[4 * q4 + e][col] = Q[e];
         const float s = row_sum16(vraw[e] * dVp[e]);
         if (r16 == 0) sm.pv[wv][4 * q4 + e] = s;
     }
@@ -779,8 +777,7 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
     const bool tv = r16 < L;
 #pragma unroll
     for (int ks = 0; ks < BKS; ks++) {
-        float fs[8], fq[8], fv[8], fy[8];
-        trow(sm.SA, ks, fs), trow(sm.Q, ks, fq);
+        float fv[8], fy[8];
         {
             const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
             const long o = at_tok(tv ? r16 : 0) + 32 * ks + 4 * q4;
@@ -792,7 +789,8 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
             for (int e = 0; e < 8; e++) fv[e] *= bc;  // V' = beta v (the lane's token r16)
         }
         uint4 sh, sl, qh, ql, vh, vl, yh, yl;
-        pack8(fs, sh, sl), pack8(fq, qh, ql), pack8(fv, vh, vl), pack8(fy, yh, yl);
+        get_split(sm.SA, lane, ks, sh, sl), get_split(sm.Q, lane, ks, qh, ql);
+        pack8(fv, vh, vl), pack8(fy, yh, yl);
         VH = mm3(VH, vh, vl, Hh[ks], Hl[ks]);
         SAH = mm3(SAH, sh, sl, Hh[ks], Hl[ks]);
         dYS = mm3(dYS, yh, yl, Sh[ks], Sl[ks]);
