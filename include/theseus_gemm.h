@@ -22,6 +22,7 @@ extern "C" {
 typedef struct ihipStream_t* hipStream_t;
 
 #define THESEUS_GEMM_MAX_ROWS 128
+#define THESEUS_GEMM_MAX_GROUP 8
 
 enum theseus_gemm_act { THESEUS_GEMM_NONE = 0, THESEUS_GEMM_TANH = 1, THESEUS_GEMM_SIGMOID = 2 };
 
@@ -39,6 +40,28 @@ size_t theseus_gemm_rows_workspace_size(int M, int N, int K);
  * Status codes are theseus_wkv7_status values; asynchronous on `stream`. */
 int theseus_gemm_rows(int M, int N, int K, int act, const void* x, const void* w, void* y, void* workspace,
                       size_t workspace_bytes, hipStream_t stream);
+
+/* One product of a group: y [M][N] = act(x [M][K] w [N][K]^T), as theseus_gemm_rows. */
+typedef struct theseus_gemm_problem {
+    int N, K, act;
+    const void* x;
+    const void* w;
+    void* y;
+} theseus_gemm_problem;
+
+/* Workspace bytes of theseus_gemm_rows_group (0: none, or sizes it refuses). */
+size_t theseus_gemm_rows_group_workspace_size(int M, int count, const theseus_gemm_problem* probs);
+
+/* 1 <= count <= THESEUS_GEMM_MAX_GROUP independent products with the same M in one launch
+ * (a serving step's r, k, v projections and LoRA first halves, which all read the step's
+ * token mixes; then the LoRA second halves): each product takes a share of the CUs in
+ * proportion to its weight bytes, so the 5120-wide projections run one workgroup per
+ * column tile with no K split and no second kernel, where a lone projection splits K to
+ * fill the chip.  Results equal theseus_gemm_rows' for each product up to the order of
+ * the float32 sums.  Errors as theseus_gemm_rows for any product; probs is read on the
+ * host during the call only. */
+int theseus_gemm_rows_group(int M, int count, const theseus_gemm_problem* probs, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

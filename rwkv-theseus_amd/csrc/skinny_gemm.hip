@@ -64,17 +64,16 @@ __device__ __forceinline__ float act(float x, int a) {
     return a == THESEUS_GEMM_TANH ? tanhf(x) : 1.f / (1.f + __expf(-x));
 }
 
+// One workgroup's part of a product: column tile `tile`, K slice ks of KS.
 template <int MT, int WV, int KST>
-__global__ __launch_bounds__(WV * 64, 1) void skinny_gemm(int M, int N, int K, int kchunk, int actf,
-                                                           const uint16_t* __restrict__ X,
-                                                           const uint16_t* __restrict__ W,
-                                                           uint16_t* __restrict__ Y, float* part) {
+__device__ __forceinline__ void gemm_tile(int M, int N, int K, int kchunk, int actf, int tile, int ks, int KS,
+                                          const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
+                                          uint16_t* __restrict__ Y, float* part) {
     using R = Ring<MT, WV, KST>;
     constexpr int CPR = R::CPR, ROWB = R::ROWB, COLS = R::COLS;
     extern __shared__ __align__(16) uint8_t lds[];  // R::D stages of R::SB bytes
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, q = lane >> 4, r16 = lane & 15;
-    const int tile = blockIdx.x, ks = blockIdx.y, KS = gridDim.y;
     const int n0 = tile * COLS + 16 * wv;  // this wave's first column
     const int k0 = ks * kchunk, kend = min(K, k0 + kchunk), nsteps = (kend - k0 + KST - 1) / KST;
 
@@ -154,11 +153,44 @@ __global__ __launch_bounds__(WV * 64, 1) void skinny_gemm(int M, int N, int K, i
         }
 }
 
+template <int MT, int WV, int KST>
+__global__ __launch_bounds__(WV * 64, 1) void skinny_gemm(int M, int N, int K, int kchunk, int actf,
+                                                           const uint16_t* __restrict__ X,
+                                                           const uint16_t* __restrict__ W,
+                                                           uint16_t* __restrict__ Y, float* part) {
+    gemm_tile<MT, WV, KST>(M, N, K, kchunk, actf, blockIdx.x, blockIdx.y, gridDim.y, X, W, Y, part);
+}
+
+// Several products with the same rows in one launch (a serving step's independent
+// projections): problem i owns workgroups blk0 .. blk0 + tiles * KS - 1, in the order given.
+constexpr int GMAX = THESEUS_GEMM_MAX_GROUP;
+struct GemmProb {
+    const uint16_t* X;
+    const uint16_t* W;
+    uint16_t* Y;
+    float* part;
+    int N, K, kchunk, KS, tiles, act, blk0, thr0;  // thr0: first reduce thread (KS > 1)
+};
+struct GemmGroup {
+    int count;
+    GemmProb p[GMAX];
+};
+template <int MT, int WV, int KST>
+__global__ __launch_bounds__(WV * 64, 1) void skinny_gemm_group(int M, GemmGroup g) {
+    const int b = blockIdx.x;
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < GMAX; j++)
+        if (j < g.count && b >= g.p[j].blk0) i = j;
+    const GemmProb& p = g.p[i];
+    const int local = b - p.blk0;
+    gemm_tile<MT, WV, KST>(M, p.N, p.K, p.kchunk, p.act, local % p.tiles, local / p.tiles, p.KS, p.X, p.W, p.Y, p.part);
+}
+
 // Y from the KS float32 slices of every tile, summed in K order (deterministic), with the
 // activation; one thread per (tile, wave, row tile, lane), as the GEMM's accumulator layout.
-__global__ __launch_bounds__(256) void gemm_reduce(int M, int N, int KS, int WV, int MT, int actf,
-                                                   const float* __restrict__ part, uint16_t* __restrict__ Y) {
-    const long t = (long)blockIdx.x * 256 + threadIdx.x;
+__device__ __forceinline__ void reduce_one(long t, int M, int N, int KS, int WV, int MT, int actf,
+                                           const float* __restrict__ part, uint16_t* __restrict__ Y) {
     const int lane = (int)(t % 64), mt = (int)(t / 64 % MT), wv = (int)(t / (64 * MT) % WV);
     const long tile = t / (64L * MT * WV);
     const int n = (int)tile * 16 * WV + 16 * wv + (lane & 15), q = lane >> 4;
@@ -172,6 +204,23 @@ __global__ __launch_bounds__(256) void gemm_reduce(int M, int N, int KS, int WV,
         const int m = 16 * mt + 4 * q + e;
         if (m < M) Y[(long)m * N + n] = f32_to_bf16(act(s[e], actf));
     }
+}
+__global__ __launch_bounds__(256) void gemm_reduce(int M, int N, int KS, int WV, int MT, int actf,
+                                                   const float* __restrict__ part, uint16_t* __restrict__ Y) {
+    reduce_one((long)blockIdx.x * 256 + threadIdx.x, M, N, KS, WV, MT, actf, part, Y);
+}
+// the slices of a group's split products (those with KS > 1; thr0 their first thread)
+__global__ __launch_bounds__(256) void gemm_reduce_group(int M, int WV, int MT, GemmGroup g) {
+    const long t = (long)blockIdx.x * 256 + threadIdx.x;
+    int i = -1;
+#pragma unroll
+    for (int j = 0; j < GMAX; j++)
+        if (j < g.count && g.p[j].KS > 1 && t >= g.p[j].thr0) i = j;
+    if (i < 0) return;
+    const GemmProb& p = g.p[i];
+    const long u = t - p.thr0;
+    if (u >= (long)p.tiles * WV * MT * 64) return;
+    reduce_one(u, M, p.N, p.KS, WV, MT, p.act, p.part, p.Y);
 }
 
 struct Plan {
@@ -222,6 +271,48 @@ inline int launch_mt(const Plan& p, int M, int N, int K, int act, const uint16_t
     }
 }
 
+// A group's plan: each product gets a share of the CUs in proportion to its weight bytes
+// and plans its K slices within that share (products of many column tiles then take one
+// slice each: no partial tiles, no reduce).  Workgroups and reduce threads are numbered in
+// the order of the products, partial tiles packed after one another in the workspace.
+inline size_t plan_group(int M, int count, const theseus_gemm_problem* pr, int cus, GemmGroup& g, int& blocks,
+                         long& rthreads, int& MT) {
+    double tot = 0;
+    for (int i = 0; i < count; i++) tot += (double)pr[i].N * pr[i].K;
+    size_t ws = 0;
+    blocks = 0, rthreads = 0;
+    g.count = count;
+    for (int i = 0; i < count; i++) {
+        const int share = std::max(1, (int)(cus * ((double)pr[i].N * pr[i].K / tot)));
+        const Plan p = plan(M, pr[i].N, pr[i].K, share);
+        MT = p.MT;
+        GemmProb& q = g.p[i];
+        q.X = static_cast<const uint16_t*>(pr[i].x), q.W = static_cast<const uint16_t*>(pr[i].w);
+        q.Y = static_cast<uint16_t*>(pr[i].y), q.part = nullptr;
+        q.N = pr[i].N, q.K = pr[i].K, q.kchunk = p.kchunk, q.KS = p.KS, q.tiles = p.tiles, q.act = pr[i].act;
+        q.blk0 = blocks, q.thr0 = (int)rthreads;
+        blocks += p.tiles * p.KS;
+        if (p.KS > 1) {
+            q.part = reinterpret_cast<float*>(ws);  // (an offset until the workspace is known)
+            ws += workspace(p);
+            rthreads += (long)p.tiles * p.WV * p.MT * 64;
+        }
+    }
+    for (int i = count; i < GMAX; i++) g.p[i] = GemmProb{};
+    return ws;
+}
+template <int MT, int WV, int KST>
+inline int launch_group(const GemmGroup& g, int M, int blocks, long rthreads, hipStream_t stream) {
+    const size_t lds = (size_t)Ring<MT, WV, KST>::D * Ring<MT, WV, KST>::SB;
+    if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_gemm_group<MT, WV, KST>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return THESEUS_WKV7_ERR_LAUNCH;
+    hipLaunchKernelGGL((skinny_gemm_group<MT, WV, KST>), dim3(blocks), dim3(WV * 64), lds, stream, M, g);
+    if (rthreads)
+        hipLaunchKernelGGL(gemm_reduce_group, dim3((unsigned)((rthreads + 255) / 256)), dim3(256), 0, stream, M, WV, MT, g);
+    return hipGetLastError() == hipSuccess ? THESEUS_WKV7_OK : THESEUS_WKV7_ERR_LAUNCH;
+}
+
 int device_cus() {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -257,6 +348,44 @@ int theseus_gemm_rows(int M, int N, int K, int act, const void* x, const void* w
     return sg::launch_mt<sg::DEF_WV, sg::DEF_KST>(p, M, N, K, act, static_cast<const uint16_t*>(x),
                                                   static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y),
                                                   static_cast<float*>(workspace), stream);
+}
+
+static int group_ok(int M, int count, const theseus_gemm_problem* probs) {
+    if (count < 1 || count > THESEUS_GEMM_MAX_GROUP || !probs) return THESEUS_WKV7_ERR_SHAPE;
+    for (int i = 0; i < count; i++) {
+        if (!gemm_shape_ok(M, probs[i].N, probs[i].K)) return THESEUS_WKV7_ERR_SHAPE;
+        if (probs[i].act < THESEUS_GEMM_NONE || probs[i].act > THESEUS_GEMM_SIGMOID) return THESEUS_WKV7_ERR_FLAGS;
+    }
+    return THESEUS_WKV7_OK;
+}
+
+size_t theseus_gemm_rows_group_workspace_size(int M, int count, const theseus_gemm_problem* probs) {
+    if (group_ok(M, count, probs)) return 0;
+    sg::GemmGroup g;
+    int blocks, MT;
+    long rthreads;
+    return sg::plan_group(M, count, probs, sg::device_cus(), g, blocks, rthreads, MT);
+}
+
+int theseus_gemm_rows_group(int M, int count, const theseus_gemm_problem* probs, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+    if (int e = group_ok(M, count, probs)) return e;
+    for (int i = 0; i < count; i++)
+        if (!probs[i].x || !probs[i].w || !probs[i].y) return THESEUS_WKV7_ERR_NULL;
+    sg::GemmGroup g;
+    int blocks, MT;
+    long rthreads;
+    const size_t need = sg::plan_group(M, count, probs, sg::device_cus(), g, blocks, rthreads, MT);
+    if (need && (!workspace || workspace_bytes < need)) return THESEUS_WKV7_ERR_WORKSPACE;
+    for (int i = 0; i < count; i++)
+        if (g.p[i].KS > 1) g.p[i].part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                                                  reinterpret_cast<size_t>(g.p[i].part));
+    switch (MT) {
+        case 1: return sg::launch_group<1, sg::DEF_WV, sg::DEF_KST>(g, M, blocks, rthreads, stream);
+        case 2: return sg::launch_group<2, sg::DEF_WV, sg::DEF_KST>(g, M, blocks, rthreads, stream);
+        case 4: return sg::launch_group<4, sg::DEF_WV, sg::DEF_KST>(g, M, blocks, rthreads, stream);
+        default: return sg::launch_group<8, sg::DEF_WV, sg::DEF_KST>(g, M, blocks, rthreads, stream);
+    }
 }
 
 }  // extern "C"

@@ -5,7 +5,8 @@ key, value, output and the w/a/g LoRAs) on one token per lane, so each product h
 rows as lanes (64 at config 4) and streams its weight matrix.  ``linear(x, weight)`` is
 ``x @ weight.T`` and ``lora(x, down, up, act)`` is ``act(x @ down) @ up`` on the
 ``theseus_gemm_rows`` kernel (bf16, float32 accumulation, split-K with a deterministic
-sum), for x with at most ``MAX_ROWS`` rows and no autograd.
+sum), for x with at most ``MAX_ROWS`` rows and no autograd; ``group`` runs several
+independent products with the same rows in one launch (theseus_gemm_rows_group).
 
 Weights are read in place when they are bf16 and already in the kernel's [out][in]
 layout (nn.Linear weights); the LoRA matrices ([in][out]) and float32 weights need a
@@ -22,9 +23,16 @@ from . import fused
 from .wkv7 import extension
 
 MAX_ROWS = 128  # THESEUS_GEMM_MAX_ROWS
+MAX_GROUP = 8  # THESEUS_GEMM_MAX_GROUP
 NONE, TANH, SIGMOID = 0, 1, 2  # theseus_gemm_act
 
 _bound = None
+
+
+class Problem(ctypes.Structure):
+    """theseus_gemm_problem: y [M][N] = act(x [M][K] w [N][K]^T)."""
+    _fields_ = [("N", ctypes.c_int), ("K", ctypes.c_int), ("act", ctypes.c_int),
+                ("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("y", ctypes.c_void_p)]
 
 
 def _lib():
@@ -36,6 +44,10 @@ def _lib():
         lib.theseus_gemm_rows_workspace_size.restype = sz
         lib.theseus_gemm_rows.argtypes = [i32] * 4 + [vp] * 4 + [sz, vp]
         lib.theseus_gemm_rows.restype = i32
+        lib.theseus_gemm_rows_group_workspace_size.argtypes = [i32, i32, ctypes.POINTER(Problem)]
+        lib.theseus_gemm_rows_group_workspace_size.restype = sz
+        lib.theseus_gemm_rows_group.argtypes = [i32, i32, ctypes.POINTER(Problem), vp, sz, vp]
+        lib.theseus_gemm_rows_group.restype = i32
         _bound = True
     return lib
 
@@ -113,6 +125,34 @@ def lora(x, down, up, act=NONE):
     mid = _gemm(_rows_bf16(x), _out_in(down, True), act)
     y = _gemm(mid, _out_in(up, True), NONE)
     return y.reshape(*x.shape[:-1], up.shape[1])
+
+
+def group(items):
+    """[(x, weight, act, transposed), ...] -> [act(x @ W^T), ...] in one launch
+    (theseus_gemm_rows_group): every x [..., in] with the same number of rows (at most
+    MAX_ROWS), weight [out, in], or [in, out] when ``transposed`` (a LoRA matrix)."""
+    if not 1 <= len(items) <= MAX_GROUP:
+        raise ValueError(f"theseus_gemm: 1 to {MAX_GROUP} products per group")
+    xs = [_rows_bf16(x) for x, _, _, _ in items]
+    rows = xs[0].shape[0]
+    if any(x2.shape[0] != rows for x2 in xs):
+        raise ValueError("theseus_gemm: the products of a group must have the same rows")
+    ws_ = [_out_in(w, tr) for _, w, _, tr in items]
+    dev = xs[0].device
+    ys = [torch.empty((rows, w.shape[0]), dtype=torch.bfloat16, device=dev) for w in ws_]
+    probs = (Problem * len(items))(*[Problem(w.shape[0], x2.shape[1], act, x2.data_ptr(), w.data_ptr(), y.data_ptr())
+                                     for (_, _, act, _), x2, w, y in zip(items, xs, ws_, ys)])
+    lib = _lib()
+    with torch.cuda.device(dev):
+        nbytes = int(lib.theseus_gemm_rows_group_workspace_size(rows, len(items), probs))
+        ws = _workspace(nbytes, dev)
+        st = lib.theseus_gemm_rows_group(rows, len(items), probs,
+                                         ctypes.c_void_p(ws.data_ptr() if ws is not None else 0),
+                                         ctypes.c_size_t(ws.numel() if ws is not None else 0),
+                                         ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    if st:
+        raise RuntimeError("theseus_gemm: " + extension().lib.theseus_wkv7_error_string(st).decode())
+    return [y.reshape(*x.shape[:-1], y.shape[1]) for (x, _, _, _), y in zip(items, ys)]
 
 
 def usable(x, *weights):

@@ -177,14 +177,21 @@ class TimeMix(nn.Module):
             # (as the torch products under bf16 autocast, with each activation applied to the
             # float32 accumulator before the bf16 rounding)
             from . import fused, gemm
-            r = gemm.linear(mixed["r"], self.receptance.weight)
-            k, v = gemm.linear(mixed["k"], self.key.weight), gemm.linear(mixed["v"], self.value.weight)
-            if fused._store is not None or self.w1.dtype != torch.bfloat16:
-                # the LoRAs too where their [out][in] bf16 copies are kept (a serving store) or
-                # a float32 -> bf16 copy is made anyway (autocast would make one per call)
-                zw = gemm.lora(mixed["w"], self.w1, self.w2, gemm.TANH)
-                za = gemm.lora(mixed["a"], self.a1, self.a2)
-                g = gemm.lora(mixed["g"], self.g1, self.g2, gemm.SIGMOID)
+            # one launch for every product of the step's mixes (r, k, v and, where their
+            # [out][in] bf16 copies are kept -- a serving store -- or a float32 -> bf16 copy is
+            # made anyway, the LoRAs' first halves), one for the LoRAs' second halves
+            first = [(mixed["r"], self.receptance.weight, gemm.NONE, False),
+                     (mixed["k"], self.key.weight, gemm.NONE, False),
+                     (mixed["v"], self.value.weight, gemm.NONE, False)]
+            loras = fused._store is not None or self.w1.dtype != torch.bfloat16
+            if loras:
+                first += [(mixed["w"], self.w1, gemm.TANH, True), (mixed["a"], self.a1, gemm.NONE, True),
+                          (mixed["g"], self.g1, gemm.SIGMOID, True)]
+            outs = gemm.group(first)
+            r, k, v = outs[:3]
+            if loras:
+                zw, za, g = gemm.group([(outs[3], self.w2, gemm.NONE, True), (outs[4], self.a2, gemm.NONE, True),
+                                        (outs[5], self.g2, gemm.NONE, True)])
             else:
                 zw = torch.tanh(mixed["w"] @ self.w1) @ self.w2
                 za = (mixed["a"] @ self.a1) @ self.a2

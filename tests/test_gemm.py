@@ -19,7 +19,8 @@ def test_gemm_abi_exported_bound_and_validated():
     """Every function of include/theseus_gemm.h is exported and bound with the header's
     arity; sizes, activation codes, pointers and workspace are checked on the host."""
     arity = declared_arity(ROOT / "include" / "theseus_gemm.h")
-    assert arity == {"theseus_gemm_rows_workspace_size": 3, "theseus_gemm_rows": 10}
+    assert arity == {"theseus_gemm_rows_workspace_size": 3, "theseus_gemm_rows": 10,
+                     "theseus_gemm_rows_group_workspace_size": 3, "theseus_gemm_rows_group": 6}
     lib = gemm._lib()
     for name, n in arity.items():
         assert len(getattr(lib, name).argtypes) == n, name
@@ -28,6 +29,18 @@ def test_gemm_abi_exported_bound_and_validated():
         assert lib.theseus_gemm_rows(M, N, K, 0, None, None, None, None, 0, None) == ERR_SHAPE
     assert lib.theseus_gemm_rows(4, 64, 64, 3, None, None, None, None, 0, None) == ERR_FLAGS
     assert lib.theseus_gemm_rows(4, 64, 64, 0, None, None, None, None, 0, None) == ERR_NULL
+    # groups: 1..8 products, every one of them valid, pointers checked
+    pr = (gemm.Problem * 9)(*[gemm.Problem(64, 64, 0, None, None, None)] * 9)
+    for count in (0, 9):
+        assert lib.theseus_gemm_rows_group_workspace_size(4, count, pr) == 0
+        assert lib.theseus_gemm_rows_group(4, count, pr, None, 0, None) == ERR_SHAPE
+    assert lib.theseus_gemm_rows_group(129, 2, pr, None, 0, None) == ERR_SHAPE
+    pr[1].N = 24
+    assert lib.theseus_gemm_rows_group(4, 2, pr, None, 0, None) == ERR_SHAPE
+    pr[1].N, pr[1].act = 64, 3
+    assert lib.theseus_gemm_rows_group(4, 2, pr, None, 0, None) == ERR_FLAGS
+    pr[1].act = 0
+    assert lib.theseus_gemm_rows_group(4, 2, pr, None, 0, None) == ERR_NULL
     assert gemm.supported(64, 5120, 5120) and gemm.supported(1, 352, 5120) and gemm.supported(128, 5120, 192)
     assert not gemm.supported(129, 64, 64) and not gemm.supported(4, 24, 64) and not gemm.supported(4, 64, 48)
 
@@ -111,3 +124,35 @@ def test_gemm_python_wrappers_and_layouts():
     assert ((y.float() - yr).abs() <= 2.0 ** -8 * yr.abs() + 1e-4).all()
     # (the middle product is rounded to bf16 on both sides; one bf16 ULP of it may flip)
     assert ((z.float() - zr).norm() / zr.norm()).item() < 4e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [64, 5, 128])
+def test_gemm_group_matches_single_products(M):
+    """theseus_gemm_rows_group on a serving step's two groups at C=5120 (r, k, v and the
+    LoRA first halves, 3 x 5120 + 192 + 192 + 352 columns; then the LoRA second halves)
+    and on a ragged group whose small products split K: every product within the single
+    call's bar of its float32 reference, and within twice that bar of theseus_gemm_rows (the
+    two differ in the order of the float32 sums); repeatable bitwise."""
+    g = torch.Generator(device="cuda").manual_seed(M + 5)
+    rn = lambda *s: torch.randn(*s, device="cuda", generator=g)  # noqa: E731
+    C = 5120
+    shapes = [[(C, C, gemm.NONE)] * 3 + [(192, C, gemm.TANH), (192, C, gemm.NONE), (352, C, gemm.SIGMOID)],
+              [(C, 192, gemm.NONE), (C, 192, gemm.NONE), (C, 352, gemm.NONE)],
+              [(96, 640, gemm.TANH), (16, 4096, gemm.NONE), (1040, 1024, gemm.SIGMOID)]]
+    for group in shapes:
+        print(f"  group M={M}: {[(n, k) for n, k, _ in group]}", flush=True)
+        xs = [rn(M, k).to(torch.bfloat16) for n, k, a in group]
+        ws = [(rn(n, k) / k ** .5).to(torch.bfloat16) for n, k, a in group]
+        with torch.no_grad():
+            outs = gemm.group([(x, w, a, False) for x, w, (n, k, a) in zip(xs, ws, group)])
+            again = gemm.group([(x, w, a, False) for x, w, (n, k, a) in zip(xs, ws, group)])
+            single = [gemm.linear(x, w, a) for x, w, (n, k, a) in zip(xs, ws, group)]
+        torch.cuda.synchronize()
+        for y, y2, y1, x, w, (n, k, a) in zip(outs, again, single, xs, ws, group):
+            assert torch.equal(y, y2)
+            ref, tol = _ref(x, w, a)
+            bar = tol + 1e-5 * ref.abs().max() + 1e-6  # (as test_gemm_rows_matches_float32_products)
+            assert bool(((y.float() - ref).abs() <= bar).all()), (n, k)
+            # (both within that bar of the float32 product, in different summation orders)
+            assert bool(((y.float() - y1.float()).abs() <= 2 * bar).all()), (n, k)
