@@ -156,7 +156,8 @@ def bench_serving(args, cfg):
 
     # the eager modes run as a serving loop that keeps the layer's derived parameter copies
     # (float32 vectors, stacked lerp coefficients, transposed LoRAs) in a store of its own,
-    # as the captured graph does (theseus.fused.param_cache)
+    # as the captured graph does (theseus.fused.param_cache); inside it each step is one
+    # native call (theseus_tm_serving_step)
     store = {}
 
     def run(mode):

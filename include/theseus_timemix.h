@@ -76,6 +76,36 @@ int theseus_tm_gn_bwd(int B, int T, int C, const void* dout, const void* y, cons
                       float* dk_a, float* workspace, size_t workspace_bytes,
                       hipStream_t stream);
 
+/* A TimeMix layer's parameters as a serving step reads them (theseus/timemix.py:18-59):
+ * the stacked shift-lerp coefficients coef [6][C] float32 (x_r, x_w, x_k, x_v, x_a, x_g);
+ * the projections w_r, w_k, w_v, w_o [C][C] bf16 in nn.Linear's [out][in] layout; the
+ * LoRA matrices transposed to [out][in] bf16: w1t, a1t, g1t [rank][C] and w2t, a2t, g2t
+ * [C][rank]; w0, a0, k_k, k_a, r_k, ln_w, ln_b [C] float32; ln_eps the GroupNorm eps. */
+typedef struct theseus_tm_layer {
+    int C, H, N, rank_w, rank_a, rank_g;
+    const float* coef;
+    const void *w_r, *w_k, *w_v, *w_o;
+    const void *w1t, *a1t, *g1t, *w2t, *a2t, *g2t;
+    const float *w0, *a0, *k_k, *k_a, *r_k, *ln_w, *ln_b;
+    float ln_eps;
+} theseus_tm_layer;
+
+/* Workspace bytes of theseus_tm_serving_step for B lanes (0: sizes it refuses). */
+size_t theseus_tm_serving_step_workspace(const theseus_tm_layer* layer, int B);
+
+/* One serving step of TimeMix.forward (theseus/timemix.py:62-89) for x [B,1,C] bf16, no
+ * autograd, N = 64, B <= THESEUS_GEMM_MAX_ROWS: the launches of the fused layer's
+ * few-row path in one call (the same kernels, order and arguments, so the same bits),
+ * every intermediate in the workspace.  shift_in [B,C] bf16 is the previous token; when
+ * shift_out is not NULL, x is copied there at the end (the in-place step).  The WKV state
+ * [B,H,N,N] float32 goes from wkv_in to wkv_out (the same pointer: in place); out [B,1,C]
+ * bf16.  The step the reference's serving loop makes per token through AttentionAdapter
+ * (theseus/hf_model.py:96-108) has no native counterpart there (~20 torch launches).
+ * Asynchronous on `stream`; status codes of theseus_wkv7.h. */
+int theseus_tm_serving_step(const theseus_tm_layer* layer, int B, const void* x, const void* shift_in,
+                            void* shift_out, const float* wkv_in, float* wkv_out, void* out,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,12 +54,25 @@ def _lib():
             lib.theseus_tm_gn_workspace.argtypes = [i32] * 3
             lib.theseus_tm_gn_workspace.restype = sz
             lib.theseus_tm_gn_bwd.argtypes = [i32] * 3 + [vp] * 12 + [f32] + [vp] * 11 + [sz, vp]
-            for n in ("shift_lerp_fwd", "shift_lerp_bwd", "add_param_fwd", "kk_fwd", "kk_bwd", "gn_fwd", "gn_bwd"):
+            lib.theseus_tm_serving_step_workspace.argtypes = [ctypes.POINTER(TmLayer), i32]
+            lib.theseus_tm_serving_step_workspace.restype = sz
+            lib.theseus_tm_serving_step.argtypes = [ctypes.POINTER(TmLayer), i32] + [vp] * 7 + [sz, vp]
+            for n in ("shift_lerp_fwd", "shift_lerp_bwd", "add_param_fwd", "kk_fwd", "kk_bwd", "gn_fwd", "gn_bwd",
+                      "serving_step"):
                 getattr(lib, "theseus_tm_" + n).restype = i32
             _ready = True
         except AttributeError:
             _ready = False
     return lib if _ready else None
+
+
+class TmLayer(ctypes.Structure):
+    """theseus_tm_layer (include/theseus_timemix.h): a TimeMix layer's parameters as the
+    native serving step reads them."""
+    _fields_ = ([(n, ctypes.c_int) for n in ("C", "H", "N", "rank_w", "rank_a", "rank_g")]
+                + [(n, ctypes.c_void_p) for n in ("coef", "w_r", "w_k", "w_v", "w_o", "w1t", "a1t", "g1t", "w2t",
+                                                   "a2t", "g2t", "w0", "a0", "k_k", "k_a", "r_k", "ln_w", "ln_b")]
+                + [("ln_eps", ctypes.c_float)])
 
 
 # The fused kernels' grids index token blocks of 64 in blockIdx.y (at most 65535).
@@ -118,7 +131,8 @@ def refresh_param_cache(store):
     try:
         with torch.no_grad():
             for _srcs, make, out in store.values():
-                out.copy_(make())
+                if isinstance(out, torch.Tensor):  # (other entries point at these tensors)
+                    out.copy_(make())
     finally:
         _store = prev
 
@@ -132,9 +146,41 @@ def _cached(slot, srcs, make):
     if hit is not None:
         return hit[2]
     out = make()
-    if not (out.is_cuda and torch.cuda.is_current_stream_capturing()):
+    on_gpu = out.is_cuda if isinstance(out, torch.Tensor) else True
+    if not (on_gpu and torch.cuda.is_current_stream_capturing()):
         store[key] = (tuple(srcs), make, out)  # (the sources stay alive with the store)
     return out
+
+
+class _NativeLayer:
+    """A layer's TmLayer and the tensors its pointers refer to (kept alive with it)."""
+
+    def __init__(self, struct, keep):
+        self.struct, self.keep = struct, keep
+
+
+def native_layer(m):
+    """The TmLayer of TimeMix ``m`` for theseus_tm_serving_step, inside a param_cache
+    store: the float32 parameter vectors and stacked coefficients, bf16 [out][in] weights
+    and transposed LoRAs are the store's derived copies (or the parameters themselves),
+    so refresh_param_cache(store) updates what it points at in place.  Keyed by the
+    parameter objects, as every derived copy."""
+    from . import gemm
+    C = m.width
+    params = (m.x_r, m.x_w, m.x_k, m.x_v, m.x_a, m.x_g, m.receptance.weight, m.key.weight, m.value.weight,
+              m.output.weight, m.w1, m.a1, m.g1, m.w2, m.a2, m.g2, m.w0, m.a0, m.k_k, m.k_a, m.r_k,
+              m.ln_x.weight, m.ln_x.bias)
+
+    def make():
+        coef = _coef_matrix(params[:6], C)
+        mats = [gemm._out_in(w, False) for w in params[6:10]] + [gemm._out_in(w, True) for w in params[10:16]]
+        vecs = [_vec(p, C) for p in params[16:]]
+        keep = (coef, *mats, *vecs)
+        st = TmLayer(C, m.heads, m.head_size, m.w1.shape[1], m.a1.shape[1], m.g1.shape[1],
+                     *[t.data_ptr() for t in keep], float(m.ln_x.eps))
+        return _NativeLayer(st, keep + params)
+
+    return _cached("tm_layer", params, make)
 
 
 def _vec(p, C):

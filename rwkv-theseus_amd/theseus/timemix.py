@@ -26,6 +26,7 @@ them), under that licence.
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 from torch import nn
@@ -161,8 +162,46 @@ class TimeMix(nn.Module):
             raise ValueError("state['wkv'] must be a contiguous [B,H,N,N] float32 tensor on x's device")
         return self._run(x, state, inplace=True)[0]
 
+    def _native_ok(self, x, state):
+        """A one-token no-grad step inside a parameter store (theseus.fused.param_cache:
+        the serving loop's or CapturedStep's) runs as one native call
+        (theseus_tm_serving_step), the same kernels the few-row path below launches.
+        THESEUS_TM_NATIVE=0 keeps the launches in Python (tests compare the two)."""
+        from . import fused
+        if x.shape[1] != 1 or fused._store is None or os.environ.get("THESEUS_TM_NATIVE", "1") == "0":
+            return False
+        wkv = state["wkv"]
+        if not (wkv.dtype == torch.float32 and wkv.is_contiguous() and wkv.is_cuda
+                and state["shift"].dim() == 2 and self._fused(x) and self._few_rows(x)):
+            return False
+        return all(p.is_cuda for p in (self.w1, self.a1, self.g1, self.w2, self.a2, self.g2))
+
+    def _native_step(self, x, state, inplace):
+        import ctypes
+        from . import fused, gemm
+        B, _, C = x.shape
+        lib = fused._lib()
+        lay = fused.native_layer(self)
+        xs = x.contiguous()
+        shift = state["shift"].to(x.dtype).contiguous()
+        wkv = state["wkv"]
+        out = torch.empty((B, 1, C), dtype=x.dtype, device=x.device)
+        wkv_out = wkv if inplace else torch.empty_like(wkv)
+        nbytes = int(lib.theseus_tm_serving_step_workspace(ctypes.byref(lay.struct), B))
+        ws = gemm._workspace(nbytes, x.device)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        with torch.cuda.device(x.device):
+            fused._check(lib.theseus_tm_serving_step(
+                ctypes.byref(lay.struct), B, p(xs), p(shift), p(state["shift"]) if inplace else None, p(wkv),
+                p(wkv_out), p(out), p(ws), ctypes.c_size_t(ws.numel()), fused._s(x.device)))
+        if inplace:
+            return out, state
+        return out, {"shift": x[:, -1], "wkv": wkv_out}
+
     def _run(self, x, state, inplace):
         B, T, _ = x.shape
+        if T == 1 and self._native_ok(x, state):
+            return self._native_step(x, state, inplace)
         shape = (B, T, self.heads, self.head_size)
         fused_ok = self._fused(x)
         if fused_ok:

@@ -61,7 +61,7 @@ def test_timemix_abi_exported_and_bound_with_header_arity():
     lib = fused._lib()
     assert lib is not None
     arity = declared_arity(ROOT / "include" / "theseus_timemix.h")
-    assert len(arity) == 10
+    assert len(arity) == 12
     for name, n in arity.items():
         fn = getattr(lib, name)
         assert fn.argtypes is not None and len(fn.argtypes) == n, (name, n)

@@ -175,3 +175,39 @@ def test_captured_step_follows_refreshed_weights():
     assert rel_l2(y_ref.float().cpu(), y_new.float().cpu()) < 1e-3
     assert rel_l2(s_graph["wkv"].cpu(), s_e["wkv"].cpu()) < 1e-4
     assert rel_l2(y_stale.float().cpu(), y_new.float().cpu()) > 2e-2  # (the update matters)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,C,dtype", [(4, 320, torch.bfloat16), (3, 640, torch.float32), (64, 5120, torch.bfloat16)],
+                         ids=["C320", "C640-fp32-weights-autocast", "config4"])
+def test_native_step_equals_the_python_launches(B, C, dtype, monkeypatch):
+    """Inside a parameter store a one-token no-grad step runs as one native call
+    (theseus_tm_serving_step) that launches the same kernels as the layer's Python path:
+    8 tokens in place (step_) and out of place (forward, the reference's serving call) give
+    bitwise the same outputs, WKV state and shift state on both paths."""
+    import contextlib
+    from theseus import fused
+    m = _model(C, seed=31, dtype=dtype)
+    x = torch.randn(B, 8, C, device="cuda", dtype=torch.bfloat16)
+    st0 = {"shift": torch.randn(B, C, device="cuda", dtype=torch.bfloat16),
+           "wkv": .1 * torch.randn(B, C // 64, 64, 64, device="cuda")}
+    ac = (lambda: torch.autocast("cuda", dtype=torch.bfloat16)) if dtype == torch.float32 else contextlib.nullcontext
+    for inplace in (True, False):
+        res = {}
+        for native in ("1", "0"):
+            monkeypatch.setenv("THESEUS_TM_NATIVE", native)
+            store, s, outs = {}, serving_state(st0), []
+            with torch.no_grad(), fused.param_cache(store), ac():
+                for t in range(8):
+                    xt = x[:, t:t + 1].contiguous()
+                    if inplace:
+                        y = m.step_(xt, s)
+                    else:
+                        y, s = m(xt, s)
+                    outs.append(y.clone())
+            torch.cuda.synchronize()
+            assert any(k[0] == "tm_layer" for k in store) == (native == "1")
+            res[native] = (outs, s)
+        (o1, s1), (o0, s0) = res["1"], res["0"]
+        assert all(torch.equal(a, b) for a, b in zip(o1, o0)), inplace
+        assert torch.equal(s1["wkv"], s0["wkv"]) and torch.equal(s1["shift"], s0["shift"]), inplace
