@@ -16,6 +16,8 @@
 #include "../../include/theseus_wkv7.h"
 #include "wkv7_common.h"
 
+#include <algorithm>
+
 namespace tmix {
 using namespace wkv7;
 
@@ -131,8 +133,8 @@ __global__ __launch_bounds__(256) void shift_lerp_fwd(long M, int T, int C, cons
     }
 }
 
-// 1-D grid of ceil(C/(64 SV)) x ceil(M/SLB) waves (channel blocks fastest), SV channels
-// per lane.  A wave walks its SLB tokens in order (the parameter-gradient partials are sums
+// 1-D grid of ceil(C/(64 SV)) x ceil(M/TBk) waves (channel blocks fastest), SV channels
+// per lane.  A wave walks its TBk tokens in order (the parameter-gradient partials are sums
 // over them), UG tokens at a time: all loads of a group -- the six gradient rows of tokens
 // m+1 .. m+UG (token m's are carried over) and the x rows of m .. m+UG-1 (x[m-1] is
 // carried) -- are issued before any is used, and with PF the next group's loads are issued
@@ -143,7 +145,15 @@ __global__ __launch_bounds__(256) void shift_lerp_fwd(long M, int T, int C, cons
 // prefetch and 48 tokens per wave 146 µs (with the partials' reduction), 4-byte rows 152-171,
 // 8-byte rows 149-167, 16-byte rows without prefetch 166-180; forcing more waves per SIMD
 // than the registers allow spills.
-constexpr int SV = 8, UG = 2, SLB = 48;
+//
+// The registers hold one wave per SIMD, and a wave's time grows with its tokens, so TBk is
+// planned (sl_tokens below) to give each SIMD of the device one wave: config 3's 8192 tokens
+// x 10 channel blocks as 100 blocks of 82 tokens (1000 waves, one round) ran in 134 µs where
+// 171 blocks of 48 (1710 waves, two rounds, the second two thirds full) ran in 145 µs;
+// 900 or 960 waves of 92 or 86 tokens, leaving SIMDs idle, 149 and 136 µs.  Shapes that
+// fit two or three waves per SIMD, each planned the same way (8-byte rows; or one token per
+// group, with or without the prefetch), were no faster: 138-159 µs.
+constexpr int SV = 8, UG = 2;
 constexpr bool SPF = true;
 template <int V>
 struct RowT;
@@ -628,7 +638,26 @@ int tm_check(int B, int T, int C) {
 }
 int tm_status() { return hipGetLastError() == hipSuccess ? THESEUS_WKV7_OK : THESEUS_WKV7_ERR_LAUNCH; }
 long nblk_t(int B, int T) { return ((long)B * T + tmix::TB - 1) / tmix::TB; }
-long nblk_sl(int B, int T) { return ((long)B * T + tmix::SLB - 1) / tmix::SLB; }
+int device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n < 1)
+        n = 256;
+    return n;
+}
+// tokens per wave of shift_lerp_bwd: as many token blocks as one round of one wave per SIMD
+// (4 per CU) holds over the channel blocks, but at least 16 tokens per wave (a block's
+// partials, 24 bytes per channel, then cost at most a tenth of its inputs, 14 bytes per
+// channel and token)
+long sl_tokens(int B, int T, int C) {
+    const long M = (long)B * T, nbx = (C + 64 * tmix::SV - 1) / (64 * tmix::SV);
+    const long per_round = std::max(1L, 4L * device_cus() / nbx);
+    return std::max(std::min(16L, M), (M + per_round - 1) / per_round);
+}
+long nblk_sl(int B, int T, int C) {
+    const long tb = sl_tokens(B, T, C);
+    return ((long)B * T + tb - 1) / tb;
+}
 }  // namespace
 
 extern "C" {
@@ -647,7 +676,7 @@ int theseus_tm_shift_lerp_fwd(int B, int T, int C, const void* x, const void* st
 }
 
 size_t theseus_tm_shift_lerp_workspace(int B, int T, int C) {
-    return tm_check(B, T, C) ? 0 : (size_t)nblk_sl(B, T) * 6 * C * sizeof(float);
+    return tm_check(B, T, C) ? 0 : (size_t)nblk_sl(B, T, C) * 6 * C * sizeof(float);
 }
 
 int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const void* x, const void* st,
@@ -659,10 +688,10 @@ int theseus_tm_shift_lerp_bwd(int B, int T, int C, const void* const* dm, const 
         if (!dm[n]) return THESEUS_WKV7_ERR_NULL;
     if (!ws || ws_bytes < theseus_tm_shift_lerp_workspace(B, T, C)) return THESEUS_WKV7_ERR_WORKSPACE;
     const long M = (long)B * T;
-    const int nb = (int)nblk_sl(B, T);
+    const int nb = (int)nblk_sl(B, T, C), tb = (int)sl_tokens(B, T, C);
     hipLaunchKernelGGL((tmix::shift_lerp_bwd<tmix::SV, tmix::UG, tmix::SPF>),
                        dim3((unsigned)((C + 64 * tmix::SV - 1) / (64 * tmix::SV) * (long)nb)), dim3(64), 0, stream, M,
-                       T, C, tmix::SLB, (const uint16_t*)dm[0], (const uint16_t*)dm[1], (const uint16_t*)dm[2],
+                       T, C, tb, (const uint16_t*)dm[0], (const uint16_t*)dm[1], (const uint16_t*)dm[2],
                        (const uint16_t*)dm[3], (const uint16_t*)dm[4], (const uint16_t*)dm[5],
                        (const uint16_t*)x, (const uint16_t*)st, coef, (uint16_t*)dx, (uint16_t*)dshift, ws);
     tmix::Outs o6{{dcoef, dcoef + C, dcoef + 2 * C, dcoef + 3 * C, dcoef + 4 * C, dcoef + 5 * C}};
