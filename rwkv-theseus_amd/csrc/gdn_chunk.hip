@@ -94,8 +94,10 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
     __shared__ float vsh[GC][NK + 4];
 
     const bool tv = r16 < L;
-    const float gt = tv ? g[(tok0 + r16) * H + h] : 0.f;
-    const float bt = tv ? beta[(tok0 + r16) * H + h] : 0.f;
+    const int tl = tv ? r16 : 0;  // (clamped: every lane loads, lane_mask in wkv7_io.h)
+    const float g_ = g[(tok0 + tl) * H + h], b_ = beta[(tok0 + tl) * H + h];
+    const uint32_t tm = lane_mask(tv);
+    const float gt = keep(tm, g_), bt = keep(tm, b_);
     const float gam = row_prefix_sum(gt);
     const float gm1 = row_prev(gam, 0.f);
     const float gL = row_last(gam);
@@ -103,26 +105,20 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
         const int c0 = 32 * ks + 4 * q4;
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4*>(&vsh[r16][c0]) = tv ? ld4f(v + row(r16) + c0) : z;
-        *reinterpret_cast<float4*>(&vsh[r16][c0 + 16]) = tv ? ld4f(v + row(r16) + c0 + 16) : z;
+        *reinterpret_cast<float4*>(&vsh[r16][c0]) = keep4(tm, ld4f(v + row(tl) + c0));
+        *reinterpret_cast<float4*>(&vsh[r16][c0 + 16]) = keep4(tm, ld4f(v + row(tl) + c0 + 16));
     }
     float kr[KS][8], qr[KS][8];
     float ssk = 0.f, ssq = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
         const int c0 = 32 * ks + 4 * q4;
-        if (tv) {
-            const float4 a = ld4f(k + row(r16) + c0), b = ld4f(k + row(r16) + c0 + 16);
-            const float4 x = ld4f(q + row(r16) + c0), y = ld4f(q + row(r16) + c0 + 16);
-            kr[ks][0] = a.x, kr[ks][1] = a.y, kr[ks][2] = a.z, kr[ks][3] = a.w;
-            kr[ks][4] = b.x, kr[ks][5] = b.y, kr[ks][6] = b.z, kr[ks][7] = b.w;
-            qr[ks][0] = x.x, qr[ks][1] = x.y, qr[ks][2] = x.z, qr[ks][3] = x.w;
-            qr[ks][4] = y.x, qr[ks][5] = y.y, qr[ks][6] = y.z, qr[ks][7] = y.w;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++) kr[ks][e] = qr[ks][e] = 0.f;
-        }
+        const float4 a = keep4(tm, ld4f(k + row(tl) + c0)), b = keep4(tm, ld4f(k + row(tl) + c0 + 16));
+        const float4 x = keep4(tm, ld4f(q + row(tl) + c0)), y = keep4(tm, ld4f(q + row(tl) + c0 + 16));
+        kr[ks][0] = a.x, kr[ks][1] = a.y, kr[ks][2] = a.z, kr[ks][3] = a.w;
+        kr[ks][4] = b.x, kr[ks][5] = b.y, kr[ks][6] = b.z, kr[ks][7] = b.w;
+        qr[ks][0] = x.x, qr[ks][1] = x.y, qr[ks][2] = x.z, qr[ks][3] = x.w;
+        qr[ks][4] = y.x, qr[ks][5] = y.y, qr[ks][6] = y.z, qr[ks][7] = y.w;
 #pragma unroll
         for (int e = 0; e < 8; e++) ssk += kr[ks][e] * kr[ks][e], ssq += qr[ks][e] * qr[ks][e];
     }
@@ -219,7 +215,8 @@ __global__ __launch_bounds__(64) void gdn_prep(int Tn, int H, int qk_norm, const
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int t = 4 * q4 + e;
-                const float kv = t < L ? io<TI>::ld(krow[e], 16 * tj) * gsh[3][t] : 0.f;
+                const float kx = io<TI>::ld(krow[e], 16 * tj);  // (krow: clamped)
+                const float kv = keep(lane_mask(t < L), kx) * gsh[3][t];  // (gsh[3]: 0 past the end)
                 at[e] = kv * ea[e];
                 bhat[e] = kv * eb[e];
                 khat[e] = kv * ek[e];
@@ -270,16 +267,16 @@ __global__ __launch_bounds__(64) void wkv7_rec_prep(int Tn, int H, const bf16_t*
     const int lane = threadIdx.x, q4 = lane >> 4, r16 = lane & 15;
     const int t0 = c * GC, L = min(GC, Tn - t0);
     const long tok0 = (long)bb * Tn + t0;
-    const long row = ((tok0 + r16) * H + h) * (long)NK;  // token r16's row (read only when r16 < L)
     const bool tv = r16 < L;
+    const long row = ((tok0 + (tv ? r16 : 0)) * H + h) * (long)NK;  // token r16's row (clamped: every lane loads)
+    const uint32_t tm = lane_mask(tv);
     // A~, B^, K^ as rows [t][j] for the D-layout reads; v as rows [t][i]
     __shared__ __attribute__((aligned(16))) float pa[GC][LP], pb[GC][LP], pkh[GC][LP], vsh[GC][LP];
     uint8_t* const rec = ws + ((size_t)bh * nchunk + c) * R::BYTES;
     f32x4_t Aab = zero4(), AabT = zero4(), Aak = zero4(), BrbT = zero4(), BrkT = zero4();
     float rt[KS][8];  // R~ of the lane's keys, kept for P2
     auto ld8 = [&](const bf16_t* x, int c0, float (&o)[8]) {
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 p = tv ? ld4f(x + row + c0) : z, q = tv ? ld4f(x + row + c0 + 16) : z;
+        const float4 p = keep4(tm, ld4f(x + row + c0)), q = keep4(tm, ld4f(x + row + c0 + 16));
         o[0] = p.x, o[1] = p.y, o[2] = p.z, o[3] = p.w, o[4] = q.x, o[5] = q.y, o[6] = q.z, o[7] = q.w;
     };
     auto st8 = [&](float (*pl)[LP], int c0, const float (&x)[8]) {

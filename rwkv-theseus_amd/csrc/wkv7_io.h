@@ -75,6 +75,26 @@ __device__ __forceinline__ void dma_kb(uint32_t lds_off, i32x4_t rs, uint32_t vo
 }
 #pragma clang diagnostic pop
 
+// Rows past a chunk's valid steps are read from a clamped (valid) address and zeroed after
+// the load by a lane mask, never loaded under a condition: a load inside a branch makes
+// the compiler wait, before the branch joins, for every load the wave issued before it, so
+// a run of such loads becomes one memory round trip after another (measured: the first
+// 20 k cycles of the head-size-128 chunk-gradient kernel's 64 k).  A plain `ok ? x : 0` of
+// a loaded x is no cure: the compiler turns such a select back into a branch around the
+// load, so the mask is hidden from it and applied with an AND.
+__device__ __forceinline__ uint32_t lane_mask(bool ok) {
+    uint32_t m = ok ? 0xffffffffu : 0u;
+    asm("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ float keep(uint32_t m, float x) { return __uint_as_float(__float_as_uint(x) & m); }
+__device__ __forceinline__ float4 keep4(uint32_t m, const float4& x) {
+    return make_float4(keep(m, x.x), keep(m, x.y), keep(m, x.z), keep(m, x.w));
+}
+__device__ __forceinline__ uint4 keepu4(uint32_t m, const uint4& x) {
+    return make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
+}
+
 // four consecutive elements as float
 __device__ __forceinline__ float4 ld4f(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 ld4f(const bf16_t* p) {

@@ -74,13 +74,13 @@ __global__ __launch_bounds__(64) void wkv7_bwd_prep(int Tn, int H, const bf16_t*
     const int bb = bh / H, h = bh - bb * H;
     const int lane = threadIdx.x, q4 = lane >> 4, r16 = lane & 15;
     const int t0 = c * BC, L = min(BC, Tn - t0);
-    const long row = (((long)bb * Tn + t0 + r16) * H + h) * (long)BNK;
     const bool tv = r16 < L;
+    const long row = (((long)bb * Tn + t0 + (tv ? r16 : 0)) * H + h) * (long)BNK;  // (clamped: read by every lane)
+    const uint32_t tm = lane_mask(tv);
     __shared__ __attribute__((aligned(16))) float pa[BC][LP], pr[BC][LP];  // A~, R~ [t][j]
     uint8_t* const rec = ws + ((size_t)bh * nchunk + c) * R::BYTES;
     auto ld8 = [&](const bf16_t* x, int c0, float (&o)[8]) {
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 p = tv ? ld4f(x + row + c0) : z, q = tv ? ld4f(x + row + c0 + 16) : z;
+        const float4 p = keep4(tm, ld4f(x + row + c0)), q = keep4(tm, ld4f(x + row + c0 + 16));
         o[0] = p.x, o[1] = p.y, o[2] = p.z, o[3] = p.w, o[4] = q.x, o[5] = q.y, o[6] = q.z, o[7] = q.w;
     };
     auto st8 = [&](float (*pl)[LP], int c0, const float (&x)[8]) {
@@ -171,14 +171,26 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, int 
         const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)recs[buf];
         for (int j = wv; j < R::DMA_BLOCKS; j += 4) dma_kb(base + 1024 * j, rs, (uint32_t)(1024 * j + 16 * lane), so);
     };
-    // dY[t0 + 4q4 + e][i_own] (zero past the end)
-    auto load_dy = [&](int c, float (&o)[4]) {
+    // dY[t0 + 4q4 + e][i_own], loaded a chunk ahead as raw element bits: rows past the end
+    // read row t0, and the bits are widened and zeroed where they are used (dy_of), so
+    // nothing waits on the loads until the chunk's closing vm_wait0
+    auto load_dy = [&](int c, uint32_t (&o)[4]) {
         const int t0 = c * BC, L = min(BC, Tn - t0);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int t = 4 * q4 + e;
-            o[e] = t < L ? io<TI>::ld(dy, (((long)bb * Tn + t0 + t) * H + h) * BNK + i_own) : 0.f;
+            const int t = 4 * q4 + e, tc = t < L ? t : 0;
+            const long i = (((long)bb * Tn + t0 + tc) * H + h) * BNK + i_own;
+            if constexpr (sizeof(TI) == 2) o[e] = reinterpret_cast<const uint16_t*>(dy)[i];
+            else o[e] = reinterpret_cast<const uint32_t*>(dy)[i];
         }
+    };
+    auto dy_of = [&](int c, const uint32_t (&o)[4]) {
+        const int L = min(BC, Tn - c * BC);
+        f32x4_t d;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            d[e] = keep(lane_mask(4 * q4 + e < L), __uint_as_float(sizeof(TI) == 2 ? o[e] << 16 : o[e]));
+        return d;
     };
     fetch(nchunk - 1, 0);
     f32x4_t Ht[BTJ];
@@ -194,14 +206,17 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, int 
             Ht[tj] = f32x4_t{x.x, x.y, x.z, x.w};
         }
     }
-    float dyn[4];
+    uint32_t dyn[4];
     load_dy(nchunk - 1, dyn);
     vm_wait0();
     __syncthreads();
     for (int c = nchunk - 1, it = 0; c >= 0; c--, it++) {
+        // (this chunk's dY, complete since the last vm_wait0, taken before the next
+        // record's DMA is issued: a wait for it after the DMA would wait for the DMA too)
+        const f32x4_t dyc = dy_of(c, dyn);
+        asm volatile("" ::"v"(dyc[0]), "v"(dyc[1]), "v"(dyc[2]), "v"(dyc[3]));  // (formed before the DMA below)
         if (c > 0) fetch(c - 1, (it + 1) & 1);
         const uint8_t* const rec = recs[it & 1];
-        const f32x4_t dyc = {dyn[0], dyn[1], dyn[2], dyn[3]};
         if (c > 0) load_dy(c - 1, dyn);
         float* const hout = hbuf + ((long)bh * nchunk + c) * BNN + (long)i_own * BNK + 4 * q4;
 #pragma unroll
@@ -271,12 +286,12 @@ __device__ __forceinline__ void get_split(const SplitPlane& P, int lane, int ks,
     h = make_uint4(a.x, a.y, b.x, b.y);
     l = make_uint4(x.x, x.y, y.x, y.y);
 }
-// the same fragment of a bf16 row in memory (exact: no lo part), zero when !ok
+// the same fragment of a bf16 row in memory (exact: no lo part), zero when !ok (the row
+// is read either way: the caller passes a valid one)
 __device__ __forceinline__ uint4 bf16_frag(const bf16_t* row, int ks, int q4, bool ok) {
-    if (!ok) return make_uint4(0, 0, 0, 0);
     const uint2 a = *reinterpret_cast<const uint2*>(row + 32 * ks + 4 * q4);
     const uint2 b = *reinterpret_cast<const uint2*>(row + 32 * ks + 16 + 4 * q4);
-    return make_uint4(a.x, a.y, b.x, b.y);
+    return keepu4(lane_mask(ok), make_uint4(a.x, a.y, b.x, b.y));
 }
 struct ChunkLds {
     SplitPlane At, Bm, Km, Rt, Bh, Kh;  // [t][j], written by the key owners
@@ -330,9 +345,10 @@ __global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int
     for (int e = 0; e < 4; e++) {
         const int t = 4 * q4 + e;
         const bool ok = t < L;
-        const long o = at_tok(ok ? t : 0) + col;
-        xr[e] = ok ? bf2f(r, o) : 0.f, xw[e] = ok ? bf2f(w, o) : 0.f, xk[e] = ok ? bf2f(k, o) : 0.f;
-        xa[e] = ok ? bf2f(a, o) : 0.f, xb[e] = ok ? bf2f(b, o) : 0.f;
+        const long o = at_tok(ok ? t : 0) + col;  // (clamped: every lane loads)
+        const float r_ = bf2f(r, o), w_ = bf2f(w, o), k_ = bf2f(k, o), a_ = bf2f(a, o), b_ = bf2f(b, o);
+        const uint32_t m = lane_mask(ok);
+        xr[e] = keep(m, r_), xw[e] = keep(m, w_), xk[e] = keep(m, k_), xa[e] = keep(m, a_), xb[e] = keep(m, b_);
     }
     float ld[4], p[4];
 #pragma unroll
@@ -406,8 +422,10 @@ __global__ __launch_bounds__(512) void wkv7_bwd_chunk(int Tn, int H, int BH, int
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int t = 4 * q4 + e;
-        vD[e] = t < L ? bf2f(v, at_tok(t) + col) : 0.f;
-        dyD[e] = t < L ? bf2f(dy, at_tok(t) + col) : 0.f;
+        const long o = at_tok(t < L ? t : 0) + col;
+        const float v_ = bf2f(v, o), y_ = bf2f(dy, o);
+        vD[e] = keep(lane_mask(t < L), v_);
+        dyD[e] = keep(lane_mask(t < L), y_);
     }
     const Pk pV = pk(vD), pdY = pk(dyD);
     const f32x4_t SA = mm16s(pTiT, pk(P1 + mm16s(pAakT, pV)));  // Ti (A~ S0^T + Aak V)
@@ -547,8 +565,10 @@ __global__ __launch_bounds__(64) void gdn_bwd_prep(int Tn, int H, const TI* __re
     const float rs = 1.f / __builtin_sqrtf((float)BNK);
     __shared__ float gsh[3][BC];  // gamma_t, gamma_{t-1}, beta_t (past the end: 0)
     const bool tv = r16 < L;
-    const float gt = tv ? g[(tok0 + r16) * H + h] : 0.f;
-    const float bt = tv ? beta[(tok0 + r16) * H + h] : 0.f;
+    const int tl = tv ? r16 : 0;  // (clamped: every lane loads)
+    const float g_ = g[(tok0 + tl) * H + h], b_ = beta[(tok0 + tl) * H + h];
+    const uint32_t tm = lane_mask(tv);
+    const float gt = keep(tm, g_), bt = keep(tm, b_);
     const float gam = row_prefix_sum(gt), gm1 = row_prev(gam, 0.f), gL = row_last(gam);
     if (q4 == 0) gsh[0][r16] = gam, gsh[1][r16] = gm1, gsh[2][r16] = bt;
     uint8_t* const rec = ws + ((size_t)bh * nchunk + c) * R::BYTES;
@@ -557,9 +577,8 @@ __global__ __launch_bounds__(64) void gdn_bwd_prep(int Tn, int H, const TI* __re
 #pragma unroll
     for (int ks = 0; ks < BKS; ks++) {
         const int c0 = 32 * ks + 4 * q4;
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 ka = tv ? ld4f(k + row(r16) + c0) : z, kb = tv ? ld4f(k + row(r16) + c0 + 16) : z;
-        const float4 qa = tv ? ld4f(q + row(r16) + c0) : z, qb = tv ? ld4f(q + row(r16) + c0 + 16) : z;
+        const float4 ka = keep4(tm, ld4f(k + row(tl) + c0)), kb = keep4(tm, ld4f(k + row(tl) + c0 + 16));
+        const float4 qa = keep4(tm, ld4f(q + row(tl) + c0)), qb = keep4(tm, ld4f(q + row(tl) + c0 + 16));
         const float kr[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
         const float qr[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         float br8[8];
@@ -652,7 +671,9 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
     // the token scalars (wave 0)
     if (wv == 0) {
         const bool tv = r16 < L;
-        const float gt = tv ? g[(tok0 + r16) * H + h] : 0.f, bt = tv ? beta[(tok0 + r16) * H + h] : 0.f;
+        const int tl = tv ? r16 : 0;  // (clamped: every lane loads)
+        const float g_ = g[(tok0 + tl) * H + h], b_ = beta[(tok0 + tl) * H + h];
+        const float gt = keep(lane_mask(tv), g_), bt = keep(lane_mask(tv), b_);
         const float gam = row_prefix_sum(gt), gm1 = row_prev(gam, 0.f);
         if (q4 == 0) sm.gam[r16] = gam, sm.gm1[r16] = gm1, sm.beta[r16] = bt;
     }
@@ -674,8 +695,10 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
     for (int e = 0; e < 4; e++) {
         const int t = 4 * q4 + e;
         const bool ok = t < L;
-        kD[e] = ok ? io<TI>::ld(k, at_tok(t) + col) : 0.f;
-        rD[e] = ok ? io<TI>::ld(q, at_tok(t) + col) * rs : 0.f;
+        const long o = at_tok(ok ? t : 0) + col;  // (clamped: every lane loads)
+        const float k_ = io<TI>::ld(k, o), q_ = io<TI>::ld(q, o);
+        kD[e] = keep(lane_mask(ok), k_);
+        rD[e] = keep(lane_mask(ok), q_) * rs;
     }
     put_split(sm.K, kD, lane, wv), put_split(sm.R, rD, lane, wv);
 #pragma unroll
@@ -744,9 +767,11 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int t = 4 * q4 + e;
-        vraw[e] = t < L ? io<TI>::ld(v, at_tok(t) + col) : 0.f;
+        const long o = at_tok(t < L ? t : 0) + col;
+        const float v_ = io<TI>::ld(v, o), y_ = io<TI>::ld(dy, o);
+        vraw[e] = keep(lane_mask(t < L), v_);
         vD[e] = br[e] * vraw[e];
-        dyD[e] = t < L ? io<TI>::ld(dy, at_tok(t) + col) : 0.f;
+        dyD[e] = keep(lane_mask(t < L), y_);
     }
     const Pk pV = pk(vD), pdY = pk(dyD);
     const f32x4_t SA = mm16s(pTiT, pk(P1 + mm16s(pAakT, pV)));
@@ -779,10 +804,10 @@ __global__ __launch_bounds__(512) void gdn_bwd_chunk(int Tn, int H, int BH, int 
     for (int ks = 0; ks < BKS; ks++) {
         float fv[8], fy[8];
         {
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
             const long o = at_tok(tv ? r16 : 0) + 32 * ks + 4 * q4;
-            const float4 v0 = tv ? ld4f(v + o) : z, v1 = tv ? ld4f(v + o + 16) : z;
-            const float4 y0 = tv ? ld4f(dy + o) : z, y1 = tv ? ld4f(dy + o + 16) : z;
+            const uint32_t m = lane_mask(tv);
+            const float4 v0 = keep4(m, ld4f(v + o)), v1 = keep4(m, ld4f(v + o + 16));
+            const float4 y0 = keep4(m, ld4f(dy + o)), y1 = keep4(m, ld4f(dy + o + 16));
             fv[0] = v0.x, fv[1] = v0.y, fv[2] = v0.z, fv[3] = v0.w, fv[4] = v1.x, fv[5] = v1.y, fv[6] = v1.z, fv[7] = v1.w;
             fy[0] = y0.x, fy[1] = y0.y, fy[2] = y0.z, fy[3] = y0.w, fy[4] = y1.x, fy[5] = y1.y, fy[6] = y1.z, fy[7] = y1.w;
 #pragma unroll
