@@ -12,6 +12,7 @@
 // flight at once), so every head of a B=64, H=80 step is resident at once; for
 // larger N it is 256 lanes (G = 16).
 #include "wkv7_common.h"
+#include "wkv7_io.h"
 
 namespace wkv7 {
 
@@ -35,13 +36,18 @@ __global__ __launch_bounds__(16 * G) void decode_step(
     for (int m = 0; m < MM; m++)
 #pragma unroll
         for (int e = 0; e < VEC; e++) {
+            // keys past N read key 0 and are masked after the load (a load under a branch
+            // would wait for every earlier load of the wave)
             const int j = VEC * (l16 + 16 * m) + e;
             const bool ok = j < N;
-            kr[m][e] = ok ? io<T>::ld(r, o + j) : 0.f;
-            kd[m][e] = ok ? decay_of<MODE>(io<T>::ld(w, o + j)) : 1.f;
-            kk[m][e] = ok ? io<T>::ld(k, o + j) : 0.f;
-            ka[m][e] = ok ? io<T>::ld(a, o + j) : 0.f;
-            kb[m][e] = ok ? io<T>::ld(b, o + j) : 0.f;
+            const long jj = o + (ok ? j : 0);
+            const uint32_t mk = lane_mask(ok);
+            kr[m][e] = keep(mk, io<T>::ld(r, jj));
+            const float dd = decay_of<MODE>(io<T>::ld(w, jj));
+            kd[m][e] = __uint_as_float((__float_as_uint(dd) & mk) | (0x3f800000u & ~mk));  // 1 past N
+            kk[m][e] = keep(mk, io<T>::ld(k, jj));
+            ka[m][e] = keep(mk, io<T>::ld(a, jj));
+            kb[m][e] = keep(mk, io<T>::ld(b, jj));
         }
     for (int r0 = 0; r0 < RR; r0 += RB) {
         // the batch's state elements are all loaded before any is stored (so the loads are
@@ -54,21 +60,24 @@ __global__ __launch_bounds__(16 * G) void decode_step(
             for (int m = 0; m < MM; m++) {
                 const int j0 = VEC * (l16 + 16 * m);
                 if constexpr (VEC == 4) {
-                    if (i < N && j0 < N) {
-                        const float4 x = *reinterpret_cast<const float4*>(S + (long)i * N + j0);
-                        s[rr][m][0] = x.x; s[rr][m][1] = x.y; s[rr][m][2] = x.z; s[rr][m][3] = x.w;
-                    } else {
-                        s[rr][m][0] = s[rr][m][1] = s[rr][m][2] = s[rr][m][3] = 0.f;
-                    }
+                    const bool ok = i < N && j0 < N;
+                    const float4 x = keep4(lane_mask(ok), *reinterpret_cast<const float4*>(S + (ok ? (long)i * N + j0 : 0)));
+                    s[rr][m][0] = x.x; s[rr][m][1] = x.y; s[rr][m][2] = x.z; s[rr][m][3] = x.w;
                 } else {
 #pragma unroll
-                    for (int e = 0; e < VEC; e++) s[rr][m][e] = (i < N && j0 + e < N) ? S[(long)i * N + j0 + e] : 0.f;
+                    for (int e = 0; e < VEC; e++) {
+                        const bool ok = i < N && j0 + e < N;
+                        s[rr][m][e] = keep(lane_mask(ok), S[ok ? (long)i * N + j0 + e : 0]);
+                    }
                 }
             }
         }
         float vi[RB];
 #pragma unroll
-        for (int rr = 0; rr < RB; rr++) vi[rr] = (G * (r0 + rr) + grp < N) ? io<T>::ld(v, o + G * (r0 + rr) + grp) : 0.f;
+        for (int rr = 0; rr < RB; rr++) {
+            const int i = G * (r0 + rr) + grp;
+            vi[rr] = keep(lane_mask(i < N), io<T>::ld(v, o + (i < N ? i : 0)));
+        }
 
 #pragma unroll
         for (int rr = 0; rr < RB; rr++) {

@@ -19,6 +19,7 @@
 // [value][key]: lane i then reads and writes element (j, i) at j*N + i, which is
 // coalesced across lanes.  Saved states always use [value][key].
 #include "wkv7_common.h"
+#include "wkv7_io.h"
 
 namespace wkv7 {
 
@@ -127,9 +128,20 @@ __global__ __launch_bounds__(NP) void seq_backward(
     // G row `tid` (gradient w.r.t. the state), kept in registers; element (i, j) of a
     // caller state at i*ei + j*ej ([value][key], or [key][value] when kv)
     const long ei = kv ? 1 : N, ej = kv ? N : 1;
+    // (edge lanes and columns read element 0 and are masked after the load, here and below:
+    // a load under a branch is waited for inside it, one after another)
+    const int tc = lane_ok ? tid : 0;
+    const uint32_t lm = lane_mask(lane_ok);
     float g[NP];
 #pragma unroll
-    for (int j = 0; j < NP; j++) g[j] = (lane_ok && j < N && dsT) ? dsT[bh * NN + tid * ei + j * ej] : 0.f;
+    for (int j = 0; j < NP; j++) g[j] = 0.f;
+    if (dsT) {
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const bool ok = lane_ok && j < N;
+            g[j] = keep(lane_mask(ok), dsT[bh * NN + (ok ? tid * ei + j * ej : 0)]);
+        }
+    }
 
     const int nseg = (Tn + CKPT - 1) / CKPT;
     for (int c = nseg - 1; c >= 0; c--) {
@@ -139,7 +151,10 @@ __global__ __launch_bounds__(NP) void seq_backward(
         // ---- replay the segment forward, storing states and sa into ws ----
         float st[NP];
 #pragma unroll
-        for (int j = 0; j < NP; j++) st[j] = (lane_ok && j < N) ? ckpt[(bh * ncp + c) * NN + (long)tid * N + j] : 0.f;
+        for (int j = 0; j < NP; j++) {
+            const bool ok = lane_ok && j < N;
+            st[j] = keep(lane_mask(ok), ckpt[(bh * ncp + c) * NN + (ok ? (long)tid * N + j : 0)]);
+        }
         if (lane_ok) {
 #pragma unroll
             for (int j = 0; j < NP; j++)
@@ -147,17 +162,15 @@ __global__ __launch_bounds__(NP) void seq_backward(
         }
         for (int u = 0; u < L; u++) {
             const long o = ((long)(bb * Tn + t0 + u) * H + h) * N;
+            const float xw = io<T>::ld(w, o + tc), xk = io<T>::ld(k, o + tc), xa = io<T>::ld(a, o + tc);
+            const float xb = io<T>::ld(b, o + tc), vi = keep(lm, io<T>::ld(v, o + tc));
             __syncthreads();
-            if (lane_ok) {
-                vd[tid] = decay_of<MODE>(io<T>::ld(w, o + tid));
-                vk[tid] = io<T>::ld(k, o + tid);
-                va[tid] = io<T>::ld(a, o + tid);
-                vb[tid] = io<T>::ld(b, o + tid);
-            } else {
-                vd[tid] = 1.f; vk[tid] = 0.f; va[tid] = 0.f; vb[tid] = 0.f;
-            }
+            const float dd = decay_of<MODE>(xw);
+            vd[tid] = __uint_as_float((__float_as_uint(dd) & lm) | (0x3f800000u & ~lm));  // (1 past N)
+            vk[tid] = keep(lm, xk);
+            va[tid] = keep(lm, xa);
+            vb[tid] = keep(lm, xb);
             __syncthreads();
-            const float vi = lane_ok ? io<T>::ld(v, o + tid) : 0.f;
             float sa = 0.f;
 #pragma unroll
             for (int j = 0; j < NP; j++) sa += st[j] * va[j];
@@ -173,22 +186,21 @@ __global__ __launch_bounds__(NP) void seq_backward(
         // ---- adjoint, reverse over the segment ----
         for (int u = L - 1; u >= 0; u--) {
             const long o = ((long)(bb * Tn + t0 + u) * H + h) * N;
-            __syncthreads();  // previous column phase done with the vectors / G^T
-            if (lane_ok) {
-                const float wv = io<T>::ld(w, o + tid);
-                const float dd = decay_of<MODE>(wv);
-                vr[tid] = io<T>::ld(r, o + tid);
-                vd[tid] = dd;
-                vf[tid] = dw_factor<MODE>(wv, dd);
-                vk[tid] = io<T>::ld(k, o + tid);
-                va[tid] = io<T>::ld(a, o + tid);
-                vb[tid] = io<T>::ld(b, o + tid);
-                vdy[tid] = io<T>::ld(dy, o + tid);
-                vv[tid] = io<T>::ld(v, o + tid);
-                vsa[tid] = wsa[(long)u * N + tid];
-            } else {
-                vr[tid] = 0.f; vd[tid] = 1.f; vf[tid] = 0.f; vk[tid] = 0.f; va[tid] = 0.f;
-                vb[tid] = 0.f; vdy[tid] = 0.f; vv[tid] = 0.f; vsa[tid] = 0.f;
+            {
+                const float wv = io<T>::ld(w, o + tc), xr = io<T>::ld(r, o + tc), xk = io<T>::ld(k, o + tc);
+                const float xa = io<T>::ld(a, o + tc), xb = io<T>::ld(b, o + tc), xy = io<T>::ld(dy, o + tc);
+                const float xv = io<T>::ld(v, o + tc), xs = wsa[(long)u * N + tc];
+                const float dd = decay_of<MODE>(wv), df = dw_factor<MODE>(wv, dd);
+                __syncthreads();  // previous column phase done with the vectors / G^T
+                vr[tid] = keep(lm, xr);
+                vd[tid] = __uint_as_float((__float_as_uint(dd) & lm) | (0x3f800000u & ~lm));  // (1 past N)
+                vf[tid] = keep(lm, df);
+                vk[tid] = keep(lm, xk);
+                va[tid] = keep(lm, xa);
+                vb[tid] = keep(lm, xb);
+                vdy[tid] = keep(lm, xy);
+                vv[tid] = keep(lm, xv);
+                vsa[tid] = keep(lm, xs);
             }
             __syncthreads();
             // row phase (lane = value row i): G += dy_i r^T; q_i; dv_i.
@@ -217,9 +229,9 @@ __global__ __launch_bounds__(NP) void seq_backward(
                     float spv[16], snv[16];
 #pragma unroll
                     for (int u = 0; u < 16; u++) {
-                        const int i = i0 + u;
-                        spv[u] = i < N ? Sp[(long)i * N + j] : 0.f;
-                        snv[u] = i < N ? Sn[(long)i * N + j] : 0.f;
+                        const int i = i0 + u < N ? i0 + u : 0;  // (rows past N: read row 0, unused)
+                        spv[u] = Sp[(long)i * N + j];
+                        snv[u] = Sn[(long)i * N + j];
                     }
 #pragma unroll
                     for (int u = 0; u < 16; u++) {
