@@ -29,6 +29,14 @@ __device__ __forceinline__ void vm_wait10() {
     __builtin_amdgcn_s_waitcnt(0x0f7a);
     asm volatile("" ::: "memory");
 }
+// vmcnt(N): all but this wave's last N memory operations done (gfx9 encoding: vmcnt bits
+// 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void vm_wait_n() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
 
 // Raw-buffer descriptor for a tensor of `bytes` bytes (gfx9 word 3:
 // 0x00020000).  Accesses at byte offsets >= bytes are dropped (stores) or read
