@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, int 
     };
     // dY[t0 + 4q4 + e][i_own], loaded a chunk ahead as raw element bits: rows past the end
     // read row t0, and the bits are widened and zeroed where they are used (dy_of), so
-    // nothing waits on the loads until the chunk's closing vm_wait0
+    // nothing waits on the loads until the chunk's closing wait
     auto load_dy = [&](int c, uint32_t (&o)[4]) {
         const int t0 = c * BC, L = min(BC, Tn - t0);
 #pragma unroll
@@ -209,15 +209,14 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, int 
     uint32_t dyn[4];
     load_dy(nchunk - 1, dyn);
     vm_wait0();
+    f32x4_t dyc = dy_of(nchunk - 1, dyn);  // this chunk's dY (the next chunk's is formed after each chunk's wait)
     __syncthreads();
     for (int c = nchunk - 1, it = 0; c >= 0; c--, it++) {
-        // (this chunk's dY, complete since the last vm_wait0, taken before the next
-        // record's DMA is issued: a wait for it after the DMA would wait for the DMA too)
-        const f32x4_t dyc = dy_of(c, dyn);
-        asm volatile("" ::"v"(dyc[0]), "v"(dyc[1]), "v"(dyc[2]), "v"(dyc[3]));  // (formed before the DMA below)
         if (c > 0) fetch(c - 1, (it + 1) & 1);
         const uint8_t* const rec = recs[it & 1];
         if (c > 0) load_dy(c - 1, dyn);
+        // H at the chunk's end, stored after the next record's DMA and left in flight by the
+        // closing wait (vmcnt(BTJ): a vmcnt(0) there had waited for these stores every chunk)
         float* const hout = hbuf + ((long)bh * nchunk + c) * BNN + (long)i_own * BNK + 4 * q4;
 #pragma unroll
         for (int tj = 0; tj < BTJ; tj++)
@@ -244,7 +243,11 @@ __global__ __launch_bounds__(256) void wkv7_bwd_scan(int Tn, int H, int BH, int 
             const f32x4_t eg = *reinterpret_cast<const f32x4_t*>(rec + R::EL + 4 * (16 * tj + 4 * q4));
             Ht[tj] = mma32(mma32(mma32(Ht[tj] * eg, ah, bhi), ah, blo), al, bhi);
         }
-        vm_wait0();
+        vm_wait_n<BTJ>();  // the next record and the dY loads after it have landed (only the stores may not)
+        // the next chunk's dY, formed here where its loads are known complete (formed at the
+        // top of the loop, the compiler's own wait there, merged with the path into the loop,
+        // would have waited for these stores too)
+        if (c > 0) dyc = dy_of(c - 1, dyn);
         __syncthreads();
     }
 #pragma unroll
