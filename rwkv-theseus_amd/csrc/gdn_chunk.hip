@@ -452,11 +452,25 @@ __global__ __launch_bounds__(256) void gdn_scan(int Tn, int H, int BH, int kv, c
     vm_wait0();
     __syncthreads();
     const long ncp = nchunk + 1;  // saved states per head
-    auto save = [&](int slot) {     // (whole float4 rows of the state)
+    // The wave's 16 rows of a saved state are 16 * NK contiguous floats; regrouped through
+    // LDS, each of its TJ stores writes 1 KB of them (from the registers, each would write
+    // 64-byte pieces of 16 rows)
+    constexpr int SQ = NK + 4;  // padded row (floats)
+    __shared__ __attribute__((aligned(16))) float sq[SPLIT ? 1 : 4][SPLIT ? 4 : 16 * SQ];
+    auto save = [&](int slot) {
+        if constexpr (!SPLIT) {
+            float* const q = sq[wv];
 #pragma unroll
-        for (int tj = 0; tj < TJ; tj++)
-            *reinterpret_cast<float4*>(ckpt + ((long)bh * ncp + slot) * NN + (long)i_own * NK + 16 * tj + 4 * q4) =
-                make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+            for (int tj = 0; tj < TJ; tj++)
+                *reinterpret_cast<float4*>(q + r16 * SQ + 16 * tj + 4 * q4) =
+                    make_float4(St[tj][0], St[tj][1], St[tj][2], St[tj][3]);
+            float* const dst = ckpt + ((long)bh * ncp + slot) * NN + (long)(16 * rb) * NK;
+#pragma unroll
+            for (int u = 0; u < TJ; u++) {  // (16 NK floats = TJ runs of 256)
+                const int f = 256 * u + 4 * lane, row = f / NK, col = f % NK;
+                *reinterpret_cast<float4*>(dst + f) = *reinterpret_cast<const float4*>(q + row * SQ + col);
+            }
+        }
     };
     for (int c = c0; c < c1; c++) {
         if (c + 1 < c1) fetch(c + 1, (c - c0 + 1) & 1);
